@@ -1,0 +1,318 @@
+#!/usr/bin/env python3
+"""Decode-attention benchmark on one MI355X (config 3 of the baseline: the HBM-roofline target).
+
+Workload ("config3"): Llama-3-8B attention shape, 32 query / 8 KV heads, head dim 128, bf16,
+batch 16, per-head spectral layout (8 groups, rank 128, row = b*8 + g), cache of 8192 tokens
+growing by one token per step, retained dims r ~ clipped Beta with mean 0.29 and tokens 0-3
+plus a seeded 5% forced to 128. Synthetic data generated on the device; the packed cache and all
+per-step inputs are resident in HBM before the timed region.
+
+One step = decode append of K and V for all 128 rows + the router decision + decode attention
+(long route: split-K kernel with two-stage semantics, then merge/projection).
+
+Output: one JSON line. ``value`` is decode-attention GB/s: algorithmic bytes of the attention
+(packed K/V coefficients read once, int32 lengths, unique bases, q and output) divided by the
+GPU time of the attention launches, summed over the timed steps (HIP events on the stream the
+kernels run on). ``roofline`` is the split kernel alone; ``cpu_baseline`` times the masked-
+dimension CPU path on a bounded sample of the same inputs.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import subprocess
+import sys
+import time
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+
+
+def _log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+class Config3:
+    name = "config3"
+    B, G, Hq, Dh, R = 16, 8, 32, 128, 128
+    S0 = 8192
+    mean = 0.29
+    theta = 500000.0
+    dtype = torch.bfloat16
+    force_first = 4
+    force_frac = 0.05
+
+
+class Config2:
+    """Config 2 shape for one layer (the 32-layer stack repeats it): fp16, B=4, S=480."""
+    name = "config2_layer"
+    B, G, Hq, Dh, R = 4, 8, 32, 128, 128
+    S0 = 480
+    mean = 0.47
+    theta = 500000.0
+    dtype = torch.float16
+    force_first = 0
+    force_frac = 0.0
+
+
+def build_workload(cfg, total_steps, dev, seed=1234):
+    from dynakv_amd.kernels.compressed_cache import CustomDynamicCache
+    from dynakv_amd.synthetic import device_lengths, random_orthogonal
+
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    rows = cfg.B * cfg.G
+    S_all = cfg.S0 + total_steps
+    lk = device_lengths(rows, S_all, cfg.R, cfg.mean, gen, dev, cfg.force_first, cfg.force_frac)
+    lv = device_lengths(rows, S_all, cfg.R, cfg.mean, gen, dev, cfg.force_first, cfg.force_frac)
+    rng = np.random.default_rng(seed)
+    kb = np.stack([random_orthogonal(cfg.R, rng).T for _ in range(cfg.G)])
+    vb = np.stack([random_orthogonal(cfg.R, rng).T for _ in range(cfg.G)])
+    k_basis = torch.from_numpy(kb).to(dev, cfg.dtype).contiguous()
+    v_basis = torch.from_numpy(vb).to(dev, cfg.dtype).contiguous()
+    cache = CustomDynamicCache()
+    kx = torch.randn((rows, cfg.S0, cfg.R), generator=gen, device=dev).to(cfg.dtype)
+    vx = torch.randn((rows, cfg.S0, cfg.R), generator=gen, device=dev).to(cfg.dtype)
+    cache.update_sp(kx, lk[:, : cfg.S0].contiguous(), vx, lv[:, : cfg.S0].contiguous(), cfg.R, 0,
+                    cfg.R)
+    del kx, vx
+    steps_k = torch.randn((total_steps, rows, 1, cfg.R), generator=gen, device=dev).to(cfg.dtype)
+    steps_v = torch.randn((total_steps, rows, 1, cfg.R), generator=gen, device=dev).to(cfg.dtype)
+    q = torch.randn((total_steps, cfg.B, cfg.Hq, cfg.Dh), generator=gen, device=dev).to(cfg.dtype)
+    lk_steps = lk[:, cfg.S0:].t().contiguous().unsqueeze(-1)  # (steps, rows, 1)
+    lv_steps = lv[:, cfg.S0:].t().contiguous().unsqueeze(-1)
+    # host copies of the per-token counts for byte accounting (outside any timed region)
+    lk_h = lk.to(torch.int64).cpu().numpy()
+    lv_h = lv.to(torch.int64).cpu().numpy()
+    torch.cuda.synchronize(dev)
+    return dict(cache=cache, k_basis=k_basis, v_basis=v_basis, steps_k=steps_k, steps_v=steps_v,
+                q=q, lk_steps=lk_steps, lv_steps=lv_steps, lk_h=lk_h, lv_h=lv_h, gen=gen)
+
+
+def attention_bytes(cfg, lk_h, lv_h, S):
+    """Algorithmic HBM bytes of one decode-attention call at cache length S."""
+    elt = 2
+    coef = elt * (int(lk_h[:, :S].sum()) + int(lv_h[:, :S].sum()))
+    lens = 8 * cfg.B * cfg.G * S
+    bases = 2 * cfg.G * cfg.R * cfg.Dh * elt
+    qo = 2 * cfg.B * cfg.Hq * cfg.Dh * elt
+    return coef + lens + bases + qo
+
+
+class SplitKRunner:
+    """Launches the three phases of dkv_decode_splitk with events around each on the current
+    stream (the stream the kernels run on)."""
+
+    def __init__(self, cfg, dev, max_S):
+        from dynakv_amd import _lib
+
+        self.lib = _lib.load()
+        self._lib = _lib
+        self.cfg = cfg
+        self.dev = dev
+        nfl = self.lib.dkv_splitk_workspace_floats(cfg.B, cfg.Hq, cfg.G, max_S, cfg.R, 0)
+        self.ws = torch.empty(int(nfl), dtype=torch.float32, device=dev)
+        self.out = torch.empty((cfg.B, cfg.Hq, cfg.Dh), dtype=cfg.dtype, device=dev)
+        self.log_theta = math.log(cfg.theta)
+
+    def run(self, q, fk, fv, lk, ok, lv, ov, kb, vb, route, ev=None):
+        cfg, L = self.cfg, self._lib
+        S = lk.shape[1]
+        st = torch.cuda.current_stream(self.dev)
+        args = (st.cuda_stream, route, L.dtype_code(cfg.dtype),
+                q.data_ptr(), q.stride(0), q.stride(1),
+                kb.data_ptr(), kb.stride(0), kb.stride(1), vb.data_ptr(), vb.stride(0), vb.stride(1),
+                fk.data_ptr(), fk.stride(0), fv.data_ptr(), fv.stride(0),
+                lk.data_ptr(), ok.data_ptr(), lk.stride(0), lk.stride(1),
+                lv.data_ptr(), ov.data_ptr(), lv.stride(0), lv.stride(1),
+                self.ws.data_ptr(), self.ws.numel(), self.out.data_ptr(), self.out.stride(0),
+                self.out.stride(1), cfg.B, cfg.Hq, cfg.G, cfg.G, S, cfg.R, cfg.Dh,
+                self.log_theta, 0)
+        if ev is not None:
+            ev[0].record(st)
+        L.check(self.lib.dkv_decode_splitk_phase(0, *args), "rope")
+        if ev is not None:
+            ev[1].record(st)
+        L.check(self.lib.dkv_decode_splitk_phase(1, *args), "split")
+        if ev is not None:
+            ev[2].record(st)
+        L.check(self.lib.dkv_decode_splitk_phase(2, *args), "merge")
+        if ev is not None:
+            ev[3].record(st)
+        return self.out
+
+
+def run_gpu(cfg, steps, warmup, dev):
+    from dynakv_amd import _lib
+    from dynakv_amd.kernels.router import KernelPolicy
+
+    total = steps + warmup
+    _log(f"building {cfg.name} workload (B={cfg.B}, S0={cfg.S0}, steps={total})")
+    W = build_workload(cfg, total, dev)
+    cache = W["cache"]
+    runner = SplitKRunner(cfg, dev, cfg.S0 + total + 16)
+    policy = KernelPolicy()
+    R = cfg.R
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
+    step_bytes = []
+
+    def one_step(i, ev):
+        fk, fv, lk, lv, ok, ov = cache.update_sp(W["steps_k"][i], W["lk_steps"][i], W["steps_v"][i],
+                                                 W["lv_steps"][i], R, 0, R)
+        L = cache.get_seq_length_sp(0)
+        route = (_lib.DKV_ROUTE_FUSED if policy.select(L) == "short_fused"
+                 else _lib.DKV_ROUTE_TWO_STAGE)
+        runner.run(W["q"][i], fk, fv, lk, ok, lv, ov, W["k_basis"], W["v_basis"], route, ev)
+        return L
+
+    for i in range(warmup):
+        one_step(i, None)
+    torch.cuda.synchronize(dev)
+    _log("timed region")
+    t0 = time.perf_counter()
+    for j in range(steps):
+        L = one_step(warmup + j, events[j])
+        step_bytes.append(attention_bytes(cfg, W["lk_h"], W["lv_h"], L))
+    torch.cuda.synchronize(dev)
+    wall = time.perf_counter() - t0
+    rope_ms = sum(e[0].elapsed_time(e[1]) for e in events)
+    split_ms = sum(e[1].elapsed_time(e[2]) for e in events)
+    merge_ms = sum(e[2].elapsed_time(e[3]) for e in events)
+    attn_ms = sum(e[0].elapsed_time(e[3]) for e in events)
+    tot_bytes = float(sum(step_bytes))
+    res = dict(
+        wall_s=wall, attn_ms=attn_ms, split_ms=split_ms, rope_ms=rope_ms, merge_ms=merge_ms,
+        bytes_total=tot_bytes, bytes_per_step=tot_bytes / steps,
+        final_len=cache.get_seq_length_sp(0), syncs=cache.device_syncs,
+        q0=W["q"][0], cache=cache, workload=W,
+    )
+    return res
+
+
+def cpu_baseline(cfg, W, cache, budget_s: float):
+    """Masked-dimension CPU path (oracle.masked_dim, fp32 torch) on batch row 0 of the same
+    cache: dense masked coefficients for the 8 groups, block-diagonal joint basis, full
+    reconstruction + RoPE + eager attention per step."""
+    from oracle import masked_dim as M
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    G, R, Dh = cfg.G, cfg.R, cfg.Dh
+    dk, dv = cache.get_origin_states(R, 0)  # (rows, S, R) on the device
+    S = dk.shape[1]
+    ck = dk[:G].float().cpu().permute(1, 0, 2).reshape(1, S, G * R).contiguous()
+    cv = dv[:G].float().cpu().permute(1, 0, 2).reshape(1, S, G * R).contiguous()
+    Uk = M.block_diag_up(W["k_basis"].float().cpu())
+    Uv = M.block_diag_up(W["v_basis"].float().cpu())
+    q = W["q"][0][:1].float().cpu()
+    n, t0 = 0, time.perf_counter()
+    while True:
+        M.decode_attention(q, ck, cv, Uk, Uv, G, cfg.theta)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or n >= 50:
+            break
+    per_call = el / n
+    lk_h, lv_h = W["lk_h"][:G], W["lv_h"][:G]
+    bytes_row = 2 * (int(lk_h[:, :S].sum()) + int(lv_h[:, :S].sum())) + 8 * G * S \
+        + 2 * G * R * Dh * 2 + 2 * cfg.Hq * Dh * 2
+    try:
+        model = subprocess.run(["lscpu"], capture_output=True, text=True).stdout
+        model = next((l.split(":", 1)[1].strip() for l in model.splitlines()
+                      if l.startswith("Model name")), platform.processor())
+    except Exception:
+        model = platform.processor()
+    return {
+        "value": bytes_row / per_call / 1e9,
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"batch row 0 of 16 (8 KV groups, S={S}), {n} decode-attention calls of the "
+                   f"masked-dimension fp32 torch path (dense 1024-d masked coefficients, "
+                   f"block-diagonal basis), {per_call * 1e3:.1f} ms/call on {model}"),
+        "ms_per_layer_step_full_batch_extrapolated": per_call * 1e3 * cfg.B,
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="config3", choices=["config3", "config2"])
+    ap.add_argument("--cpu-baseline-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (see the sharding "
+              "design); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    cfg = Config3 if args.workload == "config3" else Config2
+    r = run_gpu(cfg, args.steps, args.warmup, dev)
+    attn_s = r["attn_ms"] / 1e3
+    gbs = r["bytes_total"] / attn_s / 1e9
+    split_avg_s = r["split_ms"] / 1e3 / args.steps
+    achieved = r["bytes_per_step"] / split_avg_s / 1e9
+    line = {
+        "metric": "decode-attn GB/s (% HBM peak) + decode tokens/s, Llama-3-8B shape, 1 GPU",
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(r["wall_s"] * 1e3 / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if cfg.dtype == torch.bfloat16 else "fp16",
+        "data": "synthetic (seeded, generated on device; random orthogonal per-group bases)",
+        "config": {
+            "workload": cfg.name,
+            "batch": cfg.B, "q_heads": cfg.Hq, "kv_heads": cfg.G, "head_dim": cfg.Dh,
+            "rank": cfg.R, "cache_len_start": cfg.S0, "cache_len_end": r["final_len"],
+            "mean_retention": cfg.mean, "route": "long_two_stage", "layout": "per-head (G=8, R=128)",
+        },
+        "pct_hbm_peak": round(100.0 * gbs / HBM_PEAK_GBS, 2),
+        "decode_attn_us_per_step": round(r["attn_ms"] * 1e3 / args.steps, 3),
+        "decode_tokens_per_s_attention_only": round(cfg.B * args.steps / attn_s, 1),
+        "decode_tokens_per_s_step_wall": round(cfg.B * args.steps / r["wall_s"], 1),
+        "phase_us_per_step": {
+            "rope_table": round(r["rope_ms"] * 1e3 / args.steps, 3),
+            "split": round(r["split_ms"] * 1e3 / args.steps, 3),
+            "merge": round(r["merge_ms"] * 1e3 / args.steps, 3),
+        },
+        "host_syncs_total": r["syncs"],
+        "roofline": {
+            "kernel": "splitk_kernel<bf16, two_stage>",
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+        },
+    }
+    if not args.no_cpu_baseline:
+        _log("cpu baseline")
+        line["cpu_baseline"] = cpu_baseline(cfg, r["workload"], r["cache"], args.cpu_baseline_seconds)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,114 @@
+"""ctypes binding of ``libdynakv_amd.so`` (the C ABI declared in ``include/dynakv_amd.h``).
+
+The library is loaded lazily and only from this package's ``lib/`` directory. There is no
+fallback: if the library is missing the call raises, so a GPU run can never silently take a
+CPU or eager-PyTorch path.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import threading
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "lib" / "libdynakv_amd.so"
+
+DKV_F32, DKV_F16, DKV_BF16 = 0, 1, 2
+DKV_OK, DKV_E_ARG, DKV_E_UNSUPPORTED, DKV_E_WORKSPACE = 0, -1, -2, -3
+DKV_E_HIP_BASE = 1000
+DKV_ROUTE_FUSED, DKV_ROUTE_TWO_STAGE = 0, 1
+
+_DTYPE_CODE = {torch.float32: DKV_F32, torch.float16: DKV_F16, torch.bfloat16: DKV_BF16}
+
+_vp, _ll, _i, _f = C.c_void_p, C.c_longlong, C.c_int, C.c_float
+
+# name -> (restype, argtypes); must match include/dynakv_amd.h
+_SIGNATURES = {
+    "dkv_version": (_i, []),
+    "dkv_status_string": (C.c_char_p, [_i]),
+    "dkv_append_decode": (_i, [_vp, _i, _vp, _ll, _vp, _ll, _vp, _ll, _vp, _vp, _ll, _ll, _vp, _i, _i, _i]),
+    "dkv_append_decode_kv": (_i, [_vp, _i, _i, _i, _i,
+                                  _vp, _ll, _vp, _ll, _vp, _ll, _vp, _vp, _ll, _ll, _vp,
+                                  _vp, _ll, _vp, _ll, _vp, _ll, _vp, _vp, _ll, _ll, _vp]),
+    "dkv_append_prefill": (_i, [_vp, _i, _vp, _ll, _ll, _vp, _ll, _ll, _vp, _ll, _vp, _vp, _ll, _ll,
+                                _vp, _i, _i, _i, _i]),
+    "dkv_decompress": (_i, [_vp, _i, _vp, _ll, _vp, _vp, _ll, _ll, _vp, _i, _i, _i]),
+    "dkv_scores": (_i, [_vp, _i, _i, _i, _i, _vp, _ll, _ll, _vp, _ll, _ll, _i, _vp, _ll,
+                        _vp, _ll, _ll, _vp, _ll, _ll, _vp, _ll, _ll, _ll, _i, _i, _i, _i, _i, _f]),
+    "dkv_av": (_i, [_vp, _i, _i, _i, _i, _vp, _ll, _ll, _ll, _vp, _ll, _ll, _i, _vp, _ll,
+                    _vp, _ll, _ll, _vp, _ll, _ll, _vp, _ll, _ll, _i, _i, _i, _i, _i]),
+    "dkv_splitk_workspace_floats": (_ll, [_i, _i, _i, _i, _i, _i]),
+    "dkv_splitk_choose_split": (_i, [_i, _i, _i]),
+    "dkv_decode_splitk": (_i, [_vp, _i, _i, _vp, _ll, _ll, _vp, _ll, _ll, _vp, _ll, _ll,
+                               _vp, _ll, _vp, _ll, _vp, _vp, _ll, _ll, _vp, _vp, _ll, _ll,
+                               _vp, _ll, _vp, _ll, _ll, _i, _i, _i, _i, _i, _i, _i, _f, _i]),
+    "dkv_decode_splitk_phase": (_i, [_i, _vp, _i, _i, _vp, _ll, _ll, _vp, _ll, _ll, _vp, _ll, _ll,
+                                     _vp, _ll, _vp, _ll, _vp, _vp, _ll, _ll, _vp, _vp, _ll, _ll,
+                                     _vp, _ll, _vp, _ll, _ll, _i, _i, _i, _i, _i, _i, _i, _f, _i]),
+    "dkv_selftest_layouts": (_i, [_vp, _vp]),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+class DynaKVError(RuntimeError):
+    """A HIP runtime failure reported by the native library."""
+
+
+def load() -> C.CDLL:
+    """Load the native library (once). Raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise RuntimeError(
+                    f"dynakv_amd native library not found at {LIB_PATH}; "
+                    "build it with `python -m dynakv_amd.build`")
+            # torch is imported first so its HIP runtime (same SONAME) is the one the
+            # library binds to; streams and pointers are then shared with torch.
+            lib = C.CDLL(str(LIB_PATH))
+            for name, (res, args) in _SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = lib
+    return _lib
+
+
+def exported_symbols() -> list[str]:
+    return list(_SIGNATURES)
+
+
+def check(status: int, what: str) -> None:
+    if status == DKV_OK:
+        return
+    msg = load().dkv_status_string(status).decode()
+    if status in (DKV_E_ARG, DKV_E_WORKSPACE):
+        raise ValueError(f"{what}: {msg}")
+    if status == DKV_E_UNSUPPORTED:
+        raise NotImplementedError(f"{what}: {msg}")
+    raise DynaKVError(f"{what}: {msg} (status {status})")
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    try:
+        return _DTYPE_CODE[dt]
+    except KeyError:
+        raise ValueError(f"unsupported dtype {dt}") from None
+
+
+def stream_of(t: torch.Tensor) -> int:
+    """Raw hipStream_t of torch's current stream on t's device."""
+    if t.device.type != "cuda":
+        raise RuntimeError(
+            f"dynakv_amd kernels need device tensors (got {t.device}); there is no CPU path")
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()

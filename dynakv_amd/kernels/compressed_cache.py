@@ -1,0 +1,248 @@
+"""Variable-length packed spectral KV cache (drop-in ``CustomDynamicCache``).
+
+Mirrors the reference ``src/dynakv/kernels/compressed_cache.py:58-227``. Per layer and per K/V
+the cache holds the list ``[flat, lens, offs, ptr, seq, ub]``:
+
+* ``flat``  ``(rows, cap_flat)`` packed coefficients in the states' dtype, zero outside
+  ``[0, ptr[b])``;
+* ``lens``/``offs`` ``(rows, cap_seq)`` int32; ``offs`` is the exclusive prefix sum of ``lens``;
+* ``ptr``   ``(rows,)`` int32 on the device, next free element of each row;
+* ``seq``   host int, number of tokens stored;
+* ``ub``    host list, an upper bound of ``ptr`` that lets decode steps skip device reads.
+
+The capacity policy is the reference's, so buffer shapes match it exactly:
+sequence capacity grows to ``max(cap + 1024, seq + new)``; on a decode step the flat capacity
+is checked against ``max(ub) + new * max_dim`` and only then is ``ptr`` read back; growth goes to
+``max(cap + 1024 * (max_dim // 2), max(ptr) + added)``. Device work (append, prefill packing,
+re-expansion) runs in the gfx950 kernels of ``libdynakv_amd``; the decode step issues one
+launch for K and V together.
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from .. import _lib
+
+try:  # the HF cache base class keeps the object usable where transformers expects a Cache
+    from transformers.cache_utils import DynamicCache as _CacheBase
+except Exception:  # pragma: no cover - transformers is optional for the kernels
+    _CacheBase = object
+
+EXPAND_SEQ_STEP = 1024
+
+
+def _max_dim_of(tensor_d) -> int:
+    if isinstance(tensor_d, torch.Tensor):
+        return int(tensor_d.max().item())
+    return int(tensor_d)
+
+
+def seq_capacity_after(cap_seq: int, seq: int, new_s: int) -> int:
+    """Sequence-table capacity after adding ``new_s`` tokens (reference :135-145)."""
+    if seq + new_s > cap_seq:
+        return max(cap_seq + EXPAND_SEQ_STEP, seq + new_s)
+    return cap_seq
+
+
+def flat_capacity_after(cap_flat: int, real_ptrs: list[int], added: int, max_dim: int) -> int:
+    """Flat capacity once the true pointers are known (reference :158-168)."""
+    if max(real_ptrs) + added > cap_flat:
+        return max(cap_flat + EXPAND_SEQ_STEP * (max_dim // 2), max(real_ptrs) + added)
+    return cap_flat
+
+
+class CustomDynamicCache(_CacheBase):
+    def __init__(self, config=None, max_batch_size=None, max_cache_len=None, dtype=None,
+                 device=None, layer_device_map=None, **kwargs):
+        if _CacheBase is not object:
+            super().__init__()
+        # stored for API compatibility (the reference keeps them but never reads them)
+        self.dkv_max_batch_size = max_batch_size
+        self.dkv_max_cache_len = max_cache_len
+        self.dtype = dtype
+        self.device = device
+        self.layer_device_map = layer_device_map
+        self.key_cache_sp: list = []
+        self.value_cache_sp: list = []
+        self.device_syncs = 0  # host reads of device state (growth checks, prefill bounds)
+
+    # ------------------------------------------------------------------ queries
+    def get_origin_states(self, max_dim, layer_idx):
+        """Dense ``(rows, seq, max_dim)`` K and V coefficients (reference :70-81)."""
+        c_k = self.key_cache_sp[layer_idx]
+        c_v = self.value_cache_sp[layer_idx]
+        return self._decompress(c_k, max_dim), self._decompress(c_v, max_dim)
+
+    def reset(self):
+        self.key_cache_sp = []
+        self.value_cache_sp = []
+
+    def get_seq_length_sp(self, layer_idx: Optional[int] = 0) -> int:
+        if len(self.key_cache_sp) <= layer_idx:
+            return 0
+        if self.key_cache_sp[layer_idx] is None:
+            return 0
+        return self.key_cache_sp[layer_idx][4]
+
+    def get_seq_length(self, layer_idx: Optional[int] = 0) -> int:
+        """Expose the compressed sequence length through the HF Cache API."""
+        return self.get_seq_length_sp(layer_idx)
+
+    # ------------------------------------------------------------------ updates
+    def _prepare_slot(self, cache_list, layer_idx, new_states, new_len, max_dim, is_decode):
+        """Host-side bookkeeping of one slot; returns ``(cache, added)`` ready for the kernel."""
+        while len(cache_list) <= layer_idx:
+            cache_list.append(None)
+        B, new_s = new_len.shape
+        if cache_list[layer_idx] is None:
+            init_flat = int(new_len.sum(dim=1).max().item())
+            self.device_syncs += 1
+            flat = new_states.new_zeros(B, init_flat)
+            lens = torch.zeros(B, new_s, dtype=torch.int32, device=new_len.device)
+            offs = torch.zeros(B, new_s, dtype=torch.int32, device=new_len.device)
+            ptr = torch.zeros(B, dtype=torch.int32, device=new_states.device)
+            cache_list[layer_idx] = [flat, lens, offs, ptr, 0, [0] * B]
+        cache = cache_list[layer_idx]
+        flat, lens, offs, ptr, seq, ub = cache
+
+        new_cap = seq_capacity_after(lens.shape[1], seq, new_s)
+        if new_cap != lens.shape[1]:
+            nl = lens.new_zeros(B, new_cap)
+            nl[:, :seq].copy_(lens[:, :seq])
+            no = offs.new_zeros(B, new_cap)
+            no[:, :seq].copy_(offs[:, :seq])
+            cache[1], cache[2] = nl, no
+
+        if is_decode:
+            added = new_s * max_dim
+        else:
+            added = int(new_len.sum(dim=1).max().item())
+            self.device_syncs += 1
+        if max(ub) + added > flat.shape[1]:
+            real = ptr.cpu().tolist()
+            self.device_syncs += 1
+            cache[5] = real
+            cap = flat_capacity_after(flat.shape[1], real, added, max_dim)
+            if cap != flat.shape[1]:
+                nf = flat.new_zeros(B, cap)
+                # beyond ptr[b] the old buffer is zero, so one block copy equals the per-row
+                # prefix copies of the reference
+                nf[:, : flat.shape[1]].copy_(flat)
+                cache[0] = nf
+        return cache, added
+
+    def _finish_slot(self, cache, new_s, added, is_decode):
+        cache[4] = cache[4] + new_s
+        if is_decode:
+            cache[5] = [p + added for p in cache[5]]
+
+    def _launch_prefill(self, cache, new_states, new_len, max_dim):
+        flat, lens, offs, ptr, seq, _ = cache
+        B, new_s = new_len.shape
+        st = _lib.stream_of(flat)
+        states = new_states if new_states.stride(-1) == 1 else new_states.contiguous()
+        nl = new_len.to(torch.int32)
+        rc = _lib.load().dkv_append_prefill(
+            st, _lib.dtype_code(flat.dtype), states.data_ptr(), states.stride(0), states.stride(1),
+            nl.data_ptr(), nl.stride(0), nl.stride(1), flat.data_ptr(), flat.stride(0),
+            lens.data_ptr(), offs.data_ptr(), lens.stride(0), lens.stride(1),
+            ptr.data_ptr(), seq, B, new_s, max_dim)
+        _lib.check(rc, "dkv_append_prefill")
+        cache[5] = ptr.cpu().tolist()
+        self.device_syncs += 1
+
+    @staticmethod
+    def _decode_view(new_states, new_len):
+        states = new_states.reshape(new_states.shape[0], -1)
+        if states.stride(1) != 1:
+            states = states.contiguous()
+        nl = new_len.to(torch.int32)
+        return states, nl
+
+    def _update_layer_cache(self, cache_list, layer_idx, new_states, new_len, tensor_d,
+                            is_decode=False):
+        max_dim = _max_dim_of(tensor_d)
+        cache, added = self._prepare_slot(cache_list, layer_idx, new_states, new_len, max_dim,
+                                          is_decode)
+        if is_decode:
+            flat, lens, offs, ptr, seq, _ = cache
+            states, nl = self._decode_view(new_states, new_len)
+            rc = _lib.load().dkv_append_decode(
+                _lib.stream_of(flat), _lib.dtype_code(flat.dtype), states.data_ptr(),
+                states.stride(0), nl.data_ptr(), nl.stride(0), flat.data_ptr(), flat.stride(0),
+                lens.data_ptr(), offs.data_ptr(), lens.stride(0), lens.stride(1), ptr.data_ptr(),
+                seq, new_len.shape[0], max_dim)
+            _lib.check(rc, "dkv_append_decode")
+        else:
+            self._launch_prefill(cache, new_states, new_len, max_dim)
+        self._finish_slot(cache, new_len.shape[1], added, is_decode)
+
+    def update_sp(self, key_states, key_len, value_states, value_len, max_dim, layer_idx,
+                  tensor_d, k_scalar=None, v_scalar=None):
+        """Append K and V coefficients of ``layer_idx`` (reference :219-227).
+
+        Decode (``key_states.shape[1] == 1``) issues a single launch for both slots.
+        Returns ``(flat_k, flat_v, lens_k, lens_v, offs_k, offs_v)`` with the tables cut to the
+        stored length.
+        """
+        is_decode = key_states.shape[1] == 1
+        if is_decode:
+            md = _max_dim_of(tensor_d)
+            ck, add_k = self._prepare_slot(self.key_cache_sp, layer_idx, key_states, key_len, md, True)
+            cv, add_v = self._prepare_slot(self.value_cache_sp, layer_idx, value_states, value_len,
+                                           md, True)
+            if ck[4] != cv[4] or ck[0].dtype != cv[0].dtype:
+                # K and V slots out of step: fall back to one launch each
+                self._launch_decode_single(ck, key_states, key_len, md)
+                self._launch_decode_single(cv, value_states, value_len, md)
+            else:
+                ks, kl = self._decode_view(key_states, key_len)
+                vs, vl = self._decode_view(value_states, value_len)
+                fk, lk, ok, pk, seq, _ = ck
+                fv, lv, ov, pv, _, _ = cv
+                rc = _lib.load().dkv_append_decode_kv(
+                    _lib.stream_of(fk), _lib.dtype_code(fk.dtype), key_len.shape[0], md, seq,
+                    ks.data_ptr(), ks.stride(0), kl.data_ptr(), kl.stride(0),
+                    fk.data_ptr(), fk.stride(0), lk.data_ptr(), ok.data_ptr(),
+                    lk.stride(0), lk.stride(1), pk.data_ptr(),
+                    vs.data_ptr(), vs.stride(0), vl.data_ptr(), vl.stride(0),
+                    fv.data_ptr(), fv.stride(0), lv.data_ptr(), ov.data_ptr(),
+                    lv.stride(0), lv.stride(1), pv.data_ptr())
+                _lib.check(rc, "dkv_append_decode_kv")
+            self._finish_slot(ck, key_len.shape[1], add_k, True)
+            self._finish_slot(cv, value_len.shape[1], add_v, True)
+        else:
+            self._update_layer_cache(self.key_cache_sp, layer_idx, key_states, key_len, tensor_d,
+                                     is_decode=False)
+            self._update_layer_cache(self.value_cache_sp, layer_idx, value_states, value_len,
+                                     tensor_d, is_decode=False)
+        c_k = self.key_cache_sp[layer_idx]
+        c_v = self.value_cache_sp[layer_idx]
+        return (c_k[0], c_v[0], c_k[1][:, : c_k[4]], c_v[1][:, : c_v[4]],
+                c_k[2][:, : c_k[4]], c_v[2][:, : c_v[4]])
+
+    def _launch_decode_single(self, cache, new_states, new_len, max_dim):
+        flat, lens, offs, ptr, seq, _ = cache
+        states, nl = self._decode_view(new_states, new_len)
+        rc = _lib.load().dkv_append_decode(
+            _lib.stream_of(flat), _lib.dtype_code(flat.dtype), states.data_ptr(), states.stride(0),
+            nl.data_ptr(), nl.stride(0), flat.data_ptr(), flat.stride(0), lens.data_ptr(),
+            offs.data_ptr(), lens.stride(0), lens.stride(1), ptr.data_ptr(), seq,
+            new_len.shape[0], max_dim)
+        _lib.check(rc, "dkv_append_decode")
+
+    def _decompress(self, cache, max_dim):
+        flat, lens, offs, _, seq, _ = cache
+        rows = flat.shape[0]
+        out = flat.new_empty(rows, seq, max_dim)
+        if rows == 0 or seq == 0:
+            return out.zero_()
+        rc = _lib.load().dkv_decompress(
+            _lib.stream_of(flat), _lib.dtype_code(flat.dtype), flat.data_ptr(), flat.stride(0),
+            lens.data_ptr(), offs.data_ptr(), lens.stride(0), lens.stride(1), out.data_ptr(),
+            rows, seq, max_dim)
+        _lib.check(rc, "dkv_decompress")
+        return out

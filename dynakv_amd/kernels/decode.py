@@ -1,0 +1,140 @@
+"""Host side of the gfx950 split-K decode-attention kernel.
+
+``splitk_attention`` launches ``dkv_decode_splitk`` (RoPE table, split kernel, merge/projection)
+on torch's current stream. It is used by both router routes when the inputs fit the kernel and,
+directly, by the native multi-group layout (per-head spectral bases, one packed cache row per
+(batch, KV group)): ``grouped_decode_attention``.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+from .. import _lib
+
+SPLITK_MAX_RANK = 128
+SPLITK_HEAD_DIM = 128
+SPLITK_MAX_HPG = 16
+
+
+@dataclass(frozen=True)
+class UnitLayout:
+    """How query heads map onto the kernel's work units (one unit per KV basis)."""
+
+    n_kv: int          # distinct bases (work units per batch row)
+    k_unit: int        # element stride between consecutive bases in k_up
+    v_unit: int
+    k_basis: torch.Tensor
+    v_basis: torch.Tensor
+
+
+def _basis_ok(t: torch.Tensor) -> bool:
+    return (t.dim() == 3 and t.stride(2) == 1 and t.stride(1) % 8 == 0
+            and t.stride(0) % 8 == 0 and t.data_ptr() % 16 == 0)
+
+
+def splitk_layout(q3: torch.Tensor, k_up: torch.Tensor, v_up: torch.Tensor,
+                  k_flat: torch.Tensor, v_flat: torch.Tensor) -> UnitLayout | None:
+    """Unit layout for the split-K kernel, or ``None`` when the inputs need the vector path.
+
+    Bases of shape ``(Hb, R, Dh)`` with ``Hb < Hq`` are shared by ``Hq / Hb`` consecutive query
+    heads (the reference's ``HEADS_PER_GROUP``); ``Hb == Hq`` with a zero head stride (an
+    ``expand``) is one shared basis; otherwise every query head is its own unit.
+    """
+    dt = q3.dtype
+    if dt not in (torch.float16, torch.bfloat16) or q3.device.type != "cuda":
+        return None
+    if not (k_flat.dtype == v_flat.dtype == k_up.dtype == v_up.dtype == dt):
+        return None
+    if k_up.dim() != 3 or v_up.shape != k_up.shape:
+        return None
+    hb, r, dh = k_up.shape
+    B, hq, qdh = q3.shape
+    if dh != SPLITK_HEAD_DIM or qdh != dh or r > SPLITK_MAX_RANK or r <= 0 or hq % hb:
+        return None
+    if k_flat.dim() != 2 or v_flat.dim() != 2 or k_flat.stride(1) != 1 or v_flat.stride(1) != 1:
+        return None
+    if k_flat.stride(0) * 2 >= 2**31 or v_flat.stride(0) * 2 >= 2**31:
+        return None
+    if hb == hq and k_up.stride(0) == 0 and v_up.stride(0) == 0:
+        n_kv = 1
+    else:
+        n_kv = hb
+    if hq // n_kv > SPLITK_MAX_HPG:
+        return None
+    kb, vb = k_up, v_up
+    if not _basis_ok(kb):
+        kb = kb.contiguous()
+        if n_kv == 1 and hb == hq:
+            kb = kb[:1]
+    if not _basis_ok(vb):
+        vb = vb.contiguous()
+        if n_kv == 1 and hb == hq:
+            vb = vb[:1]
+    return UnitLayout(n_kv, kb.stride(0), vb.stride(0), kb, vb)
+
+
+def splitk_attention(q3: torch.Tensor, k_flat: torch.Tensor, v_flat: torch.Tensor,
+                     layout: UnitLayout, lens_k: torch.Tensor, offs_k: torch.Tensor,
+                     lens_v: torch.Tensor, offs_v: torch.Tensor, *, theta: float, route: int,
+                     groups: int = 1, split_len: int = 0,
+                     out: torch.Tensor | None = None) -> torch.Tensor:
+    """Run the split-K kernel. ``q3``: (B, Hq, 128); tables: (B*groups, S) int32."""
+    lib = _lib.load()
+    B, hq, dh = q3.shape
+    if q3.stride(2) != 1:
+        q3 = q3.contiguous()
+    S = lens_k.shape[1]
+    R = layout.k_basis.shape[1]
+    for t in (lens_k, offs_k, lens_v, offs_v):
+        if t.dtype != torch.int32:
+            raise ValueError("length/offset tables must be int32")
+    if offs_k.stride() != lens_k.stride() or offs_v.stride() != lens_v.stride():
+        lens_k, offs_k = lens_k.contiguous(), offs_k.contiguous()
+        lens_v, offs_v = lens_v.contiguous(), offs_v.contiguous()
+    if out is None:
+        out = torch.empty((B, hq, dh), dtype=q3.dtype, device=q3.device)
+    nfl = lib.dkv_splitk_workspace_floats(B, hq, layout.n_kv, S, R, split_len)
+    ws = torch.empty(max(int(nfl), 1), dtype=torch.float32, device=q3.device)
+    st = _lib.stream_of(q3)
+    rc = lib.dkv_decode_splitk(
+        st, route, _lib.dtype_code(q3.dtype),
+        q3.data_ptr(), q3.stride(0), q3.stride(1),
+        layout.k_basis.data_ptr(), layout.k_unit, layout.k_basis.stride(1),
+        layout.v_basis.data_ptr(), layout.v_unit, layout.v_basis.stride(1),
+        k_flat.data_ptr(), k_flat.stride(0), v_flat.data_ptr(), v_flat.stride(0),
+        lens_k.data_ptr(), offs_k.data_ptr(), lens_k.stride(0), lens_k.stride(1),
+        lens_v.data_ptr(), offs_v.data_ptr(), lens_v.stride(0), lens_v.stride(1),
+        ws.data_ptr(), ws.numel(), out.data_ptr(), out.stride(0), out.stride(1),
+        B, hq, layout.n_kv, groups, S, R, dh, math.log(theta), split_len)
+    _lib.check(rc, "dkv_decode_splitk")
+    return out
+
+
+def grouped_decode_attention(q: torch.Tensor, k_flat: torch.Tensor, v_flat: torch.Tensor,
+                             lens_k: torch.Tensor, offs_k: torch.Tensor,
+                             lens_v: torch.Tensor, offs_v: torch.Tensor,
+                             k_basis: torch.Tensor, v_basis: torch.Tensor, *, theta: float,
+                             route: str = "long_two_stage", split_len: int = 0,
+                             out: torch.Tensor | None = None) -> torch.Tensor:
+    """Per-head spectral layout: one packed row per (batch b, KV group g), row = b*G + g.
+
+    ``q``: (B, Hq, Dh) or (B, Hq, 1, Dh); ``k_basis``/``v_basis``: (G, R, Dh) with the basis of
+    group g shared by query heads ``g*Hq/G ... (g+1)*Hq/G - 1``; tables ``(B*G, S)``.
+    ``route`` is a router decision string and selects the route semantics.
+    """
+    q3 = q.squeeze(2) if q.dim() == 4 else q
+    G = k_basis.shape[0]
+    B = q3.shape[0]
+    if lens_k.shape[0] != B * G:
+        raise ValueError(f"tables have {lens_k.shape[0]} rows, expected B*G = {B * G}")
+    layout = splitk_layout(q3, k_basis, v_basis, k_flat, v_flat)
+    if layout is None or layout.n_kv != G:
+        raise NotImplementedError("grouped_decode_attention needs f16/bf16, Dh=128, R<=128, "
+                                  "Hq/G <= 16 and one basis per group")
+    rt = _lib.DKV_ROUTE_FUSED if route == "short_fused" else _lib.DKV_ROUTE_TWO_STAGE
+    return splitk_attention(q3, k_flat, v_flat, layout, lens_k, offs_k, lens_v, offs_v,
+                            theta=theta, route=rt, groups=G, split_len=split_len, out=out)

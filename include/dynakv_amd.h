@@ -1,0 +1,215 @@
+/*
+ * dynakv_amd.h — C ABI of the MI355X (gfx950) compressed-KV-cache decode path.
+ *
+ * Every entry point:
+ *   - takes plain device pointers, element strides and sizes (no framework types);
+ *   - is stream-ordered and asynchronous on `stream` (a hipStream_t passed as void*;
+ *     NULL means the default stream) and never synchronises the device;
+ *   - never allocates or frees device memory: outputs and workspaces belong to the caller;
+ *   - returns DKV_OK (0) or a negative status (DKV_E_*), or -(DKV_E_HIP_BASE + hipError_t)
+ *     when a HIP launch fails.
+ *
+ * Cache layout (one "slot" = one layer's K or V cache, mirroring the reference's
+ * per-layer list [flat, lens, offs, flat_ptr, seq_ptr, ub]):
+ *   flat  (rows, cap_flat)   coefficient payload, dtype = cache dtype; token t of row b
+ *                            occupies flat[b, offs[b,t] : offs[b,t] + lens[b,t]]
+ *   lens  (rows, cap_seq)    int32 retained-dimension count per token
+ *   offs  (rows, cap_seq)    int32 start of each token's packed row (exclusive prefix sum)
+ *   ptr   (rows,)            int32 next free element per row
+ * A row is one batch element (reference "joint" layout) or one (batch, KV-group) pair
+ * (per-head layout: row = b * G + g).
+ */
+#ifndef DYNAKV_AMD_H
+#define DYNAKV_AMD_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* dtype codes */
+#define DKV_F32 0
+#define DKV_F16 1
+#define DKV_BF16 2
+
+/* status codes */
+#define DKV_OK 0
+#define DKV_E_ARG (-1)       /* invalid argument (shape, stride, dtype, null pointer) */
+#define DKV_E_UNSUPPORTED (-2) /* valid arguments outside what the kernel implements */
+#define DKV_E_WORKSPACE (-3) /* caller workspace too small */
+#define DKV_E_HIP_BASE 1000  /* -(1000 + hipError_t) for HIP runtime failures */
+
+/* decode-attention semantics ("route") */
+#define DKV_ROUTE_FUSED 0     /* reference fused.py: -inf for len_K==0, no score rounding, acc/l */
+#define DKV_ROUTE_TWO_STAGE 1 /* reference two_stage.py: -1e4*scale for len_K==0, scores rounded
+                                 to the query dtype, acc/max(l,1e-6) */
+
+/* Library version (major*10000 + minor*100 + patch). */
+int dkv_version(void);
+
+/* Human-readable message for a status code (static storage). */
+const char* dkv_status_string(int status);
+
+/*
+ * Decode append: one new token per row.
+ * Replaces update_cache_decode_kernel and its launch
+ * (reference src/dynakv/kernels/compressed_cache.py:7-34, launch :170-181).
+ * For each row b:  off = ptr[b]; ptr[b] += new_len[b];
+ *                  lens[b, seq_pos] = new_len[b]; offs[b, seq_pos] = off;
+ *                  flat[b, off + j] = states[b, j]  for j < min(new_len[b], max_dim).
+ * states: (rows, max_dim) with row stride states_ld (elements); new_len: int32 with stride
+ * new_len_ld; lens/offs tables share strides (tab_sb, tab_ss); flat row stride flat_ld.
+ * The caller guarantees capacity (host-side growth policy), exactly as the reference does.
+ */
+int dkv_append_decode(void* stream, int dtype,
+                      const void* states, long long states_ld,
+                      const int* new_len, long long new_len_ld,
+                      void* flat, long long flat_ld,
+                      int* lens, int* offs, long long tab_sb, long long tab_ss,
+                      int* ptr, int seq_pos, int rows, int max_dim);
+
+/*
+ * Decode append for K and V of one layer in one launch (the reference issues two
+ * update_cache_decode_kernel launches per layer, compressed_cache.py:222-223).
+ * Same per-slot semantics as dkv_append_decode; *_k arguments describe the K slot and
+ * *_v arguments the V slot. Both slots have the same dtype, rows, max_dim and seq_pos.
+ */
+int dkv_append_decode_kv(void* stream, int dtype, int rows, int max_dim, int seq_pos,
+                         const void* states_k, long long states_k_ld,
+                         const int* new_len_k, long long new_len_k_ld,
+                         void* flat_k, long long flat_k_ld,
+                         int* lens_k, int* offs_k, long long tab_k_sb, long long tab_k_ss,
+                         int* ptr_k,
+                         const void* states_v, long long states_v_ld,
+                         const int* new_len_v, long long new_len_v_ld,
+                         void* flat_v, long long flat_v_ld,
+                         int* lens_v, int* offs_v, long long tab_v_sb, long long tab_v_ss,
+                         int* ptr_v);
+
+/*
+ * Prefill append of n_new tokens per row, without host synchronisation.
+ * Replaces the per-row Python loop of the prefill branch
+ * (reference src/dynakv/kernels/compressed_cache.py:182-209).
+ * For each row b, with start = ptr[b]:
+ *   offs[b, seq_pos + t] = start + sum_{t' < t} new_len[b, t']          (unclamped lengths)
+ *   lens[b, seq_pos + t] = new_len[b, t]
+ *   the first min(new_len[b,t], max_dim) elements of states[b, t, :] are written back to
+ *   back starting at start (clamped prefix sums), and ptr[b] += sum_t min(new_len[b,t], max_dim).
+ * states: (rows, n_new, max_dim) with strides (states_sb, states_ss), unit inner stride;
+ * new_len: int32 (rows, n_new) with strides (len_sb, len_ss).
+ */
+int dkv_append_prefill(void* stream, int dtype,
+                       const void* states, long long states_sb, long long states_ss,
+                       const int* new_len, long long len_sb, long long len_ss,
+                       void* flat, long long flat_ld,
+                       int* lens, int* offs, long long tab_sb, long long tab_ss,
+                       int* ptr, int seq_pos, int rows, int n_new, int max_dim);
+
+/*
+ * Dense re-expansion of a packed slot: out[b, t, j] = flat[b, offs[b,t] + j] for
+ * j < min(lens[b,t], max_dim), else 0. out is (rows, seq, max_dim) contiguous, cache dtype.
+ * Replaces simple_decompress (reference src/dynakv/kernels/compressed_cache.py:36-56),
+ * which lays tokens back to back from element 0 of each row, i.e. uses the prefix sum of the
+ * lengths rather than offs; both agree whenever offs is the exclusive prefix sum from 0.
+ */
+int dkv_decompress(void* stream, int dtype,
+                   const void* flat, long long flat_ld,
+                   const int* lens, const int* offs, long long tab_sb, long long tab_ss,
+                   void* out, int rows, int seq, int max_dim);
+
+/*
+ * Reference-semantics QK scores (abx_sparse / _abx_sparse_fwd, reference two_stage.py:48-189).
+ *   z[b,h,s] = round_out( ((len>0) ? q_h . RoPE_s(x_s @ basis[h / hpg]) : -1e4) / sqrt(Dh) )
+ * with x_s = flat[b, offs[b,s] : offs[b,s] + min(len, R)], rotate-half RoPE at position s,
+ * inv_freq_i = exp(-(2i/Dh) ln theta) in fp32, hpg = Hq / n_basis.
+ * mode 0: abx semantics (out dtype = out_dtype, -1e4 masking before the scale).
+ * mode 1: fused semantics (out must be fp32, -inf masking, no rounding).
+ * q: (B, Hq, Dh) strides (q_sb, q_sh), unit dim stride, dtype = q_dtype.
+ * basis: (n_basis, R, Dh) strides (basis_sh, basis_sr), unit dim stride, dtype = cache dtype.
+ * out: (B, Hq, S) strides (out_sb, out_sh, out_ss).
+ * Dh must be even and <= 128.
+ */
+int dkv_scores(void* stream, int mode, int q_dtype, int cache_dtype, int out_dtype,
+               const void* q, long long q_sb, long long q_sh,
+               const void* basis, long long basis_sh, long long basis_sr, int n_basis,
+               const void* flat, long long flat_ld,
+               const int* lens, long long lens_sb, long long lens_ss,
+               const int* offs, long long offs_sb, long long offs_ss,
+               void* out, long long out_sb, long long out_sh, long long out_ss,
+               int B, int Hq, int S, int R, int Dh, float log_theta);
+
+/*
+ * Reference-semantics softmax-weighted V (avx / _avx_proj_fwd, reference two_stage.py:207-324):
+ *   out[b,h] = ((sum_s e^{z_s - m} x^V_s) @ basis[h / hpg]) / D,
+ *   D = max(sum_s e^{z_s - m}, 1e-6) in mode 0 (avx), D = sum_s e^{z_s - m} in mode 1 (fused).
+ * scores: (B, Hq, S) strides (sc_sb, sc_sh, sc_ss) of dtype scores_dtype.
+ * out: (B, Hq, Dh) strides (out_sb, out_sh), unit dim stride, dtype out_dtype.
+ * R <= 1024, Dh <= 128.
+ */
+int dkv_av(void* stream, int mode, int scores_dtype, int cache_dtype, int out_dtype,
+           const void* scores, long long sc_sb, long long sc_sh, long long sc_ss,
+           const void* basis, long long basis_sh, long long basis_sr, int n_basis,
+           const void* flat, long long flat_ld,
+           const int* lens, long long lens_sb, long long lens_ss,
+           const int* offs, long long offs_sb, long long offs_ss,
+           void* out, long long out_sb, long long out_sh,
+           int B, int Hq, int S, int R, int Dh);
+
+/*
+ * Split-K compressed decode attention on MFMA (the fast path for both router routes,
+ * reference fused.py:28-170 and two_stage.py:48-324 as called from router.py:20-59).
+ * One work unit = (batch b, KV head k) with hpg = Hq / Hkv query heads sharing the K/V basis
+ * of KV head k; its coefficients live in cache row b * G + k / (Hkv / G).
+ *   q: (B, Hq, Dh) strides (q_sb, q_sh), already RoPE'd by the caller.
+ *   k_basis / v_basis: base pointers with basis of KV head k at  base + k * unit_stride,
+ *                      rank stride basis_sr, unit dim stride (R x Dh).
+ *   lens/offs tables for K and V with their own (sb, ss) strides.
+ *   partials: fp32 workspace of dkv_splitk_workspace_floats(...) floats.
+ *   out: (B, Hq, Dh) strides (out_sb, out_sh), dtype q_dtype.
+ * Requirements: q and cache dtype f16 or bf16 (same), Dh == 128, R <= 128, hpg <= 16,
+ * Hkv % G == 0. split_len is a multiple of 64 (0 = choose automatically).
+ * The launch pair is split kernel + merge kernel; both are asynchronous.
+ */
+long long dkv_splitk_workspace_floats(int B, int Hq, int Hkv, int S, int R, int split_len);
+int dkv_splitk_choose_split(int B, int Hkv, int S);
+int dkv_decode_splitk(void* stream, int route, int dtype,
+                      const void* q, long long q_sb, long long q_sh,
+                      const void* k_basis, long long k_unit_stride, long long k_basis_sr,
+                      const void* v_basis, long long v_unit_stride, long long v_basis_sr,
+                      const void* k_flat, long long k_ld, const void* v_flat, long long v_ld,
+                      const int* lens_k, const int* offs_k, long long tk_sb, long long tk_ss,
+                      const int* lens_v, const int* offs_v, long long tv_sb, long long tv_ss,
+                      float* partials, long long partials_floats,
+                      void* out, long long out_sb, long long out_sh,
+                      int B, int Hq, int Hkv, int G, int S, int R, int Dh,
+                      float log_theta, int split_len);
+
+/*
+ * One phase of dkv_decode_splitk (same arguments): 0 = RoPE cos/sin table into the workspace,
+ * 1 = split kernel (partials), 2 = merge + V projection. Running 0, 1, 2 in order on one
+ * stream equals dkv_decode_splitk; the phases exist so callers can time the split kernel alone.
+ */
+int dkv_decode_splitk_phase(int phase, void* stream, int route, int dtype,
+                            const void* q, long long q_sb, long long q_sh,
+                            const void* k_basis, long long k_unit_stride, long long k_basis_sr,
+                            const void* v_basis, long long v_unit_stride, long long v_basis_sr,
+                            const void* k_flat, long long k_ld, const void* v_flat, long long v_ld,
+                            const int* lens_k, const int* offs_k, long long tk_sb, long long tk_ss,
+                            const int* lens_v, const int* offs_v, long long tv_sb, long long tv_ss,
+                            float* partials, long long partials_floats,
+                            void* out, long long out_sb, long long out_sh,
+                            int B, int Hq, int Hkv, int G, int S, int R, int Dh,
+                            float log_theta, int split_len);
+
+/*
+ * Launch-layout self test (diagnostic, no reference counterpart): runs the MFMA operand
+ * layouts and unaligned buffer gathers the split-K kernel relies on against a scalar
+ * computation of the same products, on the device. `mismatches` points at a zeroed device
+ * buffer of at least 1280 bytes; the number of mismatching elements is added to its first
+ * int (the rest is scratch). Used by the GPU test suite before parity tests.
+ */
+int dkv_selftest_layouts(void* stream, int* mismatches);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* DYNAKV_AMD_H */

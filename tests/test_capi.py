@@ -1,0 +1,79 @@
+"""The C-ABI library loads and exports every function declared in include/dynakv_amd.h, the ctypes
+signatures match the header's parameter counts, and host-only calls behave (no device needed)."""
+import os
+import re
+
+import pytest
+import torch
+
+from dynakv_amd import _lib
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(__file__)), "include", "dynakv_amd.h")
+
+
+def _header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    out = {}
+    for m in re.finditer(r"\b(?:int|long long|const char\*)\s+(dkv_\w+)\s*\(([^)]*)\)\s*;", text):
+        params = [p.strip() for p in m.group(2).split(",") if p.strip() and p.strip() != "void"]
+        out[m.group(1)] = len(params)
+    return out
+
+
+def test_header_parses():
+    fns = _header_functions()
+    assert "dkv_decode_splitk" in fns and "dkv_append_decode" in fns
+    assert len(fns) >= 13
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in _header_functions():
+        assert hasattr(lib, name), name
+
+
+def test_ctypes_signatures_match_header():
+    fns = _header_functions()
+    assert set(fns) == set(_lib.exported_symbols())
+    for name, n in fns.items():
+        assert len(_lib._SIGNATURES[name][1]) == n, name
+
+
+def test_host_only_entry_points():
+    lib = _lib.load()
+    assert lib.dkv_version() >= 100
+    assert lib.dkv_status_string(-1) == b"invalid argument"
+    sl = lib.dkv_splitk_choose_split(16, 8, 8292)
+    assert sl % 64 == 0 and (8292 + sl - 1) // sl <= 63
+    assert lib.dkv_splitk_workspace_floats(16, 32, 8, 8292, 128, sl) > 0
+
+
+def test_argument_validation_without_device():
+    lib = _lib.load()
+    # invalid dtype / negative sizes are rejected before any launch
+    assert lib.dkv_append_decode(None, 7, None, 0, None, 0, None, 0, None, None, 0, 0, None, 0, 1, 4) == -1
+    assert lib.dkv_append_decode(None, 1, None, 0, None, 0, None, 0, None, None, 0, 0, None, 0, -1, 4) == -1
+    # zero rows is a no-op
+    assert lib.dkv_append_decode(None, 1, None, 0, None, 0, None, 0, None, None, 0, 0, None, 0, 0, 4) == 0
+    # split-K: rank above 128 is outside the kernel
+    rc = lib.dkv_decode_splitk(None, 0, 2, None, 0, 0, None, 0, 0, None, 0, 0, None, 0, None, 0,
+                               None, None, 0, 0, None, None, 0, 0, None, 0, None, 0, 0,
+                               1, 32, 8, 8, 10, 256, 128, 1.0, 0)
+    assert rc == -2
+    with pytest.raises(NotImplementedError):
+        _lib.check(rc, "dkv_decode_splitk")
+
+
+def test_no_cpu_fallback():
+    from dynakv_amd.kernels.two_stage import abx_sparse
+
+    a = torch.zeros(1, 4, 128)
+    b = torch.zeros(1, 16, 128)
+    x = torch.zeros(1, 64)
+    l = torch.ones(1, 4, dtype=torch.int32)
+    o = torch.zeros(1, 4, dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        abx_sparse(a, b, x, l, offsets=o)
+    with pytest.raises(ValueError, match="offsets are required"):
+        abx_sparse(a, b, x, l, offsets=None)

@@ -1,0 +1,107 @@
+"""Packed cache on the GPU against the packing oracle: decode appends (single and K+V launch),
+prefill packing (multi-chunk), growth/reallocation, re-expansion. Bit-exact: buffers (including
+capacity), lengths, offsets, pointers, host bookkeeping."""
+import numpy as np
+import pytest
+import torch
+
+from dynakv_amd.kernels.compressed_cache import CustomDynamicCache
+from oracle.packing import PackedSlot
+
+DTYPES = [torch.float32, torch.float16, torch.bfloat16]
+
+
+def _cmp_slot(dev_slot, ref: PackedSlot, what):
+    flat, lens, offs, ptr, seq, ub = dev_slot
+    assert tuple(flat.shape) == ref.flat.shape, (what, flat.shape, ref.flat.shape)
+    assert tuple(lens.shape) == ref.lens.shape and tuple(offs.shape) == ref.offs.shape, what
+    np.testing.assert_array_equal(flat.float().cpu().numpy(), ref.flat.astype(np.float32), what)
+    np.testing.assert_array_equal(lens.cpu().numpy(), ref.lens, what)
+    np.testing.assert_array_equal(offs.cpu().numpy(), ref.offs, what)
+    np.testing.assert_array_equal(ptr.cpu().numpy().astype(np.int64), ref.ptr, what)
+    assert seq == ref.seq and list(ub) == list(ref.ub), (what, ub, ref.ub)
+
+
+def _rounded(x, dtype):
+    return torch.from_numpy(x).to(dtype)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("max_dim,B", [(16, 3), (128, 5)])
+def test_prefill_then_decode_matches_oracle(dev, dtype, max_dim, B):
+    print(f"[gpu] cache prefill+decode dtype={dtype} max_dim={max_dim} B={B}", flush=True)
+    rng = np.random.default_rng(max_dim + B)
+    cache = CustomDynamicCache()
+    rk, rv = PackedSlot(), PackedSlot()
+    n_pre = 300  # more than one 256-token chunk of the prefill kernel
+    ks = rng.standard_normal((B, n_pre, max_dim)).astype(np.float32)
+    vs = rng.standard_normal((B, n_pre, max_dim)).astype(np.float32)
+    kl = rng.integers(0, max_dim + 1, size=(B, n_pre)).astype(np.int32)
+    vl = rng.integers(1, max_dim + 1, size=(B, n_pre)).astype(np.int32)
+    tk, tv = _rounded(ks, dtype), _rounded(vs, dtype)
+    cache.update_sp(tk.to(dev), torch.from_numpy(kl).to(dev), tv.to(dev),
+                    torch.from_numpy(vl).to(dev), max_dim, 0, max_dim)
+    rk.append_prefill(tk.float().numpy(), kl, max_dim)
+    rv.append_prefill(tv.float().numpy(), vl, max_dim)
+    _cmp_slot(cache.key_cache_sp[0], rk, "K after prefill")
+    _cmp_slot(cache.value_cache_sp[0], rv, "V after prefill")
+    for step in range(40):
+        kd = _rounded(rng.standard_normal((B, 1, max_dim)).astype(np.float32), dtype)
+        vd = _rounded(rng.standard_normal((B, 1, max_dim)).astype(np.float32), dtype)
+        kdl = rng.integers(0, max_dim + 1, size=(B, 1)).astype(np.int32)
+        vdl = rng.integers(0, max_dim + 1, size=(B, 1)).astype(np.int32)
+        out = cache.update_sp(kd.to(dev), torch.from_numpy(kdl).to(dev), vd.to(dev),
+                              torch.from_numpy(vdl).to(dev), max_dim, 0, max_dim)
+        rk.append_decode(kd.float().numpy(), kdl, max_dim)
+        rv.append_decode(vd.float().numpy(), vdl, max_dim)
+        if step in (0, 1, 39):
+            _cmp_slot(cache.key_cache_sp[0], rk, f"K step {step}")
+            _cmp_slot(cache.value_cache_sp[0], rv, f"V step {step}")
+    lk, ok = rk.tables()
+    np.testing.assert_array_equal(out[2].cpu().numpy(), lk)
+    np.testing.assert_array_equal(out[4].cpu().numpy(), ok)
+    assert cache.get_seq_length_sp(0) == n_pre + 40 == cache.get_seq_length(0)
+    dk, dv = cache.get_origin_states(max_dim, 0)
+    np.testing.assert_array_equal(dk.float().cpu().numpy(), rk.decompress(max_dim).astype(np.float32))
+    np.testing.assert_array_equal(dv.float().cpu().numpy(), rv.decompress(max_dim).astype(np.float32))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_decode_from_empty_and_reset(dev, dtype):
+    print(f"[gpu] cache decode-from-empty dtype={dtype}", flush=True)
+    rng = np.random.default_rng(7)
+    cache = CustomDynamicCache()
+    ref = PackedSlot()
+    B, D = 4, 64
+    for layer in (0, 2):  # lazy creation of a non-contiguous layer slot
+        for _ in range(30):
+            x = _rounded(rng.standard_normal((B, 1, D)).astype(np.float32), dtype)
+            l = rng.integers(1, D + 1, size=(B, 1)).astype(np.int32)
+            cache.update_sp(x.to(dev), torch.from_numpy(l).to(dev), x.to(dev),
+                            torch.from_numpy(l).to(dev), D, layer, torch.full((B, 1), D, device=dev))
+            if layer == 0:
+                ref.append_decode(x.float().numpy(), l, D)
+    _cmp_slot(cache.key_cache_sp[0], ref, "K layer 0")
+    assert cache.key_cache_sp[1] is None and cache.get_seq_length_sp(1) == 0
+    assert cache.get_seq_length_sp(2) == 30 and cache.get_seq_length_sp(7) == 0
+    cache.reset()
+    assert cache.key_cache_sp == [] and cache.get_seq_length_sp(0) == 0
+
+
+@pytest.mark.gpu
+def test_single_slot_append_path(dev):
+    """The one-slot launch (used when K and V slots are out of step) matches too."""
+    print("[gpu] cache single-slot append", flush=True)
+    rng = np.random.default_rng(3)
+    cache = CustomDynamicCache()
+    ref = PackedSlot()
+    B, D = 2, 32
+    for _ in range(10):
+        x = _rounded(rng.standard_normal((B, 1, D)).astype(np.float32), torch.float16)
+        l = rng.integers(0, D + 1, size=(B, 1)).astype(np.int32)
+        cache._update_layer_cache(cache.key_cache_sp, 0, x.to(dev), torch.from_numpy(l).to(dev), D,
+                                  is_decode=True)
+        ref.append_decode(x.float().numpy(), l, D)
+    _cmp_slot(cache.key_cache_sp[0], ref, "K single")

@@ -1,0 +1,123 @@
+"""End to end on the GPU: the packed cache fed by decode appends, the router's decision per step,
+and the attention output of each step against the oracle -- across the 500-token switch
+(config 2 shape) and for a ragged batch of per-sequence caches (config 4)."""
+import numpy as np
+import pytest
+import torch
+
+from dynakv_amd.kernels.compressed_cache import CustomDynamicCache
+from dynakv_amd.kernels.decode import grouped_decode_attention
+from dynakv_amd.kernels.router import KernelPolicy, compressed_decode_attention
+from dynakv_amd.synthetic import beta_lengths, log_uniform_lengths, make_case
+from oracle import attention as A
+from oracle import router as oracle_router
+from oracle.packing import PackedSlot
+
+from helpers import NP_OF, assert_close, cast_np
+
+
+@pytest.mark.gpu
+def test_decode_steps_across_switch(dev):
+    """Config 2 shape (fp16, B=4, 8 groups, mean retention 0.47) from S=480 for 30 steps: the
+    router turns from fused to two-stage at 500; every step matches the oracle and the cache
+    layout stays bit-exact."""
+    print("[gpu] router decode steps across switch", flush=True)
+    dtype = torch.float16
+    B, G, Hq, R, S0, steps = 4, 8, 32, 128, 480, 30
+    rows = B * G
+    case = make_case(B=B, G=G, Hq=Hq, S=S0, mean=0.47, seed=40)
+    rng = np.random.default_rng(41)
+    cache = CustomDynamicCache()
+    ok_k, ok_v = PackedSlot(), PackedSlot()
+    kc = cast_np(case.k_coef, dtype)
+    vc = cast_np(case.v_coef, dtype)
+    cache.update_sp(torch.from_numpy(kc).to(dev, dtype), torch.from_numpy(case.k_len).to(dev),
+                    torch.from_numpy(vc).to(dev, dtype), torch.from_numpy(case.v_len).to(dev),
+                    R, 0, R)
+    ok_k.append_prefill(kc, case.k_len, R)
+    ok_v.append_prefill(vc, case.v_len, R)
+    kb = torch.from_numpy(cast_np(case.k_basis, dtype)).to(dev, dtype)
+    vb = torch.from_numpy(cast_np(case.v_basis, dtype)).to(dev, dtype)
+    policy = KernelPolicy()
+    routes = []
+    for step in range(steps):
+        kx = cast_np(rng.standard_normal((rows, 1, R)), dtype)
+        vx = cast_np(rng.standard_normal((rows, 1, R)), dtype)
+        kl = beta_lengths((rows, 1), 0.47, R, rng)
+        vl = beta_lengths((rows, 1), 0.47, R, rng)
+        fk, fv, lk, lv, okk, ovv = cache.update_sp(
+            torch.from_numpy(kx).to(dev, dtype), torch.from_numpy(kl).to(dev),
+            torch.from_numpy(vx).to(dev, dtype), torch.from_numpy(vl).to(dev), R, 0, R)
+        ok_k.append_decode(kx, kl, R)
+        ok_v.append_decode(vx, vl, R)
+        L = cache.get_seq_length_sp(0)
+        route = policy.select(L)
+        assert route == oracle_router.select(L)
+        routes.append(route)
+        q = cast_np(rng.standard_normal((B, Hq, 128)), dtype)
+        got = grouped_decode_attention(torch.from_numpy(q).to(dev, dtype), fk, fv, lk, okk, lv,
+                                       ovv, kb, vb, theta=case.theta, route=route)
+        hk, ho = ok_k.tables()
+        hv, hov = ok_v.tables()
+        np.testing.assert_array_equal(lk.cpu().numpy(), hk)
+        np.testing.assert_array_equal(ovv.cpu().numpy(), hov)
+        if step % 5 == 0 or step in (19, 20):
+            ref = A.decode_attention(q, ok_k.flat, cast_np(case.k_basis, dtype), ok_v.flat,
+                                     cast_np(case.v_basis, dtype), hk, ho, hv, hov, case.theta,
+                                     route=route, q_dtype="float16",
+                                     row_of=lambda b, h: b * G + h // 4, basis_of=lambda h: h // 4)
+            assert_close(got, ref, f"step {step} ({route})")
+    assert routes[:19] == ["short_fused"] * 19 and routes[19:] == ["long_two_stage"] * 11
+
+
+@pytest.mark.gpu
+def test_config4_ragged_batch(dev):
+    """Config 4: 32 sequences with lengths log-uniform in [64, 16384], one B=1 reference cache per
+    sequence (the reference cache shares seq_ptr across a batch), fp16, mean retention 0.20;
+    append one token to every sequence, route each by its own length, compare to the oracle."""
+    print("[gpu] config4 ragged batch", flush=True)
+    dtype = torch.float16
+    G, Hq, R = 8, 32, 128
+    rng = np.random.default_rng(50)
+    lengths = log_uniform_lengths(32, 64, 16384, rng)
+    policy = KernelPolicy(switch_tokens=500)
+    n_fused = 0
+    for i, S0 in enumerate(lengths):
+        S0 = int(S0)
+        case = make_case(B=1, G=G, Hq=Hq, S=S0, mean=0.20, seed=100 + i)
+        kc, vc = cast_np(case.k_coef, dtype), cast_np(case.v_coef, dtype)
+        cache = CustomDynamicCache()
+        cache.update_sp(torch.from_numpy(kc).to(dev, dtype), torch.from_numpy(case.k_len).to(dev),
+                        torch.from_numpy(vc).to(dev, dtype), torch.from_numpy(case.v_len).to(dev),
+                        R, 0, R)
+        kx = cast_np(rng.standard_normal((G, 1, R)), dtype)
+        kl = beta_lengths((G, 1), 0.20, R, rng)
+        fk, fv, lk, lv, okk, ovv = cache.update_sp(
+            torch.from_numpy(kx).to(dev, dtype), torch.from_numpy(kl).to(dev),
+            torch.from_numpy(kx).to(dev, dtype), torch.from_numpy(kl).to(dev), R, 0, R)
+        L = cache.get_seq_length_sp(0)
+        assert L == S0 + 1
+        route = policy.select(L)
+        n_fused += route == "short_fused"
+        q = cast_np(rng.standard_normal((1, Hq, 128)), dtype)
+        kb = torch.from_numpy(cast_np(case.k_basis, dtype)).to(dev, dtype)
+        vb = torch.from_numpy(cast_np(case.v_basis, dtype)).to(dev, dtype)
+        got = grouped_decode_attention(torch.from_numpy(q).to(dev, dtype), fk, fv, lk, okk, lv,
+                                       ovv, kb, vb, theta=case.theta, route=route)
+        # oracle over the same packed tables (checked bit-exact against the packing oracle)
+        sk, sv = PackedSlot(), PackedSlot()
+        sk.append_prefill(kc, case.k_len, R)
+        sv.append_prefill(vc, case.v_len, R)
+        sk.append_decode(kx, kl, R)
+        sv.append_decode(kx, kl, R)
+        hk, ho = sk.tables()
+        hv, hov = sv.tables()
+        np.testing.assert_array_equal(okk.cpu().numpy(), ho)
+        np.testing.assert_array_equal(fk[:, : int(sk.ptr.max())].float().cpu().numpy(),
+                                      sk.flat[:, : int(sk.ptr.max())].astype(np.float32))
+        ref = A.decode_attention(q, sk.flat, cast_np(case.k_basis, dtype), sv.flat,
+                                 cast_np(case.v_basis, dtype), hk, ho, hv, hov, case.theta,
+                                 route=route, q_dtype="float16",
+                                 row_of=lambda b, h: h // 4, basis_of=lambda h: h // 4)
+        assert_close(got, ref, f"seq {i} S={L} {route}")
+    assert 0 < n_fused < 32

@@ -1,0 +1,128 @@
+"""The gfx950 split-K kernel (both routes) against the oracle, per-head layout (row = b*G + g)."""
+import numpy as np
+import pytest
+import torch
+
+from dynakv_amd.kernels.decode import grouped_decode_attention
+from dynakv_amd.kernels.router import compressed_decode_attention
+from dynakv_amd.synthetic import make_case
+
+from helpers import NP_OF, assert_close, oracle_grouped, packed_from_case
+
+ROUTES = ["short_fused", "long_two_stage"]
+
+
+def _run(p, case, route, split_len=0):
+    return grouped_decode_attention(
+        p["q"], p["k_flat"], p["v_flat"], p["lens_k"], p["offs_k"], p["lens_v"], p["offs_v"],
+        p["k_basis"], p["v_basis"], theta=case.theta, route=route, split_len=split_len)
+
+
+CASES = {
+    # name: (make_case kwargs, dtype)
+    "cfg1_shape_f16": (dict(B=1, G=8, Hq=32, S=257, uniform=(8, 128), seed=11), torch.float16),
+    "cfg1_shape_bf16": (dict(B=1, G=8, Hq=32, S=257, uniform=(8, 128), seed=12), torch.bfloat16),
+    "cfg2_shape_f16": (dict(B=4, G=8, Hq=32, S=480, mean=0.47, seed=13), torch.float16),
+    "cfg3_shape_bf16_B2": (dict(B=2, G=8, Hq=32, S=8192, mean=0.29, force_first=4,
+                                force_frac=0.05, seed=14), torch.bfloat16),
+    "S1": (dict(B=3, G=8, Hq=32, S=1, uniform=(1, 128), seed=15), torch.float16),
+    "S17_zero_lens": (dict(B=2, G=8, Hq=32, S=17, uniform=(0, 128), seed=16), torch.bfloat16),
+    "zero_len_frac": (dict(B=2, G=4, Hq=16, S=700, mean=0.3, zero_len_frac=0.2, seed=17), torch.float16),
+    "R64": (dict(B=2, G=8, Hq=32, S=333, R=64, uniform=(1, 64), seed=18), torch.bfloat16),
+    "R40": (dict(B=2, G=2, Hq=8, S=129, R=40, uniform=(1, 40), seed=19), torch.float16),
+    "hpg1": (dict(B=2, G=8, Hq=8, S=200, uniform=(1, 128), seed=20), torch.bfloat16),
+    "hpg16": (dict(B=2, G=2, Hq=32, S=200, uniform=(1, 128), seed=21), torch.float16),
+    "r_max_all": (dict(B=1, G=8, Hq=32, S=96, uniform=(128, 128), seed=22), torch.bfloat16),
+}
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("route", ROUTES)
+@pytest.mark.parametrize("name", list(CASES))
+def test_splitk_matches_oracle(dev, name, route):
+    kw, dtype = CASES[name]
+    print(f"[gpu] splitk {name} route={route}", flush=True)
+    case = make_case(**kw)
+    p = packed_from_case(case, dtype, dev)
+    got = _run(p, case, route)
+    ref = oracle_grouped(case, p["host"], route, NP_OF[dtype])
+    assert_close(got, ref, f"{name} {route}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("route", ROUTES)
+def test_split_length_invariance(dev, route):
+    print(f"[gpu] splitk split invariance route={route}", flush=True)
+    case = make_case(B=2, G=8, Hq=32, S=3000, mean=0.29, force_first=4, force_frac=0.05, seed=30)
+    p = packed_from_case(case, torch.bfloat16, dev)
+    ref = oracle_grouped(case, p["host"], route, "bfloat16")
+    outs = [_run(p, case, route, sl) for sl in (64, 192, 1024, 3008)]
+    for o in outs:
+        assert_close(o, ref, f"split {route}")
+    for o in outs[1:]:
+        assert (o.float() - outs[0].float()).abs().max().item() <= 1e-3 * outs[0].float().abs().max().item() + 1e-5
+
+
+@pytest.mark.gpu
+def test_all_keys_empty_in_one_row(dev):
+    print("[gpu] splitk empty-key row", flush=True)
+    case = make_case(B=2, G=2, Hq=8, S=150, uniform=(1, 128), seed=31)
+    case.k_len[1, :] = 0  # row (b=0, g=1): every key excluded
+    for route, dtype in (("short_fused", torch.float16), ("long_two_stage", torch.bfloat16)):
+        p = packed_from_case(case, dtype, dev)
+        got = _run(p, case, route).float().cpu().numpy()
+        ref = oracle_grouped(case, p["host"], route, NP_OF[dtype])
+        if route == "short_fused":
+            assert np.isnan(got[0, 4:8]).all() and np.isfinite(got[0, :4]).all()
+            assert_close(got[:, :4], ref[:, :4], "fused finite part")
+            assert_close(got[1], ref[1], "fused other batch")
+        else:
+            assert_close(got, ref, "two-stage with empty row")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("route", ROUTES)
+def test_full_config3_size_rows_against_oracle(dev, route):
+    """Config 3 at full size (B=16, S=8192, bf16): batch rows 0 and 15 against the oracle, and
+    properties of the whole output (finite, linear in V)."""
+    print(f"[gpu] splitk full config3 route={route}", flush=True)
+    case = make_case(B=16, G=8, Hq=32, S=8192, mean=0.29, force_first=4, force_frac=0.05, seed=32)
+    p = packed_from_case(case, torch.bfloat16, dev)
+    got = _run(p, case, route)
+    assert torch.isfinite(got.float()).all()
+    ref = oracle_grouped(case, p["host"], route, "bfloat16", batches=[0, 15])
+    assert_close(got[[0, 15]], ref, "config3 rows 0,15")
+    # linearity in the V coefficients: doubling every V coefficient doubles the output (exact
+    # in binary floating point up to the final rounding)
+    p2 = dict(p)
+    p2["v_flat"] = p["v_flat"] * 2
+    got2 = _run(p2, case, route)
+    assert_close(got2.float() / 2, got.float().cpu().numpy(), "linearity", tol_abs=1e-3, tol_rel=4e-3)
+
+
+@pytest.mark.gpu
+def test_reference_api_per_group_equals_native(dev):
+    """Per-head mode through the reference surface: one compressed_decode_attention call per KV
+    group with q[:, 4g:4g+4] and the group's basis (as B_g[None] and as an expand) equals the
+    one-launch native call."""
+    print("[gpu] reference API per group", flush=True)
+    case = make_case(B=2, G=8, Hq=32, S=620, mean=0.47, seed=33)
+    p = packed_from_case(case, torch.float16, dev)
+    B, G = case.B, case.G
+    native = _run(p, case, "long_two_stage")
+    for mode in ("slice", "expand"):
+        outs = []
+        for g in range(G):
+            rows = [b * G + g for b in range(B)]
+            kb = p["k_basis"][g: g + 1]
+            vb = p["v_basis"][g: g + 1]
+            if mode == "expand":
+                kb, vb = kb.expand(4, 128, 128), vb.expand(4, 128, 128)
+            outs.append(compressed_decode_attention(
+                q=p["q"][:, 4 * g: 4 * g + 4, None, :].contiguous(), k_flat=p["k_flat"][rows],
+                k_up=kb, v_flat=p["v_flat"][rows], v_up=vb,
+                key_lengths=p["lens_k"][rows], key_offsets=p["offs_k"][rows],
+                value_lengths=p["lens_v"][rows], value_offsets=p["offs_v"][rows],
+                theta=case.theta, cache_length=case.S))
+        per_group = torch.cat(outs, dim=1)
+        assert (per_group.float() - native.float()).abs().max().item() < 1e-3
