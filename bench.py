@@ -136,7 +136,8 @@ class SplitKRunner:
                 lk.data_ptr(), ok.data_ptr(), lk.stride(0), lk.stride(1),
                 lv.data_ptr(), ov.data_ptr(), lv.stride(0), lv.stride(1),
                 self.ws.data_ptr(), self.ws.numel(), self.out.data_ptr(), self.out.stride(0),
-                self.out.stride(1), cfg.B, cfg.Hq, cfg.G, cfg.G, S, cfg.R, cfg.Dh,
+                self.out.stride(1), L.dtype_code(cfg.dtype), cfg.B, cfg.Hq, cfg.G, cfg.G, S,
+                cfg.R, cfg.Dh,
                 self.log_theta, 0)
         if ev is not None:
             ev[0].record(st)

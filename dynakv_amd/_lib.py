@@ -43,10 +43,11 @@ _SIGNATURES = {
     "dkv_splitk_choose_split": (_i, [_i, _i, _i]),
     "dkv_decode_splitk": (_i, [_vp, _i, _i, _vp, _ll, _ll, _vp, _ll, _ll, _vp, _ll, _ll,
                                _vp, _ll, _vp, _ll, _vp, _vp, _ll, _ll, _vp, _vp, _ll, _ll,
-                               _vp, _ll, _vp, _ll, _ll, _i, _i, _i, _i, _i, _i, _i, _f, _i]),
+                               _vp, _ll, _vp, _ll, _ll, _i, _i, _i, _i, _i, _i, _i, _i, _f, _i]),
     "dkv_decode_splitk_phase": (_i, [_i, _vp, _i, _i, _vp, _ll, _ll, _vp, _ll, _ll, _vp, _ll, _ll,
                                      _vp, _ll, _vp, _ll, _vp, _vp, _ll, _ll, _vp, _vp, _ll, _ll,
-                                     _vp, _ll, _vp, _ll, _ll, _i, _i, _i, _i, _i, _i, _i, _f, _i]),
+                                     _vp, _ll, _vp, _ll, _ll, _i, _i, _i, _i, _i, _i, _i, _i, _f,
+                                     _i]),
     "dkv_selftest_layouts": (_i, [_vp, _vp]),
 }
 

@@ -89,6 +89,33 @@ __device__ __forceinline__ float elt_to_f32(uint32_t bits16) {
     return dkv_f16_bits_to_f32(bits16);
 }
 
+__device__ __forceinline__ dkv_f32x4 mfma_f16(const dkv_u32x4& a, const dkv_u32x4& b,
+                                              dkv_f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(dkv_f16x8, a),
+                                                __builtin_bit_cast(dkv_f16x8, b), c, 0, 0, 0);
+}
+
+// x ~= hi + lo with hi = fp16(x) and lo = fp16(x - hi), for two values packed per dword.
+__device__ __forceinline__ void split_f16x2(float x0, float x1, uint32_t& hi, uint32_t& lo) {
+  const _Float16 h0 = (_Float16)x0, h1 = (_Float16)x1;
+  const _Float16 l0 = (_Float16)(x0 - (float)h0), l1 = (_Float16)(x1 - (float)h1);
+  hi = __builtin_bit_cast(uint32_t, dkv_f16x2{h0, h1});
+  lo = __builtin_bit_cast(uint32_t, dkv_f16x2{l0, l1});
+}
+
+// Element-wise gather of the first nv (1..8) 16-bit values at element offset e; the rest zero.
+__device__ __forceinline__ dkv_u32x4 gather8_b16(__amdgpu_buffer_rsrc_t r, int e, int nv) {
+  uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    if (t < nv) {
+      const uint32_t v = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (e + t) * 2, 0, 0);
+      w[t >> 1] |= v << (16 * (t & 1));
+    }
+  }
+  return dkv_u32x4{w[0], w[1], w[2], w[3]};
+}
+
 // Zero the elements at index >= nv (0 <= nv < 8) of an 8 x 16-bit vector.
 __device__ __forceinline__ dkv_u32x4 mask_prefix8(dkv_u32x4 v, int nv) {
   const int nlo = min(nv, 4), nhi = max(nv - 4, 0);
@@ -174,22 +201,23 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(SplitParams p) {
 
   // ---- scaled query as the B operand of the QK MFMA: lane (head slot n, k-group g) holds
   //      (q_i, q_{i+64}) for i = 16*qi + 4*g + w, w = 0..3 --------------------------------
-  dkv_u32x4 bq[4];
+  dkv_u32x4 bq[4], bql[4];  // fp16 hi and lo parts of the scaled query
   {
     const int hs = n;
     const bool real = hs < p.hpg;
     const long long qo = (long long)b * p.q_sb + (long long)(kvh * p.hpg + (real ? hs : 0)) * p.q_sh;
 #pragma unroll
     for (int qi = 0; qi < 4; ++qi) {
-      uint32_t w4[4];
+      uint32_t w4[4], l4[4];
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
         const int i = 16 * qi + 4 * g + w;
         const float a = real ? elt_to_f32<DT>(p.q[qo + i]) * p.q_scale : 0.f;
         const float c = real ? elt_to_f32<DT>(p.q[qo + i + 64]) * p.q_scale : 0.f;
-        w4[w] = pack_f16x2(a, c);
+        split_f16x2(a, c, w4[w], l4[w]);
       }
       bq[qi] = dkv_u32x4{w4[0], w4[1], w4[2], w4[3]};
+      bql[qi] = dkv_u32x4{l4[0], l4[1], l4[2], l4[3]};
     }
   }
 
@@ -254,8 +282,15 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(SplitParams p) {
       const int j0 = 32 * c + 8 * g;
       const int nv = rkc - j0;
       const int boff = nv > 0 ? (ok + j0) * 2 : 0x7ffffff0;
-      dkv_u32x4 xv = __builtin_amdgcn_raw_buffer_load_b128(rk_src, boff, 0, 0);
-      if (nv < 8) xv = mask_prefix8(xv, max(nv, 0));
+      dkv_u32x4 xv;
+      if (nv > 0 && (long long)(ok + j0 + 8) > p.k_ld) {
+        // the 16-byte window would cross the end of the row's buffer, where an out-of-range
+        // vector access reads as all zeros: gather element by element instead
+        xv = gather8_b16(rk_src, ok + j0, nv);
+      } else {
+        xv = __builtin_amdgcn_raw_buffer_load_b128(rk_src, boff, 0, 0);
+        if (nv < 8) xv = mask_prefix8(xv, max(nv, 0));
+      }
 #pragma unroll
       for (int blk = 0; blk < 8; ++blk) {
         const dkv_u32x4 a = *(const dkv_u32x4*)&sBK[(16 * blk + n) * BK_LD + 32 * c + 8 * g];
@@ -264,19 +299,20 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(SplitParams p) {
     }
 
     // ---- 2. RoPE on (i, i+64) pairs, packed to fp16 as the QK A operand -----------------------
-    dkv_u32x4 aq[4];
+    dkv_u32x4 aq[4], aql[4];
 #pragma unroll
     for (int qi = 0; qi < 4; ++qi) {
-      uint32_t w4[4];
+      uint32_t w4[4], l4[4];
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
         const int f = qi * 4 + w;
         const float k0 = ck[qi][w], k1 = ck[qi + 4][w];
         const float r0 = k0 * rc[f] - k1 * rs[f];
         const float r1 = k1 * rc[f] + k0 * rs[f];
-        w4[w] = pack_f16x2(r0, r1);
+        split_f16x2(r0, r1, w4[w], l4[w]);
       }
       aq[qi] = dkv_u32x4{w4[0], w4[1], w4[2], w4[3]};
+      aql[qi] = dkv_u32x4{l4[0], l4[1], l4[2], l4[3]};
     }
     // advance the rotation by WAVES*TILE positions
 #pragma unroll
@@ -288,12 +324,13 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(SplitParams p) {
     }
 
     // ---- 3. scores: lane (head slot n, tokens 4g+u) -----------------------------------------
+    // scores = K'.Q with hi/lo fp16 parts on both sides (~22-bit products, fp32 accumulate)
     dkv_f32x4 sc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int qi = 0; qi < 4; ++qi) {
-      sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(dkv_f16x8, aq[qi]),
-                                                  __builtin_bit_cast(dkv_f16x8, bq[qi]), sc, 0,
-                                                  0, 0);
+      sc = mfma_f16(aql[qi], bq[qi], sc);
+      sc = mfma_f16(aq[qi], bql[qi], sc);
+      sc = mfma_f16(aq[qi], bq[qi], sc);
     }
     const unsigned long long has_bits = __ballot(valid && rk > 0);
     const unsigned long long in_bits = __ballot(valid);
@@ -413,11 +450,11 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(SplitParams p) {
 
 // One block per unit: LSE-merge the splits of each head slot, normalise, project through the
 // V basis of the unit's KV head, store in the query dtype.
-template <int DT, int ROUTE>
+template <int DT, int ROUTE, int ODT>
 __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ partials,
                                                     const uint16_t* __restrict__ v_basis,
                                                     long long v_unit, long long v_sr,
-                                                    uint16_t* __restrict__ out, long long out_sb,
+                                                    void* __restrict__ out, long long out_sb,
                                                     long long out_sh, int Hkv, int hpg,
                                                     int n_splits, int R) {
   __shared__ float s_a[16][DH];
@@ -464,10 +501,7 @@ __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ pa
     float o = 0.f;
     for (int j = 0; j < R; ++j) o = fmaf(s_a[hs][j], elt_to_f32<DT>(vb[(long long)j * v_sr + d]), o);
     const long long oi = (long long)b * out_sb + (long long)(kvh * hpg + hs) * out_sh + d;
-    if constexpr (DT == DKV_BF16)
-      out[oi] = (uint16_t)dkv_f32_to_bf16_bits(o);
-    else
-      out[oi] = (uint16_t)dkv_f32_to_f16_bits(o);
+    dkv_store_f32<ODT>(out, oi, o);
   }
 }
 
@@ -585,7 +619,7 @@ namespace {
 
 struct SplitLaunch {
   SplitParams p;
-  int route, dtype, n_tb;
+  int route, dtype, out_dtype, n_tb;
   long long units;
   const void* v_basis;
   long long v_unit, v_sr;
@@ -601,9 +635,10 @@ int splitk_prepare(SplitLaunch& L, int route, int dtype, const void* q, long lon
                    long long v_ld, const int* lens_k, const int* offs_k, long long tk_sb,
                    long long tk_ss, const int* lens_v, const int* offs_v, long long tv_sb,
                    long long tv_ss, float* partials, long long partials_floats, void* out,
-                   long long out_sb, long long out_sh, int B, int Hq, int Hkv, int G, int S,
-                   int R, int Dh, float log_theta, int split_len) {
+                   long long out_sb, long long out_sh, int out_dtype, int B, int Hq, int Hkv,
+                   int G, int S, int R, int Dh, float log_theta, int split_len) {
   if (route != DKV_ROUTE_FUSED && route != DKV_ROUTE_TWO_STAGE) return DKV_E_ARG;
+  if (out_dtype != dtype && out_dtype != DKV_F32) return DKV_E_ARG;
   if (dtype != DKV_F16 && dtype != DKV_BF16) return DKV_E_UNSUPPORTED;
   if (B < 0 || Hq <= 0 || Hkv <= 0 || G <= 0 || S < 0 || R <= 0) return DKV_E_ARG;
   if (Hq % Hkv != 0 || Hkv % G != 0) return DKV_E_ARG;
@@ -662,6 +697,7 @@ int splitk_prepare(SplitLaunch& L, int route, int dtype, const void* q, long lon
   p.masked_score = -1.0e4f * sm_scale;
   L.route = route;
   L.dtype = dtype;
+  L.out_dtype = out_dtype;
   L.v_basis = v_basis;
   L.v_unit = v_unit_stride;
   L.v_sr = v_basis_sr;
@@ -697,20 +733,27 @@ int launch_split(const SplitLaunch& L, hipStream_t st) {
   return DKV_OK;
 }
 
-int launch_merge(const SplitLaunch& L, hipStream_t st) {
+template <int DT, int RT>
+void launch_merge_t(const SplitLaunch& L, hipStream_t st) {
   const dim3 mgrid((unsigned)L.units), block(256);
-#define DKV_MERGE(DT, RT)                                                                   \
-  hipLaunchKernelGGL((merge_kernel<DT, RT>), mgrid, block, 0, st, L.p.partials,             \
-                     (const uint16_t*)L.v_basis, L.v_unit, L.v_sr, (uint16_t*)L.out, L.out_sb, \
-                     L.out_sh, L.p.Hkv, L.p.hpg, L.p.n_splits, L.p.R)
+  if (L.out_dtype == DKV_F32)
+    hipLaunchKernelGGL((merge_kernel<DT, RT, DKV_F32>), mgrid, block, 0, st, L.p.partials,
+                       (const uint16_t*)L.v_basis, L.v_unit, L.v_sr, L.out, L.out_sb, L.out_sh,
+                       L.p.Hkv, L.p.hpg, L.p.n_splits, L.p.R);
+  else
+    hipLaunchKernelGGL((merge_kernel<DT, RT, DT>), mgrid, block, 0, st, L.p.partials,
+                       (const uint16_t*)L.v_basis, L.v_unit, L.v_sr, L.out, L.out_sb, L.out_sh,
+                       L.p.Hkv, L.p.hpg, L.p.n_splits, L.p.R);
+}
+
+int launch_merge(const SplitLaunch& L, hipStream_t st) {
   if (L.dtype == DKV_BF16) {
-    if (L.route == DKV_ROUTE_FUSED) DKV_MERGE(DKV_BF16, DKV_ROUTE_FUSED);
-    else DKV_MERGE(DKV_BF16, DKV_ROUTE_TWO_STAGE);
+    if (L.route == DKV_ROUTE_FUSED) launch_merge_t<DKV_BF16, DKV_ROUTE_FUSED>(L, st);
+    else launch_merge_t<DKV_BF16, DKV_ROUTE_TWO_STAGE>(L, st);
   } else {
-    if (L.route == DKV_ROUTE_FUSED) DKV_MERGE(DKV_F16, DKV_ROUTE_FUSED);
-    else DKV_MERGE(DKV_F16, DKV_ROUTE_TWO_STAGE);
+    if (L.route == DKV_ROUTE_FUSED) launch_merge_t<DKV_F16, DKV_ROUTE_FUSED>(L, st);
+    else launch_merge_t<DKV_F16, DKV_ROUTE_TWO_STAGE>(L, st);
   }
-#undef DKV_MERGE
   DKV_HIP_CHECK_LAUNCH();
   return DKV_OK;
 }
@@ -724,12 +767,13 @@ int launch_merge(const SplitLaunch& L, hipStream_t st) {
       const void *v_flat, long long v_ld, const int *lens_k, const int *offs_k, long long tk_sb, \
       long long tk_ss, const int *lens_v, const int *offs_v, long long tv_sb, long long tv_ss,  \
       float *partials, long long partials_floats, void *out, long long out_sb, long long out_sh, \
-      int B, int Hq, int Hkv, int G, int S, int R, int Dh, float log_theta, int split_len
+      int out_dtype, int B, int Hq, int Hkv, int G, int S, int R, int Dh, float log_theta,       \
+      int split_len
 #define DKV_SPLITK_FWD                                                                          \
   route, dtype, q, q_sb, q_sh, k_basis, k_unit_stride, k_basis_sr, v_basis, v_unit_stride,      \
       v_basis_sr, k_flat, k_ld, v_flat, v_ld, lens_k, offs_k, tk_sb, tk_ss, lens_v, offs_v,     \
-      tv_sb, tv_ss, partials, partials_floats, out, out_sb, out_sh, B, Hq, Hkv, G, S, R, Dh,    \
-      log_theta, split_len
+      tv_sb, tv_ss, partials, partials_floats, out, out_sb, out_sh, out_dtype, B, Hq, Hkv, G, S,  \
+      R, Dh, log_theta, split_len
 
 extern "C" int dkv_decode_splitk(DKV_SPLITK_ARGS) {
   if (B == 0) return DKV_OK;

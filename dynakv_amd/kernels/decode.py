@@ -81,8 +81,12 @@ def splitk_attention(q3: torch.Tensor, k_flat: torch.Tensor, v_flat: torch.Tenso
                      layout: UnitLayout, lens_k: torch.Tensor, offs_k: torch.Tensor,
                      lens_v: torch.Tensor, offs_v: torch.Tensor, *, theta: float, route: int,
                      groups: int = 1, split_len: int = 0,
-                     out: torch.Tensor | None = None) -> torch.Tensor:
-    """Run the split-K kernel. ``q3``: (B, Hq, 128); tables: (B*groups, S) int32."""
+                     out: torch.Tensor | None = None,
+                     out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """Run the split-K kernel. ``q3``: (B, Hq, 128); tables: (B*groups, S) int32.
+
+    The output is in ``q3``'s dtype (the reference's contract) unless ``out_dtype=torch.float32``
+    asks for the merged result before that rounding."""
     lib = _lib.load()
     B, hq, dh = q3.shape
     if q3.stride(2) != 1:
@@ -95,8 +99,13 @@ def splitk_attention(q3: torch.Tensor, k_flat: torch.Tensor, v_flat: torch.Tenso
     if offs_k.stride() != lens_k.stride() or offs_v.stride() != lens_v.stride():
         lens_k, offs_k = lens_k.contiguous(), offs_k.contiguous()
         lens_v, offs_v = lens_v.contiguous(), offs_v.contiguous()
+    odt = out_dtype if out_dtype is not None else (out.dtype if out is not None else q3.dtype)
+    if odt not in (q3.dtype, torch.float32):
+        raise ValueError("out_dtype must be the query dtype or float32")
     if out is None:
-        out = torch.empty((B, hq, dh), dtype=q3.dtype, device=q3.device)
+        out = torch.empty((B, hq, dh), dtype=odt, device=q3.device)
+    elif out.dtype != odt or out.stride(2) != 1:
+        raise ValueError("out must have unit last stride and the requested dtype")
     nfl = lib.dkv_splitk_workspace_floats(B, hq, layout.n_kv, S, R, split_len)
     ws = torch.empty(max(int(nfl), 1), dtype=torch.float32, device=q3.device)
     st = _lib.stream_of(q3)
@@ -109,7 +118,8 @@ def splitk_attention(q3: torch.Tensor, k_flat: torch.Tensor, v_flat: torch.Tenso
         lens_k.data_ptr(), offs_k.data_ptr(), lens_k.stride(0), lens_k.stride(1),
         lens_v.data_ptr(), offs_v.data_ptr(), lens_v.stride(0), lens_v.stride(1),
         ws.data_ptr(), ws.numel(), out.data_ptr(), out.stride(0), out.stride(1),
-        B, hq, layout.n_kv, groups, S, R, dh, math.log(theta), split_len)
+        _lib.dtype_code(out.dtype), B, hq, layout.n_kv, groups, S, R, dh, math.log(theta),
+        split_len)
     _lib.check(rc, "dkv_decode_splitk")
     return out
 
@@ -119,7 +129,8 @@ def grouped_decode_attention(q: torch.Tensor, k_flat: torch.Tensor, v_flat: torc
                              lens_v: torch.Tensor, offs_v: torch.Tensor,
                              k_basis: torch.Tensor, v_basis: torch.Tensor, *, theta: float,
                              route: str = "long_two_stage", split_len: int = 0,
-                             out: torch.Tensor | None = None) -> torch.Tensor:
+                             out: torch.Tensor | None = None,
+                             out_dtype: torch.dtype | None = None) -> torch.Tensor:
     """Per-head spectral layout: one packed row per (batch b, KV group g), row = b*G + g.
 
     ``q``: (B, Hq, Dh) or (B, Hq, 1, Dh); ``k_basis``/``v_basis``: (G, R, Dh) with the basis of
@@ -137,4 +148,5 @@ def grouped_decode_attention(q: torch.Tensor, k_flat: torch.Tensor, v_flat: torc
                                   "Hq/G <= 16 and one basis per group")
     rt = _lib.DKV_ROUTE_FUSED if route == "short_fused" else _lib.DKV_ROUTE_TWO_STAGE
     return splitk_attention(q3, k_flat, v_flat, layout, lens_k, offs_k, lens_v, offs_v,
-                            theta=theta, route=rt, groups=G, split_len=split_len, out=out)
+                            theta=theta, route=rt, groups=G, split_len=split_len, out=out,
+                            out_dtype=out_dtype)

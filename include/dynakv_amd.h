@@ -164,7 +164,8 @@ int dkv_av(void* stream, int mode, int scores_dtype, int cache_dtype, int out_dt
  *                      rank stride basis_sr, unit dim stride (R x Dh).
  *   lens/offs tables for K and V with their own (sb, ss) strides.
  *   partials: fp32 workspace of dkv_splitk_workspace_floats(...) floats.
- *   out: (B, Hq, Dh) strides (out_sb, out_sh), dtype q_dtype.
+ *   out: (B, Hq, Dh) strides (out_sb, out_sh), dtype out_dtype = the cache dtype (what the
+ *        reference returns) or DKV_F32 (the merge result before rounding).
  * Requirements: q and cache dtype f16 or bf16 (same), Dh == 128, R <= 128, hpg <= 16,
  * Hkv % G == 0. split_len is a multiple of 64 (0 = choose automatically).
  * The launch pair is split kernel + merge kernel; both are asynchronous.
@@ -179,7 +180,7 @@ int dkv_decode_splitk(void* stream, int route, int dtype,
                       const int* lens_k, const int* offs_k, long long tk_sb, long long tk_ss,
                       const int* lens_v, const int* offs_v, long long tv_sb, long long tv_ss,
                       float* partials, long long partials_floats,
-                      void* out, long long out_sb, long long out_sh,
+                      void* out, long long out_sb, long long out_sh, int out_dtype,
                       int B, int Hq, int Hkv, int G, int S, int R, int Dh,
                       float log_theta, int split_len);
 
@@ -196,7 +197,7 @@ int dkv_decode_splitk_phase(int phase, void* stream, int route, int dtype,
                             const int* lens_k, const int* offs_k, long long tk_sb, long long tk_ss,
                             const int* lens_v, const int* offs_v, long long tv_sb, long long tv_ss,
                             float* partials, long long partials_floats,
-                            void* out, long long out_sb, long long out_sh,
+                            void* out, long long out_sb, long long out_sh, int out_dtype,
                             int B, int Hq, int Hkv, int G, int S, int R, int Dh,
                             float log_theta, int split_len);
 

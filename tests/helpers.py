@@ -63,6 +63,8 @@ def assert_close(got: torch.Tensor | np.ndarray, ref: np.ndarray, what: str = ""
     max_abs = float(d.max()) if d.size else 0.0
     scale = float(np.abs(r[fin]).max()) if d.size else 1.0
     max_rel = max_abs / max(scale, 1e-30)
+    print(f"[parity] {what}: max_abs={max_abs:.3e} max_rel={max_rel:.3e} |ref|max={scale:.3e}",
+          flush=True)
     assert max_abs <= tol_abs and max_rel <= tol_rel, \
         f"{what}: max_abs={max_abs:.3e} max_rel={max_rel:.3e} (|ref|max={scale:.3e})"
     return max_abs, max_rel

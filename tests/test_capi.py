@@ -58,7 +58,7 @@ def test_argument_validation_without_device():
     assert lib.dkv_append_decode(None, 1, None, 0, None, 0, None, 0, None, None, 0, 0, None, 0, 0, 4) == 0
     # split-K: rank above 128 is outside the kernel
     rc = lib.dkv_decode_splitk(None, 0, 2, None, 0, 0, None, 0, 0, None, 0, 0, None, 0, None, 0,
-                               None, None, 0, 0, None, None, 0, 0, None, 0, None, 0, 0,
+                               None, None, 0, 0, None, None, 0, 0, None, 0, None, 0, 0, 2,
                                1, 32, 8, 8, 10, 256, 128, 1.0, 0)
     assert rc == -2
     with pytest.raises(NotImplementedError):
