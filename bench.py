@@ -8,7 +8,8 @@ plus a seeded 5% forced to 128. Synthetic data generated on the device; the pack
 per-step inputs are resident in HBM before the timed region.
 
 One step = decode append of K and V for all 128 rows + the router decision + decode attention
-(long route: split-K kernel with two-stage semantics, then merge/projection).
+(long route: one split-K kernel launch with two-stage semantics; its last workgroup per unit
+merges the splits and projects through the V basis).
 
 Output: one JSON line. ``value`` is decode-attention GB/s: algorithmic bytes of the attention
 (packed K/V coefficients read once, int32 lengths, unique bases, q and output) divided by the
@@ -110,20 +111,23 @@ def attention_bytes(cfg, lk_h, lv_h, S):
 
 
 class SplitKRunner:
-    """Launches the three phases of dkv_decode_splitk with events around each on the current
-    stream (the stream the kernels run on)."""
+    """Launches dkv_decode_splitk (one kernel) with HIP events around it on the current stream
+    (the stream the kernel runs on). The RoPE table and the workspace are built once, before
+    any timed step."""
 
     def __init__(self, cfg, dev, max_S):
         from dynakv_amd import _lib
+        from dynakv_amd.kernels.decode import rope_table, workspace
 
         self.lib = _lib.load()
         self._lib = _lib
         self.cfg = cfg
         self.dev = dev
+        st = torch.cuda.current_stream(dev).cuda_stream
         nfl = self.lib.dkv_splitk_workspace_floats(cfg.B, cfg.Hq, cfg.G, max_S, cfg.R, 0)
-        self.ws = torch.empty(int(nfl), dtype=torch.float32, device=dev)
+        self.ws = workspace(dev, st, int(nfl))
+        self.rope, self.rope_tiles = rope_table(dev, st, cfg.theta, max_S)
         self.out = torch.empty((cfg.B, cfg.Hq, cfg.Dh), dtype=cfg.dtype, device=dev)
-        self.log_theta = math.log(cfg.theta)
 
     def run(self, q, fk, fv, lk, ok, lv, ov, kb, vb, route, ev=None):
         cfg, L = self.cfg, self._lib
@@ -135,21 +139,14 @@ class SplitKRunner:
                 fk.data_ptr(), fk.stride(0), fv.data_ptr(), fv.stride(0),
                 lk.data_ptr(), ok.data_ptr(), lk.stride(0), lk.stride(1),
                 lv.data_ptr(), ov.data_ptr(), lv.stride(0), lv.stride(1),
-                self.ws.data_ptr(), self.ws.numel(), self.out.data_ptr(), self.out.stride(0),
-                self.out.stride(1), L.dtype_code(cfg.dtype), cfg.B, cfg.Hq, cfg.G, cfg.G, S,
-                cfg.R, cfg.Dh,
-                self.log_theta, 0)
+                self.rope.data_ptr(), self.rope_tiles, self.ws.data_ptr(), self.ws.numel(),
+                self.out.data_ptr(), self.out.stride(0), self.out.stride(1),
+                L.dtype_code(cfg.dtype), cfg.B, cfg.Hq, cfg.G, cfg.G, S, cfg.R, cfg.Dh, 0)
         if ev is not None:
             ev[0].record(st)
-        L.check(self.lib.dkv_decode_splitk_phase(0, *args), "rope")
+        L.check(self.lib.dkv_decode_splitk(*args), "dkv_decode_splitk")
         if ev is not None:
             ev[1].record(st)
-        L.check(self.lib.dkv_decode_splitk_phase(1, *args), "split")
-        if ev is not None:
-            ev[2].record(st)
-        L.check(self.lib.dkv_decode_splitk_phase(2, *args), "merge")
-        if ev is not None:
-            ev[3].record(st)
         return self.out
 
 
@@ -164,7 +161,7 @@ def run_gpu(cfg, steps, warmup, dev):
     runner = SplitKRunner(cfg, dev, cfg.S0 + total + 16)
     policy = KernelPolicy()
     R = cfg.R
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(steps)]
     step_bytes = []
 
     def one_step(i, ev):
@@ -186,13 +183,11 @@ def run_gpu(cfg, steps, warmup, dev):
         step_bytes.append(attention_bytes(cfg, W["lk_h"], W["lv_h"], L))
     torch.cuda.synchronize(dev)
     wall = time.perf_counter() - t0
-    rope_ms = sum(e[0].elapsed_time(e[1]) for e in events)
-    split_ms = sum(e[1].elapsed_time(e[2]) for e in events)
-    merge_ms = sum(e[2].elapsed_time(e[3]) for e in events)
-    attn_ms = sum(e[0].elapsed_time(e[3]) for e in events)
+    attn_ms = sum(e[0].elapsed_time(e[1]) for e in events)
+    split_ms = attn_ms
     tot_bytes = float(sum(step_bytes))
     res = dict(
-        wall_s=wall, attn_ms=attn_ms, split_ms=split_ms, rope_ms=rope_ms, merge_ms=merge_ms,
+        wall_s=wall, attn_ms=attn_ms, split_ms=split_ms,
         bytes_total=tot_bytes, bytes_per_step=tot_bytes / steps,
         final_len=cache.get_seq_length_sp(0), syncs=cache.device_syncs,
         q0=W["q"][0], cache=cache, workload=W,
@@ -293,11 +288,6 @@ def main():
         "decode_attn_us_per_step": round(r["attn_ms"] * 1e3 / args.steps, 3),
         "decode_tokens_per_s_attention_only": round(cfg.B * args.steps / attn_s, 1),
         "decode_tokens_per_s_step_wall": round(cfg.B * args.steps / r["wall_s"], 1),
-        "phase_us_per_step": {
-            "rope_table": round(r["rope_ms"] * 1e3 / args.steps, 3),
-            "split": round(r["split_ms"] * 1e3 / args.steps, 3),
-            "merge": round(r["merge_ms"] * 1e3 / args.steps, 3),
-        },
         "host_syncs_total": r["syncs"],
         "roofline": {
             "kernel": "splitk_kernel<bf16, two_stage>",

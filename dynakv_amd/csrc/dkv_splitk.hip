@@ -3,21 +3,28 @@
 //
 // Work unit: (batch b, KV head k) with hpg query heads sharing K/V basis k; its packed
 // coefficients are cache row b*G + k/(Hkv/G). A workgroup (4 waves) owns one unit and one
-// contiguous token range ("split"); waves take 16-token tiles round-robin.
+// contiguous token range ("split", <= 512 tokens); waves take 16-token tiles round-robin.
 //
-// Per 16-token tile and wave:
-//   1. K^T[128 x 16] = BK^T[128 x R] . X^T[R x 16] on v_mfma_f32_16x16x32_{bf16,f16}.
-//      BK^T sits in LDS (staged once per workgroup); X^T is gathered straight from the
-//      packed rows with 16-byte buffer loads (one lane = one token x 8 ranks), zero-masked
-//      past the token's retained count; rank chunks of 32 stop at the tile's largest count.
-//   2. rotate-half RoPE by cache row index on the accumulator registers (lane-local pairs
-//      (i, i+64)), cos/sin advanced by an angle-addition recurrence seeded from a table.
-//   3. scores[16 tokens x hpg] on one 16x16x32 f16 MFMA chain against the scaled query.
-//   4. online softmax in the log2 domain with lazy rescaling (only when the running max grows
-//      by more than 2^11.5), then P.X^V on 16x16x16 MFMA in coefficient space (the V basis is
-//      applied once per output in the merge kernel).
-// Partials (m, l, acc[128]) per (unit, split, head) are LSE-merged and projected through the
-// V basis by merge_kernel.
+// Workgroup prologue: the K basis (transposed, [dim][rank]) and the split's length/offset
+// tables go to LDS, together with each tile's largest retained count, so a tile's gathers need
+// no dependent global round trip. Each wave then runs a two-stage software pipeline: the
+// current tile's gathered K and V coefficients are zero-masked past each token's count and
+// stored to the wave's LDS tiles, then the next tile's gathers (16-byte buffer loads, one lane =
+// one token x 8 ranks, out-of-range reads return zero) are issued and stay in flight while the
+// current tile computes from LDS:
+//   1. K^T[128 x 16] = BK^T . X^T on v_mfma_f32_16x16x32_{bf16,f16}, two 16-dim blocks at a
+//      time ((i, i+64) rotate-half pairs), rank chunks of 32 up to the tile's largest count;
+//   2. RoPE by cache row index on the accumulators (cos/sin advanced by angle addition from a
+//      precomputed table), K' split into fp16 hi/lo parts;
+//   3. scores on 16x16x32 f16 MFMA (K'hi.q + K'lo.q; a bf16 or fp16 query is exact in fp16,
+//      the softmax scale is applied to the fp32 result);
+//   4. online softmax in the log2 domain, lazily rescaled (only when the running max grows by
+//      more than 2^11.5);
+//   5. P.X^V in coefficient space on 16x16x16 MFMA; X^V goes through a per-wave LDS tile so
+//      the operand (4 tokens x 1 rank per lane) is read transposed.
+// Epilogue: the 4 waves combine through LDS into one (m, l, acc[128]) record per head; the
+// last workgroup of a unit to finish (arrival counter) LSE-merges the unit's splits and
+// projects once through the V basis.
 #include "dkv_common.h"
 
 namespace {
@@ -25,31 +32,40 @@ namespace {
 constexpr int DH = 128;
 constexpr int TILE = 16;
 constexpr int WAVES = 4;
-constexpr int BK_LD = 136;  // LDS row pitch (elements) of the transposed K basis
+constexpr int BK_LD = 136;    // LDS row pitch (elements) of the transposed K basis
+constexpr int VT_LD = 136;    // LDS row pitch (elements) of a wave's V tile
 constexpr int PREC = DH + 2;  // floats per partial record: m, l, acc[128]
+constexpr int MAX_SPLIT = 512;
+constexpr int MAX_TILES = MAX_SPLIT / TILE;
+constexpr int ROPE_FIXED_ROWS = TILE + 1;  // rows 0..15: in-tile deltas; row 16: per-step
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float RESCALE_THRESH = 11.5f;  // log2 units
+constexpr int OOB = 0x7ffffff0;          // buffer offset that reads as zero
 
 struct SplitParams {
   const uint16_t* q;
   long long q_sb, q_sh;
   const uint16_t* k_basis;
   long long k_unit, k_sr;
+  const uint16_t* v_basis;
+  long long v_unit, v_sr;
   const uint16_t* k_flat;
   const uint16_t* v_flat;
-  long long k_ld, v_ld;
+  int k_ld, v_ld;
   const int* lens_k;
   const int* offs_k;
   long long tk_sb, tk_ss;
   const int* lens_v;
   const int* offs_v;
   long long tv_sb, tv_ss;
-  const float* rope;  // [n_tb][64] (cos, sin) of tile bases, then [16][64] in-tile deltas,
-                      // then [64] per-step (64 positions) rotations
-  float* partials;
-  int B, Hq, Hkv, G, S, R, hpg, n_splits, split_len, n_tb;
-  float q_scale;      // multiplies q before the fp16 cast
-  float masked_score; // two-stage: -1e4 * (1/sqrt(Dh)) in fp32
+  const float* rope;   // rows of 64 (cos, sin): 16 in-tile deltas, 1 step, then tile bases
+  float* partials;     // [unit][split][hpg][PREC]
+  int* counters;       // [unit] arrival counters, zero on entry and on exit
+  void* out;
+  long long out_sb, out_sh;
+  int B, Hq, Hkv, G, S, R, hpg, n_splits, split_len;
+  float score_scale;   // applied to q.k' after the MFMA (fused: sm_scale*log2e, else sm_scale)
+  float masked_score;  // two-stage route: -1e4 * (1/sqrt(Dh)) in fp32
 };
 
 template <int DT>
@@ -128,39 +144,43 @@ __device__ __forceinline__ dkv_u32x4 mask_prefix8(dkv_u32x4 v, int nv) {
   return v;
 }
 
-// Wave-uniform maximum of a per-lane int, returned in a scalar register.
-__device__ __forceinline__ int wave_max_uniform(int v) {
-  return __builtin_amdgcn_readfirstlane(dkv_wave_max_i(v));
+// Zero-fill masks for the first k (0..8) 16-bit elements of an 8-element vector.
+__device__ __forceinline__ uint32_t prefix_mask_word(int k, int d) {
+  return k >= 2 * d + 2 ? 0xffffffffu : (k == 2 * d + 1 ? 0x0000ffffu : 0u);
 }
 
-// ---------------------------------------------------------------------------------------
-// RoPE table prologue: cos/sin of tile-base positions, in-tile deltas and the per-step
-// rotation, evaluated in double from the fp32 angle the reference forms
-// (angle = float(pos) * inv_freq, reference fused.py:65-66,97 / two_stage.py:36-44).
-// ---------------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void rope_table_kernel(float* __restrict__ rope, int n_tb,
-                                                         float log_theta) {
-  const int idx = blockIdx.x * 256 + threadIdx.x;
-  const int total = (n_tb + TILE + 1) * 64;
-  if (idx >= total) return;
-  const int r = idx / 64, i = idx % 64;
-  const float inv = dkv_inv_freq(i, DH, log_theta);
-  float ang;
-  if (r < n_tb)
-    ang = (float)(r * TILE) * inv;
-  else if (r < n_tb + TILE)
-    ang = (float)(r - n_tb) * inv;
-  else
-    ang = (float)(TILE * WAVES) * inv;
-  double s, c;
-  sincos((double)ang, &s, &c);
-  rope[2 * idx] = (float)c;
-  rope[2 * idx + 1] = (float)s;
+// 16-byte gather of ranks [32c + 8g, +8) of one token (offset o, clamped count r) from a row;
+// lanes with nothing to load read the out-of-range offset (zero, no memory traffic). A window
+// that would cross the end of the row's buffer falls back to element loads, because an
+// out-of-range vector access reads as zero in full.
+__device__ __forceinline__ dkv_u32x4 gather_chunk(__amdgpu_buffer_rsrc_t rs, int ld, int o, int r,
+                                                  int c, int g) {
+  const int j0 = 32 * c + 8 * g;
+  const int nv = r - j0;
+  if (nv > 0 && o + j0 + 8 > ld) return gather8_b16(rs, o + j0, min(nv, 8));
+  return __builtin_amdgcn_raw_buffer_load_b128(rs, nv > 0 ? (o + j0) * 2 : OOB, 0, 0);
 }
 
-template <int DT, int ROUTE>
+struct TileMeta {
+  int rk;   // this lane's token: raw K length (only its sign matters: has a key)
+  int rkc;  // clamped K length
+  int rvc;  // clamped V length
+  int nck;  // wave-uniform: 32-rank K chunks
+  int nvc;  // wave-uniform: 32-rank V chunks
+  int nbv;  // wave-uniform: 16-rank V blocks
+  bool valid;
+};
+
+template <int DT, int ROUTE, int ODT>
 __global__ __launch_bounds__(256, 2) void splitk_kernel(SplitParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t sBK[DH * BK_LD];
+  __shared__ __attribute__((aligned(16))) int sTab[4][MAX_SPLIT];
+  __shared__ int sTmax[2][MAX_TILES];
+  __shared__ __attribute__((aligned(16))) uint16_t sKT[WAVES][TILE * VT_LD];
+  __shared__ __attribute__((aligned(16))) uint16_t sVT[WAVES][TILE * VT_LD];
+  __shared__ __attribute__((aligned(16))) uint32_t sMask[9][4];
+  __shared__ __attribute__((aligned(16))) float sStep[2][64];
+  __shared__ int sLast;
 
   // XCD-aware mapping: consecutive workgroup ids land on different XCDs (id % 8), so give
   // every split of one unit the same id % 8 to keep that unit's basis in one L2.
@@ -182,8 +202,11 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(SplitParams p) {
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int n = lane & 15, g = lane >> 4;
   const int R = p.R;
+  const int s_begin = split * p.split_len;
+  const int s_end = min(p.S, s_begin + p.split_len);
+  const int ns = s_end - s_begin;
 
-  // ---- stage BK^T ([dim][rank], ranks >= R zero) into LDS --------------------------------
+  // ---- prologue: K basis, tables, masks, per-step rotation --------------------------------
   {
     const uint16_t* kb = p.k_basis + (long long)kvh * p.k_unit;
     for (int idx = tid; idx < 128 * 16; idx += 256) {
@@ -197,65 +220,128 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(SplitParams p) {
         sBK[(d8 + 2 * t + 1) * BK_LD + j] = (uint16_t)(e[t] >> 16);
       }
     }
+    const int* lk = p.lens_k + (long long)row * p.tk_sb;
+    const int* okp = p.offs_k + (long long)row * p.tk_sb;
+    const int* lv = p.lens_v + (long long)row * p.tv_sb;
+    const int* ovp = p.offs_v + (long long)row * p.tv_sb;
+    for (int i = tid; i < ns; i += 256) {
+      const long long t = s_begin + i;
+      sTab[0][i] = lk[t * p.tk_ss];
+      sTab[1][i] = okp[t * p.tk_ss];
+      sTab[2][i] = lv[t * p.tv_ss];
+      sTab[3][i] = ovp[t * p.tv_ss];
+    }
+    if (tid < 36) sMask[tid >> 2][tid & 3] = prefix_mask_word(tid >> 2, tid & 3);
+    if (tid < 64) {
+      sStep[0][tid] = p.rope[TILE * 128 + 2 * tid];
+      sStep[1][tid] = p.rope[TILE * 128 + 2 * tid + 1];
+    }
   }
-
-  // ---- scaled query as the B operand of the QK MFMA: lane (head slot n, k-group g) holds
-  //      (q_i, q_{i+64}) for i = 16*qi + 4*g + w, w = 0..3 --------------------------------
-  dkv_u32x4 bq[4], bql[4];  // fp16 hi and lo parts of the scaled query
-  {
-    const int hs = n;
-    const bool real = hs < p.hpg;
-    const long long qo = (long long)b * p.q_sb + (long long)(kvh * p.hpg + (real ? hs : 0)) * p.q_sh;
+  __syncthreads();
+  {  // largest clamped K and V count of each tile of the split (4 threads per tile)
+    const int tile = tid >> 2, qq = tid & 3;
+    int mk = 0, mv = 0;
 #pragma unroll
-    for (int qi = 0; qi < 4; ++qi) {
-      uint32_t w4[4], l4[4];
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const int i = 16 * qi + 4 * g + w;
-        const float a = real ? elt_to_f32<DT>(p.q[qo + i]) * p.q_scale : 0.f;
-        const float c = real ? elt_to_f32<DT>(p.q[qo + i + 64]) * p.q_scale : 0.f;
-        split_f16x2(a, c, w4[w], l4[w]);
+    for (int e = 0; e < 4; ++e) {
+      const int i = tile * TILE + qq * 4 + e;
+      if (tile < MAX_TILES && i < ns) {
+        mk = max(mk, min(max(sTab[0][i], 0), R));
+        mv = max(mv, min(max(sTab[2][i], 0), R));
       }
-      bq[qi] = dkv_u32x4{w4[0], w4[1], w4[2], w4[3]};
-      bql[qi] = dkv_u32x4{l4[0], l4[1], l4[2], l4[3]};
+    }
+    mk = max(mk, __shfl_xor(mk, 1, 64));
+    mk = max(mk, __shfl_xor(mk, 2, 64));
+    mv = max(mv, __shfl_xor(mv, 1, 64));
+    mv = max(mv, __shfl_xor(mv, 2, 64));
+    if (qq == 0 && tile < MAX_TILES) {
+      sTmax[0][tile] = mk;
+      sTmax[1][tile] = mv;
     }
   }
 
-  const int tiles_per_split = p.split_len / TILE;
-  const int tile0 = split * tiles_per_split + wave;
-  const int s_end = min(p.S, (split + 1) * p.split_len);
-
-  // ---- RoPE state for this lane's token slot n and its 16 frequencies ---------------------
-  float rc[16], rs[16], dc[16], ds[16];
+  // ---- query as the fp16 B operand of the QK MFMA: lane (head slot n, k-group g) holds
+  //      (q_i, q_{i+64}) for i = 16*pp + 4*g + w; bf16 and fp16 values are exact in fp16 ------
+  dkv_u32x4 bq[4];
   {
-    const int tb = min(tile0, p.n_tb - 1);
-    const float* base = p.rope + (long long)tb * 128;
-    const float* delt = p.rope + (long long)(p.n_tb + n) * 128;
-    const float* step = p.rope + (long long)(p.n_tb + TILE) * 128;
+    const bool real = n < p.hpg;
+    const long long qo = (long long)b * p.q_sb + (long long)(kvh * p.hpg + (real ? n : 0)) * p.q_sh;
 #pragma unroll
-    for (int qi = 0; qi < 4; ++qi)
+    for (int pp = 0; pp < 4; ++pp) {
+      uint32_t w4[4];
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
-        const int i = 16 * qi + 4 * g + w, f = qi * 4 + w;
+        const int i = 16 * pp + 4 * g + w;
+        const float a = real ? elt_to_f32<DT>(p.q[qo + i]) : 0.f;
+        const float c = real ? elt_to_f32<DT>(p.q[qo + i + 64]) : 0.f;
+        w4[w] = pack_f16x2(a, c);
+      }
+      bq[pp] = dkv_u32x4{w4[0], w4[1], w4[2], w4[3]};
+    }
+  }
+
+  const int tile_first = s_begin / TILE;  // splits are multiples of 64 tokens
+  const int tile0 = tile_first + wave;
+  const int n_tb = (p.S + TILE - 1) / TILE;
+
+  // ---- RoPE state of this lane's token slot for its 16 frequencies -----------------------
+  float rc[16], rs[16];
+  {
+    const int tb = min(tile0, n_tb - 1);
+    const float* base = p.rope + (long long)(ROPE_FIXED_ROWS + tb) * 128;
+    const float* delt = p.rope + (long long)n * 128;
+#pragma unroll
+    for (int pp = 0; pp < 4; ++pp)
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const int i = 16 * pp + 4 * g + w, f = pp * 4 + w;
         const float bc = base[2 * i], bs = base[2 * i + 1];
         const float ec = delt[2 * i], es = delt[2 * i + 1];
         rc[f] = bc * ec - bs * es;
         rs[f] = bs * ec + bc * es;
-        dc[f] = step[2 * i];
-        ds[f] = step[2 * i + 1];
       }
   }
-
-  __syncthreads();  // sBK ready
+  __syncthreads();  // sTmax ready
 
   const __amdgpu_buffer_rsrc_t rk_src =
-      dkv_make_rsrc(p.k_flat + (long long)row * p.k_ld, (uint32_t)(p.k_ld * 2));
+      dkv_make_rsrc(p.k_flat + (long long)row * p.k_ld, (uint32_t)p.k_ld * 2u);
   const __amdgpu_buffer_rsrc_t rv_src =
-      dkv_make_rsrc(p.v_flat + (long long)row * p.v_ld, (uint32_t)(p.v_ld * 2));
-  const int* lk = p.lens_k + (long long)row * p.tk_sb;
-  const int* ok_ = p.offs_k + (long long)row * p.tk_sb;
-  const int* lv = p.lens_v + (long long)row * p.tv_sb;
-  const int* ov_ = p.offs_v + (long long)row * p.tv_sb;
+      dkv_make_rsrc(p.v_flat + (long long)row * p.v_ld, (uint32_t)p.v_ld * 2u);
+  uint16_t* kt = sKT[wave];
+  uint16_t* vt = sVT[wave];
+
+  // per-tile metadata from the LDS tables
+  auto meta_of = [&](int T) {
+    TileMeta d;
+    const int tl = T * TILE + n - s_begin;
+    d.valid = T * TILE + n < s_end;
+    d.rk = d.valid ? sTab[0][tl] : 0;
+    const int rv = d.valid ? sTab[2][tl] : 0;
+    d.rkc = min(max(d.rk, 0), R);
+    d.rvc = min(max(rv, 0), R);
+    const int tt = T - tile_first;
+    const int mk = __builtin_amdgcn_readfirstlane(sTmax[0][tt]);
+    const int mv = __builtin_amdgcn_readfirstlane(sTmax[1][tt]);
+    d.nck = (mk + 31) >> 5;
+    d.nvc = (mv + 31) >> 5;
+    d.nbv = (mv + 15) >> 4;
+    return d;
+  };
+  dkv_u32x4 kx[4], vx[4];  // in-flight gathers of the next tile
+  auto issue = [&](const TileMeta& d, int T) {
+    const int tl = T * TILE + n - s_begin;
+    const int ok = d.valid ? sTab[1][tl] : 0;
+    const int ov = d.valid ? sTab[3][tl] : 0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      kx[c] = dkv_u32x4{0u, 0u, 0u, 0u};
+      if (c < d.nck) kx[c] = gather_chunk(rk_src, p.k_ld, ok, d.rkc, c, g);
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      vx[c] = dkv_u32x4{0u, 0u, 0u, 0u};
+      if (c < d.nvc) vx[c] = gather_chunk(rv_src, p.v_ld, ov, d.rvc, c, g);
+    }
+  };
 
   dkv_f32x4 acc[8];
 #pragma unroll
@@ -263,77 +349,83 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(SplitParams p) {
   float m_run = -INFINITY;  // per head slot n (log2 units), identical across g
   float l_run = 0.f;        // partial over this lane's 4 tokens per tile
 
+  TileMeta cur;
+  if (tile0 * TILE < s_end) {
+    cur = meta_of(tile0);
+    issue(cur, tile0);
+  }
   for (int T = tile0; T * TILE < s_end; T += WAVES) {
-    const int t = T * TILE + n;
-    const bool valid = t < s_end;
-    const int rk = valid ? lk[(long long)t * p.tk_ss] : 0;
-    const int ok = valid ? ok_[(long long)t * p.tk_ss] : 0;
-    const int rv = valid ? lv[(long long)t * p.tv_ss] : 0;
-    const int ov = valid ? ov_[(long long)t * p.tv_ss] : 0;
-    const int rkc = max(0, min(rk, R));
-    const int rvc = max(0, min(rv, R));
-
-    // ---- 1. K reconstruction ----------------------------------------------------------------
-    dkv_f32x4 ck[8];
+    // ---- store the current tile (masked) to the wave's LDS tiles, then issue the next ------
 #pragma unroll
-    for (int i = 0; i < 8; ++i) ck[i] = dkv_f32x4{0.f, 0.f, 0.f, 0.f};
-    const int nck = (wave_max_uniform(rkc) + 31) >> 5;
-    for (int c = 0; c < nck; ++c) {
-      const int j0 = 32 * c + 8 * g;
-      const int nv = rkc - j0;
-      const int boff = nv > 0 ? (ok + j0) * 2 : 0x7ffffff0;
-      dkv_u32x4 xv;
-      if (nv > 0 && (long long)(ok + j0 + 8) > p.k_ld) {
-        // the 16-byte window would cross the end of the row's buffer, where an out-of-range
-        // vector access reads as all zeros: gather element by element instead
-        xv = gather8_b16(rk_src, ok + j0, nv);
-      } else {
-        xv = __builtin_amdgcn_raw_buffer_load_b128(rk_src, boff, 0, 0);
-        if (nv < 8) xv = mask_prefix8(xv, max(nv, 0));
+    for (int c = 0; c < 4; ++c) {
+      if (c < cur.nck) {
+        const int nv = min(max(cur.rkc - 32 * c - 8 * g, 0), 8);
+        const dkv_u32x4 mk = *(const dkv_u32x4*)sMask[nv];
+        *(dkv_u32x4*)&kt[n * VT_LD + 32 * c + 8 * g] =
+            dkv_u32x4{kx[c].x & mk.x, kx[c].y & mk.y, kx[c].z & mk.z, kx[c].w & mk.w};
       }
-#pragma unroll
-      for (int blk = 0; blk < 8; ++blk) {
-        const dkv_u32x4 a = *(const dkv_u32x4*)&sBK[(16 * blk + n) * BK_LD + 32 * c + 8 * g];
-        ck[blk] = mfma_k<DT>(a, xv, ck[blk]);
+      if (c < cur.nvc) {
+        const int nv = min(max(cur.rvc - 32 * c - 8 * g, 0), 8);
+        const dkv_u32x4 mk = *(const dkv_u32x4*)sMask[nv];
+        *(dkv_u32x4*)&vt[n * VT_LD + 32 * c + 8 * g] =
+            dkv_u32x4{vx[c].x & mk.x, vx[c].y & mk.y, vx[c].z & mk.z, vx[c].w & mk.w};
       }
     }
+    const bool more = (T + WAVES) * TILE < s_end;
+    TileMeta nxt = cur;
+    if (more) {
+      nxt = meta_of(T + WAVES);
+      issue(nxt, T + WAVES);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-    // ---- 2. RoPE on (i, i+64) pairs, packed to fp16 as the QK A operand -----------------------
-    dkv_u32x4 aq[4], aql[4];
+    // ---- 1-3: K reconstruction, RoPE, hi/lo split, scores ---------------------------------
+    dkv_f32x4 sc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int qi = 0; qi < 4; ++qi) {
-      uint32_t w4[4], l4[4];
+    for (int pp = 0; pp < 4; ++pp) {
+      dkv_f32x4 c0 = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        if (c < cur.nck) {
+          const dkv_u32x4 xk = *(const dkv_u32x4*)&kt[n * VT_LD + 32 * c + 8 * g];
+          const dkv_u32x4 a0 = *(const dkv_u32x4*)&sBK[(16 * pp + n) * BK_LD + 32 * c + 8 * g];
+          const dkv_u32x4 a1 =
+              *(const dkv_u32x4*)&sBK[(16 * (pp + 4) + n) * BK_LD + 32 * c + 8 * g];
+          c0 = mfma_k<DT>(a0, xk, c0);
+          c1 = mfma_k<DT>(a1, xk, c1);
+        }
+      }
+      uint32_t h4[4], l4[4];
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
-        const int f = qi * 4 + w;
-        const float k0 = ck[qi][w], k1 = ck[qi + 4][w];
-        const float r0 = k0 * rc[f] - k1 * rs[f];
-        const float r1 = k1 * rc[f] + k0 * rs[f];
-        split_f16x2(r0, r1, w4[w], l4[w]);
+        const int f = pp * 4 + w;
+        const float r0 = c0[w] * rc[f] - c1[w] * rs[f];
+        const float r1 = c1[w] * rc[f] + c0[w] * rs[f];
+        split_f16x2(r0, r1, h4[w], l4[w]);
       }
-      aq[qi] = dkv_u32x4{w4[0], w4[1], w4[2], w4[3]};
-      aql[qi] = dkv_u32x4{l4[0], l4[1], l4[2], l4[3]};
+      sc = mfma_f16(dkv_u32x4{l4[0], l4[1], l4[2], l4[3]}, bq[pp], sc);
+      sc = mfma_f16(dkv_u32x4{h4[0], h4[1], h4[2], h4[3]}, bq[pp], sc);
     }
     // advance the rotation by WAVES*TILE positions
 #pragma unroll
-    for (int f = 0; f < 16; ++f) {
-      const float c2 = rc[f] * dc[f] - rs[f] * ds[f];
-      const float s2 = rs[f] * dc[f] + rc[f] * ds[f];
-      rc[f] = c2;
-      rs[f] = s2;
+    for (int pp = 0; pp < 4; ++pp) {
+      const dkv_f32x4 dc = *(const dkv_f32x4*)&sStep[0][16 * pp + 4 * g];
+      const dkv_f32x4 ds = *(const dkv_f32x4*)&sStep[1][16 * pp + 4 * g];
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const int f = pp * 4 + w;
+        const float c2 = rc[f] * dc[w] - rs[f] * ds[w];
+        const float s2 = rs[f] * dc[w] + rc[f] * ds[w];
+        rc[f] = c2;
+        rs[f] = s2;
+      }
     }
 
-    // ---- 3. scores: lane (head slot n, tokens 4g+u) -----------------------------------------
-    // scores = K'.Q with hi/lo fp16 parts on both sides (~22-bit products, fp32 accumulate)
-    dkv_f32x4 sc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int qi = 0; qi < 4; ++qi) {
-      sc = mfma_f16(aql[qi], bq[qi], sc);
-      sc = mfma_f16(aq[qi], bql[qi], sc);
-      sc = mfma_f16(aq[qi], bq[qi], sc);
-    }
-    const unsigned long long has_bits = __ballot(valid && rk > 0);
-    const unsigned long long in_bits = __ballot(valid);
+    // scores of lane (head slot n, tokens 4g+u) -> log2 domain with the route's masking
+    const unsigned long long has_bits = __ballot(cur.valid && cur.rk > 0);
+    const unsigned long long in_bits = __ballot(cur.valid);
     float z[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -342,9 +434,9 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(SplitParams p) {
       const bool inr = (in_bits >> tok) & 1ull;
       float v;
       if constexpr (ROUTE == DKV_ROUTE_FUSED) {
-        v = has ? sc[u] : -INFINITY;  // q already carries sm_scale * log2(e)
+        v = has ? sc[u] * p.score_scale : -INFINITY;  // score_scale = sm_scale * log2(e)
       } else {
-        v = dkv_round_to<DT>(has ? sc[u] : p.masked_score) * LOG2E;
+        v = dkv_round_to<DT>(has ? sc[u] * p.score_scale : p.masked_score) * LOG2E;
       }
       z[u] = inr ? v : -INFINITY;
     }
@@ -353,8 +445,7 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(SplitParams p) {
     float tmax = fmaxf(fmaxf(z[0], z[1]), fmaxf(z[2], z[3]));
     tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    const bool grow = tmax > m_run + RESCALE_THRESH;
-    if (__ballot(grow)) {
+    if (__ballot(tmax > m_run + RESCALE_THRESH)) {
       const float m_new = fmaxf(m_run, tmax);
       const float alpha = (m_new == -INFINITY) ? 1.f : exp2f(m_run - m_new);
       l_run *= alpha;
@@ -374,48 +465,41 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(SplitParams p) {
       l_run += pu[u];
     }
 
-    // ---- 5. P . X^V in coefficient space ----------------------------------------------------
-    int rvu[4], ovu[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      rvu[u] = __shfl(rvc, 4 * g + u, 64);
-      ovu[u] = __shfl(ov, 4 * g + u, 64);
-    }
-    const int nbv = (wave_max_uniform(rvc) + 15) >> 4;
+    // ---- 5. P.X^V from the wave's LDS V tile (4 tokens x 1 rank per lane) ---------------------
     dkv_u32x2 pa_hi, pa_lo;
     if constexpr (DT == DKV_F16) {
       pa_hi = dkv_u32x2{pack_f16x2(pu[0], pu[1]), pack_f16x2(pu[2], pu[3])};
       pa_lo = pa_hi;
     } else {
-      const uint32_t h0 = dkv_f32_to_bf16_bits(pu[0]), h1 = dkv_f32_to_bf16_bits(pu[1]);
-      const uint32_t h2 = dkv_f32_to_bf16_bits(pu[2]), h3 = dkv_f32_to_bf16_bits(pu[3]);
-      pa_hi = dkv_u32x2{h0 | (h1 << 16), h2 | (h3 << 16)};
-      pa_lo = dkv_u32x2{pack_bf16x2(pu[0] - dkv_bf16_bits_to_f32(h0), pu[1] - dkv_bf16_bits_to_f32(h1)),
-                        pack_bf16x2(pu[2] - dkv_bf16_bits_to_f32(h2), pu[3] - dkv_bf16_bits_to_f32(h3))};
+      const __bf16 h0 = (__bf16)pu[0], h1 = (__bf16)pu[1], h2 = (__bf16)pu[2], h3 = (__bf16)pu[3];
+      const __bf16 e0 = (__bf16)(pu[0] - (float)h0), e1 = (__bf16)(pu[1] - (float)h1);
+      const __bf16 e2 = (__bf16)(pu[2] - (float)h2), e3 = (__bf16)(pu[3] - (float)h3);
+      pa_hi = dkv_u32x2{(uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16),
+                        (uint32_t)__builtin_bit_cast(uint16_t, h2) | ((uint32_t)__builtin_bit_cast(uint16_t, h3) << 16)};
+      pa_lo = dkv_u32x2{(uint32_t)__builtin_bit_cast(uint16_t, e0) | ((uint32_t)__builtin_bit_cast(uint16_t, e1) << 16),
+                        (uint32_t)__builtin_bit_cast(uint16_t, e2) | ((uint32_t)__builtin_bit_cast(uint16_t, e3) << 16)};
     }
 #pragma unroll
     for (int blk = 0; blk < 8; ++blk) {
-      if (blk < nbv) {  // wave-uniform
-        const int j = 16 * blk + n;
-        uint32_t e[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int boff = j < rvu[u] ? (ovu[u] + j) * 2 : 0x7ffffff0;
-          e[u] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rv_src, boff, 0, 0);
-        }
-        const dkv_u32x2 xb = {e[0] | (e[1] << 16), e[2] | (e[3] << 16)};
-        // acc rows = head slots 4g+u, column = rank j
+      if (blk < cur.nbv) {  // wave-uniform
+        const uint16_t* src = vt + (4 * g) * VT_LD + 16 * blk + n;
+        const uint32_t e0 = src[0], e1 = src[VT_LD], e2 = src[2 * VT_LD], e3 = src[3 * VT_LD];
+        const dkv_u32x2 xb = {e0 | (e1 << 16), e2 | (e3 << 16)};
         acc[blk] = mfma_pv<DT>(pa_hi, xb, acc[blk]);
         if constexpr (DT == DKV_BF16) acc[blk] = mfma_pv<DT>(pa_lo, xb, acc[blk]);
       }
     }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    cur = nxt;
   }
 
   // ---- combine the 4 waves through LDS and write the partial record ----------------------
   float l_tot = l_run;
   l_tot += __shfl_xor(l_tot, 16, 64);
   l_tot += __shfl_xor(l_tot, 32, 64);
-  __syncthreads();  // all waves done with sBK
+  __syncthreads();  // all waves done with sBK and their tiles
   float* sw = reinterpret_cast<float*>(sBK);  // [WAVES][16 m | 16 l | 16 x 128 acc]
   constexpr int WREC = 32 + 16 * DH;
   float* my = sw + wave * WREC;
@@ -428,9 +512,9 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(SplitParams p) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) my[32 + (4 * g + u) * DH + 16 * i + n] = acc[i][u];
   __syncthreads();
-  float* out = p.partials + ((long long)unit * p.n_splits + split) * p.hpg * PREC;
-  for (int idx = tid; idx < p.hpg * (DH + 2); idx += 256) {
-    const int hs = idx / (DH + 2), e = idx % (DH + 2);
+  float* prec = p.partials + ((long long)unit * p.n_splits + split) * p.hpg * PREC;
+  for (int idx = tid; idx < p.hpg * PREC; idx += 256) {
+    const int hs = idx / PREC, e = idx % PREC;
     float mw[WAVES], M = -INFINITY;
 #pragma unroll
     for (int w = 0; w < WAVES; ++w) {
@@ -444,65 +528,104 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(SplitParams p) {
       const float x = e == 1 ? sw[w * WREC + 16 + hs] : (e >= 2 ? sw[w * WREC + 32 + hs * DH + (e - 2)] : 0.f);
       v += wt * x;
     }
-    out[hs * PREC + e] = e == 0 ? M : v;
+    prec[hs * PREC + e] = e == 0 ? M : v;
   }
-}
 
-// One block per unit: LSE-merge the splits of each head slot, normalise, project through the
-// V basis of the unit's KV head, store in the query dtype.
-template <int DT, int ROUTE, int ODT>
-__global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ partials,
-                                                    const uint16_t* __restrict__ v_basis,
-                                                    long long v_unit, long long v_sr,
-                                                    void* __restrict__ out, long long out_sb,
-                                                    long long out_sh, int Hkv, int hpg,
-                                                    int n_splits, int R) {
-  __shared__ float s_a[16][DH];
-  __shared__ float s_w[16][64];
-  const int unit = blockIdx.x;
-  const int b = unit / Hkv, kvh = unit % Hkv;
-  const int tid = threadIdx.x;
-  const float* pr = partials + (long long)unit * n_splits * hpg * PREC;
-  // per head slot: max over splits, then weighted sums
-  for (int hs = tid >> 4; hs < hpg; hs += 16) {
-    // 16 threads per head slot cooperate over splits
-    const int lane16 = tid & 15;
+  // ---- the last workgroup of this unit merges all splits ---------------------------------
+  __threadfence();
+  __syncthreads();
+  if (tid == 0) sLast = atomicAdd(&p.counters[unit], 1) == p.n_splits - 1;
+  __syncthreads();
+  if (!sLast) return;
+  __threadfence();
+  // V basis -> LDS as [rank][dim] (reuses sBK); merged accumulators [16][DH] (8 KiB) reuse
+  // the K tiles (17 KiB); per-head M and L reuse the V tiles
+  uint16_t* sVB = sBK;
+  float* sA = reinterpret_cast<float*>(&sKT[0][0]);
+  float* sML = reinterpret_cast<float*>(&sVT[0][0]);
+  static_assert(sizeof(sKT) >= 16 * DH * sizeof(float), "merge scratch does not fit");
+  {
+    const uint16_t* vb = p.v_basis + (long long)kvh * p.v_unit;
+    for (int idx = tid; idx < 128 * 16; idx += 256) {
+      const int j = idx >> 4, d8 = (idx & 15) * 8;
+      uint32_t w4[4] = {0u, 0u, 0u, 0u};
+      if (j < R) {
+        const uint16_t* src = vb + (long long)j * p.v_sr + d8;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) w4[t] = (uint32_t)src[2 * t] | ((uint32_t)src[2 * t + 1] << 16);
+      }
+      *(dkv_u32x4*)&sVB[j * BK_LD + d8] = dkv_u32x4{w4[0], w4[1], w4[2], w4[3]};
+    }
+  }
+  const float* pr = p.partials + (long long)unit * p.n_splits * p.hpg * PREC;
+  if (tid < 16 * 16) {
+    const int hs = tid >> 4, l16 = tid & 15;
     float M = -INFINITY;
-    for (int s = lane16; s < n_splits; s += 16) M = fmaxf(M, pr[((long long)s * hpg + hs) * PREC]);
+    if (hs < p.hpg)
+      for (int s = l16; s < p.n_splits; s += 16) M = fmaxf(M, pr[((long long)s * p.hpg + hs) * PREC]);
 #pragma unroll
     for (int m = 8; m >= 1; m >>= 1) M = fmaxf(M, __shfl_xor(M, m, 16));
     float L = 0.f;
-    for (int s = lane16; s < n_splits; s += 16) {
-      const float* rec = pr + ((long long)s * hpg + hs) * PREC;
-      const float w = (M == -INFINITY) ? 0.f : exp2f(rec[0] - M);
-      if (s < 64) s_w[hs][s] = w;
-      L += w * rec[1];
-    }
+    if (hs < p.hpg)
+      for (int s = l16; s < p.n_splits; s += 16) {
+        const float* rec = pr + ((long long)s * p.hpg + hs) * PREC;
+        L += ((M == -INFINITY) ? 0.f : exp2f(rec[0] - M)) * rec[1];
+      }
 #pragma unroll
     for (int m = 8; m >= 1; m >>= 1) L += __shfl_xor(L, m, 16);
-    if (lane16 == 0) s_w[hs][63] = L;  // slot 63 reused for L when n_splits <= 63
-  }
-  __syncthreads();
-  // weighted accumulator sums; n_splits <= 63 guaranteed by the host
-  for (int idx = tid; idx < hpg * DH; idx += 256) {
-    const int hs = idx / DH, j = idx % DH;
-    float a = 0.f;
-    if (j < R) {
-      for (int s = 0; s < n_splits; ++s) a += s_w[hs][s] * pr[((long long)s * hpg + hs) * PREC + 2 + j];
+    if (l16 == 0) {
+      sML[hs] = M;
+      sML[16 + hs] = L;
     }
-    const float L = s_w[hs][63];
-    const float den = ROUTE == DKV_ROUTE_TWO_STAGE ? fmaxf(L, 1e-6f) : L;
-    s_a[hs][j] = a / den;
   }
   __syncthreads();
-  const uint16_t* vb = v_basis + (long long)kvh * v_unit;
-  const int d = tid & 127, hh = tid >> 7;
-  for (int hs = hh; hs < hpg; hs += 2) {
-    float o = 0.f;
-    for (int j = 0; j < R; ++j) o = fmaf(s_a[hs][j], elt_to_f32<DT>(vb[(long long)j * v_sr + d]), o);
-    const long long oi = (long long)b * out_sb + (long long)(kvh * hpg + hs) * out_sh + d;
-    dkv_store_f32<ODT>(out, oi, o);
+  for (int idx = tid; idx < p.hpg * DH; idx += 256) {
+    const int hs = idx / DH, j = idx % DH;
+    const float M = sML[hs], L = sML[16 + hs];
+    float a = 0.f;
+    if (j < R && M != -INFINITY) {
+      for (int s = 0; s < p.n_splits; ++s) {
+        const float* rec = pr + ((long long)s * p.hpg + hs) * PREC;
+        a += exp2f(rec[0] - M) * rec[2 + j];
+      }
+    }
+    const float den = ROUTE == DKV_ROUTE_TWO_STAGE ? fmaxf(L, 1e-6f) : L;
+    sA[hs * DH + j] = a / den;
   }
+  __syncthreads();
+  {
+    const int d = tid & 127, hh = tid >> 7;
+    for (int hs = hh; hs < p.hpg; hs += 2) {
+      float o = 0.f;
+      for (int j = 0; j < R; ++j) o = fmaf(sA[hs * DH + j], elt_to_f32<DT>(sVB[j * BK_LD + d]), o);
+      const long long oi = (long long)b * p.out_sb + (long long)(kvh * p.hpg + hs) * p.out_sh + d;
+      dkv_store_f32<ODT>(p.out, oi, o);
+    }
+  }
+  if (tid == 0) p.counters[unit] = 0;
+}
+
+// RoPE table rows (64 x (cos, sin) each): 0..15 in-tile deltas (angle = delta * inv_freq),
+// 16 the per-step rotation (64 positions), 17 + T the base of tile T (angle = 16T * inv_freq).
+// Angles are formed in fp32 as the reference does (angle = float(pos) * inv_freq, reference
+// fused.py:65-66,97 / two_stage.py:36-44); cos/sin are evaluated in double and rounded.
+__global__ __launch_bounds__(256) void rope_table_kernel(float* __restrict__ rope, int row_from,
+                                                         int row_to, float log_theta) {
+  const int idx = blockIdx.x * 256 + threadIdx.x;
+  const int r = row_from + idx / 64, i = idx % 64;
+  if (r >= row_to) return;
+  const float inv = dkv_inv_freq(i, DH, log_theta);
+  float ang;
+  if (r < TILE)
+    ang = (float)r * inv;
+  else if (r == TILE)
+    ang = (float)(TILE * WAVES) * inv;
+  else
+    ang = (float)((r - ROPE_FIXED_ROWS) * TILE) * inv;
+  double s, c;
+  sincos((double)ang, &s, &c);
+  rope[(long long)r * 128 + 2 * i] = (float)c;
+  rope[(long long)r * 128 + 2 * i + 1] = (float)s;
 }
 
 // ---------------------------------------------------------------------------------------
@@ -588,7 +711,7 @@ __global__ __launch_bounds__(64) void selftest_kernel(int* __restrict__ mismatch
 
 }  // namespace
 
-static int splitk_tiles_bases(int S) { return (S + TILE - 1) / TILE; }
+static long long splitk_counter_floats(long long units) { return (units + 63) / 64 * 64; }
 
 extern "C" int dkv_splitk_choose_split(int B, int Hkv, int S) {
   if (B <= 0 || Hkv <= 0 || S <= 0) return 64;
@@ -597,9 +720,7 @@ extern "C" int dkv_splitk_choose_split(int B, int Hkv, int S) {
   long long sl = ((long long)S * units + target_groups - 1) / target_groups;
   sl = ((sl + 63) / 64) * 64;
   if (sl < 64) sl = 64;
-  // at most 63 splits per unit (merge kernel staging)
-  const long long min_sl = (((long long)S + 62) / 63 + 63) / 64 * 64;
-  if (sl < min_sl) sl = min_sl;
+  if (sl > MAX_SPLIT) sl = MAX_SPLIT;
   return (int)sl;
 }
 
@@ -609,69 +730,85 @@ extern "C" long long dkv_splitk_workspace_floats(int B, int Hq, int Hkv, int S, 
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || S <= 0) return 0;
   if (split_len <= 0) split_len = dkv_splitk_choose_split(B, Hkv, S);
   const long long n_splits = (S + split_len - 1) / split_len;
-  const long long hpg = Hq / Hkv;
-  const long long rope = (long long)(splitk_tiles_bases(S) + TILE + 1) * 128;
-  const long long parts = (long long)B * Hkv * n_splits * hpg * PREC;
-  return ((rope + 63) / 64) * 64 + parts;
+  const long long units = (long long)B * Hkv;
+  return splitk_counter_floats(units) + units * n_splits * (Hq / Hkv) * PREC;
 }
 
-namespace {
+extern "C" long long dkv_rope_table_floats(int n_tiles) {
+  if (n_tiles < 0) return 0;
+  return (long long)(ROPE_FIXED_ROWS + n_tiles) * 128;
+}
 
-struct SplitLaunch {
-  SplitParams p;
-  int route, dtype, out_dtype, n_tb;
-  long long units;
-  const void* v_basis;
-  long long v_unit, v_sr;
-  void* out;
-  long long out_sb, out_sh;
-  float log_theta;
-};
+extern "C" int dkv_rope_table(void* stream, float* rope, int from_tile, int to_tile,
+                              float log_theta) {
+  if (!rope || from_tile < 0 || to_tile < from_tile) return DKV_E_ARG;
+  const int row_from = from_tile == 0 ? 0 : ROPE_FIXED_ROWS + from_tile;
+  const int row_to = ROPE_FIXED_ROWS + to_tile;
+  const long long total = (long long)(row_to - row_from) * 64;
+  if (total == 0) return DKV_OK;
+  hipLaunchKernelGGL(rope_table_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, rope, row_from, row_to, log_theta);
+  DKV_HIP_CHECK_LAUNCH();
+  return DKV_OK;
+}
 
-int splitk_prepare(SplitLaunch& L, int route, int dtype, const void* q, long long q_sb,
-                   long long q_sh, const void* k_basis, long long k_unit_stride,
-                   long long k_basis_sr, const void* v_basis, long long v_unit_stride,
-                   long long v_basis_sr, const void* k_flat, long long k_ld, const void* v_flat,
-                   long long v_ld, const int* lens_k, const int* offs_k, long long tk_sb,
-                   long long tk_ss, const int* lens_v, const int* offs_v, long long tv_sb,
-                   long long tv_ss, float* partials, long long partials_floats, void* out,
-                   long long out_sb, long long out_sh, int out_dtype, int B, int Hq, int Hkv,
-                   int G, int S, int R, int Dh, float log_theta, int split_len) {
+template <int DT, int RT>
+static void launch_splitk_t(const SplitParams& p, int out_dtype, dim3 grid, hipStream_t st) {
+  if (out_dtype == DKV_F32)
+    hipLaunchKernelGGL((splitk_kernel<DT, RT, DKV_F32>), grid, dim3(256), 0, st, p);
+  else
+    hipLaunchKernelGGL((splitk_kernel<DT, RT, DT>), grid, dim3(256), 0, st, p);
+}
+
+extern "C" int dkv_decode_splitk(void* stream, int route, int dtype, const void* q, long long q_sb,
+                                 long long q_sh, const void* k_basis, long long k_unit_stride,
+                                 long long k_basis_sr, const void* v_basis,
+                                 long long v_unit_stride, long long v_basis_sr,
+                                 const void* k_flat, long long k_ld, const void* v_flat,
+                                 long long v_ld, const int* lens_k, const int* offs_k,
+                                 long long tk_sb, long long tk_ss, const int* lens_v,
+                                 const int* offs_v, long long tv_sb, long long tv_ss,
+                                 const float* rope, int rope_tiles, float* workspace,
+                                 long long workspace_floats, void* out, long long out_sb,
+                                 long long out_sh, int out_dtype, int B, int Hq, int Hkv, int G,
+                                 int S, int R, int Dh, int split_len) {
   if (route != DKV_ROUTE_FUSED && route != DKV_ROUTE_TWO_STAGE) return DKV_E_ARG;
-  if (out_dtype != dtype && out_dtype != DKV_F32) return DKV_E_ARG;
   if (dtype != DKV_F16 && dtype != DKV_BF16) return DKV_E_UNSUPPORTED;
+  if (out_dtype != dtype && out_dtype != DKV_F32) return DKV_E_ARG;
   if (B < 0 || Hq <= 0 || Hkv <= 0 || G <= 0 || S < 0 || R <= 0) return DKV_E_ARG;
   if (Hq % Hkv != 0 || Hkv % G != 0) return DKV_E_ARG;
   if (Dh != DH || R > DH || Hq / Hkv > 16) return DKV_E_UNSUPPORTED;
-  if (S == 0) return DKV_E_UNSUPPORTED;  // empty cache: the generic path defines the result
+  if (B == 0) return DKV_OK;
+  if (S == 0) return DKV_E_UNSUPPORTED;  // empty cache: the vector path defines the result
   if (!q || !k_basis || !v_basis || !k_flat || !v_flat || !lens_k || !offs_k || !lens_v ||
-      !offs_v || !partials || !out)
+      !offs_v || !rope || !workspace || !out)
     return DKV_E_ARG;
-  // 16-byte aligned basis rows for the vector LDS staging
+  // 16-byte aligned K basis rows for the vector LDS staging
   if (((uintptr_t)k_basis & 15) || (k_basis_sr & 7) || (k_unit_stride & 7))
     return DKV_E_UNSUPPORTED;
-  if (k_ld * 2 > 0x7fffffffLL || v_ld * 2 > 0x7fffffffLL) return DKV_E_UNSUPPORTED;
+  if (k_ld <= 0 || v_ld <= 0 || k_ld > (1LL << 30) || v_ld > (1LL << 30)) return DKV_E_UNSUPPORTED;
+  if (rope_tiles < (S + TILE - 1) / TILE) return DKV_E_ARG;
   if (split_len <= 0) split_len = dkv_splitk_choose_split(B, Hkv, S);
-  if (split_len % 64 != 0) return DKV_E_ARG;
-  const int n_splits = (S + split_len - 1) / split_len;
-  if (n_splits > 63) return DKV_E_ARG;
-  const long long need = dkv_splitk_workspace_floats(B, Hq, Hkv, S, R, split_len);
-  if (partials_floats < need) return DKV_E_WORKSPACE;
-  L.units = (long long)B * Hkv;
-  if (L.units * n_splits > 0x7fffffffLL) return DKV_E_UNSUPPORTED;
-  L.n_tb = splitk_tiles_bases(S);
-  const long long rope_floats = ((long long)(L.n_tb + TILE + 1) * 128 + 63) / 64 * 64;
-  SplitParams& p = L.p;
+  if (split_len % 64 != 0 || split_len > MAX_SPLIT) return DKV_E_ARG;
+  const long long n_splits = ((long long)S + split_len - 1) / split_len;
+  const long long units = (long long)B * Hkv;
+  if (units * n_splits > 0x7fffffffLL) return DKV_E_UNSUPPORTED;
+  if (workspace_floats < dkv_splitk_workspace_floats(B, Hq, Hkv, S, R, split_len))
+    return DKV_E_WORKSPACE;
+  SplitParams p;
   p.q = (const uint16_t*)q;
   p.q_sb = q_sb;
   p.q_sh = q_sh;
   p.k_basis = (const uint16_t*)k_basis;
   p.k_unit = k_unit_stride;
   p.k_sr = k_basis_sr;
+  p.v_basis = (const uint16_t*)v_basis;
+  p.v_unit = v_unit_stride;
+  p.v_sr = v_basis_sr;
   p.k_flat = (const uint16_t*)k_flat;
   p.v_flat = (const uint16_t*)v_flat;
-  p.k_ld = k_ld;
-  p.v_ld = v_ld;
+  p.k_ld = (int)k_ld;
+  p.v_ld = (int)v_ld;
   p.lens_k = lens_k;
   p.offs_k = offs_k;
   p.tk_sb = tk_sb;
@@ -680,8 +817,12 @@ int splitk_prepare(SplitLaunch& L, int route, int dtype, const void* q, long lon
   p.offs_v = offs_v;
   p.tv_sb = tv_sb;
   p.tv_ss = tv_ss;
-  p.rope = partials;
-  p.partials = partials + rope_floats;
+  p.rope = rope;
+  p.counters = reinterpret_cast<int*>(workspace);
+  p.partials = workspace + splitk_counter_floats(units);
+  p.out = out;
+  p.out_sb = out_sb;
+  p.out_sh = out_sh;
   p.B = B;
   p.Hq = Hq;
   p.Hkv = Hkv;
@@ -689,115 +830,22 @@ int splitk_prepare(SplitLaunch& L, int route, int dtype, const void* q, long lon
   p.S = S;
   p.R = R;
   p.hpg = Hq / Hkv;
-  p.n_splits = n_splits;
+  p.n_splits = (int)n_splits;
   p.split_len = split_len;
-  p.n_tb = L.n_tb;
   const float sm_scale = 1.0f / sqrtf((float)Dh);
-  p.q_scale = route == DKV_ROUTE_FUSED ? sm_scale * LOG2E : sm_scale;
+  p.score_scale = route == DKV_ROUTE_FUSED ? sm_scale * LOG2E : sm_scale;
   p.masked_score = -1.0e4f * sm_scale;
-  L.route = route;
-  L.dtype = dtype;
-  L.out_dtype = out_dtype;
-  L.v_basis = v_basis;
-  L.v_unit = v_unit_stride;
-  L.v_sr = v_basis_sr;
-  L.out = out;
-  L.out_sb = out_sb;
-  L.out_sh = out_sh;
-  L.log_theta = log_theta;
-  return DKV_OK;
-}
-
-int launch_rope(const SplitLaunch& L, hipStream_t st) {
-  const int total = (L.n_tb + TILE + 1) * 64;
-  hipLaunchKernelGGL(rope_table_kernel, dim3((total + 255) / 256), dim3(256), 0, st,
-                     const_cast<float*>(L.p.rope), L.n_tb, L.log_theta);
-  DKV_HIP_CHECK_LAUNCH();
-  return DKV_OK;
-}
-
-int launch_split(const SplitLaunch& L, hipStream_t st) {
-  const dim3 grid((unsigned)(L.units * L.p.n_splits)), block(256);
-  if (L.dtype == DKV_BF16) {
-    if (L.route == DKV_ROUTE_FUSED)
-      hipLaunchKernelGGL((splitk_kernel<DKV_BF16, DKV_ROUTE_FUSED>), grid, block, 0, st, L.p);
-    else
-      hipLaunchKernelGGL((splitk_kernel<DKV_BF16, DKV_ROUTE_TWO_STAGE>), grid, block, 0, st, L.p);
-  } else {
-    if (L.route == DKV_ROUTE_FUSED)
-      hipLaunchKernelGGL((splitk_kernel<DKV_F16, DKV_ROUTE_FUSED>), grid, block, 0, st, L.p);
-    else
-      hipLaunchKernelGGL((splitk_kernel<DKV_F16, DKV_ROUTE_TWO_STAGE>), grid, block, 0, st, L.p);
-  }
-  DKV_HIP_CHECK_LAUNCH();
-  return DKV_OK;
-}
-
-template <int DT, int RT>
-void launch_merge_t(const SplitLaunch& L, hipStream_t st) {
-  const dim3 mgrid((unsigned)L.units), block(256);
-  if (L.out_dtype == DKV_F32)
-    hipLaunchKernelGGL((merge_kernel<DT, RT, DKV_F32>), mgrid, block, 0, st, L.p.partials,
-                       (const uint16_t*)L.v_basis, L.v_unit, L.v_sr, L.out, L.out_sb, L.out_sh,
-                       L.p.Hkv, L.p.hpg, L.p.n_splits, L.p.R);
-  else
-    hipLaunchKernelGGL((merge_kernel<DT, RT, DT>), mgrid, block, 0, st, L.p.partials,
-                       (const uint16_t*)L.v_basis, L.v_unit, L.v_sr, L.out, L.out_sb, L.out_sh,
-                       L.p.Hkv, L.p.hpg, L.p.n_splits, L.p.R);
-}
-
-int launch_merge(const SplitLaunch& L, hipStream_t st) {
-  if (L.dtype == DKV_BF16) {
-    if (L.route == DKV_ROUTE_FUSED) launch_merge_t<DKV_BF16, DKV_ROUTE_FUSED>(L, st);
-    else launch_merge_t<DKV_BF16, DKV_ROUTE_TWO_STAGE>(L, st);
-  } else {
-    if (L.route == DKV_ROUTE_FUSED) launch_merge_t<DKV_F16, DKV_ROUTE_FUSED>(L, st);
-    else launch_merge_t<DKV_F16, DKV_ROUTE_TWO_STAGE>(L, st);
-  }
-  DKV_HIP_CHECK_LAUNCH();
-  return DKV_OK;
-}
-
-}  // namespace
-
-#define DKV_SPLITK_ARGS                                                                         \
-  void *stream, int route, int dtype, const void *q, long long q_sb, long long q_sh,            \
-      const void *k_basis, long long k_unit_stride, long long k_basis_sr, const void *v_basis,  \
-      long long v_unit_stride, long long v_basis_sr, const void *k_flat, long long k_ld,        \
-      const void *v_flat, long long v_ld, const int *lens_k, const int *offs_k, long long tk_sb, \
-      long long tk_ss, const int *lens_v, const int *offs_v, long long tv_sb, long long tv_ss,  \
-      float *partials, long long partials_floats, void *out, long long out_sb, long long out_sh, \
-      int out_dtype, int B, int Hq, int Hkv, int G, int S, int R, int Dh, float log_theta,       \
-      int split_len
-#define DKV_SPLITK_FWD                                                                          \
-  route, dtype, q, q_sb, q_sh, k_basis, k_unit_stride, k_basis_sr, v_basis, v_unit_stride,      \
-      v_basis_sr, k_flat, k_ld, v_flat, v_ld, lens_k, offs_k, tk_sb, tk_ss, lens_v, offs_v,     \
-      tv_sb, tv_ss, partials, partials_floats, out, out_sb, out_sh, out_dtype, B, Hq, Hkv, G, S,  \
-      R, Dh, log_theta, split_len
-
-extern "C" int dkv_decode_splitk(DKV_SPLITK_ARGS) {
-  if (B == 0) return DKV_OK;
-  SplitLaunch L;
-  int rc = splitk_prepare(L, DKV_SPLITK_FWD);
-  if (rc != DKV_OK) return rc;
+  const dim3 grid((unsigned)(units * n_splits));
   hipStream_t st = (hipStream_t)stream;
-  if ((rc = launch_rope(L, st)) != DKV_OK) return rc;
-  if ((rc = launch_split(L, st)) != DKV_OK) return rc;
-  return launch_merge(L, st);
-}
-
-extern "C" int dkv_decode_splitk_phase(int phase, DKV_SPLITK_ARGS) {
-  if (B == 0) return DKV_OK;
-  SplitLaunch L;
-  int rc = splitk_prepare(L, DKV_SPLITK_FWD);
-  if (rc != DKV_OK) return rc;
-  hipStream_t st = (hipStream_t)stream;
-  switch (phase) {
-    case 0: return launch_rope(L, st);
-    case 1: return launch_split(L, st);
-    case 2: return launch_merge(L, st);
-    default: return DKV_E_ARG;
+  if (dtype == DKV_BF16) {
+    if (route == DKV_ROUTE_FUSED) launch_splitk_t<DKV_BF16, DKV_ROUTE_FUSED>(p, out_dtype, grid, st);
+    else launch_splitk_t<DKV_BF16, DKV_ROUTE_TWO_STAGE>(p, out_dtype, grid, st);
+  } else {
+    if (route == DKV_ROUTE_FUSED) launch_splitk_t<DKV_F16, DKV_ROUTE_FUSED>(p, out_dtype, grid, st);
+    else launch_splitk_t<DKV_F16, DKV_ROUTE_TWO_STAGE>(p, out_dtype, grid, st);
   }
+  DKV_HIP_CHECK_LAUNCH();
+  return DKV_OK;
 }
 
 extern "C" int dkv_selftest_layouts(void* stream, int* mismatches) {

@@ -1,9 +1,14 @@
 """Host side of the gfx950 split-K decode-attention kernel.
 
-``splitk_attention`` launches ``dkv_decode_splitk`` (RoPE table, split kernel, merge/projection)
-on torch's current stream. It is used by both router routes when the inputs fit the kernel and,
-directly, by the native multi-group layout (per-head spectral bases, one packed cache row per
-(batch, KV group)): ``grouped_decode_attention``.
+``splitk_attention`` launches ``dkv_decode_splitk`` (one kernel: split-K attention plus the
+merge/projection done by the last workgroup of each unit) on torch's current stream. It is used
+by both router routes when the inputs fit the kernel and, directly, by the native multi-group
+layout (per-head spectral bases, one packed cache row per (batch, KV group)):
+``grouped_decode_attention``.
+
+Two device buffers are cached per (device, stream): the RoPE cos/sin table (per theta; extended
+as the cache grows, so decode steps do not rebuild it) and the zero-initialised workspace whose
+arrival counters the kernel leaves at zero.
 """
 
 from __future__ import annotations
@@ -18,6 +23,37 @@ from .. import _lib
 SPLITK_MAX_RANK = 128
 SPLITK_HEAD_DIM = 128
 SPLITK_MAX_HPG = 16
+
+_ROPE_CACHE: dict = {}  # (device, stream, theta) -> (table, tiles)
+_WS_CACHE: dict = {}    # (device, stream) -> zeroed fp32 workspace
+
+
+def rope_table(device: torch.device, stream: int, theta: float, seq_len: int):
+    """RoPE table with at least ceil(seq_len / 16) tile rows for ``theta`` (cached, grown by
+    doubling)."""
+    lib = _lib.load()
+    need = max(1, (seq_len + 15) // 16)
+    key = (device.index, stream, float(theta))
+    ent = _ROPE_CACHE.get(key)
+    if ent is None or ent[1] < need:
+        tiles = max(need, 2 * ent[1] if ent else 0, 64)
+        t = torch.empty(int(lib.dkv_rope_table_floats(tiles)), dtype=torch.float32,
+                        device=device)
+        _lib.check(lib.dkv_rope_table(stream, t.data_ptr(), 0, tiles, math.log(theta)),
+                   "dkv_rope_table")
+        ent = (t, tiles)
+        _ROPE_CACHE[key] = ent
+    return ent
+
+
+def workspace(device: torch.device, stream: int, floats: int) -> torch.Tensor:
+    """Zero-initialised split-K workspace of at least ``floats`` floats (cached)."""
+    key = (device.index, stream)
+    t = _WS_CACHE.get(key)
+    if t is None or t.numel() < floats:
+        t = torch.zeros(max(int(floats), 1 << 16), dtype=torch.float32, device=device)
+        _WS_CACHE[key] = t
+    return t
 
 
 @dataclass(frozen=True)
@@ -106,9 +142,10 @@ def splitk_attention(q3: torch.Tensor, k_flat: torch.Tensor, v_flat: torch.Tenso
         out = torch.empty((B, hq, dh), dtype=odt, device=q3.device)
     elif out.dtype != odt or out.stride(2) != 1:
         raise ValueError("out must have unit last stride and the requested dtype")
-    nfl = lib.dkv_splitk_workspace_floats(B, hq, layout.n_kv, S, R, split_len)
-    ws = torch.empty(max(int(nfl), 1), dtype=torch.float32, device=q3.device)
     st = _lib.stream_of(q3)
+    nfl = lib.dkv_splitk_workspace_floats(B, hq, layout.n_kv, S, R, split_len)
+    ws = workspace(q3.device, st, int(nfl))
+    rope, rope_tiles = rope_table(q3.device, st, theta, S)
     rc = lib.dkv_decode_splitk(
         st, route, _lib.dtype_code(q3.dtype),
         q3.data_ptr(), q3.stride(0), q3.stride(1),
@@ -117,9 +154,9 @@ def splitk_attention(q3: torch.Tensor, k_flat: torch.Tensor, v_flat: torch.Tenso
         k_flat.data_ptr(), k_flat.stride(0), v_flat.data_ptr(), v_flat.stride(0),
         lens_k.data_ptr(), offs_k.data_ptr(), lens_k.stride(0), lens_k.stride(1),
         lens_v.data_ptr(), offs_v.data_ptr(), lens_v.stride(0), lens_v.stride(1),
-        ws.data_ptr(), ws.numel(), out.data_ptr(), out.stride(0), out.stride(1),
-        _lib.dtype_code(out.dtype), B, hq, layout.n_kv, groups, S, R, dh, math.log(theta),
-        split_len)
+        rope.data_ptr(), rope_tiles, ws.data_ptr(), ws.numel(),
+        out.data_ptr(), out.stride(0), out.stride(1), _lib.dtype_code(out.dtype),
+        B, hq, layout.n_kv, groups, S, R, dh, split_len)
     _lib.check(rc, "dkv_decode_splitk")
     return out
 

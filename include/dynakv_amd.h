@@ -155,6 +155,17 @@ int dkv_av(void* stream, int mode, int scores_dtype, int cache_dtype, int out_dt
            int B, int Hq, int S, int R, int Dh);
 
 /*
+ * RoPE cos/sin table for the split-K kernel, (17 + n_tiles) rows of 64 (cos, sin) fp32 pairs:
+ * rows 0..15 the in-tile offsets (angle = d * inv_freq), row 16 the rotation by 64 positions,
+ * row 17 + T the base of 16-token tile T (angle = 16T * inv_freq); inv_freq_i =
+ * exp(-(2i/128) ln theta) and every angle formed in fp32 as the reference does (fused.py:65-66,
+ * 97; two_stage.py:36-44). dkv_rope_table fills the fixed rows when from_tile == 0 and the tile
+ * rows [from_tile, to_tile), so a caller can extend a table as the cache grows.
+ */
+long long dkv_rope_table_floats(int n_tiles);
+int dkv_rope_table(void* stream, float* rope, int from_tile, int to_tile, float log_theta);
+
+/*
  * Split-K compressed decode attention on MFMA (the fast path for both router routes,
  * reference fused.py:28-170 and two_stage.py:48-324 as called from router.py:20-59).
  * One work unit = (batch b, KV head k) with hpg = Hq / Hkv query heads sharing the K/V basis
@@ -163,12 +174,16 @@ int dkv_av(void* stream, int mode, int scores_dtype, int cache_dtype, int out_dt
  *   k_basis / v_basis: base pointers with basis of KV head k at  base + k * unit_stride,
  *                      rank stride basis_sr, unit dim stride (R x Dh).
  *   lens/offs tables for K and V with their own (sb, ss) strides.
- *   partials: fp32 workspace of dkv_splitk_workspace_floats(...) floats.
+ *   rope: table from dkv_rope_table with rope_tiles >= ceil(S / 16) tile rows (it carries theta).
+ *   workspace: fp32 buffer of dkv_splitk_workspace_floats(...) floats. Its first
+ *              ceil(B*Hkv/64)*64 floats hold arrival counters that must be zero before the
+ *              first call (allocate the workspace zero-filled); every call leaves them zero.
+ *              Calls that share a workspace must be ordered (same stream).
  *   out: (B, Hq, Dh) strides (out_sb, out_sh), dtype out_dtype = the cache dtype (what the
- *        reference returns) or DKV_F32 (the merge result before rounding).
+ *        reference returns) or DKV_F32 (the merged result before rounding).
  * Requirements: q and cache dtype f16 or bf16 (same), Dh == 128, R <= 128, hpg <= 16,
- * Hkv % G == 0. split_len is a multiple of 64 (0 = choose automatically).
- * The launch pair is split kernel + merge kernel; both are asynchronous.
+ * Hkv % G == 0, row strides < 2^30 elements. split_len is a multiple of 64 and <= 512
+ * (0 = choose automatically). One kernel launch.
  */
 long long dkv_splitk_workspace_floats(int B, int Hq, int Hkv, int S, int R, int split_len);
 int dkv_splitk_choose_split(int B, int Hkv, int S);
@@ -179,27 +194,10 @@ int dkv_decode_splitk(void* stream, int route, int dtype,
                       const void* k_flat, long long k_ld, const void* v_flat, long long v_ld,
                       const int* lens_k, const int* offs_k, long long tk_sb, long long tk_ss,
                       const int* lens_v, const int* offs_v, long long tv_sb, long long tv_ss,
-                      float* partials, long long partials_floats,
+                      const float* rope, int rope_tiles,
+                      float* workspace, long long workspace_floats,
                       void* out, long long out_sb, long long out_sh, int out_dtype,
-                      int B, int Hq, int Hkv, int G, int S, int R, int Dh,
-                      float log_theta, int split_len);
-
-/*
- * One phase of dkv_decode_splitk (same arguments): 0 = RoPE cos/sin table into the workspace,
- * 1 = split kernel (partials), 2 = merge + V projection. Running 0, 1, 2 in order on one
- * stream equals dkv_decode_splitk; the phases exist so callers can time the split kernel alone.
- */
-int dkv_decode_splitk_phase(int phase, void* stream, int route, int dtype,
-                            const void* q, long long q_sb, long long q_sh,
-                            const void* k_basis, long long k_unit_stride, long long k_basis_sr,
-                            const void* v_basis, long long v_unit_stride, long long v_basis_sr,
-                            const void* k_flat, long long k_ld, const void* v_flat, long long v_ld,
-                            const int* lens_k, const int* offs_k, long long tk_sb, long long tk_ss,
-                            const int* lens_v, const int* offs_v, long long tv_sb, long long tv_ss,
-                            float* partials, long long partials_floats,
-                            void* out, long long out_sb, long long out_sh, int out_dtype,
-                            int B, int Hq, int Hkv, int G, int S, int R, int Dh,
-                            float log_theta, int split_len);
+                      int B, int Hq, int Hkv, int G, int S, int R, int Dh, int split_len);
 
 /*
  * Launch-layout self test (diagnostic, no reference counterpart): runs the MFMA operand

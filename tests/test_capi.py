@@ -45,7 +45,8 @@ def test_host_only_entry_points():
     assert lib.dkv_version() >= 100
     assert lib.dkv_status_string(-1) == b"invalid argument"
     sl = lib.dkv_splitk_choose_split(16, 8, 8292)
-    assert sl % 64 == 0 and (8292 + sl - 1) // sl <= 63
+    assert sl % 64 == 0 and 64 <= sl <= 512
+    assert lib.dkv_rope_table_floats(10) == (17 + 10) * 128
     assert lib.dkv_splitk_workspace_floats(16, 32, 8, 8292, 128, sl) > 0
 
 
@@ -58,8 +59,8 @@ def test_argument_validation_without_device():
     assert lib.dkv_append_decode(None, 1, None, 0, None, 0, None, 0, None, None, 0, 0, None, 0, 0, 4) == 0
     # split-K: rank above 128 is outside the kernel
     rc = lib.dkv_decode_splitk(None, 0, 2, None, 0, 0, None, 0, 0, None, 0, 0, None, 0, None, 0,
-                               None, None, 0, 0, None, None, 0, 0, None, 0, None, 0, 0, 2,
-                               1, 32, 8, 8, 10, 256, 128, 1.0, 0)
+                               None, None, 0, 0, None, None, 0, 0, None, 0, None, 0,
+                               None, 0, 0, 2, 1, 32, 8, 8, 10, 256, 128, 0)
     assert rc == -2
     with pytest.raises(NotImplementedError):
         _lib.check(rc, "dkv_decode_splitk")
