@@ -52,6 +52,7 @@ struct SplitParams {
   const uint16_t* k_flat;
   const uint16_t* v_flat;
   int k_ld, v_ld;
+  uint32_t k_end, v_end;  // elements covered by the buffer resources: rows * ld
   const int* lens_k;
   const int* offs_k;
   long long tk_sb, tk_ss;
@@ -119,17 +120,15 @@ __device__ __forceinline__ void split_f16x2(float x0, float x1, uint32_t& hi, ui
   lo = __builtin_bit_cast(uint32_t, dkv_f16x2{l0, l1});
 }
 
-// Element-wise gather of the first nv (1..8) 16-bit values at element offset e; the rest zero.
+// Element-wise gather of the first nv (1..8) 16-bit values at element offset e, the rest zero:
+// eight unconditional 2-byte loads, those past nv aimed at the out-of-range offset.
 __device__ __forceinline__ dkv_u32x4 gather8_b16(__amdgpu_buffer_rsrc_t r, int e, int nv) {
-  uint32_t w[4] = {0u, 0u, 0u, 0u};
+  uint32_t v[8];
 #pragma unroll
-  for (int t = 0; t < 8; ++t) {
-    if (t < nv) {
-      const uint32_t v = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (e + t) * 2, 0, 0);
-      w[t >> 1] |= v << (16 * (t & 1));
-    }
-  }
-  return dkv_u32x4{w[0], w[1], w[2], w[3]};
+  for (int t = 0; t < 8; ++t)
+    v[t] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, t < nv ? (e + t) * 2 : 0x7ffffff0, 0, 0);
+  return dkv_u32x4{v[0] | (v[1] << 16), v[2] | (v[3] << 16), v[4] | (v[5] << 16),
+                   v[6] | (v[7] << 16)};
 }
 
 // Zero the elements at index >= nv (0 <= nv < 8) of an 8 x 16-bit vector.
@@ -149,15 +148,16 @@ __device__ __forceinline__ uint32_t prefix_mask_word(int k, int d) {
   return k >= 2 * d + 2 ? 0xffffffffu : (k == 2 * d + 1 ? 0x0000ffffu : 0u);
 }
 
-// 16-byte gather of ranks [32c + 8g, +8) of one token (offset o, clamped count r) from a row;
-// lanes with nothing to load read the out-of-range offset (zero, no memory traffic). A window
-// that would cross the end of the row's buffer falls back to element loads, because an
+// 16-byte gather of ranks [32c + 8g, +8) of one token at element offset o (from the start of
+// the buffer resource) with clamped count r; lanes with nothing to load read the out-of-range
+// offset (zero, no memory traffic). A window that would cross the end of the resource (only
+// the last token of the buffer's last row can) falls back to element loads, because an
 // out-of-range vector access reads as zero in full.
-__device__ __forceinline__ dkv_u32x4 gather_chunk(__amdgpu_buffer_rsrc_t rs, int ld, int o, int r,
-                                                  int c, int g) {
+__device__ __forceinline__ dkv_u32x4 gather_chunk(__amdgpu_buffer_rsrc_t rs, uint32_t end, int o,
+                                                  int r, int c, int g) {
   const int j0 = 32 * c + 8 * g;
   const int nv = r - j0;
-  if (nv > 0 && o + j0 + 8 > ld) return gather8_b16(rs, o + j0, min(nv, 8));
+  if (nv > 0 && (uint32_t)(o + j0 + 8) > end) return gather8_b16(rs, o + j0, min(nv, 8));
   return __builtin_amdgcn_raw_buffer_load_b128(rs, nv > 0 ? (o + j0) * 2 : OOB, 0, 0);
 }
 
@@ -264,15 +264,23 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(SplitParams p) {
   dkv_u32x4 bq[4];
   {
     const bool real = n < p.hpg;
-    const long long qo = (long long)b * p.q_sb + (long long)(kvh * p.hpg + (real ? n : 0)) * p.q_sh;
+    const long long qo = (long long)b * p.q_sb + (long long)(kvh * p.hpg + min(n, p.hpg - 1)) * p.q_sh;
+    uint32_t qa[16], qb[16];
+#pragma unroll
+    for (int pp = 0; pp < 4; ++pp)
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const int i = 16 * pp + 4 * g + w;
+        qa[pp * 4 + w] = p.q[qo + i];
+        qb[pp * 4 + w] = p.q[qo + i + 64];
+      }
 #pragma unroll
     for (int pp = 0; pp < 4; ++pp) {
       uint32_t w4[4];
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
-        const int i = 16 * pp + 4 * g + w;
-        const float a = real ? elt_to_f32<DT>(p.q[qo + i]) : 0.f;
-        const float c = real ? elt_to_f32<DT>(p.q[qo + i + 64]) : 0.f;
+        const float a = real ? elt_to_f32<DT>(qa[pp * 4 + w]) : 0.f;
+        const float c = real ? elt_to_f32<DT>(qb[pp * 4 + w]) : 0.f;
         w4[w] = pack_f16x2(a, c);
       }
       bq[pp] = dkv_u32x4{w4[0], w4[1], w4[2], w4[3]};
@@ -302,10 +310,10 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(SplitParams p) {
   }
   __syncthreads();  // sTmax ready
 
-  const __amdgpu_buffer_rsrc_t rk_src =
-      dkv_make_rsrc(p.k_flat + (long long)row * p.k_ld, (uint32_t)p.k_ld * 2u);
-  const __amdgpu_buffer_rsrc_t rv_src =
-      dkv_make_rsrc(p.v_flat + (long long)row * p.v_ld, (uint32_t)p.v_ld * 2u);
+  // one resource per buffer, ranges [flat, flat + rows * ld); row offsets go in the voffset
+  const __amdgpu_buffer_rsrc_t rk_src = dkv_make_rsrc(p.k_flat, p.k_end * 2u);
+  const __amdgpu_buffer_rsrc_t rv_src = dkv_make_rsrc(p.v_flat, p.v_end * 2u);
+  const int k_row0 = row * p.k_ld, v_row0 = row * p.v_ld;
   uint16_t* kt = sKT[wave];
   uint16_t* vt = sVT[wave];
 
@@ -329,17 +337,17 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(SplitParams p) {
   dkv_u32x4 kx[4], vx[4];  // in-flight gathers of the next tile
   auto issue = [&](const TileMeta& d, int T) {
     const int tl = T * TILE + n - s_begin;
-    const int ok = d.valid ? sTab[1][tl] : 0;
-    const int ov = d.valid ? sTab[3][tl] : 0;
+    const int ok = k_row0 + (d.valid ? sTab[1][tl] : 0);
+    const int ov = v_row0 + (d.valid ? sTab[3][tl] : 0);
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       kx[c] = dkv_u32x4{0u, 0u, 0u, 0u};
-      if (c < d.nck) kx[c] = gather_chunk(rk_src, p.k_ld, ok, d.rkc, c, g);
+      if (c < d.nck) kx[c] = gather_chunk(rk_src, p.k_end, ok, d.rkc, c, g);
     }
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       vx[c] = dkv_u32x4{0u, 0u, 0u, 0u};
-      if (c < d.nvc) vx[c] = gather_chunk(rv_src, p.v_ld, ov, d.rvc, c, g);
+      if (c < d.nvc) vx[c] = gather_chunk(rv_src, p.v_end, ov, d.rvc, c, g);
     }
   };
 
@@ -355,6 +363,10 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(SplitParams p) {
     issue(cur, tile0);
   }
   for (int T = tile0; T * TILE < s_end; T += WAVES) {
+    // chunk counts are wave-uniform: keep them in scalar registers
+    cur.nck = __builtin_amdgcn_readfirstlane(cur.nck);
+    cur.nvc = __builtin_amdgcn_readfirstlane(cur.nvc);
+    cur.nbv = __builtin_amdgcn_readfirstlane(cur.nbv);
     // ---- store the current tile (masked) to the wave's LDS tiles, then issue the next ------
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
@@ -786,7 +798,10 @@ extern "C" int dkv_decode_splitk(void* stream, int route, int dtype, const void*
   // 16-byte aligned K basis rows for the vector LDS staging
   if (((uintptr_t)k_basis & 15) || (k_basis_sr & 7) || (k_unit_stride & 7))
     return DKV_E_UNSUPPORTED;
-  if (k_ld <= 0 || v_ld <= 0 || k_ld > (1LL << 30) || v_ld > (1LL << 30)) return DKV_E_UNSUPPORTED;
+  if (k_ld <= 0 || v_ld <= 0) return DKV_E_ARG;
+  // buffer offsets are 32-bit byte offsets from the first row
+  const long long rows = (long long)B * G;
+  if (rows * k_ld >= (1LL << 30) || rows * v_ld >= (1LL << 30)) return DKV_E_UNSUPPORTED;
   if (rope_tiles < (S + TILE - 1) / TILE) return DKV_E_ARG;
   if (split_len <= 0) split_len = dkv_splitk_choose_split(B, Hkv, S);
   if (split_len % 64 != 0 || split_len > MAX_SPLIT) return DKV_E_ARG;
@@ -809,6 +824,8 @@ extern "C" int dkv_decode_splitk(void* stream, int route, int dtype, const void*
   p.v_flat = (const uint16_t*)v_flat;
   p.k_ld = (int)k_ld;
   p.v_ld = (int)v_ld;
+  p.k_end = (uint32_t)(rows * k_ld);
+  p.v_end = (uint32_t)(rows * v_ld);
   p.lens_k = lens_k;
   p.offs_k = offs_k;
   p.tk_sb = tk_sb;

@@ -182,7 +182,7 @@ int dkv_rope_table(void* stream, float* rope, int from_tile, int to_tile, float 
  *   out: (B, Hq, Dh) strides (out_sb, out_sh), dtype out_dtype = the cache dtype (what the
  *        reference returns) or DKV_F32 (the merged result before rounding).
  * Requirements: q and cache dtype f16 or bf16 (same), Dh == 128, R <= 128, hpg <= 16,
- * Hkv % G == 0, row strides < 2^30 elements. split_len is a multiple of 64 and <= 512
+ * Hkv % G == 0, (B*G) * row stride < 2^30 elements for each flat buffer. split_len is a multiple of 64 and <= 512
  * (0 = choose automatically). One kernel launch.
  */
 long long dkv_splitk_workspace_floats(int B, int Hq, int Hkv, int S, int R, int split_len);
