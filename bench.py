@@ -8,8 +8,8 @@ plus a seeded 5% forced to 128. Synthetic data generated on the device; the pack
 per-step inputs are resident in HBM before the timed region.
 
 One step = decode append of K and V for all 128 rows + the router decision + decode attention
-(long route: one split-K kernel launch with two-stage semantics; its last workgroup per unit
-merges the splits and projects through the V basis).
+(long route: the split-K kernel with two-stage semantics, then the merge kernel that projects
+through the V basis).
 
 Output: one JSON line. ``value`` is decode-attention GB/s: algorithmic bytes of the attention
 (packed K/V coefficients read once, int32 lengths, unique bases, q and output) divided by the
@@ -111,7 +111,7 @@ def attention_bytes(cfg, lk_h, lv_h, S):
 
 
 class SplitKRunner:
-    """Launches dkv_decode_splitk (one kernel) with HIP events around it on the current stream
+    """Launches dkv_decode_splitk (split + merge kernels) with HIP events around it on the current stream
     (the stream the kernel runs on). The RoPE table and the workspace are built once, before
     any timed step."""
 

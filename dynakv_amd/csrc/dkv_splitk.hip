@@ -22,9 +22,10 @@
 //      more than 2^11.5);
 //   5. P.X^V in coefficient space on 16x16x16 MFMA; X^V goes through a per-wave LDS tile so
 //      the operand (4 tokens x 1 rank per lane) is read transposed.
-// Epilogue: the 4 waves combine through LDS into one (m, l, acc[128]) record per head; the
-// last workgroup of a unit to finish (arrival counter) LSE-merges the unit's splits and
-// projects once through the V basis.
+// Epilogue: the 4 waves combine through LDS into one (m, l, acc[128]) record per head.
+// merge_kernel (same stream, one workgroup per unit) LSE-merges a unit's split records and
+// projects once through the V basis; stream order makes the records visible to it without
+// device-scope fences (an agent-scope acquire would invalidate the XCD's L2).
 #include "dkv_common.h"
 
 namespace {
@@ -61,7 +62,6 @@ struct SplitParams {
   long long tv_sb, tv_ss;
   const float* rope;   // rows of 64 (cos, sin): 16 in-tile deltas, 1 step, then tile bases
   float* partials;     // [unit][split][hpg][PREC]
-  int* counters;       // [unit] arrival counters, zero on entry and on exit
   void* out;
   long long out_sb, out_sh;
   int B, Hq, Hkv, G, S, R, hpg, n_splits, split_len;
@@ -171,7 +171,7 @@ struct TileMeta {
   bool valid;
 };
 
-template <int DT, int ROUTE, int ODT>
+template <int DT, int ROUTE>
 __global__ __launch_bounds__(256, 2) void splitk_kernel(SplitParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t sBK[DH * BK_LD];
   __shared__ __attribute__((aligned(16))) int sTab[4][MAX_SPLIT];
@@ -180,7 +180,6 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(SplitParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t sVT[WAVES][TILE * VT_LD];
   __shared__ __attribute__((aligned(16))) uint32_t sMask[9][4];
   __shared__ __attribute__((aligned(16))) float sStep[2][64];
-  __shared__ int sLast;
 
   // XCD-aware mapping: consecutive workgroup ids land on different XCDs (id % 8), so give
   // every split of one unit the same id % 8 to keep that unit's basis in one L2.
@@ -208,12 +207,21 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(SplitParams p) {
 
   // ---- prologue: K basis, tables, masks, per-step rotation --------------------------------
   {
+    // transpose to [dim][rank]: consecutive lanes take consecutive ranks, so each 2-byte LDS
+    // store of a wave covers 128 contiguous bytes (no bank conflicts)
     const uint16_t* kb = p.k_basis + (long long)kvh * p.k_unit;
-    for (int idx = tid; idx < 128 * 16; idx += 256) {
-      const int j = idx >> 4, d8 = (idx & 15) * 8;
-      dkv_u32x4 v = {0u, 0u, 0u, 0u};
-      if (j < R) v = *(const dkv_u32x4*)(kb + (long long)j * p.k_sr + d8);
-      const uint32_t e[4] = {v.x, v.y, v.z, v.w};
+    const int j = tid & 127;
+    dkv_u32x4 v[8];
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+      const int d8 = ((tid >> 7) + 2 * it) * 8;
+      v[it] = dkv_u32x4{0u, 0u, 0u, 0u};
+      if (j < R) v[it] = *(const dkv_u32x4*)(kb + (long long)j * p.k_sr + d8);
+    }
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+      const int d8 = ((tid >> 7) + 2 * it) * 8;
+      const uint32_t e[4] = {v[it].x, v[it].y, v[it].z, v[it].w};
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         sBK[(d8 + 2 * t) * BK_LD + j] = (uint16_t)(e[t] & 0xffffu);
@@ -543,22 +551,22 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(SplitParams p) {
     prec[hs * PREC + e] = e == 0 ? M : v;
   }
 
-  // ---- the last workgroup of this unit merges all splits ---------------------------------
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) sLast = atomicAdd(&p.counters[unit], 1) == p.n_splits - 1;
-  __syncthreads();
-  if (!sLast) return;
-  __threadfence();
-  // V basis -> LDS as [rank][dim] (reuses sBK); merged accumulators [16][DH] (8 KiB) reuse
-  // the K tiles (17 KiB); per-head M and L reuse the V tiles
-  uint16_t* sVB = sBK;
-  float* sA = reinterpret_cast<float*>(&sKT[0][0]);
-  float* sML = reinterpret_cast<float*>(&sVT[0][0]);
-  static_assert(sizeof(sKT) >= 16 * DH * sizeof(float), "merge scratch does not fit");
+}
+
+// One workgroup per unit: LSE-merge the unit's split records per head slot, normalise with the
+// route's denominator, project once through the unit's V basis, store in the output dtype.
+template <int DT, int ROUTE, int ODT>
+__global__ __launch_bounds__(256) void merge_kernel(SplitParams p) {
+  __shared__ __attribute__((aligned(16))) uint16_t sVB[DH * BK_LD];  // [rank][dim]
+  __shared__ float sA[16][DH];
+  __shared__ float sML[2][16];
+  const int unit = blockIdx.x;
+  const int b = unit / p.Hkv, kvh = unit % p.Hkv;
+  const int tid = threadIdx.x;
+  const int R = p.R;
   {
     const uint16_t* vb = p.v_basis + (long long)kvh * p.v_unit;
-    for (int idx = tid; idx < 128 * 16; idx += 256) {
+    for (int idx = tid; idx < DH * 16; idx += 256) {
       const int j = idx >> 4, d8 = (idx & 15) * 8;
       uint32_t w4[4] = {0u, 0u, 0u, 0u};
       if (j < R) {
@@ -570,7 +578,7 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(SplitParams p) {
     }
   }
   const float* pr = p.partials + (long long)unit * p.n_splits * p.hpg * PREC;
-  if (tid < 16 * 16) {
+  {
     const int hs = tid >> 4, l16 = tid & 15;
     float M = -INFINITY;
     if (hs < p.hpg)
@@ -586,14 +594,14 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(SplitParams p) {
 #pragma unroll
     for (int m = 8; m >= 1; m >>= 1) L += __shfl_xor(L, m, 16);
     if (l16 == 0) {
-      sML[hs] = M;
-      sML[16 + hs] = L;
+      sML[0][hs] = M;
+      sML[1][hs] = L;
     }
   }
   __syncthreads();
   for (int idx = tid; idx < p.hpg * DH; idx += 256) {
     const int hs = idx / DH, j = idx % DH;
-    const float M = sML[hs], L = sML[16 + hs];
+    const float M = sML[0][hs], L = sML[1][hs];
     float a = 0.f;
     if (j < R && M != -INFINITY) {
       for (int s = 0; s < p.n_splits; ++s) {
@@ -602,19 +610,17 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(SplitParams p) {
       }
     }
     const float den = ROUTE == DKV_ROUTE_TWO_STAGE ? fmaxf(L, 1e-6f) : L;
-    sA[hs * DH + j] = a / den;
+    sA[hs][j] = a / den;
   }
   __syncthreads();
-  {
-    const int d = tid & 127, hh = tid >> 7;
-    for (int hs = hh; hs < p.hpg; hs += 2) {
-      float o = 0.f;
-      for (int j = 0; j < R; ++j) o = fmaf(sA[hs * DH + j], elt_to_f32<DT>(sVB[j * BK_LD + d]), o);
-      const long long oi = (long long)b * p.out_sb + (long long)(kvh * p.hpg + hs) * p.out_sh + d;
-      dkv_store_f32<ODT>(p.out, oi, o);
-    }
+  const int d = tid & 127, hh = tid >> 7;
+  for (int hs = hh; hs < p.hpg; hs += 2) {
+    float o = 0.f;
+#pragma unroll 8
+    for (int j = 0; j < R; ++j) o = fmaf(sA[hs][j], elt_to_f32<DT>(sVB[j * BK_LD + d]), o);
+    const long long oi = (long long)b * p.out_sb + (long long)(kvh * p.hpg + hs) * p.out_sh + d;
+    dkv_store_f32<ODT>(p.out, oi, o);
   }
-  if (tid == 0) p.counters[unit] = 0;
 }
 
 // RoPE table rows (64 x (cos, sin) each): 0..15 in-tile deltas (angle = delta * inv_freq),
@@ -723,8 +729,6 @@ __global__ __launch_bounds__(64) void selftest_kernel(int* __restrict__ mismatch
 
 }  // namespace
 
-static long long splitk_counter_floats(long long units) { return (units + 63) / 64 * 64; }
-
 extern "C" int dkv_splitk_choose_split(int B, int Hkv, int S) {
   if (B <= 0 || Hkv <= 0 || S <= 0) return 64;
   const long long units = (long long)B * Hkv;
@@ -743,7 +747,7 @@ extern "C" long long dkv_splitk_workspace_floats(int B, int Hq, int Hkv, int S, 
   if (split_len <= 0) split_len = dkv_splitk_choose_split(B, Hkv, S);
   const long long n_splits = (S + split_len - 1) / split_len;
   const long long units = (long long)B * Hkv;
-  return splitk_counter_floats(units) + units * n_splits * (Hq / Hkv) * PREC;
+  return units * n_splits * (Hq / Hkv) * PREC;
 }
 
 extern "C" long long dkv_rope_table_floats(int n_tiles) {
@@ -765,11 +769,13 @@ extern "C" int dkv_rope_table(void* stream, float* rope, int from_tile, int to_t
 }
 
 template <int DT, int RT>
-static void launch_splitk_t(const SplitParams& p, int out_dtype, dim3 grid, hipStream_t st) {
+static void launch_splitk_t(const SplitParams& p, int out_dtype, dim3 grid, dim3 mgrid,
+                            hipStream_t st) {
+  hipLaunchKernelGGL((splitk_kernel<DT, RT>), grid, dim3(256), 0, st, p);
   if (out_dtype == DKV_F32)
-    hipLaunchKernelGGL((splitk_kernel<DT, RT, DKV_F32>), grid, dim3(256), 0, st, p);
+    hipLaunchKernelGGL((merge_kernel<DT, RT, DKV_F32>), mgrid, dim3(256), 0, st, p);
   else
-    hipLaunchKernelGGL((splitk_kernel<DT, RT, DT>), grid, dim3(256), 0, st, p);
+    hipLaunchKernelGGL((merge_kernel<DT, RT, DT>), mgrid, dim3(256), 0, st, p);
 }
 
 extern "C" int dkv_decode_splitk(void* stream, int route, int dtype, const void* q, long long q_sb,
@@ -835,8 +841,7 @@ extern "C" int dkv_decode_splitk(void* stream, int route, int dtype, const void*
   p.tv_sb = tv_sb;
   p.tv_ss = tv_ss;
   p.rope = rope;
-  p.counters = reinterpret_cast<int*>(workspace);
-  p.partials = workspace + splitk_counter_floats(units);
+  p.partials = workspace;
   p.out = out;
   p.out_sb = out_sb;
   p.out_sh = out_sh;
@@ -852,14 +857,18 @@ extern "C" int dkv_decode_splitk(void* stream, int route, int dtype, const void*
   const float sm_scale = 1.0f / sqrtf((float)Dh);
   p.score_scale = route == DKV_ROUTE_FUSED ? sm_scale * LOG2E : sm_scale;
   p.masked_score = -1.0e4f * sm_scale;
-  const dim3 grid((unsigned)(units * n_splits));
+  const dim3 grid((unsigned)(units * n_splits)), mgrid((unsigned)units);
   hipStream_t st = (hipStream_t)stream;
   if (dtype == DKV_BF16) {
-    if (route == DKV_ROUTE_FUSED) launch_splitk_t<DKV_BF16, DKV_ROUTE_FUSED>(p, out_dtype, grid, st);
-    else launch_splitk_t<DKV_BF16, DKV_ROUTE_TWO_STAGE>(p, out_dtype, grid, st);
+    if (route == DKV_ROUTE_FUSED)
+      launch_splitk_t<DKV_BF16, DKV_ROUTE_FUSED>(p, out_dtype, grid, mgrid, st);
+    else
+      launch_splitk_t<DKV_BF16, DKV_ROUTE_TWO_STAGE>(p, out_dtype, grid, mgrid, st);
   } else {
-    if (route == DKV_ROUTE_FUSED) launch_splitk_t<DKV_F16, DKV_ROUTE_FUSED>(p, out_dtype, grid, st);
-    else launch_splitk_t<DKV_F16, DKV_ROUTE_TWO_STAGE>(p, out_dtype, grid, st);
+    if (route == DKV_ROUTE_FUSED)
+      launch_splitk_t<DKV_F16, DKV_ROUTE_FUSED>(p, out_dtype, grid, mgrid, st);
+    else
+      launch_splitk_t<DKV_F16, DKV_ROUTE_TWO_STAGE>(p, out_dtype, grid, mgrid, st);
   }
   DKV_HIP_CHECK_LAUNCH();
   return DKV_OK;

@@ -1,14 +1,13 @@
 """Host side of the gfx950 split-K decode-attention kernel.
 
-``splitk_attention`` launches ``dkv_decode_splitk`` (one kernel: split-K attention plus the
-merge/projection done by the last workgroup of each unit) on torch's current stream. It is used
+``splitk_attention`` launches ``dkv_decode_splitk`` (split-K attention, then the merge and V
+projection) on torch's current stream. It is used
 by both router routes when the inputs fit the kernel and, directly, by the native multi-group
 layout (per-head spectral bases, one packed cache row per (batch, KV group)):
 ``grouped_decode_attention``.
 
 Two device buffers are cached per (device, stream): the RoPE cos/sin table (per theta; extended
-as the cache grows, so decode steps do not rebuild it) and the zero-initialised workspace whose
-arrival counters the kernel leaves at zero.
+as the cache grows, so decode steps do not rebuild it) and the split-record workspace.
 """
 
 from __future__ import annotations
@@ -47,7 +46,7 @@ def rope_table(device: torch.device, stream: int, theta: float, seq_len: int):
 
 
 def workspace(device: torch.device, stream: int, floats: int) -> torch.Tensor:
-    """Zero-initialised split-K workspace of at least ``floats`` floats (cached)."""
+    """Split-K workspace of at least ``floats`` floats (cached per device and stream)."""
     key = (device.index, stream)
     t = _WS_CACHE.get(key)
     if t is None or t.numel() < floats:

@@ -175,15 +175,13 @@ int dkv_rope_table(void* stream, float* rope, int from_tile, int to_tile, float 
  *                      rank stride basis_sr, unit dim stride (R x Dh).
  *   lens/offs tables for K and V with their own (sb, ss) strides.
  *   rope: table from dkv_rope_table with rope_tiles >= ceil(S / 16) tile rows (it carries theta).
- *   workspace: fp32 buffer of dkv_splitk_workspace_floats(...) floats. Its first
- *              ceil(B*Hkv/64)*64 floats hold arrival counters that must be zero before the
- *              first call (allocate the workspace zero-filled); every call leaves them zero.
- *              Calls that share a workspace must be ordered (same stream).
+ *   workspace: fp32 buffer of dkv_splitk_workspace_floats(...) floats (split records);
+ *              calls that share a workspace must be ordered (same stream).
  *   out: (B, Hq, Dh) strides (out_sb, out_sh), dtype out_dtype = the cache dtype (what the
  *        reference returns) or DKV_F32 (the merged result before rounding).
  * Requirements: q and cache dtype f16 or bf16 (same), Dh == 128, R <= 128, hpg <= 16,
  * Hkv % G == 0, (B*G) * row stride < 2^30 elements for each flat buffer. split_len is a multiple of 64 and <= 512
- * (0 = choose automatically). One kernel launch.
+ * (0 = choose automatically). Two launches on `stream`: the split kernel, then the merge.
  */
 long long dkv_splitk_workspace_floats(int B, int Hq, int Hkv, int S, int R, int split_len);
 int dkv_splitk_choose_split(int B, int Hkv, int S);
