@@ -23,7 +23,7 @@
 //   5. P.X^V in coefficient space on 16x16x16 MFMA; X^V goes through a per-wave LDS tile so
 //      the operand (4 tokens x 1 rank per lane) is read transposed.
 // Epilogue: the 4 waves combine through LDS into one (m, l, acc[128]) record per head.
-// merge_kernel (same stream, one workgroup per unit) LSE-merges a unit's split records and
+// merge_kernel (same stream, one workgroup per unit and head) LSE-merges the split records and
 // projects once through the V basis; stream order makes the records visible to it without
 // device-scope fences (an agent-scope acquire would invalidate the XCD's L2).
 #include "dkv_common.h"
@@ -376,20 +376,18 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(SplitParams p) {
     cur.nvc = __builtin_amdgcn_readfirstlane(cur.nvc);
     cur.nbv = __builtin_amdgcn_readfirstlane(cur.nbv);
     // ---- store the current tile (masked) to the wave's LDS tiles, then issue the next ------
+    // all four chunks are stored (chunks past the tile's count hold zeros), so the compute
+    // below is straight-line code
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      if (c < cur.nck) {
-        const int nv = min(max(cur.rkc - 32 * c - 8 * g, 0), 8);
-        const dkv_u32x4 mk = *(const dkv_u32x4*)sMask[nv];
-        *(dkv_u32x4*)&kt[n * VT_LD + 32 * c + 8 * g] =
-            dkv_u32x4{kx[c].x & mk.x, kx[c].y & mk.y, kx[c].z & mk.z, kx[c].w & mk.w};
-      }
-      if (c < cur.nvc) {
-        const int nv = min(max(cur.rvc - 32 * c - 8 * g, 0), 8);
-        const dkv_u32x4 mk = *(const dkv_u32x4*)sMask[nv];
-        *(dkv_u32x4*)&vt[n * VT_LD + 32 * c + 8 * g] =
-            dkv_u32x4{vx[c].x & mk.x, vx[c].y & mk.y, vx[c].z & mk.z, vx[c].w & mk.w};
-      }
+      const int nvk = min(max(cur.rkc - 32 * c - 8 * g, 0), 8);
+      const dkv_u32x4 mk = *(const dkv_u32x4*)sMask[nvk];
+      *(dkv_u32x4*)&kt[n * VT_LD + 32 * c + 8 * g] =
+          dkv_u32x4{kx[c].x & mk.x, kx[c].y & mk.y, kx[c].z & mk.z, kx[c].w & mk.w};
+      const int nvv = min(max(cur.rvc - 32 * c - 8 * g, 0), 8);
+      const dkv_u32x4 mv = *(const dkv_u32x4*)sMask[nvv];
+      *(dkv_u32x4*)&vt[n * VT_LD + 32 * c + 8 * g] =
+          dkv_u32x4{vx[c].x & mv.x, vx[c].y & mv.y, vx[c].z & mv.z, vx[c].w & mv.w};
     }
     const bool more = (T + WAVES) * TILE < s_end;
     TileMeta nxt = cur;
@@ -408,14 +406,11 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(SplitParams p) {
       dkv_f32x4 c0 = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        if (c < cur.nck) {
-          const dkv_u32x4 xk = *(const dkv_u32x4*)&kt[n * VT_LD + 32 * c + 8 * g];
-          const dkv_u32x4 a0 = *(const dkv_u32x4*)&sBK[(16 * pp + n) * BK_LD + 32 * c + 8 * g];
-          const dkv_u32x4 a1 =
-              *(const dkv_u32x4*)&sBK[(16 * (pp + 4) + n) * BK_LD + 32 * c + 8 * g];
-          c0 = mfma_k<DT>(a0, xk, c0);
-          c1 = mfma_k<DT>(a1, xk, c1);
-        }
+        const dkv_u32x4 xk = *(const dkv_u32x4*)&kt[n * VT_LD + 32 * c + 8 * g];
+        const dkv_u32x4 a0 = *(const dkv_u32x4*)&sBK[(16 * pp + n) * BK_LD + 32 * c + 8 * g];
+        const dkv_u32x4 a1 = *(const dkv_u32x4*)&sBK[(16 * (pp + 4) + n) * BK_LD + 32 * c + 8 * g];
+        c0 = mfma_k<DT>(a0, xk, c0);
+        c1 = mfma_k<DT>(a1, xk, c1);
       }
       uint32_t h4[4], l4[4];
 #pragma unroll
@@ -501,13 +496,11 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(SplitParams p) {
     }
 #pragma unroll
     for (int blk = 0; blk < 8; ++blk) {
-      if (blk < cur.nbv) {  // wave-uniform
-        const uint16_t* src = vt + (4 * g) * VT_LD + 16 * blk + n;
-        const uint32_t e0 = src[0], e1 = src[VT_LD], e2 = src[2 * VT_LD], e3 = src[3 * VT_LD];
-        const dkv_u32x2 xb = {e0 | (e1 << 16), e2 | (e3 << 16)};
-        acc[blk] = mfma_pv<DT>(pa_hi, xb, acc[blk]);
-        if constexpr (DT == DKV_BF16) acc[blk] = mfma_pv<DT>(pa_lo, xb, acc[blk]);
-      }
+      const uint16_t* src = vt + (4 * g) * VT_LD + 16 * blk + n;
+      const uint32_t e0 = src[0], e1 = src[VT_LD], e2 = src[2 * VT_LD], e3 = src[3 * VT_LD];
+      const dkv_u32x2 xb = {e0 | (e1 << 16), e2 | (e3 << 16)};
+      acc[blk] = mfma_pv<DT>(pa_hi, xb, acc[blk]);
+      if constexpr (DT == DKV_BF16) acc[blk] = mfma_pv<DT>(pa_lo, xb, acc[blk]);
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -553,73 +546,68 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(SplitParams p) {
 
 }
 
-// One workgroup per unit: LSE-merge the unit's split records per head slot, normalise with the
-// route's denominator, project once through the unit's V basis, store in the output dtype.
+// One workgroup per (unit, head slot): LSE-merge the split records of that head, normalise with
+// the route's denominator, project once through the unit's V basis, store in the output dtype.
 template <int DT, int ROUTE, int ODT>
 __global__ __launch_bounds__(256) void merge_kernel(SplitParams p) {
-  __shared__ __attribute__((aligned(16))) uint16_t sVB[DH * BK_LD];  // [rank][dim]
-  __shared__ float sA[16][DH];
-  __shared__ float sML[2][16];
-  const int unit = blockIdx.x;
+  __shared__ float sW[1024];  // split weights (n_splits <= 1024 handled in chunks)
+  __shared__ float sA[DH];
+  __shared__ float sO[2][DH];
+  __shared__ float sRed[2][4];
+  const int unit = blockIdx.x / p.hpg, hs = blockIdx.x % p.hpg;
   const int b = unit / p.Hkv, kvh = unit % p.Hkv;
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int R = p.R;
-  {
-    const uint16_t* vb = p.v_basis + (long long)kvh * p.v_unit;
-    for (int idx = tid; idx < DH * 16; idx += 256) {
-      const int j = idx >> 4, d8 = (idx & 15) * 8;
-      uint32_t w4[4] = {0u, 0u, 0u, 0u};
-      if (j < R) {
-        const uint16_t* src = vb + (long long)j * p.v_sr + d8;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) w4[t] = (uint32_t)src[2 * t] | ((uint32_t)src[2 * t + 1] << 16);
-      }
-      *(dkv_u32x4*)&sVB[j * BK_LD + d8] = dkv_u32x4{w4[0], w4[1], w4[2], w4[3]};
-    }
-  }
-  const float* pr = p.partials + (long long)unit * p.n_splits * p.hpg * PREC;
-  {
-    const int hs = tid >> 4, l16 = tid & 15;
-    float M = -INFINITY;
-    if (hs < p.hpg)
-      for (int s = l16; s < p.n_splits; s += 16) M = fmaxf(M, pr[((long long)s * p.hpg + hs) * PREC]);
-#pragma unroll
-    for (int m = 8; m >= 1; m >>= 1) M = fmaxf(M, __shfl_xor(M, m, 16));
-    float L = 0.f;
-    if (hs < p.hpg)
-      for (int s = l16; s < p.n_splits; s += 16) {
-        const float* rec = pr + ((long long)s * p.hpg + hs) * PREC;
-        L += ((M == -INFINITY) ? 0.f : exp2f(rec[0] - M)) * rec[1];
-      }
-#pragma unroll
-    for (int m = 8; m >= 1; m >>= 1) L += __shfl_xor(L, m, 16);
-    if (l16 == 0) {
-      sML[0][hs] = M;
-      sML[1][hs] = L;
-    }
-  }
+  const long long stride = (long long)p.hpg * PREC;  // between splits of one head
+  const float* pr = p.partials + (long long)unit * p.n_splits * stride + (long long)hs * PREC;
+  // M = max over splits
+  float M = -INFINITY;
+  for (int s = tid; s < p.n_splits; s += 256) M = fmaxf(M, pr[s * stride]);
+  M = dkv_wave_max(M);
+  if (lane == 0) sRed[0][wave] = M;
   __syncthreads();
-  for (int idx = tid; idx < p.hpg * DH; idx += 256) {
-    const int hs = idx / DH, j = idx % DH;
-    const float M = sML[0][hs], L = sML[1][hs];
+  M = fmaxf(fmaxf(sRed[0][0], sRed[0][1]), fmaxf(sRed[0][2], sRed[0][3]));
+  // weights and L
+  float L = 0.f;
+  for (int s = tid; s < p.n_splits; s += 256) {
+    const float w = (M == -INFINITY) ? 0.f : exp2f(pr[s * stride] - M);
+    if (s < 1024) sW[s] = w;
+    L += w * pr[s * stride + 1];
+  }
+  L = dkv_wave_sum(L);
+  if (lane == 0) sRed[1][wave] = L;
+  __syncthreads();
+  L = sRed[1][0] + sRed[1][1] + sRed[1][2] + sRed[1][3];
+  const float den = ROUTE == DKV_ROUTE_TWO_STAGE ? fmaxf(L, 1e-6f) : L;
+  // A[j] = sum_s w_s acc_s[j] / den; two halves of the splits per rank, summed through LDS
+  {
+    const int j = tid & 127, half = tid >> 7;
     float a = 0.f;
-    if (j < R && M != -INFINITY) {
-      for (int s = 0; s < p.n_splits; ++s) {
-        const float* rec = pr + ((long long)s * p.hpg + hs) * PREC;
-        a += exp2f(rec[0] - M) * rec[2 + j];
+    if (j < R) {
+      for (int s = half; s < p.n_splits; s += 2) {
+        const float w = s < 1024 ? sW[s] : ((M == -INFINITY) ? 0.f : exp2f(pr[s * stride] - M));
+        a += w * pr[s * stride + 2 + j];
       }
     }
-    const float den = ROUTE == DKV_ROUTE_TWO_STAGE ? fmaxf(L, 1e-6f) : L;
-    sA[hs][j] = a / den;
+    sO[half][j] = a;
+    __syncthreads();
+    if (half == 0) sA[j] = (sO[0][j] + sO[1][j]) / den;
+    __syncthreads();
   }
-  __syncthreads();
-  const int d = tid & 127, hh = tid >> 7;
-  for (int hs = hh; hs < p.hpg; hs += 2) {
+  // out[d] = sum_j A[j] * V[j][d]: two halves of the ranks, summed through LDS
+  {
+    const int d = tid & 127, half = tid >> 7;
+    const uint16_t* vb = p.v_basis + (long long)kvh * p.v_unit;
     float o = 0.f;
 #pragma unroll 8
-    for (int j = 0; j < R; ++j) o = fmaf(sA[hs][j], elt_to_f32<DT>(sVB[j * BK_LD + d]), o);
-    const long long oi = (long long)b * p.out_sb + (long long)(kvh * p.hpg + hs) * p.out_sh + d;
-    dkv_store_f32<ODT>(p.out, oi, o);
+    for (int j = half; j < R; j += 2) o = fmaf(sA[j], elt_to_f32<DT>(vb[(long long)j * p.v_sr + d]), o);
+    __syncthreads();
+    sO[half][d] = o;
+    __syncthreads();
+    if (half == 0) {
+      const long long oi = (long long)b * p.out_sb + (long long)(kvh * p.hpg + hs) * p.out_sh + d;
+      dkv_store_f32<ODT>(p.out, oi, sO[0][d] + sO[1][d]);
+    }
   }
 }
 
@@ -857,7 +845,7 @@ extern "C" int dkv_decode_splitk(void* stream, int route, int dtype, const void*
   const float sm_scale = 1.0f / sqrtf((float)Dh);
   p.score_scale = route == DKV_ROUTE_FUSED ? sm_scale * LOG2E : sm_scale;
   p.masked_score = -1.0e4f * sm_scale;
-  const dim3 grid((unsigned)(units * n_splits)), mgrid((unsigned)units);
+  const dim3 grid((unsigned)(units * n_splits)), mgrid((unsigned)(units * (Hq / Hkv)));
   hipStream_t st = (hipStream_t)stream;
   if (dtype == DKV_BF16) {
     if (route == DKV_ROUTE_FUSED)
