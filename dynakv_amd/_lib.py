@@ -47,6 +47,8 @@ _SIGNATURES = {
                                _vp, _ll, _vp, _ll, _vp, _vp, _ll, _ll, _vp, _vp, _ll, _ll,
                                _vp, _i, _vp, _ll, _vp, _ll, _ll, _i,
                                _i, _i, _i, _i, _i, _i, _i, _i]),
+    "dkv_profile_begin": (_i, [_i]),
+    "dkv_profile_end": (_i, [_vp, _vp, _vp]),
     "dkv_selftest_layouts": (_i, [_vp, _vp]),
 }
 

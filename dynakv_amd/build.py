@@ -31,6 +31,10 @@ COMMON_FLAGS = [
     "-mcode-object-version=5",
     # never emit packed-fp32 VALU ops
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results and accumulators in VGPRs: the split kernel keeps its 128-register K basis in
+    # the accumulation registers (as MFMA A operands) and post-processes every MFMA result with
+    # VALU code, which would otherwise be copied out of accumulation registers first
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wno-unused-command-line-argument",
 ]
 

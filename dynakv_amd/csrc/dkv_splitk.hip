@@ -28,6 +28,8 @@
 // device-scope fences (an agent-scope acquire would invalidate the XCD's L2).
 #include "dkv_common.h"
 
+#include <type_traits>
+
 namespace {
 
 constexpr int DH = 128;
@@ -36,8 +38,11 @@ constexpr int WAVES = 4;
 constexpr int BK_LD = 136;    // LDS row pitch (elements) of the transposed K basis
 constexpr int VT_LD = 136;    // LDS row pitch (elements) of a wave's V tile
 constexpr int PREC = DH + 2;  // floats per partial record: m, l, acc[128]
-constexpr int MAX_SPLIT = 512;
-constexpr int MAX_TILES = MAX_SPLIT / TILE;
+constexpr int NSLOT = 4;       // gather slots per wave: the current tile + three in flight
+constexpr int TSLOT = 8;       // table slots per wave (tables run two tiles ahead of gathers)
+constexpr int GSLOT_BYTES = 8192;  // 4 K chunks + 4 V chunks of 64 lanes x 16 bytes
+constexpr int MASK_BIAS = 120;  // mask-table row of count 0 for the lowest chunk start
+constexpr int MASK_ROWS = MASK_BIAS + DH + 1;
 constexpr int ROPE_FIXED_ROWS = TILE + 1;  // rows 0..15: in-tile deltas; row 16: per-step
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float RESCALE_THRESH = 11.5f;  // log2 units
@@ -113,11 +118,17 @@ __device__ __forceinline__ dkv_f32x4 mfma_f16(const dkv_u32x4& a, const dkv_u32x
 }
 
 // x ~= hi + lo with hi = fp16(x) and lo = fp16(x - hi), for two values packed per dword.
+// hi is one packed conversion; each half of lo is one mixed-precision fma, fp16(hi_k * -1 + x_k)
+// (x_k - hi_k is exact in fp32, so lo_k is that difference rounded once to fp16).
 __device__ __forceinline__ void split_f16x2(float x0, float x1, uint32_t& hi, uint32_t& lo) {
-  const _Float16 h0 = (_Float16)x0, h1 = (_Float16)x1;
-  const _Float16 l0 = (_Float16)(x0 - (float)h0), l1 = (_Float16)(x1 - (float)h1);
-  hi = __builtin_bit_cast(uint32_t, dkv_f16x2{h0, h1});
-  lo = __builtin_bit_cast(uint32_t, dkv_f16x2{l0, l1});
+  hi = __builtin_bit_cast(uint32_t, dkv_f16x2{(_Float16)x0, (_Float16)x1});
+  uint32_t l;
+  asm volatile(
+      "v_fma_mixlo_f16 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]\n\t"
+      "v_fma_mixhi_f16 %0, %1, -1.0, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+      : "=&v"(l)
+      : "v"(hi), "v"(x0), "v"(x1));
+  lo = l;
 }
 
 // Element-wise gather of the first nv (1..8) 16-bit values at element offset e, the rest zero:
@@ -129,18 +140,6 @@ __device__ __forceinline__ dkv_u32x4 gather8_b16(__amdgpu_buffer_rsrc_t r, int e
     v[t] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, t < nv ? (e + t) * 2 : 0x7ffffff0, 0, 0);
   return dkv_u32x4{v[0] | (v[1] << 16), v[2] | (v[3] << 16), v[4] | (v[5] << 16),
                    v[6] | (v[7] << 16)};
-}
-
-// Zero the elements at index >= nv (0 <= nv < 8) of an 8 x 16-bit vector.
-__device__ __forceinline__ dkv_u32x4 mask_prefix8(dkv_u32x4 v, int nv) {
-  const int nlo = min(nv, 4), nhi = max(nv - 4, 0);
-  const unsigned long long mlo = nlo >= 4 ? ~0ull : ((1ull << (16 * nlo)) - 1ull);
-  const unsigned long long mhi = nhi >= 4 ? ~0ull : ((1ull << (16 * nhi)) - 1ull);
-  v.x &= (uint32_t)mlo;
-  v.y &= (uint32_t)(mlo >> 32);
-  v.z &= (uint32_t)mhi;
-  v.w &= (uint32_t)(mhi >> 32);
-  return v;
 }
 
 // Zero-fill masks for the first k (0..8) 16-bit elements of an 8-element vector.
@@ -161,25 +160,44 @@ __device__ __forceinline__ dkv_u32x4 gather_chunk(__amdgpu_buffer_rsrc_t rs, uin
   return __builtin_amdgcn_raw_buffer_load_b128(rs, nv > 0 ? (o + j0) * 2 : OOB, 0, 0);
 }
 
-struct TileMeta {
-  int rk;   // this lane's token: raw K length (only its sign matters: has a key)
-  int rkc;  // clamped K length
-  int rvc;  // clamped V length
-  int nck;  // wave-uniform: 32-rank K chunks
-  int nvc;  // wave-uniform: 32-rank V chunks
-  int nbv;  // wave-uniform: 16-rank V blocks
-  bool valid;
-};
+// Loads that write LDS directly (M0 = wave-uniform LDS base; lane i's bytes land at
+// M0 + size*i). They are issued as inline assembly so that the compiler neither reorders LDS
+// accesses around them nor guards later LDS reads with a full drain of the load queue: the
+// kernel waits for them itself (wait_vm) at the points where the data is consumed. No other
+// code of the kernel uses M0.
+__device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t rsrc, uint32_t lds_base,
+                                           uint32_t byte_off) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               ::"s"(lds_base), "v"(byte_off), "s"(rsrc)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void lds_load4(const void* gptr, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off"
+               ::"s"(lds_base), "v"(gptr)
+               : "memory", "m0");
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
+}
+
+// Wait until at most N vector-memory loads of this wave are outstanding (loads complete in
+// issue order); the "memory" clobber keeps LDS accesses from moving across the wait.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
 
 template <int DT, int ROUTE>
-__global__ __launch_bounds__(256, 2) void splitk_kernel(SplitParams p) {
-  __shared__ __attribute__((aligned(16))) uint16_t sBK[DH * BK_LD];
-  __shared__ __attribute__((aligned(16))) int sTab[4][MAX_SPLIT];
-  __shared__ int sTmax[2][MAX_TILES];
-  __shared__ __attribute__((aligned(16))) uint16_t sKT[WAVES][TILE * VT_LD];
-  __shared__ __attribute__((aligned(16))) uint16_t sVT[WAVES][TILE * VT_LD];
-  __shared__ __attribute__((aligned(16))) uint32_t sMask[9][4];
-  __shared__ __attribute__((aligned(16))) float sStep[2][64];
+__global__ __launch_bounds__(256, 1) void splitk_kernel(SplitParams p) {
+  // per-wave LDS ring: NSLOT gather slots (K then V: 4 chunks x 64 lanes x 16 bytes each) and
+  // TSLOT table slots (lens_k, offs_k, lens_v, offs_v x 16 tokens); the K basis staging area
+  // and the epilogue scratch alias the gather slots
+  __shared__ __attribute__((aligned(16))) uint8_t sRing[WAVES * NSLOT * GSLOT_BYTES];
+  __shared__ __attribute__((aligned(16))) int sTabRing[WAVES][TSLOT][4][TILE];
+  __shared__ __attribute__((aligned(16))) uint32_t sMask[MASK_ROWS][4];
+  __shared__ __attribute__((aligned(16))) float sStep[2][64];  // rotation by WAVES*TILE positions
+  static_assert(DH * BK_LD * 2 <= WAVES * NSLOT * GSLOT_BYTES, "basis staging fits the ring");
+  uint16_t* sBK = reinterpret_cast<uint16_t*>(sRing);
 
   // XCD-aware mapping: consecutive workgroup ids land on different XCDs (id % 8), so give
   // every split of one unit the same id % 8 to keep that unit's basis in one L2.
@@ -198,14 +216,15 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(SplitParams p) {
   }
   const int b = unit / p.Hkv, kvh = unit % p.Hkv;
   const int row = b * p.G + kvh / (p.Hkv / p.G);
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15, g = lane >> 4;
   const int R = p.R;
   const int s_begin = split * p.split_len;
   const int s_end = min(p.S, s_begin + p.split_len);
   const int ns = s_end - s_begin;
 
-  // ---- prologue: K basis, tables, masks, per-step rotation --------------------------------
+  // ---- prologue: K basis through LDS into registers, mask table, query, RoPE state --------
   {
     // transpose to [dim][rank]: consecutive lanes take consecutive ranks, so each 2-byte LDS
     // store of a wave covers 128 contiguous bytes (no bank conflicts)
@@ -228,47 +247,18 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(SplitParams p) {
         sBK[(d8 + 2 * t + 1) * BK_LD + j] = (uint16_t)(e[t] >> 16);
       }
     }
-    const int* lk = p.lens_k + (long long)row * p.tk_sb;
-    const int* okp = p.offs_k + (long long)row * p.tk_sb;
-    const int* lv = p.lens_v + (long long)row * p.tv_sb;
-    const int* ovp = p.offs_v + (long long)row * p.tv_sb;
-    for (int i = tid; i < ns; i += 256) {
-      const long long t = s_begin + i;
-      sTab[0][i] = lk[t * p.tk_ss];
-      sTab[1][i] = okp[t * p.tk_ss];
-      sTab[2][i] = lv[t * p.tv_ss];
-      sTab[3][i] = ovp[t * p.tv_ss];
-    }
-    if (tid < 36) sMask[tid >> 2][tid & 3] = prefix_mask_word(tid >> 2, tid & 3);
+    // row j holds the keep-mask of the first clamp(j - MASK_BIAS, 0, 8) elements
+    for (int r = tid; r < MASK_ROWS * 4; r += 256)
+      sMask[r >> 2][r & 3] = prefix_mask_word(min(max((r >> 2) - MASK_BIAS, 0), 8), r & 3);
     if (tid < 64) {
       sStep[0][tid] = p.rope[TILE * 128 + 2 * tid];
       sStep[1][tid] = p.rope[TILE * 128 + 2 * tid + 1];
     }
   }
-  __syncthreads();
-  {  // largest clamped K and V count of each tile of the split (4 threads per tile)
-    const int tile = tid >> 2, qq = tid & 3;
-    int mk = 0, mv = 0;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int i = tile * TILE + qq * 4 + e;
-      if (tile < MAX_TILES && i < ns) {
-        mk = max(mk, min(max(sTab[0][i], 0), R));
-        mv = max(mv, min(max(sTab[2][i], 0), R));
-      }
-    }
-    mk = max(mk, __shfl_xor(mk, 1, 64));
-    mk = max(mk, __shfl_xor(mk, 2, 64));
-    mv = max(mv, __shfl_xor(mv, 1, 64));
-    mv = max(mv, __shfl_xor(mv, 2, 64));
-    if (qq == 0 && tile < MAX_TILES) {
-      sTmax[0][tile] = mk;
-      sTmax[1][tile] = mv;
-    }
-  }
 
-  // ---- query as the fp16 B operand of the QK MFMA: lane (head slot n, k-group g) holds
-  //      (q_i, q_{i+64}) for i = 16*pp + 4*g + w; bf16 and fp16 values are exact in fp16 ------
+  // query as the fp16 B operand of the QK MFMA: lane (head slot n, k-group g) holds
+  // (q_i, q_{i+64}) for i = 16*pp + 4*g + w. bf16 and fp16 values in fp16's normal range are
+  // exact in fp16 (smaller ones keep an absolute error below 2^-25).
   dkv_u32x4 bq[4];
   {
     const bool real = n < p.hpg;
@@ -298,8 +288,9 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(SplitParams p) {
   const int tile_first = s_begin / TILE;  // splits are multiples of 64 tokens
   const int tile0 = tile_first + wave;
   const int n_tb = (p.S + TILE - 1) / TILE;
+  const int n_iter = max(0, ((ns + TILE - 1) / TILE - wave + WAVES - 1) / WAVES);
 
-  // ---- RoPE state of this lane's token slot for its 16 frequencies -----------------------
+  // RoPE state of this lane's token slot for its 16 frequencies
   float rc[16], rs[16];
   {
     const int tb = min(tile0, n_tb - 1);
@@ -316,46 +307,89 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(SplitParams p) {
         rs[f] = bs * ec + bc * es;
       }
   }
-  __syncthreads();  // sTmax ready
+  __syncthreads();  // sBK, sMask, sStep ready
+
+  // recon A operands: block blk (dims 16*blk + n), rank chunk c (ranks 32c + 8g .. +8). They
+  // are read straight into accumulation registers, which the MFMAs take as their A operand:
+  // the 128 registers stay out of the VGPRs the rest of the loop needs.
+  dkv_u32x4 bA[8][4];
+  {
+    const uint32_t a0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t*)(
+        sBK + n * BK_LD + 8 * g);
+#pragma unroll
+    for (int blk = 0; blk < 8; ++blk)
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        asm volatile("ds_read_b128 %0, %1 offset:%2"
+                     : "=a"(bA[blk][c])
+                     : "v"(a0), "i"((16 * blk * BK_LD + 32 * c) * 2));
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  }
+  __syncthreads();  // every wave holds its operands: the ring may now be overwritten
 
   // one resource per buffer, ranges [flat, flat + rows * ld); row offsets go in the voffset
   const __amdgpu_buffer_rsrc_t rk_src = dkv_make_rsrc(p.k_flat, p.k_end * 2u);
   const __amdgpu_buffer_rsrc_t rv_src = dkv_make_rsrc(p.v_flat, p.v_end * 2u);
   const int k_row0 = row * p.k_ld, v_row0 = row * p.v_ld;
-  uint16_t* kt = sKT[wave];
-  uint16_t* vt = sVT[wave];
-
-  // per-tile metadata from the LDS tables
-  auto meta_of = [&](int T) {
-    TileMeta d;
-    const int tl = T * TILE + n - s_begin;
-    d.valid = T * TILE + n < s_end;
-    d.rk = d.valid ? sTab[0][tl] : 0;
-    const int rv = d.valid ? sTab[2][tl] : 0;
+  uint8_t* ring = sRing + wave * NSLOT * GSLOT_BYTES;
+  // table loads: lane (table l/16, token l%16) -> one 4-byte load per lane and tile
+  const int* tab_base;
+  int tab_ss;
+  {
+    const int tsel = lane >> 4;
+    const int* bases[4] = {p.lens_k + (long long)row * p.tk_sb, p.offs_k + (long long)row * p.tk_sb,
+                           p.lens_v + (long long)row * p.tv_sb, p.offs_v + (long long)row * p.tv_sb};
+    tab_base = tsel == 0 ? bases[0] : tsel == 1 ? bases[1] : tsel == 2 ? bases[2] : bases[3];
+    tab_ss = tsel < 2 ? (int)p.tk_ss : (int)p.tv_ss;
+  }
+  auto load_tab = [&](int j) {  // one load per lane into table slot j % TSLOT
+    const int t = min((tile0 + WAVES * j) * TILE + n, s_end - 1);
+    lds_load4(tab_base + t * tab_ss, lds_addr(&sTabRing[wave][j % TSLOT][0][0]));
+  };
+  // token metadata of this lane's token in tile j (table slot must have arrived)
+  struct Tok {
+    int rk, ko, rkc, rvc, vo;
+    bool valid;
+  };
+  auto tok_of = [&](int j) {
+    Tok d;
+    const int(*tb)[TILE] = sTabRing[wave][j % TSLOT];
+    d.valid = (tile0 + WAVES * j) * TILE + n < s_end;
+    const int lk = tb[0][n], ok = tb[1][n], lv = tb[2][n], ov = tb[3][n];
+    d.rk = d.valid ? lk : 0;
     d.rkc = min(max(d.rk, 0), R);
-    d.rvc = min(max(rv, 0), R);
-    const int tt = T - tile_first;
-    const int mk = __builtin_amdgcn_readfirstlane(sTmax[0][tt]);
-    const int mv = __builtin_amdgcn_readfirstlane(sTmax[1][tt]);
-    d.nck = (mk + 31) >> 5;
-    d.nvc = (mv + 31) >> 5;
-    d.nbv = (mv + 15) >> 4;
+    d.rvc = min(max(d.valid ? lv : 0, 0), R);
+    d.ko = k_row0 + (d.valid ? ok : 0);
+    d.vo = v_row0 + (d.valid ? ov : 0);
     return d;
   };
-  dkv_u32x4 kx[4], vx[4];  // in-flight gathers of the next tile
-  auto issue = [&](const TileMeta& d, int T) {
-    const int tl = T * TILE + n - s_begin;
-    const int ok = k_row0 + (d.valid ? sTab[1][tl] : 0);
-    const int ov = v_row0 + (d.valid ? sTab[3][tl] : 0);
+  // gathers of tile j into gather slot j % NSLOT: lane l's 16 bytes of chunk c land at
+  // slot + c*1024 + 16*l (K) and slot + 4096 + c*1024 + 16*l (V)
+  auto issue = [&](int j) {
+    const Tok d = tok_of(j);
+    const uint32_t slot = lds_addr(ring + (j % NSLOT) * GSLOT_BYTES);
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      kx[c] = dkv_u32x4{0u, 0u, 0u, 0u};
-      if (c < d.nck) kx[c] = gather_chunk(rk_src, p.k_end, ok, d.rkc, c, g);
-    }
+    for (int c = 0; c < 4; ++c) lds_load16(rk_src, slot + c * 1024, (d.ko + 8 * g + 32 * c) * 2);
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      vx[c] = dkv_u32x4{0u, 0u, 0u, 0u};
-      if (c < d.nvc) vx[c] = gather_chunk(rv_src, p.v_end, ov, d.rvc, c, g);
+    for (int c = 0; c < 4; ++c)
+      lds_load16(rv_src, slot + 4096 + c * 1024, (d.vo + 8 * g + 32 * c) * 2);
+  };
+  // A 16-byte window that crosses the end of a resource reads as zero in full; only the last
+  // tokens of the last row can need one. Such a tile is gathered again with element loads
+  // once its ring slot has landed (the ring loads are issued regardless, so the number of
+  // loads in flight stays what the waits below assume).
+  auto regather_if_needed = [&](const Tok& d, uint8_t* slot) {
+    const bool risky = (d.rkc > 0 && (uint32_t)(d.ko + d.rkc + 7) > p.k_end) ||
+                       (d.rvc > 0 && (uint32_t)(d.vo + d.rvc + 7) > p.v_end);
+    if (__builtin_expect(__ballot(risky) != 0ull, 0)) {
+      // one chunk at a time: this cold path must not raise the loop's register pressure
+#pragma unroll 1
+      for (int c = 0; c < 8; ++c) {
+        const bool isv = c >= 4;
+        *(dkv_u32x4*)(slot + c * 1024 + 16 * lane) =
+            gather_chunk(isv ? rv_src : rk_src, isv ? p.v_end : p.k_end, isv ? d.vo : d.ko,
+                         isv ? d.rvc : d.rkc, c & 3, g);
+      }
     }
   };
 
@@ -365,36 +399,49 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(SplitParams p) {
   float m_run = -INFINITY;  // per head slot n (log2 units), identical across g
   float l_run = 0.f;        // partial over this lane's 4 tokens per tile
 
-  TileMeta cur;
-  if (tile0 * TILE < s_end) {
-    cur = meta_of(tile0);
-    issue(cur, tile0);
-  }
-  for (int T = tile0; T * TILE < s_end; T += WAVES) {
-    // chunk counts are wave-uniform: keep them in scalar registers
-    cur.nck = __builtin_amdgcn_readfirstlane(cur.nck);
-    cur.nvc = __builtin_amdgcn_readfirstlane(cur.nvc);
-    cur.nbv = __builtin_amdgcn_readfirstlane(cur.nbv);
-    // ---- store the current tile (masked) to the wave's LDS tiles, then issue the next ------
-    // all four chunks are stored (chunks past the tile's count hold zeros), so the compute
-    // below is straight-line code
+  // ---- pipeline: tables run five tiles ahead, gathers three. Loads are issued for every
+  //      iteration, also past the wave's last tile (token indices clamp to the split's last
+  //      token, so those re-read cached lines), which keeps the number of loads in flight
+  //      after any given load fixed: each wait below lets exactly the loads issued after the
+  //      awaited one stay in flight. -----------------------------------------------------------
+  load_tab(0);
+  load_tab(1);
+  load_tab(2);
+  wait_vm<2>();  // T0
+  issue(0);
+  load_tab(3);
+  wait_vm<10>();  // T1 (T2, G0, T3 in flight)
+  issue(1);
+  load_tab(4);
+  wait_vm<18>();  // T2 (G0, T3, G1, T4 in flight)
+  issue(2);
+
+  for (int j = 0; j < n_iter; ++j) {
+    // G(j) and T(j+3) have landed once only G(j+1), T(j+4), G(j+2) may be in flight
+    wait_vm<17>();
+    const Tok cur = tok_of(j);
+    uint8_t* slot = ring + (j % NSLOT) * GSLOT_BYTES;
+    regather_if_needed(cur, slot);
+    // ---- masks (elements past each token's count belong to the next tokens): K into
+    //      registers, V back into the slot -----------------------------------------------------
+    dkv_u32x4 xk[4];
+    {
+      const char* mkb = (const char*)&sMask[0][0] + 16 * (cur.rkc - 8 * g + MASK_BIAS - 96);
+      const char* mvb = (const char*)&sMask[0][0] + 16 * (cur.rvc - 8 * g + MASK_BIAS - 96);
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int nvk = min(max(cur.rkc - 32 * c - 8 * g, 0), 8);
-      const dkv_u32x4 mk = *(const dkv_u32x4*)sMask[nvk];
-      *(dkv_u32x4*)&kt[n * VT_LD + 32 * c + 8 * g] =
-          dkv_u32x4{kx[c].x & mk.x, kx[c].y & mk.y, kx[c].z & mk.z, kx[c].w & mk.w};
-      const int nvv = min(max(cur.rvc - 32 * c - 8 * g, 0), 8);
-      const dkv_u32x4 mv = *(const dkv_u32x4*)sMask[nvv];
-      *(dkv_u32x4*)&vt[n * VT_LD + 32 * c + 8 * g] =
-          dkv_u32x4{vx[c].x & mv.x, vx[c].y & mv.y, vx[c].z & mv.z, vx[c].w & mv.w};
+      for (int c = 0; c < 4; ++c) {
+        const dkv_u32x4 mk = *(const dkv_u32x4*)(mkb + 16 * (96 - 32 * c));
+        const dkv_u32x4 kr = *(const dkv_u32x4*)(slot + c * 1024 + 16 * lane);
+        xk[c] = dkv_u32x4{kr.x & mk.x, kr.y & mk.y, kr.z & mk.z, kr.w & mk.w};
+        const dkv_u32x4 mv = *(const dkv_u32x4*)(mvb + 16 * (96 - 32 * c));
+        dkv_u32x4* vp = (dkv_u32x4*)(slot + 4096 + c * 1024 + 16 * lane);
+        const dkv_u32x4 vr = *vp;
+        *vp = dkv_u32x4{vr.x & mv.x, vr.y & mv.y, vr.z & mv.z, vr.w & mv.w};
+      }
     }
-    const bool more = (T + WAVES) * TILE < s_end;
-    TileMeta nxt = cur;
-    if (more) {
-      nxt = meta_of(T + WAVES);
-      issue(nxt, T + WAVES);
-    }
+    // ---- keep the pipeline full ------------------------------------------------------------
+    load_tab(j + 5);
+    issue(j + 3);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -406,41 +453,42 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(SplitParams p) {
       dkv_f32x4 c0 = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        const dkv_u32x4 xk = *(const dkv_u32x4*)&kt[n * VT_LD + 32 * c + 8 * g];
-        const dkv_u32x4 a0 = *(const dkv_u32x4*)&sBK[(16 * pp + n) * BK_LD + 32 * c + 8 * g];
-        const dkv_u32x4 a1 = *(const dkv_u32x4*)&sBK[(16 * (pp + 4) + n) * BK_LD + 32 * c + 8 * g];
-        c0 = mfma_k<DT>(a0, xk, c0);
-        c1 = mfma_k<DT>(a1, xk, c1);
+        c0 = mfma_k<DT>(bA[pp][c], xk[c], c0);
+        c1 = mfma_k<DT>(bA[pp + 4][c], xk[c], c1);
       }
       uint32_t h4[4], l4[4];
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
         const int f = pp * 4 + w;
-        const float r0 = c0[w] * rc[f] - c1[w] * rs[f];
-        const float r1 = c1[w] * rc[f] + c0[w] * rs[f];
+        float r0 = c0[w] * rc[f] - c1[w] * rs[f];
+        float r1 = c1[w] * rc[f] + c0[w] * rs[f];
+        // materialise the rotated pair once (otherwise the rotation is re-formed inside
+        // the mixed-precision conversions of both parts)
+        asm volatile("" : "+v"(r0), "+v"(r1));
         split_f16x2(r0, r1, h4[w], l4[w]);
       }
       sc = mfma_f16(dkv_u32x4{l4[0], l4[1], l4[2], l4[3]}, bq[pp], sc);
       sc = mfma_f16(dkv_u32x4{h4[0], h4[1], h4[2], h4[3]}, bq[pp], sc);
     }
-    // advance the rotation by WAVES*TILE positions
+    // advance the rotation by WAVES*TILE positions (a wave's consecutive tiles)
 #pragma unroll
     for (int pp = 0; pp < 4; ++pp) {
       const dkv_f32x4 dc = *(const dkv_f32x4*)&sStep[0][16 * pp + 4 * g];
       const dkv_f32x4 ds = *(const dkv_f32x4*)&sStep[1][16 * pp + 4 * g];
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
+        // each new value depends on its own old value and a product formed first, so the
+        // update happens in place
         const int f = pp * 4 + w;
-        const float c2 = rc[f] * dc[w] - rs[f] * ds[w];
-        const float s2 = rs[f] * dc[w] + rc[f] * ds[w];
-        rc[f] = c2;
-        rs[f] = s2;
+        const float sd = rs[f] * ds[w], cd = rc[f] * ds[w];
+        rc[f] = fmaf(rc[f], dc[w], -sd);
+        rs[f] = fmaf(rs[f], dc[w], cd);
       }
     }
 
     // scores of lane (head slot n, tokens 4g+u) -> log2 domain with the route's masking
-    const unsigned long long has_bits = __ballot(cur.valid && cur.rk > 0);
     const unsigned long long in_bits = __ballot(cur.valid);
+    const unsigned long long has_bits = __ballot(cur.valid && cur.rk > 0);
     float z[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -480,7 +528,7 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(SplitParams p) {
       l_run += pu[u];
     }
 
-    // ---- 5. P.X^V from the wave's LDS V tile (4 tokens x 1 rank per lane) ---------------------
+    // ---- 5. P.X^V from the slot's masked V chunks (4 tokens x 1 rank per lane) --------------
     dkv_u32x2 pa_hi, pa_lo;
     if constexpr (DT == DKV_F16) {
       pa_hi = dkv_u32x2{pack_f16x2(pu[0], pu[1]), pack_f16x2(pu[2], pu[3])};
@@ -494,10 +542,12 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(SplitParams p) {
       pa_lo = dkv_u32x2{(uint32_t)__builtin_bit_cast(uint16_t, e0) | ((uint32_t)__builtin_bit_cast(uint16_t, e1) << 16),
                         (uint32_t)__builtin_bit_cast(uint16_t, e2) | ((uint32_t)__builtin_bit_cast(uint16_t, e3) << 16)};
     }
+    // rank r = 16*blk + n of token t sits at chunk r/32, lane 16*((r%32)/8) + t, element r%8
+    const uint16_t* vsrc = (const uint16_t*)(slot + 4096 + 16 * (16 * (n >> 3) + 4 * g)) + (n & 7);
 #pragma unroll
     for (int blk = 0; blk < 8; ++blk) {
-      const uint16_t* src = vt + (4 * g) * VT_LD + 16 * blk + n;
-      const uint32_t e0 = src[0], e1 = src[VT_LD], e2 = src[2 * VT_LD], e3 = src[3 * VT_LD];
+      const uint16_t* src = vsrc + ((blk >> 1) * 1024 + (blk & 1) * 512) / 2;
+      const uint32_t e0 = src[0], e1 = src[8], e2 = src[16], e3 = src[24];
       const dkv_u32x2 xb = {e0 | (e1 << 16), e2 | (e3 << 16)};
       acc[blk] = mfma_pv<DT>(pa_hi, xb, acc[blk]);
       if constexpr (DT == DKV_BF16) acc[blk] = mfma_pv<DT>(pa_lo, xb, acc[blk]);
@@ -505,15 +555,15 @@ __global__ __launch_bounds__(256, 2) void splitk_kernel(SplitParams p) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    cur = nxt;
   }
+  wait_vm<0>();  // nothing may land in the ring once it is reused below
 
   // ---- combine the 4 waves through LDS and write the partial record ----------------------
   float l_tot = l_run;
   l_tot += __shfl_xor(l_tot, 16, 64);
   l_tot += __shfl_xor(l_tot, 32, 64);
   __syncthreads();  // all waves done with sBK and their tiles
-  float* sw = reinterpret_cast<float*>(sBK);  // [WAVES][16 m | 16 l | 16 x 128 acc]
+  float* sw = reinterpret_cast<float*>(sRing);  // [WAVES][16 m | 16 l | 16 x 128 acc]
   constexpr int WREC = 32 + 16 * DH;
   float* my = sw + wave * WREC;
   if (g == 0) {
@@ -719,12 +769,14 @@ __global__ __launch_bounds__(64) void selftest_kernel(int* __restrict__ mismatch
 
 extern "C" int dkv_splitk_choose_split(int B, int Hkv, int S) {
   if (B <= 0 || Hkv <= 0 || S <= 0) return 64;
+  // one resident workgroup per CU (256 CUs): as many splits per unit as fill the chip once,
+  // each as long as possible so the per-workgroup basis load is amortised
   const long long units = (long long)B * Hkv;
-  const long long target_groups = 2048;  // 256 CUs x 8
-  long long sl = ((long long)S * units + target_groups - 1) / target_groups;
+  const long long per_unit = (256 + units - 1) / units;
+  long long sl = ((long long)S + per_unit - 1) / per_unit;
   sl = ((sl + 63) / 64) * 64;
   if (sl < 64) sl = 64;
-  if (sl > MAX_SPLIT) sl = MAX_SPLIT;
+  if (sl > (1LL << 30)) sl = 1LL << 30;
   return (int)sl;
 }
 
@@ -756,14 +808,71 @@ extern "C" int dkv_rope_table(void* stream, float* rope, int from_tile, int to_t
   return DKV_OK;
 }
 
+// launch timing hooks (dkv_profile_begin / dkv_profile_end)
+struct ProfileState {
+  bool on = false;
+  int cap = 0, n = 0;
+  hipEvent_t* ev = nullptr;  // 3 per recorded call
+};
+static ProfileState g_prof;
+
 template <int DT, int RT>
 static void launch_splitk_t(const SplitParams& p, int out_dtype, dim3 grid, dim3 mgrid,
                             hipStream_t st) {
+  hipEvent_t* ev = (g_prof.on && g_prof.n < g_prof.cap) ? g_prof.ev + 3 * g_prof.n++ : nullptr;
+  if (ev) (void)hipEventRecord(ev[0], st);
   hipLaunchKernelGGL((splitk_kernel<DT, RT>), grid, dim3(256), 0, st, p);
+  if (ev) (void)hipEventRecord(ev[1], st);
   if (out_dtype == DKV_F32)
     hipLaunchKernelGGL((merge_kernel<DT, RT, DKV_F32>), mgrid, dim3(256), 0, st, p);
   else
     hipLaunchKernelGGL((merge_kernel<DT, RT, DT>), mgrid, dim3(256), 0, st, p);
+  if (ev) (void)hipEventRecord(ev[2], st);
+}
+
+static void profile_release() {
+  for (int i = 0; i < 3 * g_prof.cap; ++i) (void)hipEventDestroy(g_prof.ev[i]);
+  delete[] g_prof.ev;
+  g_prof = ProfileState{};
+}
+
+extern "C" int dkv_profile_begin(int max_calls) {
+  if (max_calls <= 0 || max_calls > (1 << 20)) return DKV_E_ARG;
+  if (g_prof.ev) profile_release();
+  g_prof.ev = new hipEvent_t[3 * (size_t)max_calls];
+  for (int i = 0; i < 3 * max_calls; ++i) {
+    const hipError_t e = hipEventCreate(&g_prof.ev[i]);
+    if (e != hipSuccess) {
+      g_prof.cap = i;
+      profile_release();
+      return -(1000 + (int)e);
+    }
+  }
+  g_prof.cap = max_calls;
+  g_prof.n = 0;
+  g_prof.on = true;
+  return DKV_OK;
+}
+
+extern "C" int dkv_profile_end(double* split_ms, double* merge_ms, int* calls) {
+  if (!split_ms || !merge_ms || !calls) return DKV_E_ARG;
+  *split_ms = *merge_ms = 0.0;
+  *calls = 0;
+  if (!g_prof.ev) return DKV_E_ARG;
+  int rc = DKV_OK;
+  for (int i = 0; i < g_prof.n && rc == DKV_OK; ++i) {
+    hipEvent_t* e = g_prof.ev + 3 * i;
+    float a = 0.f, m = 0.f;
+    hipError_t err = hipEventSynchronize(e[2]);
+    if (err == hipSuccess) err = hipEventElapsedTime(&a, e[0], e[1]);
+    if (err == hipSuccess) err = hipEventElapsedTime(&m, e[1], e[2]);
+    if (err != hipSuccess) rc = -(1000 + (int)err);
+    *split_ms += a;
+    *merge_ms += m;
+  }
+  *calls = g_prof.n;
+  profile_release();
+  return rc;
 }
 
 extern "C" int dkv_decode_splitk(void* stream, int route, int dtype, const void* q, long long q_sb,
@@ -798,7 +907,11 @@ extern "C" int dkv_decode_splitk(void* stream, int route, int dtype, const void*
   if (rows * k_ld >= (1LL << 30) || rows * v_ld >= (1LL << 30)) return DKV_E_UNSUPPORTED;
   if (rope_tiles < (S + TILE - 1) / TILE) return DKV_E_ARG;
   if (split_len <= 0) split_len = dkv_splitk_choose_split(B, Hkv, S);
-  if (split_len % 64 != 0 || split_len > MAX_SPLIT) return DKV_E_ARG;
+  if (split_len % 64 != 0) return DKV_E_ARG;
+  // token indices times table strides stay 32-bit inside the kernel
+  if ((long long)S * tk_ss >= (1LL << 31) || (long long)S * tv_ss >= (1LL << 31) || tk_ss < 0 ||
+      tv_ss < 0)
+    return DKV_E_UNSUPPORTED;
   const long long n_splits = ((long long)S + split_len - 1) / split_len;
   const long long units = (long long)B * Hkv;
   if (units * n_splits > 0x7fffffffLL) return DKV_E_UNSUPPORTED;

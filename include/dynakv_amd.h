@@ -180,8 +180,9 @@ int dkv_rope_table(void* stream, float* rope, int from_tile, int to_tile, float 
  *   out: (B, Hq, Dh) strides (out_sb, out_sh), dtype out_dtype = the cache dtype (what the
  *        reference returns) or DKV_F32 (the merged result before rounding).
  * Requirements: q and cache dtype f16 or bf16 (same), Dh == 128, R <= 128, hpg <= 16,
- * Hkv % G == 0, (B*G) * row stride < 2^30 elements for each flat buffer. split_len is a multiple of 64 and <= 512
- * (0 = choose automatically). Two launches on `stream`: the split kernel, then the merge.
+ * Hkv % G == 0, (B*G) * row stride < 2^30 elements for each flat buffer, S * table token
+ * stride < 2^31. split_len is a multiple of 64 (0 = dkv_splitk_choose_split: about one
+ * workgroup per CU). Two launches on `stream`: the split kernel, then the merge.
  */
 long long dkv_splitk_workspace_floats(int B, int Hq, int Hkv, int S, int R, int split_len);
 int dkv_splitk_choose_split(int B, int Hkv, int S);
@@ -196,6 +197,17 @@ int dkv_decode_splitk(void* stream, int route, int dtype,
                       float* workspace, long long workspace_floats,
                       void* out, long long out_sb, long long out_sh, int out_dtype,
                       int B, int Hq, int Hkv, int G, int S, int R, int Dh, int split_len);
+
+/*
+ * Launch timing hooks (measurement only, no reference counterpart). Between
+ * dkv_profile_begin(max_calls) and dkv_profile_end, each dkv_decode_splitk call (the first
+ * max_calls of them) records HIP events before its split launch, between the split and merge
+ * launches and after the merge, on its stream. dkv_profile_end waits for the recorded events,
+ * returns the summed split and merge milliseconds and the number of calls recorded, and
+ * destroys the events. Not thread-safe.
+ */
+int dkv_profile_begin(int max_calls);
+int dkv_profile_end(double* split_ms, double* merge_ms, int* calls);
 
 /*
  * Launch-layout self test (diagnostic, no reference counterpart): runs the MFMA operand

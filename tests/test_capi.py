@@ -45,7 +45,10 @@ def test_host_only_entry_points():
     assert lib.dkv_version() >= 100
     assert lib.dkv_status_string(-1) == b"invalid argument"
     sl = lib.dkv_splitk_choose_split(16, 8, 8292)
-    assert sl % 64 == 0 and 64 <= sl <= 512
+    # about one workgroup per CU (256): 128 units -> two splits of the 8292 tokens
+    assert sl % 64 == 0 and sl == 4160
+    assert lib.dkv_splitk_choose_split(1, 8, 8292) % 64 == 0
+    assert lib.dkv_splitk_choose_split(1, 8, 10) == 64
     assert lib.dkv_rope_table_floats(10) == (17 + 10) * 128
     assert lib.dkv_splitk_workspace_floats(16, 32, 8, 8292, 128, sl) > 0
 

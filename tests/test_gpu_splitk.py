@@ -59,7 +59,7 @@ def test_split_length_invariance(dev, route):
     case = make_case(B=2, G=8, Hq=32, S=3000, mean=0.29, force_first=4, force_frac=0.05, seed=30)
     p = packed_from_case(case, torch.bfloat16, dev)
     ref = oracle_grouped(case, p["host"], route, "bfloat16")
-    outs = [_run(p, case, route, sl) for sl in (64, 192, 320, 512)]
+    outs = [_run(p, case, route, sl) for sl in (64, 192, 320, 512, 1024, 3008)]
     for o in outs:
         assert_close(o, ref, f"split {route}")
     # fp32 results of different split lengths differ by summation order and, on the two-stage
