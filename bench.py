@@ -21,6 +21,7 @@ dimension CPU path on a bounded sample of the same inputs.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -100,14 +101,18 @@ def build_workload(cfg, total_steps, dev, seed=1234):
                 q=q, lk_steps=lk_steps, lv_steps=lv_steps, lk_h=lk_h, lv_h=lv_h, gen=gen)
 
 
-def attention_bytes(cfg, lk_h, lv_h, S):
-    """Algorithmic HBM bytes of one decode-attention call at cache length S."""
+def attention_bytes(cfg, lk_h, lv_h, S, split_only=False):
+    """Algorithmic HBM bytes of one decode-attention call at cache length S: packed K and V
+    coefficients read once, one int32 length per token, row and K|V, the unique bases, q and the
+    output. ``split_only``: what the split kernel alone must move (no V basis, no output)."""
     elt = 2
     coef = elt * (int(lk_h[:, :S].sum()) + int(lv_h[:, :S].sum()))
     lens = 8 * cfg.B * cfg.G * S
-    bases = 2 * cfg.G * cfg.R * cfg.Dh * elt
-    qo = 2 * cfg.B * cfg.Hq * cfg.Dh * elt
-    return coef + lens + bases + qo
+    basis = cfg.G * cfg.R * cfg.Dh * elt
+    q = cfg.B * cfg.Hq * cfg.Dh * elt
+    if split_only:
+        return coef + lens + basis + q
+    return coef + lens + 2 * basis + 2 * q
 
 
 class SplitKRunner:
@@ -176,18 +181,27 @@ def run_gpu(cfg, steps, warmup, dev):
     for i in range(warmup):
         one_step(i, None)
     torch.cuda.synchronize(dev)
+    lib = _lib.load()
     _log("timed region")
+    # library-side HIP events around the split and merge launches of each call (same stream)
+    _lib.check(lib.dkv_profile_begin(steps), "dkv_profile_begin")
+    lens = []
     t0 = time.perf_counter()
     for j in range(steps):
-        L = one_step(warmup + j, events[j])
-        step_bytes.append(attention_bytes(cfg, W["lk_h"], W["lv_h"], L))
+        lens.append(one_step(warmup + j, events[j]))
     torch.cuda.synchronize(dev)
     wall = time.perf_counter() - t0
+    step_bytes = [attention_bytes(cfg, W["lk_h"], W["lv_h"], L) for L in lens]
+    split_bytes = [attention_bytes(cfg, W["lk_h"], W["lv_h"], L, split_only=True) for L in lens]
+    sm, mm, nc = ctypes.c_double(), ctypes.c_double(), ctypes.c_int()
+    _lib.check(lib.dkv_profile_end(ctypes.byref(sm), ctypes.byref(mm), ctypes.byref(nc)),
+               "dkv_profile_end")
+    assert nc.value == steps, (nc.value, steps)
     attn_ms = sum(e[0].elapsed_time(e[1]) for e in events)
-    split_ms = attn_ms
     tot_bytes = float(sum(step_bytes))
     res = dict(
-        wall_s=wall, attn_ms=attn_ms, split_ms=split_ms,
+        wall_s=wall, attn_ms=attn_ms, split_ms=sm.value, merge_ms=mm.value,
+        split_bytes_per_step=float(sum(split_bytes)) / steps,
         bytes_total=tot_bytes, bytes_per_step=tot_bytes / steps,
         final_len=cache.get_seq_length_sp(0), syncs=cache.device_syncs,
         q0=W["q"][0], cache=cache, workload=W,
@@ -240,6 +254,22 @@ def cpu_baseline(cfg, W, cache, budget_s: float):
     }
 
 
+def load_traffic(workload):
+    """HBM bytes per split-kernel launch measured by rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs
+    of this script (scaled by a plain copy of known size), as committed under profiles/; used
+    only when it was measured on the library version that is loaded now."""
+    from dynakv_amd import _lib
+
+    path = os.path.join(ROOT, "profiles", f"splitk_{workload}_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        t = json.load(f)
+    if t.get("dkv_version") != _lib.load().dkv_version():
+        return None
+    return {"bytes_per_launch": t["bytes_per_launch"], "source": os.path.relpath(path, ROOT)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -248,6 +278,8 @@ def main():
     ap.add_argument("--workload", default="config3", choices=["config3", "config2"])
     ap.add_argument("--cpu-baseline-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="run one device copy of this many MiB first (counter calibration)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -260,11 +292,23 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda:0")
     cfg = Config3 if args.workload == "config3" else Config2
+    if args.copy_probe_mib > 0:
+        # a plain device copy of known size: the reference point that scales the FETCH_SIZE and
+        # WRITE_SIZE counters of a rocprofv3 --pmc run of this command
+        nb = args.copy_probe_mib << 20
+        src = torch.ones(nb, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize(dev)
+        dst.copy_(src)
+        torch.cuda.synchronize(dev)
+        _log(f"copy probe: {args.copy_probe_mib} MiB read + {args.copy_probe_mib} MiB written")
+        del src, dst
     r = run_gpu(cfg, args.steps, args.warmup, dev)
     attn_s = r["attn_ms"] / 1e3
     gbs = r["bytes_total"] / attn_s / 1e9
     split_avg_s = r["split_ms"] / 1e3 / args.steps
-    achieved = r["bytes_per_step"] / split_avg_s / 1e9
+    achieved = r["split_bytes_per_step"] / split_avg_s / 1e9
+    traffic = load_traffic(cfg.name)
     line = {
         "metric": "decode-attn GB/s (% HBM peak) + decode tokens/s, Llama-3-8B shape, 1 GPU",
         "value": round(gbs, 2),
@@ -296,7 +340,11 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic["bytes_per_launch"] if traffic else None,
+            "split_kernel_us": round(r["split_ms"] * 1e3 / args.steps, 3),
+            "merge_kernel_us": round(r["merge_ms"] * 1e3 / args.steps, 3),
+            "algorithmic_bytes_per_launch": round(r["split_bytes_per_step"]),
+            "traffic_source": traffic["source"] if traffic else None,
         },
     }
     if not args.no_cpu_baseline:

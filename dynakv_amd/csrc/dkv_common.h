@@ -4,7 +4,7 @@
 #include <stdint.h>
 #include "../../include/dynakv_amd.h"
 
-#define DKV_VERSION 100
+#define DKV_VERSION 101
 
 typedef __attribute__((ext_vector_type(8))) __bf16 dkv_bf16x8;
 typedef __attribute__((ext_vector_type(4))) __bf16 dkv_bf16x4;
@@ -14,6 +14,8 @@ typedef __attribute__((ext_vector_type(2))) _Float16 dkv_f16x2;
 typedef __attribute__((ext_vector_type(4))) float dkv_f32x4;
 typedef __attribute__((ext_vector_type(4))) unsigned dkv_u32x4;
 typedef __attribute__((ext_vector_type(2))) unsigned dkv_u32x2;
+typedef __attribute__((ext_vector_type(4))) int dkv_i32x4;
+typedef __attribute__((ext_vector_type(4))) short dkv_i16x4;
 
 #define DKV_HIP_CHECK_LAUNCH()                                  \
   do {                                                          \
@@ -34,12 +36,9 @@ __device__ __forceinline__ float dkv_bf16_bits_to_f32(uint32_t bits16) {
 __device__ __forceinline__ float dkv_f16_bits_to_f32(uint32_t bits16) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
 }
-// Round-to-nearest-even fp32 -> bf16 bits (NaN kept quiet).
+// Round-to-nearest-even fp32 -> bf16 bits (NaN stays NaN): gfx950's conversion instruction.
 __device__ __forceinline__ uint32_t dkv_f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return ((u >> 16) | 0x40u) & 0xffffu;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+  return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f);
 }
 __device__ __forceinline__ uint32_t dkv_f32_to_f16_bits(float f) {
   return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f);

@@ -123,8 +123,7 @@ __device__ __forceinline__ dkv_f32x4 mfma_f16(const dkv_u32x4& a, const dkv_u32x
 __device__ __forceinline__ void split_f16x2(float x0, float x1, uint32_t& hi, uint32_t& lo) {
   hi = __builtin_bit_cast(uint32_t, dkv_f16x2{(_Float16)x0, (_Float16)x1});
   uint32_t l;
-  asm volatile(
-      "v_fma_mixlo_f16 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]\n\t"
+  asm("v_fma_mixlo_f16 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]\n\t"
       "v_fma_mixhi_f16 %0, %1, -1.0, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
       : "=&v"(l)
       : "v"(hi), "v"(x0), "v"(x1));
@@ -178,6 +177,19 @@ __device__ __forceinline__ void lds_load4(const void* gptr, uint32_t lds_base) {
 }
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
+}
+
+// max(x, x of lane l ^ 32) and max(x, x of lane l ^ 16): a permlane swap of a value with
+// itself leaves each lane its own value in one result and its partner's in the other.
+__device__ __forceinline__ float lane_max32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float lane_max16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
 // Wait until at most N vector-memory loads of this wave are outstanding (loads complete in
@@ -464,7 +476,7 @@ __global__ __launch_bounds__(256, 1) void splitk_kernel(SplitParams p) {
         float r1 = c1[w] * rc[f] + c0[w] * rs[f];
         // materialise the rotated pair once (otherwise the rotation is re-formed inside
         // the mixed-precision conversions of both parts)
-        asm volatile("" : "+v"(r0), "+v"(r1));
+        asm("" : "+v"(r0), "+v"(r1));
         split_f16x2(r0, r1, h4[w], l4[w]);
       }
       sc = mfma_f16(dkv_u32x4{l4[0], l4[1], l4[2], l4[3]}, bq[pp], sc);
@@ -477,40 +489,48 @@ __global__ __launch_bounds__(256, 1) void splitk_kernel(SplitParams p) {
       const dkv_f32x4 ds = *(const dkv_f32x4*)&sStep[1][16 * pp + 4 * g];
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
-        // each new value depends on its own old value and a product formed first, so the
-        // update happens in place
+        // (c, s) <- (c*dc - s*ds, s*dc + c*ds), updated in place: both products that need the
+        // old values are formed first (left to the compiler, the new pair lands in fresh
+        // registers and is copied back at the end of every iteration)
         const int f = pp * 4 + w;
-        const float sd = rs[f] * ds[w], cd = rc[f] * ds[w];
-        rc[f] = fmaf(rc[f], dc[w], -sd);
-        rs[f] = fmaf(rs[f], dc[w], cd);
+        float t0, t1;
+        asm("v_mul_f32 %2, %1, %5\n\t"
+            "v_mul_f32 %3, %0, %5\n\t"
+            "v_fma_f32 %0, %0, %4, -%2\n\t"
+            "v_fma_f32 %1, %1, %4, %3"
+            : "+v"(rc[f]), "+v"(rs[f]), "=&v"(t0), "=&v"(t1)
+            : "v"(dc[w]), "v"(ds[w]));
       }
     }
 
-    // scores of lane (head slot n, tokens 4g+u) -> log2 domain with the route's masking
-    const unsigned long long in_bits = __ballot(cur.valid);
-    const unsigned long long has_bits = __ballot(cur.valid && cur.rk > 0);
+    // scores of lane (head slot n, tokens 4g+u) -> log2 domain with the route's masking; the
+    // lane reads the lengths of its four tokens from the tile's table
     float z[4];
+    {
+      const dkv_i32x4 lk4 = *(const dkv_i32x4*)&sTabRing[wave][j % TSLOT][0][4 * g];
+      const int nvalid = s_end - (tile0 + WAVES * j) * TILE;  // tokens of the tile in range
+      const int lk[4] = {lk4.x, lk4.y, lk4.z, lk4.w};
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int tok = 4 * g + u;
-      const bool has = (has_bits >> tok) & 1ull;
-      const bool inr = (in_bits >> tok) & 1ull;
-      float v;
-      if constexpr (ROUTE == DKV_ROUTE_FUSED) {
-        v = has ? sc[u] * p.score_scale : -INFINITY;  // score_scale = sm_scale * log2(e)
-      } else {
-        v = dkv_round_to<DT>(has ? sc[u] * p.score_scale : p.masked_score) * LOG2E;
+      for (int u = 0; u < 4; ++u) {
+        const bool inr = 4 * g + u < nvalid;
+        const bool has = lk[u] > 0;
+        float v;
+        if constexpr (ROUTE == DKV_ROUTE_FUSED) {
+          v = has ? sc[u] * p.score_scale : -INFINITY;  // score_scale = sm_scale * log2(e)
+        } else {
+          v = dkv_round_to<DT>(has ? sc[u] * p.score_scale : p.masked_score) * LOG2E;
+        }
+        z[u] = inr ? v : -INFINITY;
       }
-      z[u] = inr ? v : -INFINITY;
     }
 
-    // ---- 4. online softmax (per head slot) --------------------------------------------------
+    // ---- 4. online softmax (per head slot; its 16 tokens sit in lanes n, n+16, n+32, n+48) --
     float tmax = fmaxf(fmaxf(z[0], z[1]), fmaxf(z[2], z[3]));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    tmax = lane_max32(tmax);
+    tmax = lane_max16(tmax);
     if (__ballot(tmax > m_run + RESCALE_THRESH)) {
       const float m_new = fmaxf(m_run, tmax);
-      const float alpha = (m_new == -INFINITY) ? 1.f : exp2f(m_run - m_new);
+      const float alpha = (m_new == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
       l_run *= alpha;
       m_run = m_new;
       float au[4];
@@ -524,7 +544,8 @@ __global__ __launch_bounds__(256, 1) void splitk_kernel(SplitParams p) {
     float pu[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      pu[u] = (z[u] == -INFINITY) ? 0.f : exp2f(z[u] - m_run);
+      // exp2 of a value <= RESCALE_THRESH; results below fp32's normal range may flush to zero
+      pu[u] = (z[u] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(z[u] - m_run);
       l_run += pu[u];
     }
 
@@ -542,15 +563,23 @@ __global__ __launch_bounds__(256, 1) void splitk_kernel(SplitParams p) {
       pa_lo = dkv_u32x2{(uint32_t)__builtin_bit_cast(uint16_t, e0) | ((uint32_t)__builtin_bit_cast(uint16_t, e1) << 16),
                         (uint32_t)__builtin_bit_cast(uint16_t, e2) | ((uint32_t)__builtin_bit_cast(uint16_t, e3) << 16)};
     }
-    // rank r = 16*blk + n of token t sits at chunk r/32, lane 16*((r%32)/8) + t, element r%8
-    const uint16_t* vsrc = (const uint16_t*)(slot + 4096 + 16 * (16 * (n >> 3) + 4 * g)) + (n & 7);
+    // B operand (tokens 4g..4g+3 x rank 16*blk + n) by transposed reads: within each 16-lane
+    // group, lane i receives element i%4 of the 8 bytes read by lane 4*u + i/4 of that group,
+    // so lane (g, u = n/4, q = n%4) reads ranks 16*blk + 4q .. +3 of token 4g + u. Rank r of
+    // token t sits in chunk r/32 at lane slot 16*((r%32)/8) + t, element r%8.
+    {
+      const int u = n >> 2, q = n & 3;
+      const uint8_t* vbase = slot + 4096 + 16 * (16 * (q >> 1) + 4 * g + u) + 8 * (q & 1);
 #pragma unroll
-    for (int blk = 0; blk < 8; ++blk) {
-      const uint16_t* src = vsrc + ((blk >> 1) * 1024 + (blk & 1) * 512) / 2;
-      const uint32_t e0 = src[0], e1 = src[8], e2 = src[16], e3 = src[24];
-      const dkv_u32x2 xb = {e0 | (e1 << 16), e2 | (e3 << 16)};
-      acc[blk] = mfma_pv<DT>(pa_hi, xb, acc[blk]);
-      if constexpr (DT == DKV_BF16) acc[blk] = mfma_pv<DT>(pa_lo, xb, acc[blk]);
+      for (int blk = 0; blk < 8; ++blk) {
+        const uint8_t* src = vbase + (blk >> 1) * 1024 + (blk & 1) * 512;
+        const dkv_u32x2 xb = __builtin_bit_cast(
+            dkv_u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                           (__attribute__((address_space(3))) dkv_i16x4*)(
+                               (__attribute__((address_space(3))) uint8_t*)src)));
+        acc[blk] = mfma_pv<DT>(pa_hi, xb, acc[blk]);
+        if constexpr (DT == DKV_BF16) acc[blk] = mfma_pv<DT>(pa_lo, xb, acc[blk]);
+      }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
