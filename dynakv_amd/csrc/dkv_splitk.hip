@@ -40,6 +40,7 @@ constexpr int VT_LD = 136;    // LDS row pitch (elements) of a wave's V tile
 constexpr int PREC = DH + 2;  // floats per partial record: m, l, acc[128]
 constexpr int NSLOT = 4;       // gather slots per wave: the current tile + three in flight
 constexpr int TSLOT = 8;       // table slots per wave (tables run two tiles ahead of gathers)
+static_assert(NSLOT == 4 && TSLOT == 8, "the pipeline waits below assume these depths");
 constexpr int GSLOT_BYTES = 8192;  // 4 K chunks + 4 V chunks of 64 lanes x 16 bytes
 constexpr int MASK_BIAS = 120;  // mask-table row of count 0 for the lowest chunk start
 constexpr int MASK_ROWS = MASK_BIAS + DH + 1;
@@ -72,6 +73,7 @@ struct SplitParams {
   int B, Hq, Hkv, G, S, R, hpg, n_splits, split_len;
   float score_scale;   // applied to q.k' after the MFMA (fused: sm_scale*log2e, else sm_scale)
   float masked_score;  // two-stage route: -1e4 * (1/sqrt(Dh)) in fp32
+  float minus_one;     // -1.0f (see split_f16x2)
 };
 
 template <int DT>
@@ -117,17 +119,18 @@ __device__ __forceinline__ dkv_f32x4 mfma_f16(const dkv_u32x4& a, const dkv_u32x
                                                 __builtin_bit_cast(dkv_f16x8, b), c, 0, 0, 0);
 }
 
-// x ~= hi + lo with hi = fp16(x) and lo = fp16(x - hi), for two values packed per dword.
-// hi is one packed conversion; each half of lo is one mixed-precision fma, fp16(hi_k * -1 + x_k)
-// (x_k - hi_k is exact in fp32, so lo_k is that difference rounded once to fp16).
-__device__ __forceinline__ void split_f16x2(float x0, float x1, uint32_t& hi, uint32_t& lo) {
-  hi = __builtin_bit_cast(uint32_t, dkv_f16x2{(_Float16)x0, (_Float16)x1});
-  uint32_t l;
-  asm("v_fma_mixlo_f16 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]\n\t"
-      "v_fma_mixhi_f16 %0, %1, -1.0, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
-      : "=&v"(l)
-      : "v"(hi), "v"(x0), "v"(x1));
-  lo = l;
+// x ~= hi + lo with hi = fp16(x) and lo = fp16(x - hi), for two values packed per dword
+// (x - hi is exact in fp32, so lo is that difference rounded once to fp16). minus_one is -1.0f
+// passed at run time: as a literal the compiler folds fma(h, -1, x) into a subtraction and
+// converts in several steps, while fma(h, m, x) maps to one mixed-precision fma per half.
+__device__ __forceinline__ void split_f16x2(float x0, float x1, float minus_one, uint32_t& hi,
+                                            uint32_t& lo) {
+  typedef __attribute__((ext_vector_type(2))) float f32x2;
+  const dkv_f16x2 hv = __builtin_convertvector(f32x2{x0, x1}, dkv_f16x2);  // one packed convert
+  const _Float16 l0 = (_Float16)__builtin_fmaf((float)hv[0], minus_one, x0);
+  const _Float16 l1 = (_Float16)__builtin_fmaf((float)hv[1], minus_one, x1);
+  hi = __builtin_bit_cast(uint32_t, hv);
+  lo = __builtin_bit_cast(uint32_t, dkv_f16x2{l0, l1});
 }
 
 // Element-wise gather of the first nv (1..8) 16-bit values at element offset e, the rest zero:
@@ -411,121 +414,176 @@ __global__ __launch_bounds__(256, 1) void splitk_kernel(SplitParams p) {
   float m_run = -INFINITY;  // per head slot n (log2 units), identical across g
   float l_run = 0.f;        // partial over this lane's 4 tokens per tile
 
-  // ---- pipeline: tables run five tiles ahead, gathers three. Loads are issued for every
-  //      iteration, also past the wave's last tile (token indices clamp to the split's last
-  //      token, so those re-read cached lines), which keeps the number of loads in flight
-  //      after any given load fixed: each wait below lets exactly the loads issued after the
-  //      awaited one stay in flight. -----------------------------------------------------------
-  load_tab(0);
-  load_tab(1);
-  load_tab(2);
-  wait_vm<2>();  // T0
-  issue(0);
-  load_tab(3);
-  wait_vm<10>();  // T1 (T2, G0, T3 in flight)
-  issue(1);
-  load_tab(4);
-  wait_vm<18>();  // T2 (G0, T3, G1, T4 in flight)
-  issue(2);
-
-  for (int j = 0; j < n_iter; ++j) {
-    // G(j) and T(j+3) have landed once only G(j+1), T(j+4), G(j+2) may be in flight
-    wait_vm<17>();
-    const Tok cur = tok_of(j);
-    uint8_t* slot = ring + (j % NSLOT) * GSLOT_BYTES;
-    regather_if_needed(cur, slot);
-    // ---- masks (elements past each token's count belong to the next tokens): K into
-    //      registers, V back into the slot -----------------------------------------------------
-    dkv_u32x4 xk[4];
-    {
-      const char* mkb = (const char*)&sMask[0][0] + 16 * (cur.rkc - 8 * g + MASK_BIAS - 96);
-      const char* mvb = (const char*)&sMask[0][0] + 16 * (cur.rvc - 8 * g + MASK_BIAS - 96);
+  // ---- per-tile pieces ------------------------------------------------------------------
+  // masks (elements past each token's count belong to the next tokens): K into registers,
+  // V back into the slot
+  auto mask_tile = [&](const Tok& d, uint8_t* slot, dkv_u32x4 (&xk)[4]) {
+    const char* mkb = (const char*)&sMask[0][0] + 16 * (d.rkc - 8 * g + MASK_BIAS - 96);
+    const char* mvb = (const char*)&sMask[0][0] + 16 * (d.rvc - 8 * g + MASK_BIAS - 96);
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const dkv_u32x4 mk = *(const dkv_u32x4*)(mkb + 16 * (96 - 32 * c));
-        const dkv_u32x4 kr = *(const dkv_u32x4*)(slot + c * 1024 + 16 * lane);
-        xk[c] = dkv_u32x4{kr.x & mk.x, kr.y & mk.y, kr.z & mk.z, kr.w & mk.w};
-        const dkv_u32x4 mv = *(const dkv_u32x4*)(mvb + 16 * (96 - 32 * c));
-        dkv_u32x4* vp = (dkv_u32x4*)(slot + 4096 + c * 1024 + 16 * lane);
-        const dkv_u32x4 vr = *vp;
-        *vp = dkv_u32x4{vr.x & mv.x, vr.y & mv.y, vr.z & mv.z, vr.w & mv.w};
-      }
+    for (int c = 0; c < 4; ++c) {
+      const dkv_u32x4 mk = *(const dkv_u32x4*)(mkb + 16 * (96 - 32 * c));
+      const dkv_u32x4 kr = *(const dkv_u32x4*)(slot + c * 1024 + 16 * lane);
+      xk[c] = dkv_u32x4{kr.x & mk.x, kr.y & mk.y, kr.z & mk.z, kr.w & mk.w};
+      const dkv_u32x4 mv = *(const dkv_u32x4*)(mvb + 16 * (96 - 32 * c));
+      dkv_u32x4* vp = (dkv_u32x4*)(slot + 4096 + c * 1024 + 16 * lane);
+      const dkv_u32x4 vr = *vp;
+      *vp = dkv_u32x4{vr.x & mv.x, vr.y & mv.y, vr.z & mv.z, vr.w & mv.w};
     }
-    // ---- keep the pipeline full ------------------------------------------------------------
-    load_tab(j + 5);
-    issue(j + 3);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-    // ---- 1-3: K reconstruction, RoPE, hi/lo split, scores ---------------------------------
-    dkv_f32x4 sc = {0.f, 0.f, 0.f, 0.f};
+  };
+  // K' = RoPE(BK^T . X^T) for 16-dim blocks pp and pp+4 of one tile, split into fp16 hi/lo
+  // parts, accumulated into the tile's scores (lane: head slot n, tokens 4g+u)
+  auto rope_qk = [&](int pp, const dkv_f32x4& c0, const dkv_f32x4& c1, const float (&cc)[16],
+                     const float (&ss)[16], dkv_f32x4& sc) {
+    uint32_t h4[4], l4[4];
 #pragma unroll
-    for (int pp = 0; pp < 4; ++pp) {
-      dkv_f32x4 c0 = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        c0 = mfma_k<DT>(bA[pp][c], xk[c], c0);
-        c1 = mfma_k<DT>(bA[pp + 4][c], xk[c], c1);
-      }
-      uint32_t h4[4], l4[4];
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const int f = pp * 4 + w;
-        float r0 = c0[w] * rc[f] - c1[w] * rs[f];
-        float r1 = c1[w] * rc[f] + c0[w] * rs[f];
-        // materialise the rotated pair once (otherwise the rotation is re-formed inside
-        // the mixed-precision conversions of both parts)
-        asm("" : "+v"(r0), "+v"(r1));
-        split_f16x2(r0, r1, h4[w], l4[w]);
-      }
-      sc = mfma_f16(dkv_u32x4{l4[0], l4[1], l4[2], l4[3]}, bq[pp], sc);
-      sc = mfma_f16(dkv_u32x4{h4[0], h4[1], h4[2], h4[3]}, bq[pp], sc);
+    for (int w = 0; w < 4; ++w) {
+      const int f = pp * 4 + w;
+      float r0 = c0[w] * cc[f] - c1[w] * ss[f];
+      float r1 = c1[w] * cc[f] + c0[w] * ss[f];
+      // materialise the rotated pair once (otherwise the rotation is re-formed inside the
+      // mixed-precision conversions of both parts)
+      asm("" : "+v"(r0), "+v"(r1));
+      split_f16x2(r0, r1, p.minus_one, h4[w], l4[w]);
     }
-    // advance the rotation by WAVES*TILE positions (a wave's consecutive tiles)
+    sc = mfma_f16(dkv_u32x4{l4[0], l4[1], l4[2], l4[3]}, bq[pp], sc);
+    sc = mfma_f16(dkv_u32x4{h4[0], h4[1], h4[2], h4[3]}, bq[pp], sc);
+  };
+  // scores -> log2 domain with the route's masking; the lane reads its four tokens' lengths
+  auto scores_to_z = [&](int j, const dkv_f32x4& sc, float (&z)[4]) {
+    const dkv_i32x4 lk4 = *(const dkv_i32x4*)&sTabRing[wave][j % TSLOT][0][4 * g];
+    const int nvalid = s_end - (tile0 + WAVES * j) * TILE;  // tokens of the tile in range
+    const int lk[4] = {lk4.x, lk4.y, lk4.z, lk4.w};
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const bool inr = 4 * g + u < nvalid;
+      const bool has = lk[u] > 0;
+      float v;
+      if constexpr (ROUTE == DKV_ROUTE_FUSED) {
+        v = has ? sc[u] * p.score_scale : -INFINITY;  // score_scale = sm_scale * log2(e)
+      } else {
+        v = dkv_round_to<DT>(has ? sc[u] * p.score_scale : p.masked_score) * LOG2E;
+      }
+      z[u] = inr ? v : -INFINITY;
+    }
+  };
+  // P of one tile as the A operand of the PV MFMA (fp16, or a bf16 hi + lo pair)
+  auto p_operand = [&](const float (&pu)[4], dkv_u32x2& hi, dkv_u32x2& lo) {
+    if constexpr (DT == DKV_F16) {
+      hi = dkv_u32x2{pack_f16x2(pu[0], pu[1]), pack_f16x2(pu[2], pu[3])};
+      lo = hi;
+    } else {
+      const __bf16 h0 = (__bf16)pu[0], h1 = (__bf16)pu[1], h2 = (__bf16)pu[2], h3 = (__bf16)pu[3];
+      const __bf16 e0 = (__bf16)(pu[0] - (float)h0), e1 = (__bf16)(pu[1] - (float)h1);
+      const __bf16 e2 = (__bf16)(pu[2] - (float)h2), e3 = (__bf16)(pu[3] - (float)h3);
+      hi = dkv_u32x2{(uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16),
+                     (uint32_t)__builtin_bit_cast(uint16_t, h2) | ((uint32_t)__builtin_bit_cast(uint16_t, h3) << 16)};
+      lo = dkv_u32x2{(uint32_t)__builtin_bit_cast(uint16_t, e0) | ((uint32_t)__builtin_bit_cast(uint16_t, e1) << 16),
+                     (uint32_t)__builtin_bit_cast(uint16_t, e2) | ((uint32_t)__builtin_bit_cast(uint16_t, e3) << 16)};
+    }
+  };
+  // acc += P . X^V for one tile; the B operand (tokens 4g..4g+3 x rank 16*blk + n) comes from
+  // transposed reads: within each 16-lane group, lane i receives element i%4 of the 8 bytes
+  // read by lane 4*u + i/4 of that group, so lane (g, u = n/4, q = n%4) reads ranks
+  // 16*blk + 4q .. +3 of token 4g + u. Rank r of token t sits in chunk r/32 at lane slot
+  // 16*((r%32)/8) + t, element r%8.
+  auto pv_tile = [&](const uint8_t* slot, const dkv_u32x2& hi, const dkv_u32x2& lo) {
+    const int u = n >> 2, q = n & 3;
+    const uint8_t* vbase = slot + 4096 + 16 * (16 * (q >> 1) + 4 * g + u) + 8 * (q & 1);
+#pragma unroll
+    for (int blk = 0; blk < 8; ++blk) {
+      const uint8_t* src = vbase + (blk >> 1) * 1024 + (blk & 1) * 512;
+      const dkv_u32x2 xb = __builtin_bit_cast(
+          dkv_u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                         (__attribute__((address_space(3))) dkv_i16x4*)(
+                             (__attribute__((address_space(3))) uint8_t*)src)));
+      acc[blk] = mfma_pv<DT>(hi, xb, acc[blk]);
+      if constexpr (DT == DKV_BF16) acc[blk] = mfma_pv<DT>(lo, xb, acc[blk]);
+    }
+  };
+  // (c, s) <- (c, s) rotated by WAVES*TILE positions (a wave's consecutive tiles)
+  auto rotate_step = [&](const float (&ci)[16], const float (&si)[16], float (&co)[16],
+                         float (&so)[16]) {
 #pragma unroll
     for (int pp = 0; pp < 4; ++pp) {
       const dkv_f32x4 dc = *(const dkv_f32x4*)&sStep[0][16 * pp + 4 * g];
       const dkv_f32x4 ds = *(const dkv_f32x4*)&sStep[1][16 * pp + 4 * g];
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
-        // (c, s) <- (c*dc - s*ds, s*dc + c*ds), updated in place: both products that need the
-        // old values are formed first (left to the compiler, the new pair lands in fresh
-        // registers and is copied back at the end of every iteration)
         const int f = pp * 4 + w;
-        float t0, t1;
-        asm("v_mul_f32 %2, %1, %5\n\t"
-            "v_mul_f32 %3, %0, %5\n\t"
-            "v_fma_f32 %0, %0, %4, -%2\n\t"
-            "v_fma_f32 %1, %1, %4, %3"
-            : "+v"(rc[f]), "+v"(rs[f]), "=&v"(t0), "=&v"(t1)
-            : "v"(dc[w]), "v"(ds[w]));
+        co[f] = ci[f] * dc[w] - si[f] * ds[w];
+        so[f] = si[f] * dc[w] + ci[f] * ds[w];
       }
     }
+  };
 
-    // scores of lane (head slot n, tokens 4g+u) -> log2 domain with the route's masking; the
-    // lane reads the lengths of its four tokens from the tile's table
-    float z[4];
+  // ---- pipeline: each iteration takes two of the wave's tiles (A = 2i, B = 2i+1; their
+  //      instruction streams are independent until the softmax, so the matrix and vector
+  //      pipes overlap). Gathers are issued one iteration ahead, at the end of the iteration
+  //      that frees their slots; tables one iteration before that. Loads are issued for every
+  //      iteration, also past the wave's last tile (token indices clamp to the split's last
+  //      token, so those re-read cached lines): the number of loads in flight after any
+  //      given load is then fixed, and each wait lets exactly those stay in flight. ---------
+  load_tab(0);
+  load_tab(1);
+  load_tab(2);
+  load_tab(3);
+  wait_vm<2>();  // T0, T1 (T2, T3 in flight)
+  issue(0);
+  issue(1);
+  load_tab(4);
+  load_tab(5);
+  wait_vm<18>();  // T2, T3 (G0, G1, T4, T5 in flight)
+  issue(2);
+  issue(3);
+
+  const int n_pairs = (n_iter + 1) / 2;
+  for (int i = 0; i < n_pairs; ++i) {
+    const int jA = 2 * i, jB = 2 * i + 1;
+    // G(jA), G(jB) have landed once only T(jA+4), T(jA+5), G(jA+2), G(jA+3) may be in flight
+    wait_vm<18>();
+    uint8_t* slotA = ring + (jA % NSLOT) * GSLOT_BYTES;
+    uint8_t* slotB = ring + (jB % NSLOT) * GSLOT_BYTES;
+    dkv_u32x4 xkA[4], xkB[4];
     {
-      const dkv_i32x4 lk4 = *(const dkv_i32x4*)&sTabRing[wave][j % TSLOT][0][4 * g];
-      const int nvalid = s_end - (tile0 + WAVES * j) * TILE;  // tokens of the tile in range
-      const int lk[4] = {lk4.x, lk4.y, lk4.z, lk4.w};
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const bool inr = 4 * g + u < nvalid;
-        const bool has = lk[u] > 0;
-        float v;
-        if constexpr (ROUTE == DKV_ROUTE_FUSED) {
-          v = has ? sc[u] * p.score_scale : -INFINITY;  // score_scale = sm_scale * log2(e)
-        } else {
-          v = dkv_round_to<DT>(has ? sc[u] * p.score_scale : p.masked_score) * LOG2E;
-        }
-        z[u] = inr ? v : -INFINITY;
-      }
+      const Tok dA = tok_of(jA);
+      regather_if_needed(dA, slotA);
+      const Tok dB = tok_of(jB);
+      regather_if_needed(dB, slotB);
+      mask_tile(dA, slotA, xkA);
+      mask_tile(dB, slotB, xkB);
     }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-    // ---- 4. online softmax (per head slot; its 16 tokens sit in lanes n, n+16, n+32, n+48) --
-    float tmax = fmaxf(fmaxf(z[0], z[1]), fmaxf(z[2], z[3]));
+    // ---- 1-3: K reconstruction, RoPE, hi/lo split, scores for both tiles ---------------
+    float rbc[16], rbs[16];  // rotation of tile B
+    rotate_step(rc, rs, rbc, rbs);
+    dkv_f32x4 scA = {0.f, 0.f, 0.f, 0.f}, scB = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int pp = 0; pp < 4; ++pp) {
+      dkv_f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = a0, b0 = a0, b1 = a0;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        a0 = mfma_k<DT>(bA[pp][c], xkA[c], a0);
+        a1 = mfma_k<DT>(bA[pp + 4][c], xkA[c], a1);
+        b0 = mfma_k<DT>(bA[pp][c], xkB[c], b0);
+        b1 = mfma_k<DT>(bA[pp + 4][c], xkB[c], b1);
+      }
+      rope_qk(pp, a0, a1, rc, rs, scA);
+      rope_qk(pp, b0, b1, rbc, rbs, scB);
+    }
+    rotate_step(rbc, rbs, rc, rs);  // rotation of the next iteration's tile A
+
+    float zA[4], zB[4];
+    scores_to_z(jA, scA, zA);
+    scores_to_z(jB, scB, zB);
+
+    // ---- 4. online softmax over the 32 tokens (per head slot; a tile's 16 tokens sit in
+    //      lanes n, n+16, n+32, n+48) ---------------------------------------------------------
+    float tmax = fmaxf(fmaxf(fmaxf(zA[0], zA[1]), fmaxf(zA[2], zA[3])),
+                       fmaxf(fmaxf(zB[0], zB[1]), fmaxf(zB[2], zB[3])));
     tmax = lane_max32(tmax);
     tmax = lane_max16(tmax);
     if (__ballot(tmax > m_run + RESCALE_THRESH)) {
@@ -537,53 +595,36 @@ __global__ __launch_bounds__(256, 1) void splitk_kernel(SplitParams p) {
 #pragma unroll
       for (int u = 0; u < 4; ++u) au[u] = __shfl(alpha, 4 * g + u, 64);
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
+      for (int b2 = 0; b2 < 8; ++b2)
 #pragma unroll
-        for (int u = 0; u < 4; ++u) acc[i][u] *= au[u];
+        for (int u = 0; u < 4; ++u) acc[b2][u] *= au[u];
     }
-    float pu[4];
+    float pA[4], pB[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       // exp2 of a value <= RESCALE_THRESH; results below fp32's normal range may flush to zero
-      pu[u] = (z[u] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(z[u] - m_run);
-      l_run += pu[u];
+      pA[u] = (zA[u] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(zA[u] - m_run);
+      pB[u] = (zB[u] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(zB[u] - m_run);
+      l_run += pA[u] + pB[u];
     }
 
-    // ---- 5. P.X^V from the slot's masked V chunks (4 tokens x 1 rank per lane) --------------
-    dkv_u32x2 pa_hi, pa_lo;
-    if constexpr (DT == DKV_F16) {
-      pa_hi = dkv_u32x2{pack_f16x2(pu[0], pu[1]), pack_f16x2(pu[2], pu[3])};
-      pa_lo = pa_hi;
-    } else {
-      const __bf16 h0 = (__bf16)pu[0], h1 = (__bf16)pu[1], h2 = (__bf16)pu[2], h3 = (__bf16)pu[3];
-      const __bf16 e0 = (__bf16)(pu[0] - (float)h0), e1 = (__bf16)(pu[1] - (float)h1);
-      const __bf16 e2 = (__bf16)(pu[2] - (float)h2), e3 = (__bf16)(pu[3] - (float)h3);
-      pa_hi = dkv_u32x2{(uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16),
-                        (uint32_t)__builtin_bit_cast(uint16_t, h2) | ((uint32_t)__builtin_bit_cast(uint16_t, h3) << 16)};
-      pa_lo = dkv_u32x2{(uint32_t)__builtin_bit_cast(uint16_t, e0) | ((uint32_t)__builtin_bit_cast(uint16_t, e1) << 16),
-                        (uint32_t)__builtin_bit_cast(uint16_t, e2) | ((uint32_t)__builtin_bit_cast(uint16_t, e3) << 16)};
-    }
-    // B operand (tokens 4g..4g+3 x rank 16*blk + n) by transposed reads: within each 16-lane
-    // group, lane i receives element i%4 of the 8 bytes read by lane 4*u + i/4 of that group,
-    // so lane (g, u = n/4, q = n%4) reads ranks 16*blk + 4q .. +3 of token 4g + u. Rank r of
-    // token t sits in chunk r/32 at lane slot 16*((r%32)/8) + t, element r%8.
-    {
-      const int u = n >> 2, q = n & 3;
-      const uint8_t* vbase = slot + 4096 + 16 * (16 * (q >> 1) + 4 * g + u) + 8 * (q & 1);
-#pragma unroll
-      for (int blk = 0; blk < 8; ++blk) {
-        const uint8_t* src = vbase + (blk >> 1) * 1024 + (blk & 1) * 512;
-        const dkv_u32x2 xb = __builtin_bit_cast(
-            dkv_u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                           (__attribute__((address_space(3))) dkv_i16x4*)(
-                               (__attribute__((address_space(3))) uint8_t*)src)));
-        acc[blk] = mfma_pv<DT>(pa_hi, xb, acc[blk]);
-        if constexpr (DT == DKV_BF16) acc[blk] = mfma_pv<DT>(pa_lo, xb, acc[blk]);
-      }
-    }
+    // ---- 5. P.X^V in coefficient space --------------------------------------------------------
+    dkv_u32x2 hA, lA, hB, lB;
+    p_operand(pA, hA, lA);
+    p_operand(pB, hB, lB);
+    pv_tile(slotA, hA, lA);
+    pv_tile(slotB, hB, lB);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // ---- refill: tables of tiles jA+6, jA+7, then (once T(jA+4), T(jA+5) have landed) the
+    //      gathers of tiles jA+4, jA+5 into the slots just consumed -------------------------
+    load_tab(jA + 6);
+    load_tab(jA + 7);
+    wait_vm<18>();
+    issue(jA + 4);
+    issue(jA + 5);
   }
   wait_vm<0>();  // nothing may land in the ring once it is reused below
 
@@ -987,6 +1028,7 @@ extern "C" int dkv_decode_splitk(void* stream, int route, int dtype, const void*
   const float sm_scale = 1.0f / sqrtf((float)Dh);
   p.score_scale = route == DKV_ROUTE_FUSED ? sm_scale * LOG2E : sm_scale;
   p.masked_score = -1.0e4f * sm_scale;
+  p.minus_one = -1.0f;
   const dim3 grid((unsigned)(units * n_splits)), mgrid((unsigned)(units * (Hq / Hkv)));
   hipStream_t st = (hipStream_t)stream;
   if (dtype == DKV_BF16) {
