@@ -116,9 +116,9 @@ def attention_bytes(cfg, lk_h, lv_h, S, split_only=False):
 
 
 class SplitKRunner:
-    """Launches dkv_decode_splitk (split + merge kernels) with HIP events around it on the current stream
-    (the stream the kernel runs on). The RoPE table and the workspace are built once, before
-    any timed step."""
+    """Launches dkv_decode_splitk on the current stream (the split kernel merges its own splits;
+    the library times it with HIP events on that stream). The RoPE table and the workspace are
+    built once, before any timed step."""
 
     def __init__(self, cfg, dev, max_S):
         from dynakv_amd import _lib
@@ -134,7 +134,7 @@ class SplitKRunner:
         self.rope, self.rope_tiles = rope_table(dev, st, cfg.theta, max_S)
         self.out = torch.empty((cfg.B, cfg.Hq, cfg.Dh), dtype=cfg.dtype, device=dev)
 
-    def run(self, q, fk, fv, lk, ok, lv, ov, kb, vb, route, ev=None):
+    def run(self, q, fk, fv, lk, ok, lv, ov, kb, vb, route):
         cfg, L = self.cfg, self._lib
         S = lk.shape[1]
         st = torch.cuda.current_stream(self.dev)
@@ -147,11 +147,7 @@ class SplitKRunner:
                 self.rope.data_ptr(), self.rope_tiles, self.ws.data_ptr(), self.ws.numel(),
                 self.out.data_ptr(), self.out.stride(0), self.out.stride(1),
                 L.dtype_code(cfg.dtype), cfg.B, cfg.Hq, cfg.G, cfg.G, S, cfg.R, cfg.Dh, 0)
-        if ev is not None:
-            ev[0].record(st)
         L.check(self.lib.dkv_decode_splitk(*args), "dkv_decode_splitk")
-        if ev is not None:
-            ev[1].record(st)
         return self.out
 
 
@@ -166,20 +162,19 @@ def run_gpu(cfg, steps, warmup, dev):
     runner = SplitKRunner(cfg, dev, cfg.S0 + total + 16)
     policy = KernelPolicy()
     R = cfg.R
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(steps)]
     step_bytes = []
 
-    def one_step(i, ev):
+    def one_step(i):
         fk, fv, lk, lv, ok, ov = cache.update_sp(W["steps_k"][i], W["lk_steps"][i], W["steps_v"][i],
                                                  W["lv_steps"][i], R, 0, R)
         L = cache.get_seq_length_sp(0)
         route = (_lib.DKV_ROUTE_FUSED if policy.select(L) == "short_fused"
                  else _lib.DKV_ROUTE_TWO_STAGE)
-        runner.run(W["q"][i], fk, fv, lk, ok, lv, ov, W["k_basis"], W["v_basis"], route, ev)
+        runner.run(W["q"][i], fk, fv, lk, ok, lv, ov, W["k_basis"], W["v_basis"], route)
         return L
 
     for i in range(warmup):
-        one_step(i, None)
+        one_step(i)
     torch.cuda.synchronize(dev)
     lib = _lib.load()
     _log("timed region")
@@ -188,7 +183,7 @@ def run_gpu(cfg, steps, warmup, dev):
     lens = []
     t0 = time.perf_counter()
     for j in range(steps):
-        lens.append(one_step(warmup + j, events[j]))
+        lens.append(one_step(warmup + j))
     torch.cuda.synchronize(dev)
     wall = time.perf_counter() - t0
     step_bytes = [attention_bytes(cfg, W["lk_h"], W["lv_h"], L) for L in lens]
@@ -197,7 +192,9 @@ def run_gpu(cfg, steps, warmup, dev):
     _lib.check(lib.dkv_profile_end(ctypes.byref(sm), ctypes.byref(mm), ctypes.byref(nc)),
                "dkv_profile_end")
     assert nc.value == steps, (nc.value, steps)
-    attn_ms = sum(e[0].elapsed_time(e[1]) for e in events)
+    # attention GPU time: the library's events around the split launch (and the merge launch,
+    # when one runs), recorded on the kernels' stream for every timed call
+    attn_ms = sm.value + mm.value
     tot_bytes = float(sum(step_bytes))
     res = dict(
         wall_s=wall, attn_ms=attn_ms, split_ms=sm.value, merge_ms=mm.value,

@@ -34,14 +34,17 @@ namespace {
 
 constexpr int DH = 128;
 constexpr int TILE = 16;
-constexpr int WAVES = 4;
+constexpr int WAVES = 8;        // per workgroup: two per SIMD
+constexpr int NTHREADS = WAVES * 64;
 constexpr int BK_LD = 136;    // LDS row pitch (elements) of the transposed K basis
 constexpr int VT_LD = 136;    // LDS row pitch (elements) of a wave's V tile
 constexpr int PREC = DH + 2;  // floats per partial record: m, l, acc[128]
-constexpr int NSLOT = 4;       // gather slots per wave: the current tile + three in flight
-constexpr int TSLOT = 8;       // table slots per wave (tables run two tiles ahead of gathers)
-static_assert(NSLOT == 4 && TSLOT == 8, "the pipeline waits below assume these depths");
+constexpr int NSLOT = 2;        // gather slots per wave: the current tile + one in flight
+constexpr int TSLOT = 4;        // table slots per wave (tables run a tile ahead of gathers)
 constexpr int GSLOT_BYTES = 8192;  // 4 K chunks + 4 V chunks of 64 lanes x 16 bytes
+constexpr int QSTAGE = 65536;      // ring offset of the query staging copy (prologue only)
+constexpr int MERGE_COUNTERS = 16384;  // leading workspace ints: per-unit arrival counters
+constexpr int VB_CHUNKS = DH * DH / 8 / NTHREADS;  // 16-byte V-basis pieces per thread
 constexpr int MASK_BIAS = 120;  // mask-table row of count 0 for the lowest chunk start
 constexpr int MASK_ROWS = MASK_BIAS + DH + 1;
 constexpr int ROPE_FIXED_ROWS = TILE + 1;  // rows 0..15: in-tile deltas; row 16: per-step
@@ -68,6 +71,9 @@ struct SplitParams {
   long long tv_sb, tv_ss;
   const float* rope;   // rows of 64 (cos, sin): 16 in-tile deltas, 1 step, then tile bases
   float* partials;     // [unit][split][hpg][PREC]
+  int* counters;       // [unit] arrival counts of the fused merge (zero between calls)
+  int fused_merge;     // 1: the last split of a unit merges; 0: merge_kernel follows
+  int out_f32;         // output dtype: 1 fp32, 0 the cache dtype
   void* out;
   long long out_sb, out_sh;
   int B, Hq, Hkv, G, S, R, hpg, n_splits, split_len;
@@ -202,16 +208,83 @@ __device__ __forceinline__ void wait_vm() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// LSE-merge the split records of one unit, normalise with the route's denominator, project
+// once through the unit's V basis and store the hpg output rows (all threads of the block).
+// vbr: this thread's share of the V basis, loaded by the caller (vb_chunks 16-byte pieces);
+// scratch: LDS for the basis ([rank][DH] bf16/fp16) and (32 + 16 * DH) floats.
+template <int DT, int ROUTE, int ODT>
+__device__ __forceinline__ void merge_unit_t(const SplitParams& p, int unit, uint8_t* scratch,
+                                             const dkv_u32x4 (&vbr)[VB_CHUNKS]) {
+  const int b = unit / p.Hkv, kvh = unit % p.Hkv;
+  const int tid = threadIdx.x;
+  const long long stride = (long long)p.hpg * PREC;  // between splits of one head
+  const float* base = p.partials + (long long)unit * p.n_splits * stride;
+  uint16_t* sVB = reinterpret_cast<uint16_t*>(scratch);  // [R][DH]
+  float* sM = reinterpret_cast<float*>(scratch + DH * DH * 2);  // [16] max of each head
+  float* sInv = sM + 16;                                      // [16] 1 / denominator
+  float* sA = sM + 32;                                        // [16][DH] merged accumulators
+#pragma unroll
+  for (int k = 0; k < VB_CHUNKS; ++k) {
+    const int ch = tid + k * NTHREADS;  // 16-byte piece: rank ch / 16, dims 8 * (ch % 16)
+    if (ch < p.R * (DH / 8)) *(dkv_u32x4*)(sVB + ch * 8) = vbr[k];
+  }
+  if (tid < p.hpg) {
+    float M = -INFINITY;
+    for (int sp = 0; sp < p.n_splits; ++sp) M = fmaxf(M, base[sp * stride + tid * PREC]);
+    float L = 0.f;
+    for (int sp = 0; sp < p.n_splits; ++sp) {
+      const float* r = base + sp * stride + tid * PREC;
+      L += (M == -INFINITY) ? 0.f : exp2f(r[0] - M) * r[1];
+    }
+    const float den = ROUTE == DKV_ROUTE_TWO_STAGE ? fmaxf(L, 1e-6f) : L;
+    sM[tid] = M;
+    sInv[tid] = 1.f / den;
+  }
+  __syncthreads();
+  for (int idx = tid; idx < p.hpg * DH; idx += NTHREADS) {
+    const int hs = idx / DH, r = idx % DH;
+    const float M = sM[hs];
+    float a = 0.f;
+    if (r < p.R)
+      for (int sp = 0; sp < p.n_splits; ++sp) {
+        const float* rec = base + sp * stride + hs * PREC;
+        a += (M == -INFINITY) ? 0.f : exp2f(rec[0] - M) * rec[2 + r];
+      }
+    sA[hs * DH + r] = a * sInv[hs];
+  }
+  __syncthreads();
+  for (int idx = tid; idx < p.hpg * DH; idx += NTHREADS) {
+    const int hs = idx / DH, d = idx % DH;
+    const float* a = sA + hs * DH;
+    float o = 0.f;
+#pragma unroll 8
+    for (int j = 0; j < p.R; ++j) o = fmaf(a[j], elt_to_f32<DT>(sVB[j * DH + d]), o);
+    const long long oi = (long long)b * p.out_sb + (long long)(kvh * p.hpg + hs) * p.out_sh + d;
+    dkv_store_f32<ODT>(p.out, oi, o);
+  }
+}
 template <int DT, int ROUTE>
-__global__ __launch_bounds__(256, 1) void splitk_kernel(SplitParams p) {
-  // per-wave LDS ring: NSLOT gather slots (K then V: 4 chunks x 64 lanes x 16 bytes each) and
-  // TSLOT table slots (lens_k, offs_k, lens_v, offs_v x 16 tokens); the K basis staging area
-  // and the epilogue scratch alias the gather slots
+__device__ __forceinline__ void merge_unit(const SplitParams& p, int unit, uint8_t* scratch,
+                                           const dkv_u32x4 (&vbr)[VB_CHUNKS]) {
+  if (p.out_f32)
+    merge_unit_t<DT, ROUTE, DKV_F32>(p, unit, scratch, vbr);
+  else
+    merge_unit_t<DT, ROUTE, DT>(p, unit, scratch, vbr);
+}
+
+template <int DT, int ROUTE>
+__global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
+  // LDS: per-wave rings (NSLOT gather slots: K then V, 4 chunks x 64 lanes x 16 bytes each;
+  // TSLOT table slots: lens_k, offs_k, lens_v, offs_v x 16 tokens), the streamed half of the
+  // K basis ([dim][rank] rows of dims 32..63 and 96..127), the mask table and the rotation
+  // step. The full basis staging copy and the epilogue scratch alias the rings.
   __shared__ __attribute__((aligned(16))) uint8_t sRing[WAVES * NSLOT * GSLOT_BYTES];
   __shared__ __attribute__((aligned(16))) int sTabRing[WAVES][TSLOT][4][TILE];
+  __shared__ __attribute__((aligned(16))) uint16_t sBH[DH / 2 * BK_LD];
   __shared__ __attribute__((aligned(16))) uint32_t sMask[MASK_ROWS][4];
   __shared__ __attribute__((aligned(16))) float sStep[2][64];  // rotation by WAVES*TILE positions
-  static_assert(DH * BK_LD * 2 <= WAVES * NSLOT * GSLOT_BYTES, "basis staging fits the ring");
+  static_assert(DH * BK_LD * 2 <= QSTAGE && QSTAGE + WAVES * 64 * 64 <= WAVES * NSLOT * GSLOT_BYTES,
+                "basis and query staging fit the rings");
   uint16_t* sBK = reinterpret_cast<uint16_t*>(sRing);
 
   // XCD-aware mapping: consecutive workgroup ids land on different XCDs (id % 8), so give
@@ -239,31 +312,31 @@ __global__ __launch_bounds__(256, 1) void splitk_kernel(SplitParams p) {
   const int s_end = min(p.S, s_begin + p.split_len);
   const int ns = s_end - s_begin;
 
-  // ---- prologue: K basis through LDS into registers, mask table, query, RoPE state --------
+  // ---- prologue: K basis, mask table, rotation step ---------------------------------------
   {
     // transpose to [dim][rank]: consecutive lanes take consecutive ranks, so each 2-byte LDS
-    // store of a wave covers 128 contiguous bytes (no bank conflicts)
+    // store of a wave covers 128 contiguous bytes (no bank conflicts). Dims 32..63 and 96..127
+    // go to their permanent place (sBH rows 0..31 and 32..63), the others to the staging copy.
     const uint16_t* kb = p.k_basis + (long long)kvh * p.k_unit;
-    const int j = tid & 127;
-    dkv_u32x4 v[8];
+    const int j = tid & 127, dq = tid >> 7;  // 4 groups of 8-dim slices
 #pragma unroll
-    for (int it = 0; it < 8; ++it) {
-      const int d8 = ((tid >> 7) + 2 * it) * 8;
-      v[it] = dkv_u32x4{0u, 0u, 0u, 0u};
-      if (j < R) v[it] = *(const dkv_u32x4*)(kb + (long long)j * p.k_sr + d8);
-    }
+    for (int it = 0; it < 4; ++it) {
+      const int d8 = (dq + 4 * it) * 8;
+      dkv_u32x4 v = dkv_u32x4{0u, 0u, 0u, 0u};
+      if (j < R) v = *(const dkv_u32x4*)(kb + (long long)j * p.k_sr + d8);
+      const uint32_t e[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-    for (int it = 0; it < 8; ++it) {
-      const int d8 = ((tid >> 7) + 2 * it) * 8;
-      const uint32_t e[4] = {v[it].x, v[it].y, v[it].z, v[it].w};
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        sBK[(d8 + 2 * t) * BK_LD + j] = (uint16_t)(e[t] & 0xffffu);
-        sBK[(d8 + 2 * t + 1) * BK_LD + j] = (uint16_t)(e[t] >> 16);
+      for (int t = 0; t < 8; ++t) {
+        const int d = d8 + t;
+        const uint16_t x = (uint16_t)((e[t >> 1] >> (16 * (t & 1))) & 0xffffu);
+        if ((d & 32) != 0)
+          sBH[(((d >> 6) << 5) + (d & 31)) * BK_LD + j] = x;
+        else
+          sBK[d * BK_LD + j] = x;
       }
     }
     // row j holds the keep-mask of the first clamp(j - MASK_BIAS, 0, 8) elements
-    for (int r = tid; r < MASK_ROWS * 4; r += 256)
+    for (int r = tid; r < MASK_ROWS * 4; r += NTHREADS)
       sMask[r >> 2][r & 3] = prefix_mask_word(min(max((r >> 2) - MASK_BIAS, 0), 8), r & 3);
     if (tid < 64) {
       sStep[0][tid] = p.rope[TILE * 128 + 2 * tid];
@@ -296,11 +369,13 @@ __global__ __launch_bounds__(256, 1) void splitk_kernel(SplitParams p) {
         const float c = real ? elt_to_f32<DT>(qb[pp * 4 + w]) : 0.f;
         w4[w] = pack_f16x2(a, c);
       }
-      bq[pp] = dkv_u32x4{w4[0], w4[1], w4[2], w4[3]};
+      // staged in LDS, then read into accumulation registers with the K basis below
+      *(dkv_u32x4*)(sRing + QSTAGE + (wave * 64 + lane) * 64 + pp * 16) =
+          dkv_u32x4{w4[0], w4[1], w4[2], w4[3]};
     }
   }
 
-  const int tile_first = s_begin / TILE;  // splits are multiples of 64 tokens
+  const int tile_first = s_begin / TILE;  // splits are whole tiles (multiples of 64 tokens)
   const int tile0 = tile_first + wave;
   const int n_tb = (p.S + TILE - 1) / TILE;
   const int n_iter = max(0, ((ns + TILE - 1) / TILE - wave + WAVES - 1) / WAVES);
@@ -322,30 +397,41 @@ __global__ __launch_bounds__(256, 1) void splitk_kernel(SplitParams p) {
         rs[f] = bs * ec + bc * es;
       }
   }
-  __syncthreads();  // sBK, sMask, sStep ready
+  __syncthreads();  // staging copy, sBH, sMask, sStep ready
 
-  // recon A operands: block blk (dims 16*blk + n), rank chunk c (ranks 32c + 8g .. +8). They
-  // are read straight into accumulation registers, which the MFMAs take as their A operand:
-  // the 128 registers stay out of the VGPRs the rest of the loop needs.
-  dkv_u32x4 bA[8][4];
+  // recon A operands of blocks 0, 4, 1, 5 (dims 0..31 and 64..95; block blk = dims
+  // 16*blk + n, rank chunk c = ranks 32c + 8g .. +8), read straight into accumulation
+  // registers, which the MFMAs take as their A operand; blocks 2, 6, 3, 7 are read from sBH
+  // per tile.
+  dkv_u32x4 bA[4][4];  // [k][c], k -> block (k&1 ? 4 : 0) + (k >> 1)
   {
     const uint32_t a0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t*)(
         sBK + n * BK_LD + 8 * g);
 #pragma unroll
-    for (int blk = 0; blk < 8; ++blk)
+    for (int k = 0; k < 4; ++k)
 #pragma unroll
-      for (int c = 0; c < 4; ++c)
+      for (int c = 0; c < 4; ++c) {
+        const int blk = (k & 1 ? 4 : 0) + (k >> 1);
         asm volatile("ds_read_b128 %0, %1 offset:%2"
-                     : "=a"(bA[blk][c])
+                     : "=v"(bA[k][c])
                      : "v"(a0), "i"((16 * blk * BK_LD + 32 * c) * 2));
+      }
+    // the query operand (the B operand of the QK MFMAs), staged above
+    const uint32_t q0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)(
+        sRing + QSTAGE + (wave * 64 + lane) * 64);
+#pragma unroll
+    for (int pp = 0; pp < 4; ++pp)
+      asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(bq[pp]) : "v"(q0), "i"(pp * 16));
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   }
-  __syncthreads();  // every wave holds its operands: the ring may now be overwritten
+  __syncthreads();  // every wave holds its operands: the rings may now be overwritten
 
   // one resource per buffer, ranges [flat, flat + rows * ld); row offsets go in the voffset
   const __amdgpu_buffer_rsrc_t rk_src = dkv_make_rsrc(p.k_flat, p.k_end * 2u);
   const __amdgpu_buffer_rsrc_t rv_src = dkv_make_rsrc(p.v_flat, p.v_end * 2u);
   const int k_row0 = row * p.k_ld, v_row0 = row * p.v_ld;
+  // only the buffers' last row can hold a token whose 16-byte window crosses the end
+  const bool last_row = row == p.B * p.G - 1;
   uint8_t* ring = sRing + wave * NSLOT * GSLOT_BYTES;
   // table loads: lane (table l/16, token l%16) -> one 4-byte load per lane and tile
   const int* tab_base;
@@ -379,20 +465,23 @@ __global__ __launch_bounds__(256, 1) void splitk_kernel(SplitParams p) {
     return d;
   };
   // gathers of tile j into gather slot j % NSLOT: lane l's 16 bytes of chunk c land at
-  // slot + c*1024 + 16*l (K) and slot + 4096 + c*1024 + 16*l (V)
+  // slot + c*1024 + 16*l (K) and slot + 4096 + c*1024 + 16*l (V). A lane whose token has no
+  // element in its 8-rank piece reads the out-of-range offset instead (no memory traffic; the
+  // masks zero whatever its LDS bytes hold).
   auto issue = [&](int j) {
     const Tok d = tok_of(j);
     const uint32_t slot = lds_addr(ring + (j % NSLOT) * GSLOT_BYTES);
 #pragma unroll
-    for (int c = 0; c < 4; ++c) lds_load16(rk_src, slot + c * 1024, (d.ko + 8 * g + 32 * c) * 2);
+    for (int c = 0; c < 4; ++c)
+      lds_load16(rk_src, slot + c * 1024, d.rkc > 8 * g + 32 * c ? (d.ko + 8 * g + 32 * c) * 2 : OOB);
 #pragma unroll
     for (int c = 0; c < 4; ++c)
-      lds_load16(rv_src, slot + 4096 + c * 1024, (d.vo + 8 * g + 32 * c) * 2);
+      lds_load16(rv_src, slot + 4096 + c * 1024,
+                 d.rvc > 8 * g + 32 * c ? (d.vo + 8 * g + 32 * c) * 2 : OOB);
   };
   // A 16-byte window that crosses the end of a resource reads as zero in full; only the last
   // tokens of the last row can need one. Such a tile is gathered again with element loads
-  // once its ring slot has landed (the ring loads are issued regardless, so the number of
-  // loads in flight stays what the waits below assume).
+  // once its slot has landed.
   auto regather_if_needed = [&](const Tok& d, uint8_t* slot) {
     const bool risky = (d.rkc > 0 && (uint32_t)(d.ko + d.rkc + 7) > p.k_end) ||
                        (d.rvc > 0 && (uint32_t)(d.vo + d.rvc + 7) > p.v_end);
@@ -414,96 +503,82 @@ __global__ __launch_bounds__(256, 1) void splitk_kernel(SplitParams p) {
   float m_run = -INFINITY;  // per head slot n (log2 units), identical across g
   float l_run = 0.f;        // partial over this lane's 4 tokens per tile
 
-  // ---- per-tile pieces ------------------------------------------------------------------
-  // masks (elements past each token's count belong to the next tokens): K into registers,
-  // V back into the slot
-  auto mask_tile = [&](const Tok& d, uint8_t* slot, dkv_u32x4 (&xk)[4]) {
-    const char* mkb = (const char*)&sMask[0][0] + 16 * (d.rkc - 8 * g + MASK_BIAS - 96);
-    const char* mvb = (const char*)&sMask[0][0] + 16 * (d.rvc - 8 * g + MASK_BIAS - 96);
+  // ---- pipeline: one tile per iteration; the gathers of tile j+1 and the table of tile j+2
+  //      are in flight while tile j computes (two waves per SIMD hide each other's latency).
+  //      Loads are issued for every iteration, also past the wave's last tile (indices clamp
+  //      to the split's last token), so at the top of iteration j nothing but G(j) and T(j+1)
+  //      can be in flight and a full wait costs nothing extra. -------------------------------
+  load_tab(0);
+  load_tab(1);
+  wait_vm<1>();  // T0
+  issue(0);
+
+  // one tile: the rotation (ci, si) of this tile's token slot in, the next tile's out
+  auto tile = [&](int j, const float (&ci)[16], const float (&si)[16], float (&co)[16],
+                  float (&so)[16]) {
+    wait_vm<0>();  // G(j), T(j+1)
+    const Tok cur = tok_of(j);
+    uint8_t* slot = ring + (j % NSLOT) * GSLOT_BYTES;
+    if (last_row) regather_if_needed(cur, slot);
+    load_tab(j + 2);
+    issue(j + 1);
+    // ---- masks (elements past each token's count belong to the next tokens): K into
+    //      registers, V back into the slot -----------------------------------------------------
+    dkv_u32x4 xk[4];
+    {
+      const char* mkb = (const char*)&sMask[0][0] + 16 * (cur.rkc - 8 * g + MASK_BIAS - 96);
+      const char* mvb = (const char*)&sMask[0][0] + 16 * (cur.rvc - 8 * g + MASK_BIAS - 96);
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const dkv_u32x4 mk = *(const dkv_u32x4*)(mkb + 16 * (96 - 32 * c));
-      const dkv_u32x4 kr = *(const dkv_u32x4*)(slot + c * 1024 + 16 * lane);
-      xk[c] = dkv_u32x4{kr.x & mk.x, kr.y & mk.y, kr.z & mk.z, kr.w & mk.w};
-      const dkv_u32x4 mv = *(const dkv_u32x4*)(mvb + 16 * (96 - 32 * c));
-      dkv_u32x4* vp = (dkv_u32x4*)(slot + 4096 + c * 1024 + 16 * lane);
-      const dkv_u32x4 vr = *vp;
-      *vp = dkv_u32x4{vr.x & mv.x, vr.y & mv.y, vr.z & mv.z, vr.w & mv.w};
-    }
-  };
-  // K' = RoPE(BK^T . X^T) for 16-dim blocks pp and pp+4 of one tile, split into fp16 hi/lo
-  // parts, accumulated into the tile's scores (lane: head slot n, tokens 4g+u)
-  auto rope_qk = [&](int pp, const dkv_f32x4& c0, const dkv_f32x4& c1, const float (&cc)[16],
-                     const float (&ss)[16], dkv_f32x4& sc) {
-    uint32_t h4[4], l4[4];
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const int f = pp * 4 + w;
-      float r0 = c0[w] * cc[f] - c1[w] * ss[f];
-      float r1 = c1[w] * cc[f] + c0[w] * ss[f];
-      // materialise the rotated pair once (otherwise the rotation is re-formed inside the
-      // mixed-precision conversions of both parts)
-      asm("" : "+v"(r0), "+v"(r1));
-      split_f16x2(r0, r1, p.minus_one, h4[w], l4[w]);
-    }
-    sc = mfma_f16(dkv_u32x4{l4[0], l4[1], l4[2], l4[3]}, bq[pp], sc);
-    sc = mfma_f16(dkv_u32x4{h4[0], h4[1], h4[2], h4[3]}, bq[pp], sc);
-  };
-  // scores -> log2 domain with the route's masking; the lane reads its four tokens' lengths
-  auto scores_to_z = [&](int j, const dkv_f32x4& sc, float (&z)[4]) {
-    const dkv_i32x4 lk4 = *(const dkv_i32x4*)&sTabRing[wave][j % TSLOT][0][4 * g];
-    const int nvalid = s_end - (tile0 + WAVES * j) * TILE;  // tokens of the tile in range
-    const int lk[4] = {lk4.x, lk4.y, lk4.z, lk4.w};
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const bool inr = 4 * g + u < nvalid;
-      const bool has = lk[u] > 0;
-      float v;
-      if constexpr (ROUTE == DKV_ROUTE_FUSED) {
-        v = has ? sc[u] * p.score_scale : -INFINITY;  // score_scale = sm_scale * log2(e)
-      } else {
-        v = dkv_round_to<DT>(has ? sc[u] * p.score_scale : p.masked_score) * LOG2E;
+      for (int c = 0; c < 4; ++c) {
+        const dkv_u32x4 mk = *(const dkv_u32x4*)(mkb + 16 * (96 - 32 * c));
+        const dkv_u32x4 kr = *(const dkv_u32x4*)(slot + c * 1024 + 16 * lane);
+        xk[c] = dkv_u32x4{kr.x & mk.x, kr.y & mk.y, kr.z & mk.z, kr.w & mk.w};
+        const dkv_u32x4 mv = *(const dkv_u32x4*)(mvb + 16 * (96 - 32 * c));
+        dkv_u32x4* vp = (dkv_u32x4*)(slot + 4096 + c * 1024 + 16 * lane);
+        const dkv_u32x4 vr = *vp;
+        *vp = dkv_u32x4{vr.x & mv.x, vr.y & mv.y, vr.z & mv.z, vr.w & mv.w};
       }
-      z[u] = inr ? v : -INFINITY;
     }
-  };
-  // P of one tile as the A operand of the PV MFMA (fp16, or a bf16 hi + lo pair)
-  auto p_operand = [&](const float (&pu)[4], dkv_u32x2& hi, dkv_u32x2& lo) {
-    if constexpr (DT == DKV_F16) {
-      hi = dkv_u32x2{pack_f16x2(pu[0], pu[1]), pack_f16x2(pu[2], pu[3])};
-      lo = hi;
-    } else {
-      const __bf16 h0 = (__bf16)pu[0], h1 = (__bf16)pu[1], h2 = (__bf16)pu[2], h3 = (__bf16)pu[3];
-      const __bf16 e0 = (__bf16)(pu[0] - (float)h0), e1 = (__bf16)(pu[1] - (float)h1);
-      const __bf16 e2 = (__bf16)(pu[2] - (float)h2), e3 = (__bf16)(pu[3] - (float)h3);
-      hi = dkv_u32x2{(uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16),
-                     (uint32_t)__builtin_bit_cast(uint16_t, h2) | ((uint32_t)__builtin_bit_cast(uint16_t, h3) << 16)};
-      lo = dkv_u32x2{(uint32_t)__builtin_bit_cast(uint16_t, e0) | ((uint32_t)__builtin_bit_cast(uint16_t, e1) << 16),
-                     (uint32_t)__builtin_bit_cast(uint16_t, e2) | ((uint32_t)__builtin_bit_cast(uint16_t, e3) << 16)};
-    }
-  };
-  // acc += P . X^V for one tile; the B operand (tokens 4g..4g+3 x rank 16*blk + n) comes from
-  // transposed reads: within each 16-lane group, lane i receives element i%4 of the 8 bytes
-  // read by lane 4*u + i/4 of that group, so lane (g, u = n/4, q = n%4) reads ranks
-  // 16*blk + 4q .. +3 of token 4g + u. Rank r of token t sits in chunk r/32 at lane slot
-  // 16*((r%32)/8) + t, element r%8.
-  auto pv_tile = [&](const uint8_t* slot, const dkv_u32x2& hi, const dkv_u32x2& lo) {
-    const int u = n >> 2, q = n & 3;
-    const uint8_t* vbase = slot + 4096 + 16 * (16 * (q >> 1) + 4 * g + u) + 8 * (q & 1);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // ---- 1-3: K reconstruction, RoPE, hi/lo split, scores ---------------------------------
+    dkv_f32x4 sc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int blk = 0; blk < 8; ++blk) {
-      const uint8_t* src = vbase + (blk >> 1) * 1024 + (blk & 1) * 512;
-      const dkv_u32x2 xb = __builtin_bit_cast(
-          dkv_u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                         (__attribute__((address_space(3))) dkv_i16x4*)(
-                             (__attribute__((address_space(3))) uint8_t*)src)));
-      acc[blk] = mfma_pv<DT>(hi, xb, acc[blk]);
-      if constexpr (DT == DKV_BF16) acc[blk] = mfma_pv<DT>(lo, xb, acc[blk]);
+    for (int pp = 0; pp < 4; ++pp) {
+      dkv_f32x4 c0 = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
+      if (pp < 2) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          c0 = mfma_k<DT>(bA[2 * pp][c], xk[c], c0);
+          c1 = mfma_k<DT>(bA[2 * pp + 1][c], xk[c], c1);
+        }
+      } else {
+        // blocks pp and pp+4 from the streamed half: sBH rows (pp-2)*16 + n and 32 + ...
+        const uint16_t* r0 = sBH + ((pp - 2) * 16 + n) * BK_LD + 8 * g;
+        const uint16_t* r1 = r0 + 32 * BK_LD;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          c0 = mfma_k<DT>(*(const dkv_u32x4*)(r0 + 32 * c), xk[c], c0);
+          c1 = mfma_k<DT>(*(const dkv_u32x4*)(r1 + 32 * c), xk[c], c1);
+        }
+      }
+      uint32_t h4[4], l4[4];
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const int f = pp * 4 + w;
+        float r0 = c0[w] * ci[f] - c1[w] * si[f];
+        float r1 = c1[w] * ci[f] + c0[w] * si[f];
+        // materialise the rotated pair once (otherwise the rotation is re-formed inside the
+        // mixed-precision conversions of both parts)
+        asm("" : "+v"(r0), "+v"(r1));
+        split_f16x2(r0, r1, p.minus_one, h4[w], l4[w]);
+      }
+      sc = mfma_f16(dkv_u32x4{l4[0], l4[1], l4[2], l4[3]}, bq[pp], sc);
+      sc = mfma_f16(dkv_u32x4{h4[0], h4[1], h4[2], h4[3]}, bq[pp], sc);
     }
-  };
-  // (c, s) <- (c, s) rotated by WAVES*TILE positions (a wave's consecutive tiles)
-  auto rotate_step = [&](const float (&ci)[16], const float (&si)[16], float (&co)[16],
-                         float (&so)[16]) {
+    // advance the rotation to the wave's next tile (WAVES*TILE positions further)
 #pragma unroll
     for (int pp = 0; pp < 4; ++pp) {
       const dkv_f32x4 dc = *(const dkv_f32x4*)&sStep[0][16 * pp + 4 * g];
@@ -515,75 +590,30 @@ __global__ __launch_bounds__(256, 1) void splitk_kernel(SplitParams p) {
         so[f] = si[f] * dc[w] + ci[f] * ds[w];
       }
     }
-  };
 
-  // ---- pipeline: each iteration takes two of the wave's tiles (A = 2i, B = 2i+1; their
-  //      instruction streams are independent until the softmax, so the matrix and vector
-  //      pipes overlap). Gathers are issued one iteration ahead, at the end of the iteration
-  //      that frees their slots; tables one iteration before that. Loads are issued for every
-  //      iteration, also past the wave's last tile (token indices clamp to the split's last
-  //      token, so those re-read cached lines): the number of loads in flight after any
-  //      given load is then fixed, and each wait lets exactly those stay in flight. ---------
-  load_tab(0);
-  load_tab(1);
-  load_tab(2);
-  load_tab(3);
-  wait_vm<2>();  // T0, T1 (T2, T3 in flight)
-  issue(0);
-  issue(1);
-  load_tab(4);
-  load_tab(5);
-  wait_vm<18>();  // T2, T3 (G0, G1, T4, T5 in flight)
-  issue(2);
-  issue(3);
-
-  const int n_pairs = (n_iter + 1) / 2;
-  for (int i = 0; i < n_pairs; ++i) {
-    const int jA = 2 * i, jB = 2 * i + 1;
-    // G(jA), G(jB) have landed once only T(jA+4), T(jA+5), G(jA+2), G(jA+3) may be in flight
-    wait_vm<18>();
-    uint8_t* slotA = ring + (jA % NSLOT) * GSLOT_BYTES;
-    uint8_t* slotB = ring + (jB % NSLOT) * GSLOT_BYTES;
-    dkv_u32x4 xkA[4], xkB[4];
+    // scores of lane (head slot n, tokens 4g+u) -> log2 domain with the route's masking; the
+    // lane reads the lengths of its four tokens from the tile's table
+    float z[4];
     {
-      const Tok dA = tok_of(jA);
-      regather_if_needed(dA, slotA);
-      const Tok dB = tok_of(jB);
-      regather_if_needed(dB, slotB);
-      mask_tile(dA, slotA, xkA);
-      mask_tile(dB, slotB, xkB);
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-    // ---- 1-3: K reconstruction, RoPE, hi/lo split, scores for both tiles ---------------
-    float rbc[16], rbs[16];  // rotation of tile B
-    rotate_step(rc, rs, rbc, rbs);
-    dkv_f32x4 scA = {0.f, 0.f, 0.f, 0.f}, scB = {0.f, 0.f, 0.f, 0.f};
+      const dkv_i32x4 lk4 = *(const dkv_i32x4*)&sTabRing[wave][j % TSLOT][0][4 * g];
+      const int nvalid = s_end - (tile0 + WAVES * j) * TILE;  // tokens of the tile in range
+      const int lk[4] = {lk4.x, lk4.y, lk4.z, lk4.w};
 #pragma unroll
-    for (int pp = 0; pp < 4; ++pp) {
-      dkv_f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = a0, b0 = a0, b1 = a0;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        a0 = mfma_k<DT>(bA[pp][c], xkA[c], a0);
-        a1 = mfma_k<DT>(bA[pp + 4][c], xkA[c], a1);
-        b0 = mfma_k<DT>(bA[pp][c], xkB[c], b0);
-        b1 = mfma_k<DT>(bA[pp + 4][c], xkB[c], b1);
+      for (int u = 0; u < 4; ++u) {
+        const bool inr = 4 * g + u < nvalid;
+        const bool has = lk[u] > 0;
+        float v;
+        if constexpr (ROUTE == DKV_ROUTE_FUSED) {
+          v = has ? sc[u] * p.score_scale : -INFINITY;  // score_scale = sm_scale * log2(e)
+        } else {
+          v = dkv_round_to<DT>(has ? sc[u] * p.score_scale : p.masked_score) * LOG2E;
+        }
+        z[u] = inr ? v : -INFINITY;
       }
-      rope_qk(pp, a0, a1, rc, rs, scA);
-      rope_qk(pp, b0, b1, rbc, rbs, scB);
     }
-    rotate_step(rbc, rbs, rc, rs);  // rotation of the next iteration's tile A
 
-    float zA[4], zB[4];
-    scores_to_z(jA, scA, zA);
-    scores_to_z(jB, scB, zB);
-
-    // ---- 4. online softmax over the 32 tokens (per head slot; a tile's 16 tokens sit in
-    //      lanes n, n+16, n+32, n+48) ---------------------------------------------------------
-    float tmax = fmaxf(fmaxf(fmaxf(zA[0], zA[1]), fmaxf(zA[2], zA[3])),
-                       fmaxf(fmaxf(zB[0], zB[1]), fmaxf(zB[2], zB[3])));
+    // ---- 4. online softmax (per head slot; its 16 tokens sit in lanes n, n+16, n+32, n+48) --
+    float tmax = fmaxf(fmaxf(z[0], z[1]), fmaxf(z[2], z[3]));
     tmax = lane_max32(tmax);
     tmax = lane_max16(tmax);
     if (__ballot(tmax > m_run + RESCALE_THRESH)) {
@@ -595,46 +625,75 @@ __global__ __launch_bounds__(256, 1) void splitk_kernel(SplitParams p) {
 #pragma unroll
       for (int u = 0; u < 4; ++u) au[u] = __shfl(alpha, 4 * g + u, 64);
 #pragma unroll
-      for (int b2 = 0; b2 < 8; ++b2)
+      for (int i = 0; i < 8; ++i)
 #pragma unroll
-        for (int u = 0; u < 4; ++u) acc[b2][u] *= au[u];
+        for (int u = 0; u < 4; ++u) acc[i][u] *= au[u];
     }
-    float pA[4], pB[4];
+    float pu[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       // exp2 of a value <= RESCALE_THRESH; results below fp32's normal range may flush to zero
-      pA[u] = (zA[u] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(zA[u] - m_run);
-      pB[u] = (zB[u] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(zB[u] - m_run);
-      l_run += pA[u] + pB[u];
+      pu[u] = (z[u] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(z[u] - m_run);
+      l_run += pu[u];
     }
 
-    // ---- 5. P.X^V in coefficient space --------------------------------------------------------
-    dkv_u32x2 hA, lA, hB, lB;
-    p_operand(pA, hA, lA);
-    p_operand(pB, hB, lB);
-    pv_tile(slotA, hA, lA);
-    pv_tile(slotB, hB, lB);
+    // ---- 5. P.X^V in coefficient space ----------------------------------------------------------
+    dkv_u32x2 pa_hi, pa_lo;
+    if constexpr (DT == DKV_F16) {
+      pa_hi = dkv_u32x2{pack_f16x2(pu[0], pu[1]), pack_f16x2(pu[2], pu[3])};
+      pa_lo = pa_hi;
+    } else {
+      const __bf16 h0 = (__bf16)pu[0], h1 = (__bf16)pu[1], h2 = (__bf16)pu[2], h3 = (__bf16)pu[3];
+      const __bf16 e0 = (__bf16)(pu[0] - (float)h0), e1 = (__bf16)(pu[1] - (float)h1);
+      const __bf16 e2 = (__bf16)(pu[2] - (float)h2), e3 = (__bf16)(pu[3] - (float)h3);
+      pa_hi = dkv_u32x2{(uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16),
+                        (uint32_t)__builtin_bit_cast(uint16_t, h2) | ((uint32_t)__builtin_bit_cast(uint16_t, h3) << 16)};
+      pa_lo = dkv_u32x2{(uint32_t)__builtin_bit_cast(uint16_t, e0) | ((uint32_t)__builtin_bit_cast(uint16_t, e1) << 16),
+                        (uint32_t)__builtin_bit_cast(uint16_t, e2) | ((uint32_t)__builtin_bit_cast(uint16_t, e3) << 16)};
+    }
+    // B operand (tokens 4g..4g+3 x rank 16*blk + n) by transposed reads: within each 16-lane
+    // group, lane i receives element i%4 of the 8 bytes read by lane 4*u + i/4 of that group,
+    // so lane (g, u = n/4, q = n%4) reads ranks 16*blk + 4q .. +3 of token 4g + u. Rank r of
+    // token t sits in chunk r/32 at lane slot 16*((r%32)/8) + t, element r%8.
+    {
+      const int u = n >> 2, q = n & 3;
+      const uint8_t* vbase = slot + 4096 + 16 * (16 * (q >> 1) + 4 * g + u) + 8 * (q & 1);
+#pragma unroll
+      for (int blk = 0; blk < 8; ++blk) {
+        const uint8_t* src = vbase + (blk >> 1) * 1024 + (blk & 1) * 512;
+        const dkv_u32x2 xb = __builtin_bit_cast(
+            dkv_u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                           (__attribute__((address_space(3))) dkv_i16x4*)(
+                               (__attribute__((address_space(3))) uint8_t*)src)));
+        acc[blk] = mfma_pv<DT>(pa_hi, xb, acc[blk]);
+        if constexpr (DT == DKV_BF16) acc[blk] = mfma_pv<DT>(pa_lo, xb, acc[blk]);
+      }
+    }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
 
-    // ---- refill: tables of tiles jA+6, jA+7, then (once T(jA+4), T(jA+5) have landed) the
-    //      gathers of tiles jA+4, jA+5 into the slots just consumed -------------------------
-    load_tab(jA + 6);
-    load_tab(jA + 7);
-    wait_vm<18>();
-    issue(jA + 4);
-    issue(jA + 5);
+  // two tiles per loop iteration with the rotation alternating between two register sets (a
+  // single loop-carried set is copied back every iteration); the scheduling barrier keeps the
+  // two tiles from being interleaved, which would double the live registers
+  float rbc[16], rbs[16];
+  for (int j = 0; j < n_iter; j += 2) {
+    tile(j, rc, rs, rbc, rbs);
+    __builtin_amdgcn_sched_barrier(0);
+    if (j + 1 < n_iter) tile(j + 1, rbc, rbs, rc, rs);
+    __builtin_amdgcn_sched_barrier(0);
   }
   wait_vm<0>();  // nothing may land in the ring once it is reused below
 
-  // ---- combine the 4 waves through LDS and write the partial record ----------------------
+  // ---- combine the waves through LDS and write the partial record -----------------------
   float l_tot = l_run;
   l_tot += __shfl_xor(l_tot, 16, 64);
   l_tot += __shfl_xor(l_tot, 32, 64);
-  __syncthreads();  // all waves done with sBK and their tiles
+  __syncthreads();  // all waves done with their rings
   float* sw = reinterpret_cast<float*>(sRing);  // [WAVES][16 m | 16 l | 16 x 128 acc]
   constexpr int WREC = 32 + 16 * DH;
+  static_assert(WAVES * WREC * 4 <= WAVES * NSLOT * GSLOT_BYTES, "epilogue scratch fits");
   float* my = sw + wave * WREC;
   if (g == 0) {
     my[n] = m_run;
@@ -646,7 +705,7 @@ __global__ __launch_bounds__(256, 1) void splitk_kernel(SplitParams p) {
     for (int u = 0; u < 4; ++u) my[32 + (4 * g + u) * DH + 16 * i + n] = acc[i][u];
   __syncthreads();
   float* prec = p.partials + ((long long)unit * p.n_splits + split) * p.hpg * PREC;
-  for (int idx = tid; idx < p.hpg * PREC; idx += 256) {
+  for (int idx = tid; idx < p.hpg * PREC; idx += NTHREADS) {
     const int hs = idx / PREC, e = idx % PREC;
     float mw[WAVES], M = -INFINITY;
 #pragma unroll
@@ -663,7 +722,45 @@ __global__ __launch_bounds__(256, 1) void splitk_kernel(SplitParams p) {
     }
     prec[hs * PREC + e] = e == 0 ? M : v;
   }
+  if (!p.fused_merge) return;
 
+  // ---- fused merge: the last split of the unit to finish combines the unit's records -------
+  // Every wave's record stores are released at agent scope before the arrival is counted; the
+  // last arrival acquires them (the splits of a unit may run on different XCDs). The V basis
+  // loads are issued first so their latency overlaps the arrival round trip.
+  __shared__ int sLast;
+  dkv_u32x4 vbr[VB_CHUNKS];
+  {
+    const uint16_t* vb = p.v_basis + (long long)kvh * p.v_unit;
+#pragma unroll
+    for (int k = 0; k < VB_CHUNKS; ++k) {
+      const int ch = tid + k * NTHREADS;
+      vbr[k] = dkv_u32x4{0u, 0u, 0u, 0u};
+      if (ch < R * (DH / 8))
+        vbr[k] = *(const dkv_u32x4*)(vb + (long long)(ch >> 4) * p.v_sr + 8 * (ch & 15));
+    }
+  }
+  // Each wave waits until its record stores have reached the XCD's L2; after the barrier one
+  // wave releases them at agent scope (one L2 write-back covers every wave of the block: they
+  // share the L2) and counts the arrival. The last arrival acquires once (L1 and L2
+  // invalidation are per CU / per XCD, so one wave's acquire serves the whole block).
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (tid < 64) {
+    int last = 0;
+    if (tid == 0) {
+      const int old = __hip_atomic_fetch_add(p.counters + unit, 1, __ATOMIC_RELEASE,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+      last = old == p.n_splits - 1;
+    }
+    last = __shfl(last, 0, 64);
+    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    if (tid == 0) sLast = last;
+  }
+  __syncthreads();
+  if (!sLast) return;
+  merge_unit<DT, ROUTE>(p, unit, sRing, vbr);
+  if (tid == 0) p.counters[unit] = 0;  // ready for the next call (calls are stream-ordered)
 }
 
 // One workgroup per (unit, head slot): LSE-merge the split records of that head, normalise with
@@ -857,7 +954,7 @@ extern "C" long long dkv_splitk_workspace_floats(int B, int Hq, int Hkv, int S, 
   if (split_len <= 0) split_len = dkv_splitk_choose_split(B, Hkv, S);
   const long long n_splits = (S + split_len - 1) / split_len;
   const long long units = (long long)B * Hkv;
-  return units * n_splits * (Hq / Hkv) * PREC;
+  return MERGE_COUNTERS + units * n_splits * (Hq / Hkv) * PREC;
 }
 
 extern "C" long long dkv_rope_table_floats(int n_tiles) {
@@ -883,26 +980,32 @@ struct ProfileState {
   bool on = false;
   int cap = 0, n = 0;
   hipEvent_t* ev = nullptr;  // 3 per recorded call
+  bool* merged = nullptr;    // per recorded call: a separate merge kernel ran (events 1..2)
 };
 static ProfileState g_prof;
 
 template <int DT, int RT>
 static void launch_splitk_t(const SplitParams& p, int out_dtype, dim3 grid, dim3 mgrid,
                             hipStream_t st) {
-  hipEvent_t* ev = (g_prof.on && g_prof.n < g_prof.cap) ? g_prof.ev + 3 * g_prof.n++ : nullptr;
+  const int slot = (g_prof.on && g_prof.n < g_prof.cap) ? g_prof.n++ : -1;
+  hipEvent_t* ev = slot >= 0 ? g_prof.ev + 3 * slot : nullptr;
   if (ev) (void)hipEventRecord(ev[0], st);
-  hipLaunchKernelGGL((splitk_kernel<DT, RT>), grid, dim3(256), 0, st, p);
+  hipLaunchKernelGGL((splitk_kernel<DT, RT>), grid, dim3(NTHREADS), 0, st, p);
   if (ev) (void)hipEventRecord(ev[1], st);
-  if (out_dtype == DKV_F32)
-    hipLaunchKernelGGL((merge_kernel<DT, RT, DKV_F32>), mgrid, dim3(256), 0, st, p);
-  else
-    hipLaunchKernelGGL((merge_kernel<DT, RT, DT>), mgrid, dim3(256), 0, st, p);
-  if (ev) (void)hipEventRecord(ev[2], st);
+  if (!p.fused_merge) {
+    if (out_dtype == DKV_F32)
+      hipLaunchKernelGGL((merge_kernel<DT, RT, DKV_F32>), mgrid, dim3(256), 0, st, p);
+    else
+      hipLaunchKernelGGL((merge_kernel<DT, RT, DT>), mgrid, dim3(256), 0, st, p);
+    if (ev) (void)hipEventRecord(ev[2], st);
+  }
+  if (slot >= 0) g_prof.merged[slot] = !p.fused_merge;
 }
 
 static void profile_release() {
   for (int i = 0; i < 3 * g_prof.cap; ++i) (void)hipEventDestroy(g_prof.ev[i]);
   delete[] g_prof.ev;
+  delete[] g_prof.merged;
   g_prof = ProfileState{};
 }
 
@@ -910,6 +1013,7 @@ extern "C" int dkv_profile_begin(int max_calls) {
   if (max_calls <= 0 || max_calls > (1 << 20)) return DKV_E_ARG;
   if (g_prof.ev) profile_release();
   g_prof.ev = new hipEvent_t[3 * (size_t)max_calls];
+  g_prof.merged = new bool[(size_t)max_calls]();
   for (int i = 0; i < 3 * max_calls; ++i) {
     const hipError_t e = hipEventCreate(&g_prof.ev[i]);
     if (e != hipSuccess) {
@@ -933,9 +1037,9 @@ extern "C" int dkv_profile_end(double* split_ms, double* merge_ms, int* calls) {
   for (int i = 0; i < g_prof.n && rc == DKV_OK; ++i) {
     hipEvent_t* e = g_prof.ev + 3 * i;
     float a = 0.f, m = 0.f;
-    hipError_t err = hipEventSynchronize(e[2]);
+    hipError_t err = hipEventSynchronize(g_prof.merged[i] ? e[2] : e[1]);
     if (err == hipSuccess) err = hipEventElapsedTime(&a, e[0], e[1]);
-    if (err == hipSuccess) err = hipEventElapsedTime(&m, e[1], e[2]);
+    if (err == hipSuccess && g_prof.merged[i]) err = hipEventElapsedTime(&m, e[1], e[2]);
     if (err != hipSuccess) rc = -(1000 + (int)err);
     *split_ms += a;
     *merge_ms += m;
@@ -970,6 +1074,9 @@ extern "C" int dkv_decode_splitk(void* stream, int route, int dtype, const void*
     return DKV_E_ARG;
   // 16-byte aligned K basis rows for the vector LDS staging
   if (((uintptr_t)k_basis & 15) || (k_basis_sr & 7) || (k_unit_stride & 7))
+    return DKV_E_UNSUPPORTED;
+  // 16-byte aligned V basis rows for the vector loads of the fused merge
+  if (((uintptr_t)v_basis & 15) || (v_basis_sr & 7) || (v_unit_stride & 7))
     return DKV_E_UNSUPPORTED;
   if (k_ld <= 0 || v_ld <= 0) return DKV_E_ARG;
   // buffer offsets are 32-bit byte offsets from the first row
@@ -1012,7 +1119,11 @@ extern "C" int dkv_decode_splitk(void* stream, int route, int dtype, const void*
   p.tv_sb = tv_sb;
   p.tv_ss = tv_ss;
   p.rope = rope;
-  p.partials = workspace;
+  // workspace: MERGE_COUNTERS ints (zero between calls), then the split records
+  p.counters = reinterpret_cast<int*>(workspace);
+  p.partials = workspace + MERGE_COUNTERS;
+  p.fused_merge = units <= MERGE_COUNTERS ? 1 : 0;
+  p.out_f32 = out_dtype == DKV_F32 ? 1 : 0;
   p.out = out;
   p.out_sb = out_sb;
   p.out_sh = out_sh;

@@ -46,7 +46,9 @@ def rope_table(device: torch.device, stream: int, theta: float, seq_len: int):
 
 
 def workspace(device: torch.device, stream: int, floats: int) -> torch.Tensor:
-    """Split-K workspace of at least ``floats`` floats (cached per device and stream)."""
+    """Split-K workspace of at least ``floats`` floats (cached per device and stream). It is
+    zero-filled when allocated: its leading merge counters must start at zero, and every call
+    leaves them zero."""
     key = (device.index, stream)
     t = _WS_CACHE.get(key)
     if t is None or t.numel() < floats:

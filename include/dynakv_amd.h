@@ -156,7 +156,7 @@ int dkv_av(void* stream, int mode, int scores_dtype, int cache_dtype, int out_dt
 
 /*
  * RoPE cos/sin table for the split-K kernel, (17 + n_tiles) rows of 64 (cos, sin) fp32 pairs:
- * rows 0..15 the in-tile offsets (angle = d * inv_freq), row 16 the rotation by 64 positions,
+ * rows 0..15 the in-tile offsets (angle = d * inv_freq), row 16 the rotation by 128 positions (8 waves x 16),
  * row 17 + T the base of 16-token tile T (angle = 16T * inv_freq); inv_freq_i =
  * exp(-(2i/128) ln theta) and every angle formed in fp32 as the reference does (fused.py:65-66,
  * 97; two_stage.py:36-44). dkv_rope_table fills the fixed rows when from_tile == 0 and the tile
@@ -175,14 +175,18 @@ int dkv_rope_table(void* stream, float* rope, int from_tile, int to_tile, float 
  *                      rank stride basis_sr, unit dim stride (R x Dh).
  *   lens/offs tables for K and V with their own (sb, ss) strides.
  *   rope: table from dkv_rope_table with rope_tiles >= ceil(S / 16) tile rows (it carries theta).
- *   workspace: fp32 buffer of dkv_splitk_workspace_floats(...) floats (split records);
- *              calls that share a workspace must be ordered (same stream).
+ *   workspace: fp32 buffer of dkv_splitk_workspace_floats(...) floats: 16384 leading ints of
+ *              per-unit arrival counters, then the split records. The counters must be zero
+ *              before the first call (a zero-filled buffer) and every call leaves them zero;
+ *              calls that share a workspace must be ordered (same stream). With at most 16384
+ *              units the last split of each unit to finish merges the unit's records itself
+ *              (one launch); beyond that a merge kernel follows on the same stream.
  *   out: (B, Hq, Dh) strides (out_sb, out_sh), dtype out_dtype = the cache dtype (what the
  *        reference returns) or DKV_F32 (the merged result before rounding).
  * Requirements: q and cache dtype f16 or bf16 (same), Dh == 128, R <= 128, hpg <= 16,
  * Hkv % G == 0, (B*G) * row stride < 2^30 elements for each flat buffer, S * table token
  * stride < 2^31. split_len is a multiple of 64 (0 = dkv_splitk_choose_split: about one
- * workgroup per CU). Two launches on `stream`: the split kernel, then the merge.
+ * workgroup per CU).
  */
 long long dkv_splitk_workspace_floats(int B, int Hq, int Hkv, int S, int R, int split_len);
 int dkv_splitk_choose_split(int B, int Hkv, int S);
@@ -201,10 +205,10 @@ int dkv_decode_splitk(void* stream, int route, int dtype,
 /*
  * Launch timing hooks (measurement only, no reference counterpart). Between
  * dkv_profile_begin(max_calls) and dkv_profile_end, each dkv_decode_splitk call (the first
- * max_calls of them) records HIP events before its split launch, between the split and merge
- * launches and after the merge, on its stream. dkv_profile_end waits for the recorded events,
- * returns the summed split and merge milliseconds and the number of calls recorded, and
- * destroys the events. Not thread-safe.
+ * max_calls of them) records HIP events on its stream before and after its split launch and,
+ * when a separate merge kernel runs, after the merge. dkv_profile_end waits for the recorded
+ * events, returns the summed split and merge milliseconds (merge 0 when the split kernel
+ * merged itself) and the number of calls recorded, and destroys the events. Not thread-safe.
  */
 int dkv_profile_begin(int max_calls);
 int dkv_profile_end(double* split_ms, double* merge_ms, int* calls);
