@@ -8,6 +8,7 @@
 
 typedef __attribute__((ext_vector_type(8))) __bf16 dkv_bf16x8;
 typedef __attribute__((ext_vector_type(4))) __bf16 dkv_bf16x4;
+typedef __attribute__((ext_vector_type(2))) __bf16 dkv_bf16x2;
 typedef __attribute__((ext_vector_type(8))) _Float16 dkv_f16x8;
 typedef __attribute__((ext_vector_type(4))) _Float16 dkv_f16x4;
 typedef __attribute__((ext_vector_type(2))) _Float16 dkv_f16x2;

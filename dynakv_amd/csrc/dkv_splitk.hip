@@ -500,7 +500,10 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
   dkv_f32x4 acc[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = dkv_f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY;  // per head slot n (log2 units), identical across g
+  // running max per head slot n (log2 units), identical across g. It starts at a finite floor
+  // far below any score, so that excluded tokens (-inf) give exp2(-inf) = 0 without a select
+  // and a record without any included token carries l = 0 and acc = 0 under that floor.
+  float m_run = -1.0e30f;
   float l_run = 0.f;        // partial over this lane's 4 tokens per tile
 
   // ---- pipeline: one tile per iteration; the gathers of tile j+1 and the table of tile j+2
@@ -593,22 +596,26 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
 
     // scores of lane (head slot n, tokens 4g+u) -> log2 domain with the route's masking; the
     // lane reads the lengths of its four tokens from the tile's table
+    // scores of lane (head slot n, tokens 4g+u) with the route's masking: the fused route in
+    // log2 units, the two-stage route as the rounded scores (natural units; the factor log2(e)
+    // is applied to their maximum and inside the exponent's fma)
     float z[4];
     {
       const dkv_i32x4 lk4 = *(const dkv_i32x4*)&sTabRing[wave][j % TSLOT][0][4 * g];
-      const int nvalid = s_end - (tile0 + WAVES * j) * TILE;  // tokens of the tile in range
       const int lk[4] = {lk4.x, lk4.y, lk4.z, lk4.w};
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const bool inr = 4 * g + u < nvalid;
         const bool has = lk[u] > 0;
-        float v;
-        if constexpr (ROUTE == DKV_ROUTE_FUSED) {
-          v = has ? sc[u] * p.score_scale : -INFINITY;  // score_scale = sm_scale * log2(e)
-        } else {
-          v = dkv_round_to<DT>(has ? sc[u] * p.score_scale : p.masked_score) * LOG2E;
-        }
-        z[u] = inr ? v : -INFINITY;
+        if constexpr (ROUTE == DKV_ROUTE_FUSED)
+          z[u] = has ? sc[u] * p.score_scale : -INFINITY;  // score_scale = sm_scale * log2(e)
+        else
+          z[u] = dkv_round_to<DT>(has ? sc[u] * p.score_scale : p.masked_score);
+      }
+      const int nvalid = s_end - (tile0 + WAVES * j) * TILE;  // tokens of the tile in range
+      if (__builtin_expect(nvalid < TILE, 0)) {  // wave-uniform: the split's last tile
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          if (4 * g + u >= nvalid) z[u] = -INFINITY;
       }
     }
 
@@ -616,9 +623,10 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
     float tmax = fmaxf(fmaxf(z[0], z[1]), fmaxf(z[2], z[3]));
     tmax = lane_max32(tmax);
     tmax = lane_max16(tmax);
+    if constexpr (ROUTE != DKV_ROUTE_FUSED) tmax *= LOG2E;
     if (__ballot(tmax > m_run + RESCALE_THRESH)) {
       const float m_new = fmaxf(m_run, tmax);
-      const float alpha = (m_new == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // m_run is finite
       l_run *= alpha;
       m_run = m_new;
       float au[4];
@@ -632,8 +640,12 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
     float pu[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      // exp2 of a value <= RESCALE_THRESH; results below fp32's normal range may flush to zero
-      pu[u] = (z[u] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(z[u] - m_run);
+      // exp2 of a value <= RESCALE_THRESH (-inf for excluded tokens gives 0); results below
+      // fp32's normal range may flush to zero
+      if constexpr (ROUTE == DKV_ROUTE_FUSED)
+        pu[u] = __builtin_amdgcn_exp2f(z[u] - m_run);
+      else
+        pu[u] = __builtin_amdgcn_exp2f(__builtin_fmaf(z[u], LOG2E, -m_run));
       l_run += pu[u];
     }
 
@@ -643,13 +655,16 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
       pa_hi = dkv_u32x2{pack_f16x2(pu[0], pu[1]), pack_f16x2(pu[2], pu[3])};
       pa_lo = pa_hi;
     } else {
-      const __bf16 h0 = (__bf16)pu[0], h1 = (__bf16)pu[1], h2 = (__bf16)pu[2], h3 = (__bf16)pu[3];
-      const __bf16 e0 = (__bf16)(pu[0] - (float)h0), e1 = (__bf16)(pu[1] - (float)h1);
-      const __bf16 e2 = (__bf16)(pu[2] - (float)h2), e3 = (__bf16)(pu[3] - (float)h3);
-      pa_hi = dkv_u32x2{(uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16),
-                        (uint32_t)__builtin_bit_cast(uint16_t, h2) | ((uint32_t)__builtin_bit_cast(uint16_t, h3) << 16)};
-      pa_lo = dkv_u32x2{(uint32_t)__builtin_bit_cast(uint16_t, e0) | ((uint32_t)__builtin_bit_cast(uint16_t, e1) << 16),
-                        (uint32_t)__builtin_bit_cast(uint16_t, e2) | ((uint32_t)__builtin_bit_cast(uint16_t, e3) << 16)};
+      // P = hi + lo in bf16 (hi = bf16(p), lo = bf16(p - hi); p - hi is exact in fp32)
+      typedef __attribute__((ext_vector_type(2))) float f32x2;
+      const dkv_bf16x2 h01 = __builtin_convertvector(f32x2{pu[0], pu[1]}, dkv_bf16x2);
+      const dkv_bf16x2 h23 = __builtin_convertvector(f32x2{pu[2], pu[3]}, dkv_bf16x2);
+      const dkv_bf16x2 l01 = __builtin_convertvector(
+          f32x2{pu[0] - (float)h01[0], pu[1] - (float)h01[1]}, dkv_bf16x2);
+      const dkv_bf16x2 l23 = __builtin_convertvector(
+          f32x2{pu[2] - (float)h23[0], pu[3] - (float)h23[1]}, dkv_bf16x2);
+      pa_hi = dkv_u32x2{__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23)};
+      pa_lo = dkv_u32x2{__builtin_bit_cast(uint32_t, l01), __builtin_bit_cast(uint32_t, l23)};
     }
     // B operand (tokens 4g..4g+3 x rank 16*blk + n) by transposed reads: within each 16-lane
     // group, lane i receives element i%4 of the 8 bytes read by lane 4*u + i/4 of that group,
@@ -665,8 +680,14 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
             dkv_u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                            (__attribute__((address_space(3))) dkv_i16x4*)(
                                (__attribute__((address_space(3))) uint8_t*)src)));
-        acc[blk] = mfma_pv<DT>(pa_hi, xb, acc[blk]);
-        if constexpr (DT == DKV_BF16) acc[blk] = mfma_pv<DT>(pa_lo, xb, acc[blk]);
+        if constexpr (DT == DKV_BF16)
+          // hi and lo parts in one 16x16x32 product: k = 8*g + e pairs part e/4 of token
+          // 4*g + e%4 (A: this lane's hi then lo values) with that token's coefficients (B: the
+          // same four values twice)
+          acc[blk] = mfma_k<DT>(dkv_u32x4{pa_hi.x, pa_hi.y, pa_lo.x, pa_lo.y},
+                                dkv_u32x4{xb.x, xb.y, xb.x, xb.y}, acc[blk]);
+        else
+          acc[blk] = mfma_pv<DT>(pa_hi, xb, acc[blk]);
       }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
