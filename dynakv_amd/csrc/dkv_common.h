@@ -15,6 +15,7 @@ typedef __attribute__((ext_vector_type(2))) _Float16 dkv_f16x2;
 typedef __attribute__((ext_vector_type(4))) float dkv_f32x4;
 typedef __attribute__((ext_vector_type(4))) unsigned dkv_u32x4;
 typedef __attribute__((ext_vector_type(2))) unsigned dkv_u32x2;
+typedef __attribute__((ext_vector_type(2))) unsigned long long dkv_u64x2;
 typedef __attribute__((ext_vector_type(4))) int dkv_i32x4;
 typedef __attribute__((ext_vector_type(4))) short dkv_i16x4;
 

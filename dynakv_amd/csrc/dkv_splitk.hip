@@ -45,7 +45,7 @@ constexpr int GSLOT_BYTES = 8192;  // 4 K chunks + 4 V chunks of 64 lanes x 16 b
 constexpr int QSTAGE = 65536;      // ring offset of the query staging copy (prologue only)
 constexpr int MERGE_COUNTERS = 16384;  // leading workspace ints: per-unit arrival counters
 constexpr int VB_CHUNKS = DH * DH / 8 / NTHREADS;  // 16-byte V-basis pieces per thread
-constexpr int MASK_BIAS = 120;  // mask-table row of count 0 for the lowest chunk start
+constexpr int MASK_BIAS = 24;  // mask-table row of dk = 0 (dk: a lane's elements, -24 .. 128)
 constexpr int MASK_ROWS = MASK_BIAS + DH + 1;
 constexpr int ROPE_FIXED_ROWS = TILE + 1;  // rows 0..15: in-tile deltas; row 16: per-step
 constexpr float LOG2E = 1.4426950408889634f;
@@ -179,6 +179,16 @@ __device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t rsrc, uint32_t
                ::"s"(lds_base), "v"(byte_off), "s"(rsrc)
                : "memory", "m0");
 }
+// Chunk C of a lane's 8-rank pieces: the 16 bytes at byte offset off + 64*C, through the
+// instruction offset. The hardware adds the instruction offset to the LDS address too, so M0
+// is the chunk's LDS base minus 64*C. An out-of-range offset loads nothing and writes zeros.
+template <int C>
+__device__ __forceinline__ void lds_load16_chunk(__amdgpu_buffer_rsrc_t rsrc, uint32_t lds_chunk,
+                                                 uint32_t off) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen offset:%3 lds"
+               ::"s"(lds_chunk - 64u * C), "v"(off), "s"(rsrc), "i"(64 * C)
+               : "memory", "m0");
+}
 __device__ __forceinline__ void lds_load4(const void* gptr, uint32_t lds_base) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off"
                ::"s"(lds_base), "v"(gptr)
@@ -188,17 +198,30 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
 }
 
+// Float maxima without the NaN-quieting the compiler adds around fmaxf (the scores are never NaN
+// for finite inputs; -inf is an ordinary operand here).
+__device__ __forceinline__ float max2_f32(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+__device__ __forceinline__ float max3_f32(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
 // max(x, x of lane l ^ 32) and max(x, x of lane l ^ 16): a permlane swap of a value with
 // itself leaves each lane its own value in one result and its partner's in the other.
 __device__ __forceinline__ float lane_max32(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
                                                   false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return max2_f32(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 __device__ __forceinline__ float lane_max16(float x) {
   const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
                                                   false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return max2_f32(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
 // Wait until at most N vector-memory loads of this wave are outstanding (loads complete in
@@ -278,11 +301,11 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
   // TSLOT table slots: lens_k, offs_k, lens_v, offs_v x 16 tokens), the streamed half of the
   // K basis ([dim][rank] rows of dims 32..63 and 96..127), the mask table and the rotation
   // step. The full basis staging copy and the epilogue scratch alias the rings.
-  __shared__ __attribute__((aligned(16))) uint8_t sRing[WAVES * NSLOT * GSLOT_BYTES];
-  __shared__ __attribute__((aligned(16))) int sTabRing[WAVES][TSLOT][4][TILE];
-  __shared__ __attribute__((aligned(16))) uint16_t sBH[DH / 2 * BK_LD];
   __shared__ __attribute__((aligned(16))) uint32_t sMask[MASK_ROWS][4];
   __shared__ __attribute__((aligned(16))) float sStep[2][64];  // rotation by WAVES*TILE positions
+  __shared__ __attribute__((aligned(16))) int sTabRing[WAVES][TSLOT][4][TILE];
+  __shared__ __attribute__((aligned(16))) uint16_t sBH[DH / 2 * BK_LD];
+  __shared__ __attribute__((aligned(16))) uint8_t sRing[WAVES * NSLOT * GSLOT_BYTES];
   static_assert(DH * BK_LD * 2 <= QSTAGE && QSTAGE + WAVES * 64 * 64 <= WAVES * NSLOT * GSLOT_BYTES,
                 "basis and query staging fit the rings");
   uint16_t* sBK = reinterpret_cast<uint16_t*>(sRing);
@@ -335,9 +358,13 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
           sBK[d * BK_LD + j] = x;
       }
     }
-    // row j holds the keep-mask of the first clamp(j - MASK_BIAS, 0, 8) elements
-    for (int r = tid; r < MASK_ROWS * 4; r += NTHREADS)
-      sMask[r >> 2][r & 3] = prefix_mask_word(min(max((r >> 2) - MASK_BIAS, 0), 8), r & 3);
+    // row MASK_BIAS + dk: keep-mask of the lane's last piece when its token has dk elements from
+    // the lane's first piece on (that piece is chunk clamp((dk - 1) / 32, 0, 3))
+    for (int r = tid; r < MASK_ROWS * 4; r += NTHREADS) {
+      const int dk = (r >> 2) - MASK_BIAS;
+      const int ck = min(max((dk - 1) >> 5, 0), 3);
+      sMask[r >> 2][r & 3] = prefix_mask_word(min(max(dk - 32 * ck, 0), 8), r & 3);
+    }
     if (tid < 64) {
       sStep[0][tid] = p.rope[TILE * 128 + 2 * tid];
       sStep[1][tid] = p.rope[TILE * 128 + 2 * tid + 1];
@@ -444,40 +471,41 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
     tab_ss = tsel < 2 ? (int)p.tk_ss : (int)p.tv_ss;
   }
   auto load_tab = [&](int j) {  // one load per lane into table slot j % TSLOT
-    const int t = min((tile0 + WAVES * j) * TILE + n, s_end - 1);
-    lds_load4(tab_base + t * tab_ss, lds_addr(&sTabRing[wave][j % TSLOT][0][0]));
+    const uint32_t t = (uint32_t)min((tile0 + WAVES * j) * TILE + n, s_end - 1);
+    lds_load4(tab_base + __umul24(t, (uint32_t)tab_ss), lds_addr(&sTabRing[wave][j % TSLOT][0][0]));
   };
-  // token metadata of this lane's token in tile j (table slot must have arrived)
+  // token metadata of this lane's token in tile j (table slot must have arrived). A slot past
+  // the split's end holds the entries of the split's last token (the table loads clamp): its
+  // gathers read real data and its score is excluded in the softmax.
   struct Tok {
-    int rk, ko, rkc, rvc, vo;
-    bool valid;
+    int ko, rkc, rvc, vo;
   };
   auto tok_of = [&](int j) {
     Tok d;
     const int(*tb)[TILE] = sTabRing[wave][j % TSLOT];
-    d.valid = (tile0 + WAVES * j) * TILE + n < s_end;
-    const int lk = tb[0][n], ok = tb[1][n], lv = tb[2][n], ov = tb[3][n];
-    d.rk = d.valid ? lk : 0;
-    d.rkc = min(max(d.rk, 0), R);
-    d.rvc = min(max(d.valid ? lv : 0, 0), R);
-    d.ko = k_row0 + (d.valid ? ok : 0);
-    d.vo = v_row0 + (d.valid ? ov : 0);
+    d.rkc = min(max(tb[0][n], 0), R);
+    d.rvc = min(max(tb[2][n], 0), R);
+    d.ko = k_row0 + tb[1][n];
+    d.vo = v_row0 + tb[3][n];
     return d;
   };
   // gathers of tile j into gather slot j % NSLOT: lane l's 16 bytes of chunk c land at
   // slot + c*1024 + 16*l (K) and slot + 4096 + c*1024 + 16*l (V). A lane whose token has no
-  // element in its 8-rank piece reads the out-of-range offset instead (no memory traffic; the
-  // masks zero whatever its LDS bytes hold).
+  // element in its 8-rank piece of chunk c reads the out-of-range offset instead: no memory
+  // traffic, and zeros land in its LDS bytes.
   auto issue = [&](int j) {
     const Tok d = tok_of(j);
     const uint32_t slot = lds_addr(ring + (j % NSLOT) * GSLOT_BYTES);
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-      lds_load16(rk_src, slot + c * 1024, d.rkc > 8 * g + 32 * c ? (d.ko + 8 * g + 32 * c) * 2 : OOB);
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-      lds_load16(rv_src, slot + 4096 + c * 1024,
-                 d.rvc > 8 * g + 32 * c ? (d.vo + 8 * g + 32 * c) * 2 : OOB);
+    const int dk = d.rkc - 8 * g, dv = d.rvc - 8 * g;  // elements from the lane's first piece
+    const uint32_t kb = (uint32_t)(d.ko + 8 * g) * 2u, vb = (uint32_t)(d.vo + 8 * g) * 2u;
+    lds_load16_chunk<0>(rk_src, slot, dk > 0 ? kb : OOB);
+    lds_load16_chunk<1>(rk_src, slot + 1024, dk > 32 ? kb : OOB);
+    lds_load16_chunk<2>(rk_src, slot + 2048, dk > 64 ? kb : OOB);
+    lds_load16_chunk<3>(rk_src, slot + 3072, dk > 96 ? kb : OOB);
+    lds_load16_chunk<0>(rv_src, slot + 4096, dv > 0 ? vb : OOB);
+    lds_load16_chunk<1>(rv_src, slot + 5120, dv > 32 ? vb : OOB);
+    lds_load16_chunk<2>(rv_src, slot + 6144, dv > 64 ? vb : OOB);
+    lds_load16_chunk<3>(rv_src, slot + 7168, dv > 96 ? vb : OOB);
   };
   // A 16-byte window that crosses the end of a resource reads as zero in full; only the last
   // tokens of the last row can need one. Such a tile is gathered again with element loads
@@ -525,23 +553,24 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
     if (last_row) regather_if_needed(cur, slot);
     load_tab(j + 2);
     issue(j + 1);
-    // ---- masks (elements past each token's count belong to the next tokens): K into
-    //      registers, V back into the slot -----------------------------------------------------
-    dkv_u32x4 xk[4];
+    // ---- masks: elements past a token's count belong to the next tokens. Pieces wholly past
+    //      the count were loaded as zeros, so only the partial piece of each token needs one:
+    //      the lane masks its own partial K and V piece in place, then reads the K windows ----
     {
-      const char* mkb = (const char*)&sMask[0][0] + 16 * (cur.rkc - 8 * g + MASK_BIAS - 96);
-      const char* mvb = (const char*)&sMask[0][0] + 16 * (cur.rvc - 8 * g + MASK_BIAS - 96);
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const dkv_u32x4 mk = *(const dkv_u32x4*)(mkb + 16 * (96 - 32 * c));
-        const dkv_u32x4 kr = *(const dkv_u32x4*)(slot + c * 1024 + 16 * lane);
-        xk[c] = dkv_u32x4{kr.x & mk.x, kr.y & mk.y, kr.z & mk.z, kr.w & mk.w};
-        const dkv_u32x4 mv = *(const dkv_u32x4*)(mvb + 16 * (96 - 32 * c));
-        dkv_u32x4* vp = (dkv_u32x4*)(slot + 4096 + c * 1024 + 16 * lane);
-        const dkv_u32x4 vr = *vp;
-        *vp = dkv_u32x4{vr.x & mv.x, vr.y & mv.y, vr.z & mv.z, vr.w & mv.w};
-      }
+      const int dk = cur.rkc - 8 * g, dv = cur.rvc - 8 * g;
+      const int ck = min(max((dk - 1) >> 5, 0), 3);  // chunk of the lane's last K element
+      const int cv = min(max((dv - 1) >> 5, 0), 3);
+      dkv_u32x4* kp = (dkv_u32x4*)(slot + ck * 1024 + 16 * lane);
+      dkv_u32x4* vp = (dkv_u32x4*)(slot + 4096 + cv * 1024 + 16 * lane);
+      const dkv_u32x4 mk = *(const dkv_u32x4*)&sMask[dk + MASK_BIAS][0];
+      const dkv_u32x4 mv = *(const dkv_u32x4*)&sMask[dv + MASK_BIAS][0];
+      const dkv_u32x4 kr = *kp, vr = *vp;
+      *kp = dkv_u32x4{kr.x & mk.x, kr.y & mk.y, kr.z & mk.z, kr.w & mk.w};
+      *vp = dkv_u32x4{vr.x & mv.x, vr.y & mv.y, vr.z & mv.z, vr.w & mv.w};
     }
+    dkv_u32x4 xk[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) xk[c] = *(const dkv_u32x4*)(slot + c * 1024 + 16 * lane);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -620,7 +649,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
     }
 
     // ---- 4. online softmax (per head slot; its 16 tokens sit in lanes n, n+16, n+32, n+48) --
-    float tmax = fmaxf(fmaxf(z[0], z[1]), fmaxf(z[2], z[3]));
+    float tmax = max3_f32(max3_f32(z[0], z[1], z[2]), z[3], z[3]);
     tmax = lane_max32(tmax);
     tmax = lane_max16(tmax);
     if constexpr (ROUTE != DKV_ROUTE_FUSED) tmax *= LOG2E;
@@ -684,8 +713,11 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
           // hi and lo parts in one 16x16x32 product: k = 8*g + e pairs part e/4 of token
           // 4*g + e%4 (A: this lane's hi then lo values) with that token's coefficients (B: the
           // same four values twice)
-          acc[blk] = mfma_k<DT>(dkv_u32x4{pa_hi.x, pa_hi.y, pa_lo.x, pa_lo.y},
-                                dkv_u32x4{xb.x, xb.y, xb.x, xb.y}, acc[blk]);
+          acc[blk] = mfma_k<DT>(
+              dkv_u32x4{pa_hi.x, pa_hi.y, pa_lo.x, pa_lo.y},
+              __builtin_bit_cast(dkv_u32x4, dkv_u64x2{__builtin_bit_cast(uint64_t, xb),
+                                                      __builtin_bit_cast(uint64_t, xb)}),
+              acc[blk]);
         else
           acc[blk] = mfma_pv<DT>(pa_hi, xb, acc[blk]);
       }
@@ -1106,9 +1138,9 @@ extern "C" int dkv_decode_splitk(void* stream, int route, int dtype, const void*
   if (rope_tiles < (S + TILE - 1) / TILE) return DKV_E_ARG;
   if (split_len <= 0) split_len = dkv_splitk_choose_split(B, Hkv, S);
   if (split_len % 64 != 0) return DKV_E_ARG;
-  // token indices times table strides stay 32-bit inside the kernel
+  // token indices times table strides stay 32-bit inside the kernel, both factors 24-bit
   if ((long long)S * tk_ss >= (1LL << 31) || (long long)S * tv_ss >= (1LL << 31) || tk_ss < 0 ||
-      tv_ss < 0)
+      tv_ss < 0 || S >= (1 << 24) || tk_ss >= (1 << 24) || tv_ss >= (1 << 24))
     return DKV_E_UNSUPPORTED;
   const long long n_splits = ((long long)S + split_len - 1) / split_len;
   const long long units = (long long)B * Hkv;
