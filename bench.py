@@ -7,15 +7,17 @@ growing by one token per step, retained dims r ~ clipped Beta with mean 0.29 and
 plus a seeded 5% forced to 128. Synthetic data generated on the device; the packed cache and all
 per-step inputs are resident in HBM before the timed region.
 
-One step = decode append of K and V for all 128 rows + the router decision + decode attention
-(long route: the split-K kernel with two-stage semantics, then the merge kernel that projects
-through the V basis).
+One step = for each of 4 independent layer caches (a model's decode step runs all its layers),
+the decode append of K and V for all 128 rows + the router decision + decode attention (long
+route: the split-K kernel with two-stage semantics, which also merges the splits and projects
+through the V basis). Four layers (~190 MB of packed cache each) keep a layer's cache from
+staying in the 256 MB last-level cache between its calls, so the attention streams from HBM.
 
 Output: one JSON line. ``value`` is decode-attention GB/s: algorithmic bytes of the attention
 (packed K/V coefficients read once, int32 lengths, unique bases, q and output) divided by the
-GPU time of the attention launches, summed over the timed steps (HIP events on the stream the
-kernels run on). ``roofline`` is the split kernel alone; ``cpu_baseline`` times the masked-
-dimension CPU path on a bounded sample of the same inputs.
+GPU time of the attention launches, summed over the timed layer-steps (HIP events on the stream
+the kernels run on). ``roofline`` is the split kernel (one launch per call); ``cpu_baseline``
+times the masked-dimension CPU path on a bounded sample of the same inputs.
 """
 
 from __future__ import annotations
@@ -151,20 +153,23 @@ class SplitKRunner:
         return self.out
 
 
-def run_gpu(cfg, steps, warmup, dev):
+def run_gpu(cfg, steps, warmup, dev, layers):
+    """Time ``steps`` decode steps; each step runs append + router + attention for every one of
+    ``layers`` independent layer caches, as a model's decode step does. Several layers keep a
+    layer's cache from staying resident in the 256 MB last-level cache between its calls, so
+    the attention streams its coefficients from HBM."""
     from dynakv_amd import _lib
     from dynakv_amd.kernels.router import KernelPolicy
 
     total = steps + warmup
-    _log(f"building {cfg.name} workload (B={cfg.B}, S0={cfg.S0}, steps={total})")
-    W = build_workload(cfg, total, dev)
-    cache = W["cache"]
+    _log(f"building {cfg.name} workload (B={cfg.B}, S0={cfg.S0}, steps={total}, layers={layers})")
+    Ws = [build_workload(cfg, total, dev, seed=1234 + 7919 * l) for l in range(layers)]
     runner = SplitKRunner(cfg, dev, cfg.S0 + total + 16)
     policy = KernelPolicy()
     R = cfg.R
-    step_bytes = []
 
-    def one_step(i):
+    def one_layer_step(W, i):
+        cache = W["cache"]
         fk, fv, lk, lv, ok, ov = cache.update_sp(W["steps_k"][i], W["lk_steps"][i], W["steps_v"][i],
                                                  W["lv_steps"][i], R, 0, R)
         L = cache.get_seq_length_sp(0)
@@ -174,36 +179,40 @@ def run_gpu(cfg, steps, warmup, dev):
         return L
 
     for i in range(warmup):
-        one_step(i)
+        for W in Ws:
+            one_layer_step(W, i)
     torch.cuda.synchronize(dev)
     lib = _lib.load()
     _log("timed region")
     # library-side HIP events around the split and merge launches of each call (same stream)
-    _lib.check(lib.dkv_profile_begin(steps), "dkv_profile_begin")
+    _lib.check(lib.dkv_profile_begin(steps * layers), "dkv_profile_begin")
     lens = []
     t0 = time.perf_counter()
     for j in range(steps):
-        lens.append(one_step(warmup + j))
+        for l, W in enumerate(Ws):
+            lens.append((l, one_layer_step(W, warmup + j)))
     torch.cuda.synchronize(dev)
     wall = time.perf_counter() - t0
-    step_bytes = [attention_bytes(cfg, W["lk_h"], W["lv_h"], L) for L in lens]
-    split_bytes = [attention_bytes(cfg, W["lk_h"], W["lv_h"], L, split_only=True) for L in lens]
+    step_bytes = [attention_bytes(cfg, Ws[l]["lk_h"], Ws[l]["lv_h"], L) for l, L in lens]
     sm, mm, nc = ctypes.c_double(), ctypes.c_double(), ctypes.c_int()
     _lib.check(lib.dkv_profile_end(ctypes.byref(sm), ctypes.byref(mm), ctypes.byref(nc)),
                "dkv_profile_end")
-    assert nc.value == steps, (nc.value, steps)
+    assert nc.value == steps * layers, (nc.value, steps, layers)
     # attention GPU time: the library's events around the split launch (and the merge launch,
     # when one runs), recorded on the kernels' stream for every timed call
     attn_ms = sm.value + mm.value
     tot_bytes = float(sum(step_bytes))
-    res = dict(
-        wall_s=wall, attn_ms=attn_ms, split_ms=sm.value, merge_ms=mm.value,
-        split_bytes_per_step=float(sum(split_bytes)) / steps,
-        bytes_total=tot_bytes, bytes_per_step=tot_bytes / steps,
-        final_len=cache.get_seq_length_sp(0), syncs=cache.device_syncs,
-        q0=W["q"][0], cache=cache, workload=W,
+    calls = steps * layers
+    return dict(
+        wall_s=wall, attn_ms=attn_ms, split_ms=sm.value, merge_ms=mm.value, calls=calls,
+        merged_in_split=mm.value == 0.0,
+        bytes_total=tot_bytes, bytes_per_call=tot_bytes / calls,
+        split_bytes_per_call=float(sum(attention_bytes(cfg, Ws[l]["lk_h"], Ws[l]["lv_h"], L,
+                                                       split_only=True) for l, L in lens)) / calls,
+        final_len=Ws[0]["cache"].get_seq_length_sp(0),
+        syncs=sum(W["cache"].device_syncs for W in Ws),
+        cache=Ws[0]["cache"], workload=Ws[0],
     )
-    return res
 
 
 def cpu_baseline(cfg, W, cache, budget_s: float):
@@ -273,6 +282,8 @@ def main():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="config3", choices=["config3", "config2"])
+    ap.add_argument("--layers", type=int, default=4,
+                    help="independent layer caches per decode step (4 x ~190 MB at config 3)")
     ap.add_argument("--cpu-baseline-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
@@ -300,11 +311,15 @@ def main():
         torch.cuda.synchronize(dev)
         _log(f"copy probe: {args.copy_probe_mib} MiB read + {args.copy_probe_mib} MiB written")
         del src, dst
-    r = run_gpu(cfg, args.steps, args.warmup, dev)
+    r = run_gpu(cfg, args.steps, args.warmup, dev, args.layers)
     attn_s = r["attn_ms"] / 1e3
     gbs = r["bytes_total"] / attn_s / 1e9
-    split_avg_s = r["split_ms"] / 1e3 / args.steps
-    achieved = r["split_bytes_per_step"] / split_avg_s / 1e9
+    calls = r["calls"]
+    split_avg_s = r["split_ms"] / 1e3 / calls
+    # the split kernel merges its own splits (one launch per call) unless a merge kernel ran
+    launch_bytes = r["bytes_per_call"] if r["merged_in_split"] else r["split_bytes_per_call"]
+    achieved = launch_bytes / split_avg_s / 1e9
+    layer_step_s = attn_s / calls
     traffic = load_traffic(cfg.name)
     line = {
         "metric": "decode-attn GB/s (% HBM peak) + decode tokens/s, Llama-3-8B shape, 1 GPU",
@@ -326,8 +341,10 @@ def main():
             "mean_retention": cfg.mean, "route": "long_two_stage", "layout": "per-head (G=8, R=128)",
         },
         "pct_hbm_peak": round(100.0 * gbs / HBM_PEAK_GBS, 2),
-        "decode_attn_us_per_step": round(r["attn_ms"] * 1e3 / args.steps, 3),
-        "decode_tokens_per_s_attention_only": round(cfg.B * args.steps / attn_s, 1),
+        "layers_per_step": args.layers,
+        "decode_attn_us_per_layer_step": round(layer_step_s * 1e6, 3),
+        # a Llama-3-8B decode step runs 32 such layers: attention-only tokens/s of that stack
+        "decode_tokens_per_s_attention_only_32_layers": round(cfg.B / (32 * layer_step_s), 1),
         "decode_tokens_per_s_step_wall": round(cfg.B * args.steps / r["wall_s"], 1),
         "host_syncs_total": r["syncs"],
         "roofline": {
@@ -338,9 +355,9 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic["bytes_per_launch"] if traffic else None,
-            "split_kernel_us": round(r["split_ms"] * 1e3 / args.steps, 3),
-            "merge_kernel_us": round(r["merge_ms"] * 1e3 / args.steps, 3),
-            "algorithmic_bytes_per_launch": round(r["split_bytes_per_step"]),
+            "split_kernel_us": round(r["split_ms"] * 1e3 / calls, 3),
+            "merge_kernel_us": round(r["merge_ms"] * 1e3 / calls, 3),
+            "algorithmic_bytes_per_launch": round(launch_bytes),
             "traffic_source": traffic["source"] if traffic else None,
         },
     }

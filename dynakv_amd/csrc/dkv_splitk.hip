@@ -623,8 +623,6 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
       }
     }
 
-    // scores of lane (head slot n, tokens 4g+u) -> log2 domain with the route's masking; the
-    // lane reads the lengths of its four tokens from the tile's table
     // scores of lane (head slot n, tokens 4g+u) with the route's masking: the fused route in
     // log2 units, the two-stage route as the rounded scores (natural units; the factor log2(e)
     // is applied to their maximum and inside the exponent's fma)
