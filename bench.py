@@ -260,6 +260,57 @@ def cpu_baseline(cfg, W, cache, budget_s: float):
     }
 
 
+def bench_cutoff(cfg, dev, iters=50):
+    """Cutoff head (reference kv_process_fused, compressed_attention.py:84-119) for K and V at
+    this workload's decode shape: per-head (G groups of D = R dims) and the reference's joint
+    head (one 1024-d group). GPU time per call from HIP events on the current stream, against
+    the reference formula evaluated by torch's own GPU kernels (addmm, softmax, cumsum, flip,
+    compare, sum, multiply) on the same inputs."""
+    from dynakv_amd.kernels.cutoff import CutoffHead
+
+    res = {}
+    g = torch.Generator(device="cpu").manual_seed(99)
+    for mode, G, D in (("per_head", cfg.G, cfg.R), ("joint", 1, cfg.G * cfg.Dh)):
+        M = cfg.B
+        W = [(torch.randn(G, D, D, generator=g) * 3 / D ** 0.5).to(dev, cfg.dtype) for _ in range(2)]
+        b = [torch.randn(G, D, generator=g).to(dev, cfg.dtype) for _ in range(2)]
+        head = CutoffHead(W[0] if G > 1 else W[0][0], b[0], W[1] if G > 1 else W[1][0], b[1],
+                          groups=G)
+        x = [torch.randn(M, 1, G * D, generator=g).to(dev, cfg.dtype) for _ in range(2)]
+
+        def torch_ref():
+            outs = []
+            for t in range(2):
+                xf = x[t].view(M, G, D).transpose(0, 1).contiguous()  # (G, M, D)
+                lg = torch.baddbmm(b[t].unsqueeze(1), xf, W[t])
+                mask = torch.softmax(lg, dim=-1).cumsum(dim=-1).flip(dims=[-1]) >= 0.1
+                outs.append((xf * mask, mask.sum(dim=-1, dtype=torch.int32)))
+            return outs
+
+        for fn in (lambda: head.kv_process_fused(x[0], x[1]), torch_ref):
+            for _ in range(5):
+                fn()
+        torch.cuda.synchronize(dev)
+        times = {}
+        for name, fn in (("dynakv", lambda: head.kv_process_fused(x[0], x[1])), ("torch", torch_ref)):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(iters):
+                fn()
+            e1.record()
+            torch.cuda.synchronize(dev)
+            times[name] = e0.elapsed_time(e1) * 1e3 / iters
+        nbytes = 2 * (G * D * D * 2 + G * D * 2 + 2 * M * G * D * 2 + M * G * 4)
+        res[mode] = {
+            "shape": f"M={M} tokens, G={G} x D={D}, K and V",
+            "us_per_call": round(times["dynakv"], 2),
+            "torch_eager_us_per_call": round(times["torch"], 2),
+            "algorithmic_bytes": nbytes,
+            "gbs": round(nbytes / (times["dynakv"] * 1e-6) / 1e9, 1),
+        }
+    return res
+
+
 def load_traffic(workload):
     """HBM bytes per split-kernel launch measured by rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs
     of this script (scaled by a plain copy of known size), as committed under profiles/; used
@@ -286,6 +337,7 @@ def main():
                     help="independent layer caches per decode step (4 x ~190 MB at config 3)")
     ap.add_argument("--cpu-baseline-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-cutoff", action="store_true", help="skip the cutoff-head timing")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="run one device copy of this many MiB first (counter calibration)")
     args = ap.parse_args()
@@ -361,6 +413,9 @@ def main():
             "traffic_source": traffic["source"] if traffic else None,
         },
     }
+    if not args.no_cutoff:
+        _log("cutoff head")
+        line["cutoff_head"] = bench_cutoff(cfg, dev)
     if not args.no_cpu_baseline:
         _log("cpu baseline")
         line["cpu_baseline"] = cpu_baseline(cfg, r["workload"], r["cache"], args.cpu_baseline_seconds)

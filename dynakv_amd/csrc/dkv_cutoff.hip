@@ -1,0 +1,265 @@
+// Cutoff head: the per-token retained-dimension count r and the masked coefficients that feed
+// the cache append, for K and V in one call.
+//
+// Reference behaviour: src/dynakv/kernels/compressed_attention.py:84-119 (kv_process_fused):
+//   logits = b + x @ W                      (addmm in the compute dtype, :92-93)
+//   mask   = flip(cumsum(softmax(logits)))  (:99)
+//   hard   = mask >= 0.1                    (:100; 0.1 compared in the compute dtype)
+//   hard[..., low_rank:] = 0                (:106-107)
+//   len    = sum(hard) (int32), out = x * hard (:113-117)
+// Here every group g of a row (G groups of D dims; G = 1 is the reference's joint 1024-d head,
+// G = 8 with D = 128 its per-head form) has its own W_g and b_g.
+//
+// Because cumsum of the non-negative softmax is non-decreasing, flip(cumsum) >= thr is a prefix
+// mask: its length is the number of positions m whose prefix sum c_m reaches thr, and
+// out = x on the first len dims (min(len, low_rank)), x * 0 after them.
+//
+// Two kernels on the caller's stream:
+//   cutoff_logits_kernel  16 rows x 64 logits per workgroup (4 waves, 16x16x32 MFMA over D),
+//                         bias added in fp32, rounded to the compute dtype (addmm's output),
+//                         written to the caller's workspace;
+//   cutoff_rows_kernel    one wave per (row, group, K|V): softmax in fp32 of the rounded
+//                         logits (probabilities rounded to the compute dtype, as torch.softmax
+//                         returns them), prefix sums accumulated in fp32 and rounded to the
+//                         compute dtype, the count against the threshold rounded to the
+//                         compute dtype, the masked copy and the int32 length.
+// W is taken transposed, Wt[g][n][k] = W_g[k][n] (the input dimension contiguous), so both MFMA
+// operands are 16-byte row loads; the Python layer prepares that copy once per weight.
+#include "dkv_common.h"
+
+namespace {
+
+constexpr int CT_ROWS = 16;   // rows per logits workgroup
+constexpr int CT_COLS = 64;   // logits per workgroup (16 per wave)
+
+struct CutoffMat {
+  const uint16_t* x;   // (M, G*D) rows, stride x_ld
+  const uint16_t* wt;  // (G, D, D): wt[g][n][k]
+  const uint16_t* b;   // (G, D)
+  uint16_t* out;       // (M, G*D) rows, stride out_ld
+  int* lens;           // (M, G) rows, stride len_ld
+  uint16_t* logits;    // workspace (M, G, D)
+};
+
+struct CutoffParams {
+  CutoffMat mat[2];
+  long long x_ld, out_ld, len_ld;
+  int M, G, D, low_rank;
+  float threshold;     // already rounded to the compute dtype
+};
+
+template <int DT>
+__device__ __forceinline__ dkv_f32x4 mfma_16x16x32(const dkv_u32x4& a, const dkv_u32x4& b,
+                                                   dkv_f32x4 c) {
+  if constexpr (DT == DKV_BF16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(dkv_bf16x8, a),
+                                                   __builtin_bit_cast(dkv_bf16x8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(dkv_f16x8, a),
+                                                  __builtin_bit_cast(dkv_f16x8, b), c, 0, 0, 0);
+}
+
+template <int DT>
+__device__ __forceinline__ float elt_f32(uint16_t v) {
+  if constexpr (DT == DKV_BF16)
+    return dkv_bf16_bits_to_f32(v);
+  else
+    return dkv_f16_bits_to_f32(v);
+}
+template <int DT>
+__device__ __forceinline__ uint16_t f32_elt(float v) {
+  if constexpr (DT == DKV_BF16)
+    return (uint16_t)dkv_f32_to_bf16_bits(v);
+  else
+    return (uint16_t)dkv_f32_to_f16_bits(v);
+}
+
+// grid: (D / 64, ceil(M / 16), 2 * G); wave w computes logits n0 + 16w .. +16 of 16 rows.
+// MFMA operands: A = x rows (lane: row i = lane % 16, inputs 8*(lane/16) .. +8 of the k-step),
+// B = Wt rows (lane: output n = lane % 16, the same inputs); the result lane holds rows
+// 4*(lane/16) + u of output column lane % 16.
+template <int DT>
+__global__ __launch_bounds__(256) void cutoff_logits_kernel(CutoffParams p) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int i = lane & 15, kg = lane >> 4;
+  const int mat = blockIdx.z & 1, g = blockIdx.z >> 1;
+  const CutoffMat& cm = p.mat[mat];
+  const int D = p.D;
+  const int row0 = blockIdx.y * CT_ROWS;
+  const int n0 = blockIdx.x * CT_COLS + wave * 16;
+  const int xrow = min(row0 + i, p.M - 1);  // rows past M compute a copy of the last row
+  const uint16_t* xa = cm.x + (long long)xrow * p.x_ld + (long long)g * D + 8 * kg;
+  const uint16_t* wb = cm.wt + ((long long)g * D + n0 + i) * D + 8 * kg;
+  dkv_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  int k = 0;
+  for (; k + 128 <= D; k += 128) {
+    dkv_u32x4 a[4], b[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      a[s] = *(const dkv_u32x4*)(xa + k + 32 * s);
+      b[s] = *(const dkv_u32x4*)(wb + k + 32 * s);
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) acc = mfma_16x16x32<DT>(a[s], b[s], acc);
+  }
+  for (; k < D; k += 32)
+    acc = mfma_16x16x32<DT>(*(const dkv_u32x4*)(xa + k), *(const dkv_u32x4*)(wb + k), acc);
+  const float bias = elt_f32<DT>(cm.b[(long long)g * D + n0 + i]);
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int m = row0 + 4 * kg + u;
+    if (m < p.M)
+      cm.logits[((long long)m * p.G + g) * D + n0 + i] = f32_elt<DT>(acc[u] + bias);
+  }
+}
+
+// One wave per (row m, group g, K|V). Lane l owns the E = D / 64 consecutive positions
+// l*E .. l*E + E - 1 of the row.
+template <int DT, int E>
+__global__ __launch_bounds__(256) void cutoff_rows_kernel(CutoffParams p) {
+  const int lane = threadIdx.x & 63;
+  const long long task = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const long long n_rows = (long long)p.M * p.G;
+  if (task >= 2 * n_rows) return;
+  const int mat = (int)(task / n_rows);
+  const long long rg = task % n_rows;
+  const int m = (int)(rg / p.G), g = (int)(rg % p.G);
+  const CutoffMat& cm = p.mat[mat];
+  const int D = p.D;
+  const uint16_t* lg = cm.logits + rg * D + lane * E;
+
+  float x[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) x[e] = elt_f32<DT>(lg[e]);
+  float mx = x[0];
+#pragma unroll
+  for (int e = 1; e < E; ++e) mx = fmaxf(mx, x[e]);
+  mx = dkv_wave_max(mx);
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    x[e] = expf(x[e] - mx);
+    s += x[e];
+  }
+  s = dkv_wave_sum(s);
+  // probabilities in the compute dtype, then their prefix sums accumulated in fp32
+  float run = 0.f;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    run += dkv_round_to<DT>(x[e] / s);
+    x[e] = run;  // inclusive prefix within the lane
+  }
+  float inc = run;  // inclusive scan of the lane totals across the wave
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const float o = __shfl_up(inc, d, 64);
+    if (lane >= d) inc += o;
+  }
+  const float excl = inc - run;
+  int cnt = 0;
+#pragma unroll
+  for (int e = 0; e < E; ++e) cnt += dkv_round_to<DT>(excl + x[e]) >= p.threshold ? 1 : 0;
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) cnt += __shfl_xor(cnt, d, 64);
+  const int len = min(cnt, max(p.low_rank, 0));
+
+  const uint16_t* xs = cm.x + (long long)m * p.x_ld + (long long)g * D + lane * E;
+  uint16_t* xo = cm.out + (long long)m * p.out_ld + (long long)g * D + lane * E;
+  // x * 1 or x * 0 in the compute dtype, written out bitwise: x * 0 is a zero with x's sign,
+  // or NaN for an infinite or NaN x (a multiply would do the same, but the compiler may turn
+  // it into an fma with a +0 addend, which loses the sign of -0)
+  constexpr uint16_t EXP = DT == DKV_BF16 ? 0x7f80 : 0x7c00;
+  constexpr uint16_t QNAN = DT == DKV_BF16 ? 0x7fc0 : 0x7e00;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const uint16_t xb = xs[e];
+    const uint16_t zb = (xb & EXP) == EXP ? QNAN : (uint16_t)(xb & 0x8000);
+    xo[e] = lane * E + e < len ? xb : zb;
+  }
+  if (lane == 0) cm.lens[(long long)m * p.len_ld + g] = len;
+}
+
+template <int DT, int E>
+void launch_rows(const CutoffParams& p, hipStream_t st) {
+  const long long tasks = 2LL * p.M * p.G;
+  hipLaunchKernelGGL((cutoff_rows_kernel<DT, E>), dim3((unsigned)((tasks + 3) / 4)), dim3(256), 0,
+                     st, p);
+}
+
+}  // namespace
+
+extern "C" long long dkv_cutoff_workspace_bytes(int M, int G, int D) {
+  if (M < 0 || G <= 0 || D <= 0) return -1;
+  return 2LL * M * G * D * 2;
+}
+
+extern "C" int dkv_cutoff_kv(void* stream, int dtype, const void* xk, const void* xv,
+                             long long x_ld, const void* wt_k, const void* wt_v, const void* b_k,
+                             const void* b_v, float threshold, int low_rank, void* out_k,
+                             void* out_v, long long out_ld, int* len_k, int* len_v,
+                             long long len_ld, void* workspace, long long workspace_bytes, int M,
+                             int G, int D) {
+  if (dtype != DKV_F16 && dtype != DKV_BF16) return DKV_E_UNSUPPORTED;
+  if (M < 0 || G <= 0 || D <= 0) return DKV_E_ARG;
+  if (M == 0) return DKV_OK;
+  if (!xk || !xv || !wt_k || !wt_v || !b_k || !b_v || !out_k || !out_v || !len_k || !len_v ||
+      !workspace)
+    return DKV_E_ARG;
+  if (D % 64 != 0 || D > 1024) return DKV_E_UNSUPPORTED;
+  if (x_ld < (long long)G * D || out_ld < (long long)G * D || len_ld < G) return DKV_E_ARG;
+  if (x_ld % 8 != 0 || ((uintptr_t)xk | (uintptr_t)xv | (uintptr_t)wt_k | (uintptr_t)wt_v) % 16)
+    return DKV_E_UNSUPPORTED;  // 16-byte operand loads
+  if (workspace_bytes < dkv_cutoff_workspace_bytes(M, G, D)) return DKV_E_WORKSPACE;
+  if ((long long)M * G * D >= (1LL << 31) / 2) return DKV_E_UNSUPPORTED;
+  CutoffParams p;
+  const void* xs[2] = {xk, xv};
+  const void* ws[2] = {wt_k, wt_v};
+  const void* bs[2] = {b_k, b_v};
+  void* os[2] = {out_k, out_v};
+  int* ls[2] = {len_k, len_v};
+  for (int t = 0; t < 2; ++t) {
+    p.mat[t].x = (const uint16_t*)xs[t];
+    p.mat[t].wt = (const uint16_t*)ws[t];
+    p.mat[t].b = (const uint16_t*)bs[t];
+    p.mat[t].out = (uint16_t*)os[t];
+    p.mat[t].lens = ls[t];
+    p.mat[t].logits = (uint16_t*)workspace + (long long)t * M * G * D;
+  }
+  p.x_ld = x_ld;
+  p.out_ld = out_ld;
+  p.len_ld = len_ld;
+  p.M = M;
+  p.G = G;
+  p.D = D;
+  p.low_rank = low_rank < 0 ? D : min(low_rank, D);
+  // the reference compares against 0.1 in the compute dtype
+  p.threshold = dtype == DKV_BF16 ? (float)(__bf16)threshold : (float)(_Float16)threshold;
+  const int E = D / 64;
+  if (E != 1 && E != 2 && E != 4 && E != 8 && E != 16) return DKV_E_UNSUPPORTED;
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 lgrid(D / CT_COLS, (M + CT_ROWS - 1) / CT_ROWS, 2 * G);
+  if (dtype == DKV_BF16)
+    hipLaunchKernelGGL(cutoff_logits_kernel<DKV_BF16>, lgrid, dim3(256), 0, st, p);
+  else
+    hipLaunchKernelGGL(cutoff_logits_kernel<DKV_F16>, lgrid, dim3(256), 0, st, p);
+  DKV_HIP_CHECK_LAUNCH();
+#define DKV_ROWS_CASE(e)                                        \
+  case e:                                                       \
+    if (dtype == DKV_BF16)                                      \
+      launch_rows<DKV_BF16, e>(p, st);                          \
+    else                                                        \
+      launch_rows<DKV_F16, e>(p, st);                           \
+    break;
+  switch (E) {
+    DKV_ROWS_CASE(1)
+    DKV_ROWS_CASE(2)
+    DKV_ROWS_CASE(4)
+    DKV_ROWS_CASE(8)
+    DKV_ROWS_CASE(16)
+    default:
+      return DKV_E_UNSUPPORTED;
+  }
+#undef DKV_ROWS_CASE
+  DKV_HIP_CHECK_LAUNCH();
+  return DKV_OK;
+}

@@ -222,6 +222,27 @@ int dkv_profile_end(double* split_ms, double* merge_ms, int* calls);
  */
 int dkv_selftest_layouts(void* stream, int* mismatches);
 
+/*
+ * Cutoff head for K and V (reference KVProcessor.kv_process_fused,
+ * src/dynakv/kernels/compressed_attention.py:84-119, replayed per decode step at :321-327).
+ * Per row m (M = B*S tokens) and group g (G groups of D dims; G = 1 is the reference's joint
+ * head): logits = round(b_g + x_g @ W_g), p = round(softmax(logits)), c_m = round(prefix sums
+ * of p accumulated in fp32), all rounded to the compute dtype; len = min(#{m : c_m >= thr},
+ * low_rank) with thr = threshold rounded to the compute dtype (the reference's
+ * flip(cumsum) >= 0.1 prefix mask, mask[low_rank:] = 0); out = x * (j < len).
+ *   x*, out*: (M, G*D) rows with row strides x_ld / out_ld (x_ld a multiple of 8 elements,
+ *             x and wt 16-byte aligned); len*: (M, G) int32, row stride len_ld.
+ *   wt*: (G, D, D) transposed weights, wt[g][n][k] = W_g[k][n]; b*: (G, D).
+ *   low_rank < 0 means D. dtype: DKV_F16 or DKV_BF16; D a power of two in 64 .. 1024.
+ *   workspace: >= dkv_cutoff_workspace_bytes(M, G, D) bytes (the rounded logits).
+ */
+long long dkv_cutoff_workspace_bytes(int M, int G, int D);
+int dkv_cutoff_kv(void* stream, int dtype, const void* xk, const void* xv, long long x_ld,
+                  const void* wt_k, const void* wt_v, const void* b_k, const void* b_v,
+                  float threshold, int low_rank, void* out_k, void* out_v, long long out_ld,
+                  int* len_k, int* len_v, long long len_ld, void* workspace,
+                  long long workspace_bytes, int M, int G, int D);
+
 #ifdef __cplusplus
 }
 #endif
