@@ -51,6 +51,10 @@ _SIGNATURES = {
     "dkv_profile_end": (_i, [_vp, _vp, _vp]),
     "dkv_selftest_layouts": (_i, [_vp, _vp]),
     "dkv_cutoff_workspace_bytes": (_ll, [_i, _i, _i]),
+    "dkv_rope_dense": (_i, [_vp, _i, _vp, _ll, _ll, _i, _i, _i, _f]),
+    "dkv_prefill_attention": (_i, [_vp, _i, _vp, _ll, _ll, _ll, _vp, _ll, _ll, _ll, _ll,
+                                   _vp, _ll, _ll, _ll, _ll, _vp, _i, _ll, _ll, _ll,
+                                   _i, _i, _i, _i, _i, _i, _i, _f]),
     "dkv_cutoff_kv": (_i, [_vp, _i, _vp, _vp, _ll, _vp, _vp, _vp, _vp, _f, _i, _vp, _vp, _ll,
                            _vp, _vp, _ll, _vp, _ll, _i, _i, _i]),
 }

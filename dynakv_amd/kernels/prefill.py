@@ -1,0 +1,105 @@
+"""Prefill attention over the compressed cache (host side of ``dkv_prefill.hip``).
+
+Reference: the prefill branch of ``CustomAttention.forward``
+(src/dynakv/kernels/compressed_attention.py:359-386) with ``kv_down_up`` (:130-191):
+``update_sp`` packs the prompt, ``get_origin_states`` re-expands the cache, ``k_up`` / ``v_up``
+project it back to head space, RoPE at positions ``0..S-1`` rotates K, and causal attention
+runs over the result.
+
+``reconstruct_kv`` does the re-expansion (``dkv_decompress``), the projection through the
+per-head bases (one batched library GEMM per matrix) and the RoPE of K (``dkv_rope_dense``);
+``prefill_attention`` is the causal GQA attention kernel; ``compressed_prefill_attention``
+chains them for the per-head layout (cache rows ``b*G + g``).
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from .. import _lib
+
+
+def _extent(t: torch.Tensor) -> int:
+    """Elements addressable from ``t.data_ptr()`` by its strides."""
+    return 1 + sum((s - 1) * st for s, st in zip(t.shape, t.stride()) if s > 0)
+
+
+def rope_dense_(x: torch.Tensor, *, theta: float, pos0: int = 0) -> torch.Tensor:
+    """In place: rotate-half RoPE over the last dim (128) of ``x`` (..., S, 128) at positions
+    ``pos0 + s``."""
+    if x.shape[-1] != 128 or x.stride(-1) != 1:
+        raise ValueError("rope_dense_ needs (..., S, 128) with unit last stride")
+    if x.dim() < 2:
+        raise ValueError("rope_dense_ needs a token dimension")
+    S = x.shape[-2]
+    lead = x.shape[:-2]
+    rows = int(math.prod(lead)) if lead else 1
+    x2 = x.reshape(rows, S, 128)
+    if x2.data_ptr() != x.data_ptr():
+        raise ValueError("rope_dense_ needs a tensor whose leading dims flatten without a copy")
+    lib = _lib.load()
+    _lib.check(lib.dkv_rope_dense(_lib.stream_of(x), _lib.dtype_code(x.dtype), x2.data_ptr(),
+                                  x2.stride(0), x2.stride(1), rows, S, int(pos0),
+                                  math.log(theta)), "dkv_rope_dense")
+    return x
+
+
+def prefill_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, causal: bool = True,
+                      scale: float | None = None, out: torch.Tensor | None = None,
+                      out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """Causal GQA attention: ``q`` (B, Hq, Sq, 128), ``k``/``v`` (B, Hkv, Sk, 128) ->
+    (B, Hq, Sq, 128) in q's dtype (or ``out_dtype=torch.float32``: the result before that
+    rounding). With ``causal`` the queries are the last ``Sq`` positions."""
+    B, Hq, Sq, Dh = q.shape
+    _, Hkv, Sk, _ = k.shape
+    if v.shape != k.shape or k.shape[0] != B or k.shape[3] != Dh:
+        raise ValueError("k and v must be (B, Hkv, Sk, Dh) matching q")
+    if not (q.dtype == k.dtype == v.dtype) or q.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("prefill_attention runs in float16 or bfloat16")
+    for t in (q, k, v):
+        if t.stride(-1) != 1:
+            raise ValueError("unit last stride required")
+    odt = out_dtype if out_dtype is not None else (out.dtype if out is not None else q.dtype)
+    if odt not in (q.dtype, torch.float32):
+        raise ValueError("out_dtype must be the query dtype or float32")
+    if out is None:
+        out = torch.empty((B, Hq, Sq, Dh), dtype=odt, device=q.device)
+    elif out.dtype != odt or out.stride(-1) != 1:
+        raise ValueError("out must have unit last stride and the requested dtype")
+    scale = 1.0 / math.sqrt(Dh) if scale is None else float(scale)
+    lib = _lib.load()
+    rc = lib.dkv_prefill_attention(
+        _lib.stream_of(q), _lib.dtype_code(q.dtype),
+        q.data_ptr(), q.stride(0), q.stride(1), q.stride(2),
+        k.data_ptr(), k.stride(0), k.stride(1), k.stride(2), _extent(k),
+        v.data_ptr(), v.stride(0), v.stride(1), v.stride(2), _extent(v),
+        out.data_ptr(), _lib.dtype_code(out.dtype), out.stride(0), out.stride(1), out.stride(2),
+        B, Hq, Hkv, Sq, Sk, Dh, 1 if causal else 0, scale)
+    _lib.check(rc, "dkv_prefill_attention")
+    return out
+
+
+def reconstruct_kv(cache, layer_idx: int, k_basis: torch.Tensor, v_basis: torch.Tensor, *,
+                   batch: int, theta: float):
+    """Dense head-space K (RoPE'd at positions 0..S-1) and V ``(B, G, S, Dh)`` of a per-head
+    cache (rows ``b*G + g``, bases ``(G, R, Dh)``)."""
+    G, R, Dh = k_basis.shape
+    dk, dv = cache.get_origin_states(R, layer_idx)  # (B*G, S, R), zero past each length
+    rows, S, _ = dk.shape
+    if rows != batch * G:
+        raise ValueError(f"cache has {rows} rows, expected batch * G = {batch * G}")
+    k = torch.matmul(dk.view(batch, G, S, R), k_basis.contiguous())
+    v = torch.matmul(dv.view(batch, G, S, R), v_basis.contiguous())
+    rope_dense_(k, theta=theta, pos0=0)
+    return k, v
+
+
+def compressed_prefill_attention(q: torch.Tensor, cache, layer_idx: int, k_basis: torch.Tensor,
+                                 v_basis: torch.Tensor, *, theta: float,
+                                 out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """The reference's prefill attention for the per-head layout: ``q`` (B, Hq, Sq, 128)
+    already RoPE'd at its positions (the last ``Sq`` of the cache)."""
+    k, v = reconstruct_kv(cache, layer_idx, k_basis, v_basis, batch=q.shape[0], theta=theta)
+    return prefill_attention(q, k, v, causal=True, out_dtype=out_dtype)

@@ -243,6 +243,34 @@ int dkv_cutoff_kv(void* stream, int dtype, const void* xk, const void* xv, long 
                   int* len_k, int* len_v, long long len_ld, void* workspace,
                   long long workspace_bytes, int M, int G, int D);
 
+/*
+ * Prefill attention over the reconstructed cache (reference prefill branch,
+ * src/dynakv/kernels/compressed_attention.py:359-386: get_origin_states, the k_up / v_up
+ * projection, RoPE of K at positions 0..S-1 via calc_cos_sin :193-200, causal attention).
+ *
+ * dkv_rope_dense: in-place rotate-half RoPE of dense rows x[r][s][0..127] (row stride row_ld,
+ * token stride tok_ld, unit dim stride) at positions pos0 + s; angle float(pos) * inv_freq_i
+ * in fp32 (inv_freq_i = exp(-(2i/128) ln theta)), rotation in fp32, result rounded to dtype.
+ * Replaces the reference's apply_rotary_pos_emb_ on the projected K (:375-378).
+ *
+ * dkv_prefill_attention: out[b,h,i] = softmax_j(scale * q[b,h,i] . k[b,h/(Hq/Hkv),j]) v[...]
+ * over keys j <= (Sk - Sq) + i when causal (queries are the last Sq positions), else all Sk.
+ * q (B,Hq,Sq,128), k/v (B,Hkv,Sk,128), out (B,Hq,Sq,128): strides in elements per batch, head
+ * and token, unit dim stride, 16-byte aligned rows; k_elems / v_elems: elements addressable
+ * from k / v (bounds of the buffer loads). fp32 softmax, probabilities as a hi + lo pair in
+ * the compute dtype for the P.V product. dtype: DKV_F16 or DKV_BF16; out_dtype: dtype or
+ * DKV_F32 (the normalised result before rounding). Replaces the eager /
+ * SDPA attention call of the prefill branch (:373-383).
+ */
+int dkv_rope_dense(void* stream, int dtype, void* x, long long row_ld, long long tok_ld,
+                   int rows, int S, int pos0, float log_theta);
+int dkv_prefill_attention(void* stream, int dtype, const void* q, long long q_sb, long long q_sh,
+                          long long q_ss, const void* k, long long k_sb, long long k_sh,
+                          long long k_ss, long long k_elems, const void* v, long long v_sb,
+                          long long v_sh, long long v_ss, long long v_elems, void* out,
+                          int out_dtype, long long o_sb, long long o_sh, long long o_ss, int B,
+                          int Hq, int Hkv, int Sq, int Sk, int Dh, int causal, float scale);
+
 #ifdef __cplusplus
 }
 #endif
