@@ -311,6 +311,46 @@ def bench_cutoff(cfg, dev, iters=50):
     return res
 
 
+def bench_prefill(dev, iters=10, B=4, S=2048, Hq=32, Hkv=8, dtype=torch.bfloat16):
+    """Causal prefill attention at the config-5 prompt shape (B=4 prompts of 2048 tokens,
+    Llama-3-8B heads): dkv_prefill_attention against torch's scaled_dot_product_attention on
+    the same inputs (K/V repeated over the query heads for it). GPU time from events around
+    ``iters`` back-to-back calls."""
+    from dynakv_amd.kernels.prefill import prefill_attention
+
+    g = torch.Generator(device="cpu").manual_seed(7)
+    q = torch.randn(B, Hq, S, 128, generator=g).to(dev, dtype)
+    k = torch.randn(B, Hkv, S, 128, generator=g).to(dev, dtype)
+    v = torch.randn(B, Hkv, S, 128, generator=g).to(dev, dtype)
+    kr = k.repeat_interleave(Hq // Hkv, dim=1).contiguous()
+    vr = v.repeat_interleave(Hq // Hkv, dim=1).contiguous()
+    fns = {
+        "dynakv": lambda: prefill_attention(q, k, v, causal=True),
+        "torch_sdpa": lambda: torch.nn.functional.scaled_dot_product_attention(q, kr, vr,
+                                                                             is_causal=True),
+    }
+    times = {}
+    for name, fn in fns.items():
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize(dev)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(iters):
+            fn()
+        e1.record()
+        torch.cuda.synchronize(dev)
+        times[name] = e0.elapsed_time(e1) / iters
+    flops = 2.0 * 2 * B * Hq * (S * (S + 1) / 2) * 128  # QK and PV over the causal triangle
+    return {
+        "shape": f"B={B}, S={S}, {Hq}/{Hkv} heads, Dh 128, causal, {str(dtype).split('.')[-1]}",
+        "ms_per_call": round(times["dynakv"], 4),
+        "tflops": round(flops / (times["dynakv"] * 1e-3) / 1e12, 1),
+        "torch_sdpa_ms_per_call": round(times["torch_sdpa"], 4),
+        "torch_sdpa_tflops": round(flops / (times["torch_sdpa"] * 1e-3) / 1e12, 1),
+    }
+
+
 def load_traffic(workload):
     """HBM bytes per split-kernel launch measured by rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs
     of this script (scaled by a plain copy of known size), as committed under profiles/; used
@@ -338,6 +378,7 @@ def main():
     ap.add_argument("--cpu-baseline-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-cutoff", action="store_true", help="skip the cutoff-head timing")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the prefill-attention timing")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="run one device copy of this many MiB first (counter calibration)")
     args = ap.parse_args()
@@ -416,6 +457,9 @@ def main():
     if not args.no_cutoff:
         _log("cutoff head")
         line["cutoff_head"] = bench_cutoff(cfg, dev)
+    if not args.no_prefill:
+        _log("prefill attention")
+        line["prefill_attention"] = bench_prefill(dev)
     if not args.no_cpu_baseline:
         _log("cpu baseline")
         line["cpu_baseline"] = cpu_baseline(cfg, r["workload"], r["cache"], args.cpu_baseline_seconds)
