@@ -324,11 +324,13 @@ def bench_prefill(dev, iters=10, B=4, S=2048, Hq=32, Hkv=8, dtype=torch.bfloat16
     v = torch.randn(B, Hkv, S, 128, generator=g).to(dev, dtype)
     kr = k.repeat_interleave(Hq // Hkv, dim=1).contiguous()
     vr = v.repeat_interleave(Hq // Hkv, dim=1).contiguous()
-    fns = {
-        "dynakv": lambda: prefill_attention(q, k, v, causal=True),
-        "torch_sdpa": lambda: torch.nn.functional.scaled_dot_product_attention(q, kr, vr,
-                                                                             is_causal=True),
-    }
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    def sdpa():
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+            return torch.nn.functional.scaled_dot_product_attention(q, kr, vr, is_causal=True)
+
+    fns = {"dynakv": lambda: prefill_attention(q, k, v, causal=True), "torch_sdpa": sdpa}
     times = {}
     for name, fn in fns.items():
         for _ in range(3):
@@ -349,6 +351,49 @@ def bench_prefill(dev, iters=10, B=4, S=2048, Hq=32, Hkv=8, dtype=torch.bfloat16
         "torch_sdpa_ms_per_call": round(times["torch_sdpa"], 4),
         "torch_sdpa_tflops": round(flops / (times["torch_sdpa"] * 1e-3) / 1e12, 1),
     }
+
+
+def bench_e2e(dev, batches=(1, 2, 4), prompt_len=2048, new_tokens=100):
+    """Config 5: greedy generation with a random-init Llama-3-8B (bf16 N(0, 0.02) weights,
+    per-head random orthogonal bases, cutoff heads set for mean retention 0.47) over the
+    compressed cache, against the same weights with an uncompressed cache (torch's fused
+    attention kernels). tokens/s = batch * new tokens / wall time with prefill, as the
+    reference's benchmark_throughput.py:73 counts it; decode-only tokens/s beside it. Both
+    models run eagerly (one launch per op, no graph capture)."""
+    from dynakv_amd.model import CompressedLlama, DenseLlama, LlamaShape, RandomLlama
+
+    shape = LlamaShape()
+    model = RandomLlama(shape, device=dev, seed=5)
+    comp, dense = CompressedLlama(model), DenseLlama(model, max_len=prompt_len + new_tokens + 8)
+    g = torch.Generator(device="cpu").manual_seed(11)
+    res = {"model": "random-init Llama-3-8B shape (32 layers, 4096 hidden, 32/8 heads, FFN "
+                    "14336, vocab 128256), bf16", "prompt_len": prompt_len,
+           "new_tokens": new_tokens, "runs": []}
+    # one short warm-up of each path (kernel loading, library handles)
+    warm = torch.randint(0, shape.vocab, (1, 64), generator=g).to(dev)
+    comp.generate(warm, 4)
+    dense.generate(warm, 4)
+    for B in batches:
+        prompt = torch.randint(0, shape.vocab, (B, prompt_len), generator=g).to(dev)
+        rc = comp.generate(prompt, new_tokens)
+        rd = dense.generate(prompt, new_tokens)
+        lens = [int(c[1][:, :c[4]].float().mean().item()) for c in comp.cache.key_cache_sp[:1]]
+        res["runs"].append({
+            "batch": B,
+            "compressed_tokens_per_s": round(rc["tokens_per_s"], 1),
+            "dense_tokens_per_s": round(rd["tokens_per_s"], 1),
+            "compressed_decode_tokens_per_s": round(rc["decode_tokens_per_s"], 1),
+            "dense_decode_tokens_per_s": round(rd["decode_tokens_per_s"], 1),
+            "compressed_prefill_s": round(rc["prefill_s"], 4),
+            "dense_prefill_s": round(rd["prefill_s"], 4),
+            "compressed_kv_bytes": rc["kv_bytes"],
+            "dense_kv_bytes": rd["kv_bytes"],
+            "mean_retained_dims_layer0_k": lens[0] if lens else None,
+            "same_tokens_frac": round(float((rc["tokens"] == rd["tokens"]).float().mean()), 3),
+        })
+    del comp, dense, model
+    torch.cuda.empty_cache()
+    return res
 
 
 def load_traffic(workload):
@@ -379,6 +424,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-cutoff", action="store_true", help="skip the cutoff-head timing")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill-attention timing")
+    ap.add_argument("--e2e", action="store_true",
+                    help="also run config 5: greedy generation with a random Llama-3-8B, "
+                         "compressed against uncompressed cache (about a minute)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="run one device copy of this many MiB first (counter calibration)")
     args = ap.parse_args()
@@ -460,6 +508,9 @@ def main():
     if not args.no_prefill:
         _log("prefill attention")
         line["prefill_attention"] = bench_prefill(dev)
+    if args.e2e:
+        _log("end-to-end generation (config 5)")
+        line["e2e"] = bench_e2e(dev)
     if not args.no_cpu_baseline:
         _log("cpu baseline")
         line["cpu_baseline"] = cpu_baseline(cfg, r["workload"], r["cache"], args.cpu_baseline_seconds)

@@ -1,0 +1,325 @@
+"""End-to-end Llama decoder over the compressed cache, and the same model with a dense cache.
+
+The reference runs DynaKV inside HF's Llama (``custom_llama.py:93-323``, the attention module
+``compressed_attention.py:204-386``) and times greedy generation with
+``benchmark_throughput.py:17-82`` (tokens/s = batch * new tokens / wall time, prefill included).
+This module is that model path for this build, written against the kernels directly (no
+transformers model classes: their Cache API differs across versions, and the benchmark needs
+only the forward math):
+
+* ``RandomLlama``: Llama weights drawn on the device (N(0, 0.02) in bf16 by default) for a
+  given shape (config 5: Llama-3-8B -- hidden 4096, 32 layers, 32/8 heads, head dim 128, FFN
+  14336, vocab 128256), plus the DynaKV parameters per layer: a random orthogonal 128x128
+  spectral basis per KV head for K and for V, the K/V projections merged with the basis
+  transposes so that they emit coefficients (the one-time merge of
+  ``compressed_attention.py:263-292``), and per-head cutoff heads whose bias ramps over the
+  rank so that the retained fraction is close to a target (``retention``).
+* ``CompressedLlama.generate``: prefill (cutoff head, packed append, reconstruct-and-attend)
+  then greedy decode steps (cutoff head, decode append, routed decode attention), with
+  RMSNorm, rotary queries, SwiGLU MLP and the output head as plain library GEMMs.
+* ``DenseLlama.generate``: the uncompressed-cache baseline of the same weights (K/V kept in
+  full in a preallocated cache, attention by torch's scaled_dot_product_attention).
+"""
+
+from __future__ import annotations
+
+import math
+import time
+from dataclasses import dataclass, field
+
+import torch
+import torch.nn.functional as F
+from torch.nn.attention import SDPBackend, sdpa_kernel
+
+from .kernels.compressed_cache import CustomDynamicCache
+from .kernels.cutoff import CutoffHead
+from .kernels.decode import grouped_decode_attention
+from .kernels.prefill import compressed_prefill_attention, rope_dense_
+from .kernels.router import KernelPolicy
+
+
+@dataclass(frozen=True)
+class LlamaShape:
+    hidden: int = 4096
+    layers: int = 32
+    heads: int = 32
+    kv_heads: int = 8
+    head_dim: int = 128
+    ffn: int = 14336
+    vocab: int = 128256
+    theta: float = 500000.0
+    eps: float = 1e-5
+
+
+@dataclass
+class LayerWeights:
+    ln1: torch.Tensor
+    wq: torch.Tensor
+    wk: torch.Tensor      # dense K projection (the baseline)
+    wv: torch.Tensor
+    wk_c: torch.Tensor    # merged: emits per-head K coefficients
+    wv_c: torch.Tensor
+    wo: torch.Tensor
+    ln2: torch.Tensor
+    w_gate: torch.Tensor
+    w_up: torch.Tensor
+    w_down: torch.Tensor
+    k_basis: torch.Tensor  # (G, R, Dh) rank-major
+    v_basis: torch.Tensor
+    cutoff: CutoffHead = field(repr=False)
+
+
+def _orthogonal(n: int, count: int, gen: torch.Generator, device) -> torch.Tensor:
+    a = torch.randn(count, n, n, generator=gen, device=device, dtype=torch.float32)
+    q, r = torch.linalg.qr(a)
+    return q * torch.sign(torch.diagonal(r, dim1=-2, dim2=-1)).unsqueeze(-2)
+
+
+def ramp_for_retention(D: int, retention: float) -> float:
+    """Slope beta of the cutoff bias beta * j / D for which flip(cumsum(softmax)) >= 0.1 keeps
+    ``retention * D`` dims when the input term is small: the mass below index D * (1 - r) is
+    0.1, i.e. (e^{beta (1-r)} - 1) / (e^{beta} - 1) = 0.1, solved by bisection."""
+    lo, hi = 1e-3, 60.0
+    target_m = 1.0 - retention
+    for _ in range(100):
+        mid = 0.5 * (lo + hi)
+        frac = math.expm1(mid * target_m) / math.expm1(mid)
+        if frac > 0.1:
+            lo = mid
+        else:
+            hi = mid
+    return 0.5 * (lo + hi)
+
+
+class RandomLlama:
+    def __init__(self, shape: LlamaShape = LlamaShape(), *, device="cuda", dtype=torch.bfloat16,
+                 seed: int = 0, retention: float = 0.47, std: float = 0.02):
+        self.shape = shape
+        self.dtype = dtype
+        self.device = torch.device(device)
+        g = torch.Generator(device=self.device)
+        g.manual_seed(seed)
+        s = shape
+        H, Dh, G = s.hidden, s.head_dim, s.kv_heads
+
+        def rnd(*dims):
+            return (torch.randn(*dims, generator=g, device=self.device, dtype=torch.float32)
+                    * std).to(dtype)
+
+        self.embed = rnd(s.vocab, H)
+        self.norm = torch.ones(H, device=self.device, dtype=dtype)
+        self.lm_head = rnd(s.vocab, H)
+        beta = ramp_for_retention(Dh, retention)
+        ramp = (beta * torch.arange(Dh, device=self.device, dtype=torch.float32) / Dh).to(dtype)
+        self.layers = []
+        for _ in range(s.layers):
+            wk, wv = rnd(G * Dh, H), rnd(G * Dh, H)
+            Uk = _orthogonal(Dh, G, g, self.device)  # (G, d, r): K_g = U_g c_g
+            Uv = _orthogonal(Dh, G, g, self.device)
+            # coefficients c_g = U_g^T k_g: the projection merged with the basis transpose
+            wk_c = torch.matmul(Uk.transpose(1, 2), wk.float().view(G, Dh, H)).reshape(G * Dh, H)
+            wv_c = torch.matmul(Uv.transpose(1, 2), wv.float().view(G, Dh, H)).reshape(G * Dh, H)
+            cut = [rnd(G, Dh, Dh) for _ in range(2)]
+            bias = [ramp.expand(G, Dh).contiguous() for _ in range(2)]
+            self.layers.append(LayerWeights(
+                ln1=torch.ones(H, device=self.device, dtype=dtype), wq=rnd(H, H), wk=wk, wv=wv,
+                wk_c=wk_c.to(dtype), wv_c=wv_c.to(dtype), wo=rnd(H, H),
+                ln2=torch.ones(H, device=self.device, dtype=dtype),
+                w_gate=rnd(s.ffn, H), w_up=rnd(s.ffn, H), w_down=rnd(H, s.ffn),
+                k_basis=Uk.transpose(1, 2).contiguous().to(dtype),
+                v_basis=Uv.transpose(1, 2).contiguous().to(dtype),
+                cutoff=CutoffHead(cut[0], bias[0], cut[1], bias[1], groups=G)))
+
+
+def _rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+    xf = x.float()
+    return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)).to(x.dtype) * w
+
+
+def _mlp(lw: LayerWeights, h: torch.Tensor) -> torch.Tensor:
+    return F.linear(F.silu(F.linear(h, lw.w_gate)) * F.linear(h, lw.w_up), lw.w_down)
+
+
+def _rope_q(q: torch.Tensor, pos0: int, theta: float) -> torch.Tensor:
+    """q (B, S, Hq, Dh) -> rotated (B, Hq, S, Dh) contiguous."""
+    qh = q.transpose(1, 2).contiguous()
+    return rope_dense_(qh, theta=theta, pos0=pos0)
+
+
+class _Generator:
+    def __init__(self, model: RandomLlama):
+        self.m = model
+        self.s = model.shape
+
+    def logits(self, x: torch.Tensor) -> torch.Tensor:
+        return F.linear(_rmsnorm(x, self.m.norm, self.s.eps), self.m.lm_head)
+
+    def generate(self, prompt: torch.Tensor, new_tokens: int) -> dict:
+        """Greedy decode; returns tokens, timings and cache bytes."""
+        torch.cuda.synchronize(self.m.device)
+        t0 = time.perf_counter()
+        x = self.prefill(prompt)
+        tok = self.logits(x[:, -1:]).argmax(-1)  # (B, 1)
+        out = [tok]
+        torch.cuda.synchronize(self.m.device)
+        t1 = time.perf_counter()
+        pos = prompt.shape[1]
+        for _ in range(new_tokens - 1):
+            x = self.decode(tok, pos)
+            tok = self.logits(x).argmax(-1)
+            out.append(tok)
+            pos += 1
+        torch.cuda.synchronize(self.m.device)
+        t2 = time.perf_counter()
+        B = prompt.shape[0]
+        return {
+            "tokens": torch.cat(out, dim=1),
+            "prefill_s": t1 - t0,
+            "decode_s": t2 - t1,
+            "tokens_per_s": B * new_tokens / (t2 - t0),
+            "decode_tokens_per_s": B * (new_tokens - 1) / max(t2 - t1, 1e-9),
+            "kv_bytes": self.kv_bytes(),
+        }
+
+
+class CompressedLlama(_Generator):
+    """The model over DynaKV's packed cache (per-head layout, rows b*G + g)."""
+
+    def __init__(self, model: RandomLlama, policy: KernelPolicy | None = None):
+        super().__init__(model)
+        self.policy = policy or KernelPolicy()
+        self.cache = CustomDynamicCache()
+
+    def _qkv(self, lw, h):
+        B, S, _ = h.shape
+        s = self.s
+        q = F.linear(h, lw.wq).view(B, S, s.heads, s.head_dim)
+        kc = F.linear(h, lw.wk_c)  # (B, S, G*Dh) coefficients
+        vc = F.linear(h, lw.wv_c)
+        k_out, v_out, len_k, len_v, _, _ = lw.cutoff.kv_process_fused(kc, vc)
+        G, Dh = s.kv_heads, s.head_dim
+        rows_k = k_out.view(B, S, G, Dh).transpose(1, 2).reshape(B * G, S, Dh)
+        rows_v = v_out.view(B, S, G, Dh).transpose(1, 2).reshape(B * G, S, Dh)
+        lk = len_k.view(B, S, G).transpose(1, 2).reshape(B * G, S).contiguous()
+        lv = len_v.view(B, S, G).transpose(1, 2).reshape(B * G, S).contiguous()
+        return q, rows_k, lk, rows_v, lv
+
+    def prefill(self, prompt: torch.Tensor) -> torch.Tensor:
+        s = self.s
+        self.cache.reset()
+        x = F.embedding(prompt, self.m.embed)
+        B, S = prompt.shape
+        for i, lw in enumerate(self.m.layers):
+            h = _rmsnorm(x, lw.ln1, s.eps)
+            q, rk, lk, rv, lv = self._qkv(lw, h)
+            self.cache.update_sp(rk.contiguous(), lk, rv.contiguous(), lv, s.head_dim, i,
+                                 s.head_dim)
+            qh = _rope_q(q, 0, s.theta)
+            a = compressed_prefill_attention(qh, self.cache, i, lw.k_basis, lw.v_basis,
+                                             theta=s.theta)
+            x = x + F.linear(a.transpose(1, 2).reshape(B, S, s.hidden), lw.wo)
+            x = x + _mlp(lw, _rmsnorm(x, lw.ln2, s.eps))
+        return x
+
+    def decode(self, tok: torch.Tensor, pos: int) -> torch.Tensor:
+        s = self.s
+        x = F.embedding(tok, self.m.embed)  # (B, 1, H)
+        B = tok.shape[0]
+        for i, lw in enumerate(self.m.layers):
+            h = _rmsnorm(x, lw.ln1, s.eps)
+            q, rk, lk, rv, lv = self._qkv(lw, h)
+            fk, fv, tk, tv, ok, ov = self.cache.update_sp(rk, lk, rv, lv, s.head_dim, i,
+                                                          s.head_dim)
+            L = self.cache.get_seq_length_sp(i)
+            qh = _rope_q(q, pos, s.theta)[:, :, 0]  # (B, Hq, Dh)
+            a = grouped_decode_attention(qh, fk, fv, tk, ok, tv, ov, lw.k_basis, lw.v_basis,
+                                         theta=s.theta, route=self.policy.select(L))
+            x = x + F.linear(a.reshape(B, 1, s.hidden), lw.wo)
+            x = x + _mlp(lw, _rmsnorm(x, lw.ln2, s.eps))
+        return x
+
+    def kv_bytes(self) -> int:
+        """Stored bytes of the packed caches: the used part of each row plus 8 bytes of
+        lengths/offsets per token and row."""
+        tot = 0
+        for slots in (self.cache.key_cache_sp, self.cache.value_cache_sp):
+            for c in slots:
+                if c is None:
+                    continue
+                flat, lens, offs, ptr, seq = c[0], c[1], c[2], c[3], c[4]
+                tot += int(ptr.sum()) * flat.element_size() + 8 * lens.shape[0] * seq
+        return tot
+
+
+# torch's fused attention kernels only: an input they do not take raises instead of running the
+# composite (math) path
+_FAST_SDPA = [SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]
+
+
+class DenseLlama(_Generator):
+    """The same weights with an uncompressed cache (K/V of every layer kept in full)."""
+
+    def __init__(self, model: RandomLlama, max_len: int = 4096):
+        super().__init__(model)
+        self.max_len = max_len
+        self.k = self.v = None
+        self.len = 0
+
+    def _kv(self, lw, h, pos0):
+        B, S, _ = h.shape
+        s = self.s
+        q = F.linear(h, lw.wq).view(B, S, s.heads, s.head_dim)
+        k = F.linear(h, lw.wk).view(B, S, s.kv_heads, s.head_dim).transpose(1, 2).contiguous()
+        v = F.linear(h, lw.wv).view(B, S, s.kv_heads, s.head_dim).transpose(1, 2)
+        rope_dense_(k, theta=s.theta, pos0=pos0)
+        return _rope_q(q, pos0, s.theta), k, v
+
+    def prefill(self, prompt: torch.Tensor) -> torch.Tensor:
+        s = self.s
+        B, S = prompt.shape
+        dev, dt = self.m.device, self.m.dtype
+        shape = (B, s.kv_heads, self.max_len, s.head_dim)
+        self.k = [torch.empty(shape, device=dev, dtype=dt) for _ in range(s.layers)]
+        self.v = [torch.empty(shape, device=dev, dtype=dt) for _ in range(s.layers)]
+        hpg = s.heads // s.kv_heads
+        x = F.embedding(prompt, self.m.embed)
+        for i, lw in enumerate(self.m.layers):
+            h = _rmsnorm(x, lw.ln1, s.eps)
+            qh, k, v = self._kv(lw, h, 0)
+            self.k[i][:, :, :S] = k
+            self.v[i][:, :, :S] = v
+            with sdpa_kernel(_FAST_SDPA):
+                a = F.scaled_dot_product_attention(qh, k.repeat_interleave(hpg, dim=1),
+                                                   v.repeat_interleave(hpg, dim=1),
+                                                   is_causal=True)
+            x = x + F.linear(a.transpose(1, 2).reshape(B, S, s.hidden), lw.wo)
+            x = x + _mlp(lw, _rmsnorm(x, lw.ln2, s.eps))
+        self.len = S
+        return x
+
+    def decode(self, tok: torch.Tensor, pos: int) -> torch.Tensor:
+        """One token: K/V appended at position len, then the query heads of each KV group
+        attend as that group's queries (no copy of the cache per step)."""
+        s = self.s
+        x = F.embedding(tok, self.m.embed)
+        B = tok.shape[0]
+        L = self.len
+        hpg = s.heads // s.kv_heads
+        for i, lw in enumerate(self.m.layers):
+            h = _rmsnorm(x, lw.ln1, s.eps)
+            qh, k, v = self._kv(lw, h, pos)
+            self.k[i][:, :, L:L + 1] = k
+            self.v[i][:, :, L:L + 1] = v
+            qg = qh.view(B, s.kv_heads, hpg, s.head_dim)
+            with sdpa_kernel(_FAST_SDPA):
+                a = F.scaled_dot_product_attention(qg, self.k[i][:, :, :L + 1],
+                                                   self.v[i][:, :, :L + 1])
+            x = x + F.linear(a.reshape(B, 1, s.hidden), lw.wo)
+            x = x + _mlp(lw, _rmsnorm(x, lw.ln2, s.eps))
+        self.len = L + 1
+        return x
+
+    def kv_bytes(self) -> int:
+        s = self.s
+        B = self.k[0].shape[0] if self.k else 0
+        return 2 * s.layers * B * s.kv_heads * self.len * s.head_dim * self.m.embed.element_size()
