@@ -52,12 +52,32 @@ _SIGNATURES = {
     "dkv_selftest_layouts": (_i, [_vp, _vp]),
     "dkv_cutoff_workspace_bytes": (_ll, [_i, _i, _i]),
     "dkv_rope_dense": (_i, [_vp, _i, _vp, _ll, _ll, _i, _i, _i, _f]),
+    "dkv_decode_layer": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i]),
     "dkv_prefill_attention": (_i, [_vp, _i, _vp, _ll, _ll, _ll, _vp, _ll, _ll, _ll, _ll,
                                    _vp, _ll, _ll, _ll, _ll, _vp, _i, _ll, _ll, _ll,
                                    _i, _i, _i, _i, _i, _i, _i, _f]),
     "dkv_cutoff_kv": (_i, [_vp, _i, _vp, _vp, _ll, _vp, _vp, _vp, _vp, _f, _i, _vp, _vp, _ll,
                            _vp, _vp, _ll, _vp, _ll, _i, _i, _i]),
 }
+
+class DecodeLayerArgs(C.Structure):
+    """``DkvDecodeLayer`` of include/dynakv_amd.h (field order and types must match)."""
+
+    _fields_ = [
+        ("dtype", _i), ("B", _i), ("G", _i), ("Hq", _i), ("R", _i), ("Dh", _i),
+        ("low_rank", _i), ("switch_tokens", _i), ("threshold", _f), ("log_theta", _f),
+        ("wt_k", _vp), ("wt_v", _vp), ("b_k", _vp), ("b_v", _vp),
+        ("cut_ws", _vp), ("cut_ws_bytes", _ll),
+        ("coef_k", _vp), ("coef_v", _vp), ("len_k", _vp), ("len_v", _vp),
+        ("flat_k", _vp), ("flat_k_ld", _ll), ("lens_k", _vp), ("offs_k", _vp),
+        ("tab_k_sb", _ll), ("tab_k_ss", _ll), ("ptr_k", _vp),
+        ("flat_v", _vp), ("flat_v_ld", _ll), ("lens_v", _vp), ("offs_v", _vp),
+        ("tab_v_sb", _ll), ("tab_v_ss", _ll), ("ptr_v", _vp),
+        ("k_basis", _vp), ("k_unit", _ll), ("k_sr", _ll),
+        ("v_basis", _vp), ("v_unit", _ll), ("v_sr", _ll),
+        ("rope", _vp), ("rope_tiles", _i), ("split_ws", _vp), ("split_ws_floats", _ll),
+    ]
+
 
 _lock = threading.Lock()
 _lib = None

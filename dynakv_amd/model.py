@@ -34,6 +34,7 @@ from torch.nn.attention import SDPBackend, sdpa_kernel
 from .kernels.compressed_cache import CustomDynamicCache
 from .kernels.cutoff import CutoffHead
 from .kernels.decode import grouped_decode_attention
+from .kernels.layer import DecodeLayerPlan
 from .kernels.prefill import compressed_prefill_attention, rope_dense_
 from .kernels.router import KernelPolicy
 
@@ -185,10 +186,13 @@ class _Generator:
 class CompressedLlama(_Generator):
     """The model over DynaKV's packed cache (per-head layout, rows b*G + g)."""
 
-    def __init__(self, model: RandomLlama, policy: KernelPolicy | None = None):
+    def __init__(self, model: RandomLlama, policy: KernelPolicy | None = None,
+                 one_call_layers: bool = True):
         super().__init__(model)
         self.policy = policy or KernelPolicy()
         self.cache = CustomDynamicCache()
+        self.one_call_layers = one_call_layers
+        self.plans: dict = {}
 
     def _qkv(self, lw, h):
         B, S, _ = h.shape
@@ -207,6 +211,7 @@ class CompressedLlama(_Generator):
     def prefill(self, prompt: torch.Tensor) -> torch.Tensor:
         s = self.s
         self.cache.reset()
+        self.plans = {}
         x = F.embedding(prompt, self.m.embed)
         B, S = prompt.shape
         for i, lw in enumerate(self.m.layers):
@@ -227,13 +232,25 @@ class CompressedLlama(_Generator):
         B = tok.shape[0]
         for i, lw in enumerate(self.m.layers):
             h = _rmsnorm(x, lw.ln1, s.eps)
-            q, rk, lk, rv, lv = self._qkv(lw, h)
-            fk, fv, tk, tv, ok, ov = self.cache.update_sp(rk, lk, rv, lv, s.head_dim, i,
-                                                          s.head_dim)
-            L = self.cache.get_seq_length_sp(i)
-            qh = _rope_q(q, pos, s.theta)[:, :, 0]  # (B, Hq, Dh)
-            a = grouped_decode_attention(qh, fk, fv, tk, ok, tv, ov, lw.k_basis, lw.v_basis,
-                                         theta=s.theta, route=self.policy.select(L))
+            plan = self.plans.get(i)
+            if plan is not None and plan.can_step():
+                # one call: cutoff head, K+V append, q RoPE, routed attention
+                q = F.linear(h, lw.wq).view(B, s.heads, s.head_dim)
+                kc = F.linear(h, lw.wk_c).view(B, -1)
+                vc = F.linear(h, lw.wv_c).view(B, -1)
+                a = plan.step(q, kc, vc, pos)
+            else:
+                q, rk, lk, rv, lv = self._qkv(lw, h)
+                fk, fv, tk, tv, ok, ov = self.cache.update_sp(rk, lk, rv, lv, s.head_dim, i,
+                                                              s.head_dim)
+                L = self.cache.get_seq_length_sp(i)
+                qh = _rope_q(q, pos, s.theta)[:, :, 0]  # (B, Hq, Dh)
+                a = grouped_decode_attention(qh, fk, fv, tk, ok, tv, ov, lw.k_basis, lw.v_basis,
+                                             theta=s.theta, route=self.policy.select(L))
+                if self.one_call_layers:
+                    self.plans[i] = DecodeLayerPlan(self.cache, i, lw.cutoff, lw.k_basis,
+                                                    lw.v_basis, batch=B, heads=s.heads,
+                                                    theta=s.theta, policy=self.policy)
             x = x + F.linear(a.reshape(B, 1, s.hidden), lw.wo)
             x = x + _mlp(lw, _rmsnorm(x, lw.ln2, s.eps))
         return x

@@ -271,6 +271,49 @@ int dkv_prefill_attention(void* stream, int dtype, const void* q, long long q_sb
                           int out_dtype, long long o_sb, long long o_sh, long long o_ss, int B,
                           int Hq, int Hkv, int Sq, int Sk, int Dh, int causal, float scale);
 
+/*
+ * One decode step of one attention layer (per-head layout, rows b*G + g) in one call: the
+ * reference's decode branch, src/dynakv/kernels/compressed_attention.py:312-357 -- cutoff head
+ * (:321-327, dkv_cutoff_kv), K+V append at position seq (:330-334, dkv_append_decode_kv), RoPE
+ * of q at position pos (:314, dkv_rope_dense), decode attention over seq + 1 tokens routed at
+ * switch_tokens (:335-348 and router.py:20-59, dkv_decode_splitk). The caller fills a
+ * DkvDecodeLayer once per layer (and again after the cache grows or the RoPE table is
+ * extended) and calls dkv_decode_layer per step with the step's q (B, Hq, Dh) contiguous,
+ * rotated in place, the layer's K/V coefficients (B, G*R) contiguous and the output
+ * (B, Hq, Dh) contiguous in the cache dtype. The caller guarantees room for one more token:
+ * seq + 1 <= the tables' capacity, every row's used length + R <= the flat capacity, and
+ * rope_tiles * 16 >= seq + 1. Scratch: coef_k / coef_v (B, G*R) and len_k / len_v (B*G) int32.
+ */
+typedef struct DkvDecodeLayer {
+  int dtype, B, G, Hq, R, Dh, low_rank, switch_tokens;
+  float threshold, log_theta;
+  const void *wt_k, *wt_v, *b_k, *b_v;         /* cutoff head, (G, R, R) transposed / (G, R) */
+  void* cut_ws;
+  long long cut_ws_bytes;
+  void *coef_k, *coef_v;
+  int *len_k, *len_v;
+  void* flat_k;
+  long long flat_k_ld;
+  int *lens_k, *offs_k;
+  long long tab_k_sb, tab_k_ss;
+  int* ptr_k;
+  void* flat_v;
+  long long flat_v_ld;
+  int *lens_v, *offs_v;
+  long long tab_v_sb, tab_v_ss;
+  int* ptr_v;
+  const void* k_basis;
+  long long k_unit, k_sr;
+  const void* v_basis;
+  long long v_unit, v_sr;
+  const float* rope;
+  int rope_tiles;
+  float* split_ws;
+  long long split_ws_floats;
+} DkvDecodeLayer;
+int dkv_decode_layer(void* stream, const DkvDecodeLayer* layer, void* q, const void* k_coef,
+                     const void* v_coef, void* out, int seq, int pos);
+
 #ifdef __cplusplus
 }
 #endif

@@ -81,3 +81,26 @@ def test_no_cpu_fallback():
         abx_sparse(a, b, x, l, offsets=o)
     with pytest.raises(ValueError, match="offsets are required"):
         abx_sparse(a, b, x, l, offsets=None)
+
+
+def test_decode_layer_struct_layout(tmp_path):
+    """The ctypes mirror of DkvDecodeLayer has the C layout (offsets and size from gcc)."""
+    import ctypes
+    import shutil
+    import subprocess
+
+    if shutil.which("gcc") is None:
+        pytest.skip("gcc not available")
+    fields = [f[0] for f in _lib.DecodeLayerArgs._fields_]
+    src = tmp_path / "layout.c"
+    body = "".join(f'  printf("{n} %zu\\n", offsetof(DkvDecodeLayer, {n}));\n' for n in fields)
+    src.write_text('#include <stdio.h>\n#include <stddef.h>\n#include "dynakv_amd.h"\n'
+                   "int main(void) {\n" + body +
+                   '  printf("__size__ %zu\\n", sizeof(DkvDecodeLayer));\n  return 0;\n}\n')
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", os.path.dirname(HEADER), str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()
+    got = dict(zip(out[0::2], map(int, out[1::2])))
+    for n in fields:
+        assert getattr(_lib.DecodeLayerArgs, n).offset == got[n], n
+    assert ctypes.sizeof(_lib.DecodeLayerArgs) == got["__size__"]

@@ -68,11 +68,16 @@ def _close(got, ref, what, rel=0.05):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("kind", ["compressed", "dense"])
+@pytest.mark.parametrize("kind", ["compressed", "compressed_per_op", "dense"])
 def test_model_matches_float32_forward(dev, kind):
+    """compressed: the first decode step per layer takes the regular path, the later ones one
+    dkv_decode_layer call; compressed_per_op: every step the regular path."""
     print(f"[gpu] model {kind}", flush=True)
     model = RandomLlama(SHAPE, device=dev, seed=3, std=0.05)
-    gen = CompressedLlama(model) if kind == "compressed" else DenseLlama(model, max_len=64)
+    if kind == "dense":
+        gen = DenseLlama(model, max_len=64)
+    else:
+        gen = CompressedLlama(model, one_call_layers=(kind == "compressed"))
     g = torch.Generator(device="cpu").manual_seed(1)
     B, S = 2, 37
     tokens = torch.randint(0, SHAPE.vocab, (B, S), generator=g)
@@ -84,7 +89,7 @@ def test_model_matches_float32_forward(dev, kind):
         got.append(gen.logits(x).float().cpu())
     got = torch.cat(got, dim=1)  # prompt positions, then the three decoded positions
     lk = lv = None
-    if kind == "compressed":
+    if kind != "dense":
         lk = [c[1][:, :S].cpu() for c in gen.cache.key_cache_sp]
         lv = [c[1][:, :S].cpu() for c in gen.cache.value_cache_sp]
         frac = torch.stack(lk).float().mean().item() / SHAPE.head_dim
