@@ -17,7 +17,10 @@ Output: one JSON line. ``value`` is decode-attention GB/s: algorithmic bytes of 
 (packed K/V coefficients read once, int32 lengths, unique bases, q and output) divided by the
 GPU time of the attention launches, summed over the timed layer-steps (HIP events on the stream
 the kernels run on). ``roofline`` is the split kernel (one launch per call); ``cpu_baseline``
-times the masked-dimension CPU path on a bounded sample of the same inputs.
+times the masked-dimension CPU path on a bounded sample of the same inputs. Beside them:
+``cutoff_head`` (the cutoff head at the decode shape), ``prefill_attention`` (config 5's prompt
+shape) and ``e2e`` (config 5: greedy generation with a random-init Llama-3-8B, compressed
+against uncompressed cache).
 """
 
 from __future__ import annotations
@@ -424,9 +427,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-cutoff", action="store_true", help="skip the cutoff-head timing")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill-attention timing")
-    ap.add_argument("--e2e", action="store_true",
-                    help="also run config 5: greedy generation with a random Llama-3-8B, "
-                         "compressed against uncompressed cache (about a minute)")
+    ap.add_argument("--no-e2e", action="store_true",
+                    help="skip config 5 (greedy generation with a random Llama-3-8B, compressed "
+                         "against uncompressed cache; about 10 s)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="run one device copy of this many MiB first (counter calibration)")
     args = ap.parse_args()
@@ -508,7 +511,7 @@ def main():
     if not args.no_prefill:
         _log("prefill attention")
         line["prefill_attention"] = bench_prefill(dev)
-    if args.e2e:
+    if not args.no_e2e:
         _log("end-to-end generation (config 5)")
         line["e2e"] = bench_e2e(dev)
     if not args.no_cpu_baseline:
