@@ -2,30 +2,29 @@
 // routes (reference src/dynakv/kernels/fused.py:28-170, two_stage.py:48-324, router.py:20-59).
 //
 // Work unit: (batch b, KV head k) with hpg query heads sharing K/V basis k; its packed
-// coefficients are cache row b*G + k/(Hkv/G). A workgroup (4 waves) owns one unit and one
-// contiguous token range ("split", <= 512 tokens); waves take 16-token tiles round-robin.
+// coefficients are cache row b*G + k/(Hkv/G). A workgroup (8 waves, one per CU) owns one unit
+// and one contiguous token range ("split", a multiple of 64 tokens); waves take 16-token tiles
+// round-robin.
 //
-// Workgroup prologue: the K basis (transposed, [dim][rank]) and the split's length/offset
-// tables go to LDS, together with each tile's largest retained count, so a tile's gathers need
-// no dependent global round trip. Each wave then runs a two-stage software pipeline: the
-// current tile's gathered K and V coefficients are zero-masked past each token's count and
-// stored to the wave's LDS tiles, then the next tile's gathers (16-byte buffer loads, one lane =
-// one token x 8 ranks, out-of-range reads return zero) are issued and stay in flight while the
-// current tile computes from LDS:
-//   1. K^T[128 x 16] = BK^T . X^T on v_mfma_f32_16x16x32_{bf16,f16}, two 16-dim blocks at a
-//      time ((i, i+64) rotate-half pairs), rank chunks of 32 up to the tile's largest count;
-//   2. RoPE by cache row index on the accumulators (cos/sin advanced by angle addition from a
-//      precomputed table), K' split into fp16 hi/lo parts;
-//   3. scores on 16x16x32 f16 MFMA (K'hi.q + K'lo.q; a bf16 or fp16 query is exact in fp16,
-//      the softmax scale is applied to the fp32 result);
+// Prologue: half of the K basis goes to registers (MFMA A operands), the other half to LDS
+// ([dim][rank], read per tile), plus the mask table; each lane keeps its token slot's fixed
+// rotation R(n) and the query pairs of its frequency. Each wave then runs a software pipeline
+// over its tiles: the length/offset tables of tile j+2 and the coefficient windows of tile j+1
+// (direct-to-LDS buffer loads, one lane = one token x 8 ranks, empty pieces read from an
+// out-of-range offset as zeros) are in flight while tile j computes:
+//   1. the partial piece of each token is masked in place; the K windows go to registers;
+//   2. the query rotated back by the tile's base position, R(-16T) q (RoPE by angle addition:
+//      q . R(16T+n) k = (R(-16T) q) . (R(n) k)), split into fp16 hi/lo and staged through LDS
+//      into the B operand of the score MFMA;
+//   3. K^T[128 x 16] = BK^T . X^T on v_mfma_f32_16x16x32_{bf16,f16}, two 16-dim blocks at a
+//      time ((i, i+64) rotate-half pairs), R(n) per lane and fp16 conversion, scores on
+//      16x16x32 f16 MFMA (hi and lo query columns added by one DPP step);
 //   4. online softmax in the log2 domain, lazily rescaled (only when the running max grows by
 //      more than 2^11.5);
-//   5. P.X^V in coefficient space on 16x16x16 MFMA; X^V goes through a per-wave LDS tile so
-//      the operand (4 tokens x 1 rank per lane) is read transposed.
-// Epilogue: the 4 waves combine through LDS into one (m, l, acc[128]) record per head.
-// merge_kernel (same stream, one workgroup per unit and head) LSE-merges the split records and
-// projects once through the V basis; stream order makes the records visible to it without
-// device-scope fences (an agent-scope acquire would invalidate the XCD's L2).
+//   5. P.X^V in coefficient space on MFMA, the X^V operand read transposed from the windows.
+// Epilogue: the 8 waves combine through LDS into one (m, l, acc[128]) record per head; the
+// last split of a unit to arrive merges the unit's records by LSE and projects once through
+// the V basis (merge_kernel does this instead when a call has more units than counters).
 #include "dkv_common.h"
 
 #include <type_traits>
@@ -42,7 +41,7 @@ constexpr int PREC = DH + 2;  // floats per partial record: m, l, acc[128]
 constexpr int NSLOT = 2;        // gather slots per wave: the current tile + one in flight
 constexpr int TSLOT = 4;        // table slots per wave (tables run a tile ahead of gathers)
 constexpr int GSLOT_BYTES = 8192;  // 4 K chunks + 4 V chunks of 64 lanes x 16 bytes
-constexpr int QSTAGE = 65536;      // ring offset of the query staging copy (prologue only)
+constexpr int QROW_BYTES = 256;    // one row of the per-tile query operand (64 dwords)
 constexpr int MERGE_COUNTERS = 16384;  // leading workspace ints: per-unit arrival counters
 constexpr int VB_CHUNKS = DH * DH / 8 / NTHREADS;  // 16-byte V-basis pieces per thread
 constexpr int MASK_BIAS = 24;  // mask-table row of dk = 0 (dk: a lane's elements, -24 .. 128)
@@ -51,6 +50,7 @@ constexpr int ROPE_FIXED_ROWS = TILE + 1;  // rows 0..15: in-tile deltas; row 16
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float RESCALE_THRESH = 11.5f;  // log2 units
 constexpr int OOB = 0x7ffffff0;          // buffer offset that reads as zero
+constexpr int DPP_ROW_SHL8 = 0x108;      // DPP row_shl:8: lane i of a 16-lane row reads lane i+8
 
 struct SplitParams {
   const uint16_t* q;
@@ -224,6 +224,14 @@ __device__ __forceinline__ float lane_max16(float x) {
   return max2_f32(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
+// An opaque definition of x: a value loaded before a loop and settled after the load is, to the
+// compiler's wait insertion, produced here rather than by the load, so no wait for that load
+// is placed inside the loop.
+template <typename T>
+__device__ __forceinline__ void settle(T& x) {
+  asm volatile("" : "+v"(x));
+}
+
 // Wait until at most N vector-memory loads of this wave are outstanding (loads complete in
 // issue order); the "memory" clobber keeps LDS accesses from moving across the wait.
 template <int N>
@@ -295,19 +303,23 @@ __device__ __forceinline__ void merge_unit(const SplitParams& p, int unit, uint8
     merge_unit_t<DT, ROUTE, DT>(p, unit, scratch, vbr);
 }
 
-template <int DT, int ROUTE>
+// WIDE: more than 8 query heads per unit (up to 16). The query operand then carries the heads'
+// hi parts in its 16 columns and a second product takes the lo parts; with up to 8 heads the
+// hi parts sit in columns 0..7 and the lo parts in columns 8..15 of one product.
+template <int DT, int ROUTE, bool WIDE>
 __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
   // LDS: per-wave rings (NSLOT gather slots: K then V, 4 chunks x 64 lanes x 16 bytes each;
   // TSLOT table slots: lens_k, offs_k, lens_v, offs_v x 16 tokens), the streamed half of the
-  // K basis ([dim][rank] rows of dims 32..63 and 96..127), the mask table and the rotation
-  // step. The full basis staging copy and the epilogue scratch alias the rings.
+  // K basis ([dim][rank] rows of dims 32..63 and 96..127) and the mask table. The full basis
+  // staging copy, the per-tile query operand and the epilogue scratch alias the rings.
   __shared__ __attribute__((aligned(16))) uint32_t sMask[MASK_ROWS][4];
-  __shared__ __attribute__((aligned(16))) float sStep[2][64];  // rotation by WAVES*TILE positions
   __shared__ __attribute__((aligned(16))) int sTabRing[WAVES][TSLOT][4][TILE];
   __shared__ __attribute__((aligned(16))) uint16_t sBH[DH / 2 * BK_LD];
-  __shared__ __attribute__((aligned(16))) uint8_t sRing[WAVES * NSLOT * GSLOT_BYTES];
-  static_assert(DH * BK_LD * 2 <= QSTAGE && QSTAGE + WAVES * 64 * 64 <= WAVES * NSLOT * GSLOT_BYTES,
-                "basis and query staging fit the rings");
+  // 256-byte aligned: the query operand's row swizzle XORs bits 4..7 of ring addresses
+  __shared__ __attribute__((aligned(256))) uint8_t sRing[WAVES * NSLOT * GSLOT_BYTES];
+  static_assert(DH * BK_LD * 2 <= WAVES * NSLOT * GSLOT_BYTES, "basis staging fits the rings");
+  static_assert(16 * QROW_BYTES <= GSLOT_BYTES / 2, "query operand fits a slot's K half");
+  constexpr int QH = WIDE ? 16 : 8;  // head registers per lane
   uint16_t* sBK = reinterpret_cast<uint16_t*>(sRing);
 
   // XCD-aware mapping: consecutive workgroup ids land on different XCDs (id % 8), so give
@@ -365,66 +377,60 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
       const int ck = min(max((dk - 1) >> 5, 0), 3);
       sMask[r >> 2][r & 3] = prefix_mask_word(min(max(dk - 32 * ck, 0), 8), r & 3);
     }
-    if (tid < 64) {
-      sStep[0][tid] = p.rope[TILE * 128 + 2 * tid];
-      sStep[1][tid] = p.rope[TILE * 128 + 2 * tid + 1];
-    }
   }
 
-  // query as the fp16 B operand of the QK MFMA: lane (head slot n, k-group g) holds
-  // (q_i, q_{i+64}) for i = 16*pp + 4*g + w. bf16 and fp16 values in fp16's normal range are
-  // exact in fp16 (smaller ones keep an absolute error below 2^-25).
-  dkv_u32x4 bq[4];
+  // RoPE is split by angle addition: the key of position 16*T + n is rotated by R(n) here,
+  // on its own lane (token slot n, fixed for the whole kernel), and R(16*T) goes to the query
+  // of tile T instead: q . R(16T + n) k = (R(-16T) q) . (R(n) k).
+  // qh[h]: (q_i, q_{i+64}) of head h for frequency i = lane, as the cache's 16-bit values.
+  uint32_t qh[QH];
   {
-    const bool real = n < p.hpg;
-    const long long qo = (long long)b * p.q_sb + (long long)(kvh * p.hpg + min(n, p.hpg - 1)) * p.q_sh;
-    uint32_t qa[16], qb[16];
+    const long long qo = (long long)b * p.q_sb + (long long)kvh * p.hpg * p.q_sh + lane;
 #pragma unroll
-    for (int pp = 0; pp < 4; ++pp)
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const int i = 16 * pp + 4 * g + w;
-        qa[pp * 4 + w] = p.q[qo + i];
-        qb[pp * 4 + w] = p.q[qo + i + 64];
-      }
-#pragma unroll
-    for (int pp = 0; pp < 4; ++pp) {
-      uint32_t w4[4];
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const float a = real ? elt_to_f32<DT>(qa[pp * 4 + w]) : 0.f;
-        const float c = real ? elt_to_f32<DT>(qb[pp * 4 + w]) : 0.f;
-        w4[w] = pack_f16x2(a, c);
-      }
-      // staged in LDS, then read into accumulation registers with the K basis below
-      *(dkv_u32x4*)(sRing + QSTAGE + (wave * 64 + lane) * 64 + pp * 16) =
-          dkv_u32x4{w4[0], w4[1], w4[2], w4[3]};
+    for (int h = 0; h < QH; ++h) {
+      qh[h] = 0u;
+      if (h < p.hpg)
+        qh[h] = (uint32_t)p.q[qo + h * p.q_sh] | ((uint32_t)p.q[qo + h * p.q_sh + 64] << 16);
     }
   }
-
-  const int tile_first = s_begin / TILE;  // splits are whole tiles (multiples of 64 tokens)
-  const int tile0 = tile_first + wave;
-  const int n_tb = (p.S + TILE - 1) / TILE;
-  const int n_iter = max(0, ((ns + TILE - 1) / TILE - wave + WAVES - 1) / WAVES);
-
-  // RoPE state of this lane's token slot for its 16 frequencies
+  // R(n) of this lane's token slot for its 16 frequencies i = 16*pp + 4*g + w
   float rc[16], rs[16];
   {
-    const int tb = min(tile0, n_tb - 1);
-    const float* base = p.rope + (long long)(ROPE_FIXED_ROWS + tb) * 128;
     const float* delt = p.rope + (long long)n * 128;
 #pragma unroll
     for (int pp = 0; pp < 4; ++pp)
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
         const int i = 16 * pp + 4 * g + w, f = pp * 4 + w;
-        const float bc = base[2 * i], bs = base[2 * i + 1];
-        const float ec = delt[2 * i], es = delt[2 * i + 1];
-        rc[f] = bc * ec - bs * es;
-        rs[f] = bs * ec + bc * es;
+        rc[f] = delt[2 * i];
+        rs[f] = delt[2 * i + 1];
       }
   }
-  __syncthreads();  // staging copy, sBH, sMask, sStep ready
+  // The per-tile query operand lives in the K half of the tile's gather slot once the K
+  // coefficients are in registers: row r (one per operand column), chunk c (16 bytes: dwords
+  // 4c..4c+3, i.e. frequencies 4c..4c+3) stored at chunk position c ^ r, so that the 16 rows
+  // read by one k-group land in 16 different bank groups. Column n reads row qrow: its head's
+  // hi (n < 8) or lo (n >= 8) row, or, for columns past the heads, a real row (finite values
+  // in columns that are never used).
+  uint8_t* ring = sRing + wave * NSLOT * GSLOT_BYTES;
+  uint32_t q_rd[4];  // LDS address of chunk 4*pp + g of row qrow in slot 0
+  uint32_t q_wr;     // ring base | 4*lane: this lane's dword in row r of slot 0 is q_wr ^ (16*r)
+  {
+    const int hn = WIDE ? n : (n & 7);
+    const int head = hn < p.hpg ? hn : hn % p.hpg;
+    const int qrow = WIDE ? head : (n & 8) + head;
+    const uint32_t rb = lds_addr(ring);
+#pragma unroll
+    for (int pp = 0; pp < 4; ++pp)
+      q_rd[pp] = rb + (uint32_t)(qrow * QROW_BYTES) + 16u * (uint32_t)((4 * pp + g) ^ qrow);
+    q_wr = rb | (4u * (uint32_t)lane);
+  }
+
+  const int tile_first = s_begin / TILE;  // splits are whole tiles (multiples of 64 tokens)
+  const int tile0 = tile_first + wave;
+  const int n_tb = (p.S + TILE - 1) / TILE;
+  const int n_iter = max(0, ((ns + TILE - 1) / TILE - wave + WAVES - 1) / WAVES);
+  __syncthreads();  // staging copy, sBH, sMask ready
 
   // recon A operands of blocks 0, 4, 1, 5 (dims 0..31 and 64..95; block blk = dims
   // 16*blk + n, rank chunk c = ranks 32c + 8g .. +8), read straight into accumulation
@@ -443,12 +449,6 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
                      : "=v"(bA[k][c])
                      : "v"(a0), "i"((16 * blk * BK_LD + 32 * c) * 2));
       }
-    // the query operand (the B operand of the QK MFMAs), staged above
-    const uint32_t q0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)(
-        sRing + QSTAGE + (wave * 64 + lane) * 64);
-#pragma unroll
-    for (int pp = 0; pp < 4; ++pp)
-      asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(bq[pp]) : "v"(q0), "i"(pp * 16));
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   }
   __syncthreads();  // every wave holds its operands: the rings may now be overwritten
@@ -459,7 +459,6 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
   const int k_row0 = row * p.k_ld, v_row0 = row * p.v_ld;
   // only the buffers' last row can hold a token whose 16-byte window crosses the end
   const bool last_row = row == p.B * p.G - 1;
-  uint8_t* ring = sRing + wave * NSLOT * GSLOT_BYTES;
   // table loads: lane (table l/16, token l%16) -> one 4-byte load per lane and tile
   const int* tab_base;
   int tab_ss;
@@ -539,17 +538,43 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
   //      Loads are issued for every iteration, also past the wave's last tile (indices clamp
   //      to the split's last token), so at the top of iteration j nothing but G(j) and T(j+1)
   //      can be in flight and a full wait costs nothing extra. -------------------------------
+  // rotation R(16*T) of the wave's current tile T for frequency i = lane, times the score
+  // scale (the fused route's scores come out in log2 units, the two-stage route's in natural
+  // units), advanced by angle addition (WAVES*TILE positions per tile); bc/bs start at the
+  // table's exact value for the wave's first tile
+  float bc, bs, stc, sts;
+  {
+    const int t = min(tile0, n_tb - 1);
+    const float* row = p.rope + (long long)(ROPE_FIXED_ROWS + t) * 128 + 2 * lane;
+    bc = row[0] * p.score_scale;
+    bs = row[1] * p.score_scale;
+    stc = p.rope[TILE * 128 + 2 * lane];
+    sts = p.rope[TILE * 128 + 2 * lane + 1];
+  }
+  // loop-invariant loaded values: settled here, so the loop carries no wait for their loads
+  // (such a wait would also drain the gathers in flight)
+  settle(bc);
+  settle(bs);
+  settle(stc);
+  settle(sts);
+#pragma unroll
+  for (int f = 0; f < 16; ++f) {
+    settle(rc[f]);
+    settle(rs[f]);
+  }
+#pragma unroll
+  for (int h = 0; h < QH; ++h) settle(qh[h]);
+
   load_tab(0);
   load_tab(1);
   wait_vm<1>();  // T0
   issue(0);
 
-  // one tile: the rotation (ci, si) of this tile's token slot in, the next tile's out
-  auto tile = [&](int j, const float (&ci)[16], const float (&si)[16], float (&co)[16],
-                  float (&so)[16]) {
+  // one tile; par = j % NSLOT
+  auto tile = [&](int j, const int par) {
     wait_vm<0>();  // G(j), T(j+1)
     const Tok cur = tok_of(j);
-    uint8_t* slot = ring + (j % NSLOT) * GSLOT_BYTES;
+    uint8_t* slot = ring + par * GSLOT_BYTES;
     if (last_row) regather_if_needed(cur, slot);
     load_tab(j + 2);
     issue(j + 1);
@@ -575,7 +600,68 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-    // ---- 1-3: K reconstruction, RoPE, hi/lo split, scores ---------------------------------
+    // ---- query of this tile: R(-16T) q times the score scale, as fp16 hi + lo, written to the
+    //      K half of the slot (its coefficients are in xk; LDS accesses of a wave run in order)
+    //      and read back as the B operand of the score MFMAs (lane: column n, k-group g) ----
+    dkv_u32x4 bq[4], bq_lo[4];
+    {
+      const float cb = bc, sb = bs;
+      const uint32_t wr = q_wr + (uint32_t)(par * GSLOT_BYTES);
+      auto rotate = [&](int h, uint32_t& hi, uint32_t& lo) {
+        const float x = elt_to_f32<DT>(qh[h] & 0xffffu), y = elt_to_f32<DT>(qh[h] >> 16);
+        split_f16x2(cb * x + sb * y, cb * y - sb * x, p.minus_one, hi, lo);
+      };
+      // the next tile's base rotation
+      bc = cb * stc - sb * sts;
+      bs = sb * stc + cb * sts;
+      auto put = [&](uint32_t v, int r) {
+        *(__attribute__((address_space(3))) uint32_t*)(uintptr_t)(
+            (wr ^ (16u * r)) + (uint32_t)(r * QROW_BYTES)) = v;
+      };
+      auto get = [&](dkv_u32x4 (&dst)[4]) {
+#pragma unroll
+        for (int pp = 0; pp < 4; ++pp)
+          dst[pp] = *(const __attribute__((address_space(3))) dkv_u32x4*)(uintptr_t)(
+              q_rd[pp] + (uint32_t)(par * GSLOT_BYTES));
+      };
+      if constexpr (!WIDE) {
+#pragma unroll
+        for (int h = 0; h < QH; ++h)
+          if (h < p.hpg) {
+            uint32_t hi, lo;
+            rotate(h, hi, lo);
+            put(hi, h);
+            put(lo, 8 + h);
+          }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        get(bq);
+      } else {
+        uint32_t lo16[QH];
+#pragma unroll
+        for (int h = 0; h < QH; ++h)
+          if (h < p.hpg) {
+            uint32_t hi;
+            rotate(h, hi, lo16[h]);
+            put(hi, h);
+          }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        get(bq);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // hi rows read before the lo rows
+#pragma unroll
+        for (int h = 0; h < QH; ++h)
+          if (h < p.hpg) put(lo16[h], h);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        get(bq_lo);
+      }
+    }
+
+    // ---- 1-3: K reconstruction, R(n) on the lane's token, fp16 K', scores -------------------
     dkv_f32x4 sc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int pp = 0; pp < 4; ++pp) {
@@ -596,31 +682,22 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
           c1 = mfma_k<DT>(*(const dkv_u32x4*)(r1 + 32 * c), xk[c], c1);
         }
       }
-      uint32_t h4[4], l4[4];
+      uint32_t k4[4];
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
         const int f = pp * 4 + w;
-        float r0 = c0[w] * ci[f] - c1[w] * si[f];
-        float r1 = c1[w] * ci[f] + c0[w] * si[f];
-        // materialise the rotated pair once (otherwise the rotation is re-formed inside the
-        // mixed-precision conversions of both parts)
-        asm("" : "+v"(r0), "+v"(r1));
-        split_f16x2(r0, r1, p.minus_one, h4[w], l4[w]);
+        k4[w] = pack_f16x2(c0[w] * rc[f] - c1[w] * rs[f], c1[w] * rc[f] + c0[w] * rs[f]);
       }
-      sc = mfma_f16(dkv_u32x4{l4[0], l4[1], l4[2], l4[3]}, bq[pp], sc);
-      sc = mfma_f16(dkv_u32x4{h4[0], h4[1], h4[2], h4[3]}, bq[pp], sc);
+      const dkv_u32x4 ka = dkv_u32x4{k4[0], k4[1], k4[2], k4[3]};
+      sc = mfma_f16(ka, bq[pp], sc);
+      if constexpr (WIDE) sc = mfma_f16(ka, bq_lo[pp], sc);
     }
-    // advance the rotation to the wave's next tile (WAVES*TILE positions further)
+    if constexpr (!WIDE) {
+      // column n += column n + 8 (the lo part of head n) within each row of 16 lanes
 #pragma unroll
-    for (int pp = 0; pp < 4; ++pp) {
-      const dkv_f32x4 dc = *(const dkv_f32x4*)&sStep[0][16 * pp + 4 * g];
-      const dkv_f32x4 ds = *(const dkv_f32x4*)&sStep[1][16 * pp + 4 * g];
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const int f = pp * 4 + w;
-        co[f] = ci[f] * dc[w] - si[f] * ds[w];
-        so[f] = si[f] * dc[w] + ci[f] * ds[w];
-      }
+      for (int u = 0; u < 4; ++u)
+        sc[u] += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sc[u]),
+                                                            DPP_ROW_SHL8, 0xf, 0xf, false));
     }
 
     // scores of lane (head slot n, tokens 4g+u) with the route's masking: the fused route in
@@ -634,9 +711,9 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
       for (int u = 0; u < 4; ++u) {
         const bool has = lk[u] > 0;
         if constexpr (ROUTE == DKV_ROUTE_FUSED)
-          z[u] = has ? sc[u] * p.score_scale : -INFINITY;  // score_scale = sm_scale * log2(e)
+          z[u] = has ? sc[u] : -INFINITY;
         else
-          z[u] = dkv_round_to<DT>(has ? sc[u] * p.score_scale : p.masked_score);
+          z[u] = dkv_round_to<DT>(has ? sc[u] : p.masked_score);
       }
       const int nvalid = s_end - (tile0 + WAVES * j) * TILE;  // tokens of the tile in range
       if (__builtin_expect(nvalid < TILE, 0)) {  // wave-uniform: the split's last tile
@@ -725,14 +802,14 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     };
 
-  // two tiles per loop iteration with the rotation alternating between two register sets (a
-  // single loop-carried set is copied back every iteration); the scheduling barrier keeps the
-  // two tiles from being interleaved, which would double the live registers
-  float rbc[16], rbs[16];
+  // two tiles per loop iteration, so that the gather slot of each is a constant; the
+  // scheduling barrier keeps the two tiles from being interleaved, which would double the
+  // live registers
+  static_assert(NSLOT == 2, "tile j uses gather slot j % 2");
   for (int j = 0; j < n_iter; j += 2) {
-    tile(j, rc, rs, rbc, rbs);
+    tile(j, 0);
     __builtin_amdgcn_sched_barrier(0);
-    if (j + 1 < n_iter) tile(j + 1, rbc, rbs, rc, rs);
+    if (j + 1 < n_iter) tile(j + 1, 1);
     __builtin_amdgcn_sched_barrier(0);
   }
   wait_vm<0>();  // nothing may land in the ring once it is reused below
@@ -1041,7 +1118,10 @@ static void launch_splitk_t(const SplitParams& p, int out_dtype, dim3 grid, dim3
   const int slot = (g_prof.on && g_prof.n < g_prof.cap) ? g_prof.n++ : -1;
   hipEvent_t* ev = slot >= 0 ? g_prof.ev + 3 * slot : nullptr;
   if (ev) (void)hipEventRecord(ev[0], st);
-  hipLaunchKernelGGL((splitk_kernel<DT, RT>), grid, dim3(NTHREADS), 0, st, p);
+  if (p.hpg > 8)
+    hipLaunchKernelGGL((splitk_kernel<DT, RT, true>), grid, dim3(NTHREADS), 0, st, p);
+  else
+    hipLaunchKernelGGL((splitk_kernel<DT, RT, false>), grid, dim3(NTHREADS), 0, st, p);
   if (ev) (void)hipEventRecord(ev[1], st);
   if (!p.fused_merge) {
     if (out_dtype == DKV_F32)
