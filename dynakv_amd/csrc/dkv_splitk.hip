@@ -36,6 +36,10 @@ constexpr int TILE = 16;
 constexpr int WAVES = 8;        // per workgroup: two per SIMD
 constexpr int NTHREADS = WAVES * 64;
 constexpr int BK_LD = 136;    // LDS row pitch (elements) of the transposed K basis
+// K^T is formed as 4 pairs pp of 16-dim blocks (pp, pp + 4); the basis rows of the first
+// NREG_PP pairs stay in registers, the others are read from LDS per tile
+constexpr int NREG_PP = 3;
+constexpr int SBH_ROWS = 32 * (4 - NREG_PP);
 constexpr int VT_LD = 136;    // LDS row pitch (elements) of a wave's V tile
 constexpr int PREC = DH + 2;  // floats per partial record: m, l, acc[128]
 constexpr int NSLOT = 2;        // gather slots per wave: the current tile + one in flight
@@ -241,57 +245,91 @@ __device__ __forceinline__ void wait_vm() {
 
 // LSE-merge the split records of one unit, normalise with the route's denominator, project
 // once through the unit's V basis and store the hpg output rows (all threads of the block).
-// vbr: this thread's share of the V basis, loaded by the caller (vb_chunks 16-byte pieces);
-// scratch: LDS for the basis ([rank][DH] bf16/fp16) and (32 + 16 * DH) floats.
+// vbr: this thread's share of the V basis, loaded by the caller (VB_CHUNKS 16-byte pieces, zero
+// past rank R); scratch: LDS for the basis ([128][DH] bf16/fp16) and 16 * DH floats.
 template <int DT, int ROUTE, int ODT>
 __device__ __forceinline__ void merge_unit_t(const SplitParams& p, int unit, uint8_t* scratch,
                                              const dkv_u32x4 (&vbr)[VB_CHUNKS]) {
   const int b = unit / p.Hkv, kvh = unit % p.Hkv;
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n = lane & 15, g = lane >> 4;
   const long long stride = (long long)p.hpg * PREC;  // between splits of one head
   const float* base = p.partials + (long long)unit * p.n_splits * stride;
-  uint16_t* sVB = reinterpret_cast<uint16_t*>(scratch);  // [R][DH]
-  float* sM = reinterpret_cast<float*>(scratch + DH * DH * 2);  // [16] max of each head
-  float* sInv = sM + 16;                                      // [16] 1 / denominator
-  float* sA = sM + 32;                                        // [16][DH] merged accumulators
+  uint16_t* sVB = reinterpret_cast<uint16_t*>(scratch);          // [128][DH], rank-major
+  float* sA = reinterpret_cast<float*>(scratch + DH * DH * 2);    // [16][DH] merged, normalised
 #pragma unroll
-  for (int k = 0; k < VB_CHUNKS; ++k) {
-    const int ch = tid + k * NTHREADS;  // 16-byte piece: rank ch / 16, dims 8 * (ch % 16)
-    if (ch < p.R * (DH / 8)) *(dkv_u32x4*)(sVB + ch * 8) = vbr[k];
-  }
-  if (tid < p.hpg) {
-    float M = -INFINITY;
-    for (int sp = 0; sp < p.n_splits; ++sp) M = fmaxf(M, base[sp * stride + tid * PREC]);
-    float L = 0.f;
-    for (int sp = 0; sp < p.n_splits; ++sp) {
-      const float* r = base + sp * stride + tid * PREC;
-      L += (M == -INFINITY) ? 0.f : exp2f(r[0] - M) * r[1];
-    }
-    const float den = ROUTE == DKV_ROUTE_TWO_STAGE ? fmaxf(L, 1e-6f) : L;
-    sM[tid] = M;
-    sInv[tid] = 1.f / den;
-  }
-  __syncthreads();
-  for (int idx = tid; idx < p.hpg * DH; idx += NTHREADS) {
+  for (int k = 0; k < VB_CHUNKS; ++k)  // 16-byte piece ch: rank ch / 16, dims 8 * (ch % 16)
+    *(dkv_u32x4*)(sVB + (tid + k * NTHREADS) * 8) = vbr[k];
+  // merged coefficient of (head slot hs, rank r): one pass over the splits with a running
+  // maximum (all loads of a thread are independent); slots past hpg are zero
+  for (int idx = tid; idx < 16 * DH; idx += NTHREADS) {
     const int hs = idx / DH, r = idx % DH;
-    const float M = sM[hs];
     float a = 0.f;
-    if (r < p.R)
+    if (hs < p.hpg) {
+      float M = -INFINITY, L = 0.f, A = 0.f;
       for (int sp = 0; sp < p.n_splits; ++sp) {
         const float* rec = base + sp * stride + hs * PREC;
-        a += (M == -INFINITY) ? 0.f : exp2f(rec[0] - M) * rec[2 + r];
+        const float m = rec[0], l = rec[1], x = r < p.R ? rec[2 + r] : 0.f;
+        const float Mn = fmaxf(M, m);
+        const float so = M == -INFINITY ? 0.f : exp2f(M - Mn);
+        const float sn = m == -INFINITY ? 0.f : exp2f(m - Mn);
+        L = L * so + l * sn;
+        A = A * so + x * sn;
+        M = Mn;
       }
-    sA[hs * DH + r] = a * sInv[hs];
+      const float den = ROUTE == DKV_ROUTE_TWO_STAGE ? fmaxf(L, 1e-6f) : L;
+      a = A / den;
+    }
+    sA[idx] = a;
   }
   __syncthreads();
-  for (int idx = tid; idx < p.hpg * DH; idx += NTHREADS) {
-    const int hs = idx / DH, d = idx % DH;
-    const float* a = sA + hs * DH;
-    float o = 0.f;
-#pragma unroll 8
-    for (int j = 0; j < p.R; ++j) o = fmaf(a[j], elt_to_f32<DT>(sVB[j * DH + d]), o);
-    const long long oi = (long long)b * p.out_sb + (long long)(kvh * p.hpg + hs) * p.out_sh + d;
-    dkv_store_f32<ODT>(p.out, oi, o);
+  // out[hs][d] = sum_r a[hs][r] VB[r][d] on 16x16x32 MFMA: wave w takes dims 16w..16w+15.
+  // A: the merged coefficients of head slot n, ranks 32c + 8g..+7, as hi + lo parts in the
+  // basis dtype (two products); B: the basis read transposed -- within a 16-lane group, lane i
+  // gets element i%4 of the 8 bytes read by lane 4j + i/4 as its element j, so lane L reading
+  // VB[k0 + L/4][d0 + 4*(L%4) ..] hands lane i the four ranks k0..k0+3 of dim d0 + i.
+  const int d0 = 16 * wave;
+  dkv_f32x4 o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int k0 = 32 * c + 8 * g;
+    const float* ar = sA + n * DH + k0;
+    const dkv_f32x4 x0 = *(const dkv_f32x4*)ar, x1 = *(const dkv_f32x4*)(ar + 4);
+    const float xs[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+    uint32_t hi[4], lo[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if constexpr (DT == DKV_BF16) {
+        typedef __attribute__((ext_vector_type(2))) float f32x2;
+        const dkv_bf16x2 h = __builtin_convertvector(f32x2{xs[2 * e], xs[2 * e + 1]}, dkv_bf16x2);
+        const dkv_bf16x2 l = __builtin_convertvector(
+            f32x2{xs[2 * e] - (float)h[0], xs[2 * e + 1] - (float)h[1]}, dkv_bf16x2);
+        hi[e] = __builtin_bit_cast(uint32_t, h);
+        lo[e] = __builtin_bit_cast(uint32_t, l);
+      } else {
+        split_f16x2(xs[2 * e], xs[2 * e + 1], p.minus_one, hi[e], lo[e]);
+      }
+    }
+    const uint16_t* src = sVB + (k0 + (n >> 2)) * DH + d0 + 4 * (n & 3);
+    typedef __attribute__((address_space(3))) dkv_i16x4 lds_i16x4;
+    const dkv_u32x2 b0 = __builtin_bit_cast(
+        dkv_u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                       (lds_i16x4*)(__attribute__((address_space(3))) uint16_t*)src));
+    const dkv_u32x2 b1 = __builtin_bit_cast(
+        dkv_u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                       (lds_i16x4*)(__attribute__((address_space(3))) uint16_t*)(src + 4 * DH)));
+    const dkv_u32x4 bop = dkv_u32x4{b0.x, b0.y, b1.x, b1.y};
+    o = mfma_k<DT>(dkv_u32x4{lo[0], lo[1], lo[2], lo[3]}, bop, o);
+    o = mfma_k<DT>(dkv_u32x4{hi[0], hi[1], hi[2], hi[3]}, bop, o);
+  }
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int hs = 4 * g + u;
+    if (hs < p.hpg) {
+      const long long oi =
+          (long long)b * p.out_sb + (long long)(kvh * p.hpg + hs) * p.out_sh + d0 + n;
+      dkv_store_f32<ODT>(p.out, oi, o[u]);
+    }
   }
 }
 template <int DT, int ROUTE>
@@ -314,7 +352,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
   // staging copy, the per-tile query operand and the epilogue scratch alias the rings.
   __shared__ __attribute__((aligned(16))) uint32_t sMask[MASK_ROWS][4];
   __shared__ __attribute__((aligned(16))) int sTabRing[WAVES][TSLOT][4][TILE];
-  __shared__ __attribute__((aligned(16))) uint16_t sBH[DH / 2 * BK_LD];
+  __shared__ __attribute__((aligned(16))) uint16_t sBH[SBH_ROWS * BK_LD];
   // 256-byte aligned: the query operand's row swizzle XORs bits 4..7 of ring addresses
   __shared__ __attribute__((aligned(256))) uint8_t sRing[WAVES * NSLOT * GSLOT_BYTES];
   static_assert(DH * BK_LD * 2 <= WAVES * NSLOT * GSLOT_BYTES, "basis staging fits the rings");
@@ -347,11 +385,35 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
   const int s_end = min(p.S, s_begin + p.split_len);
   const int ns = s_end - s_begin;
 
+  const int tile_first = s_begin / TILE;  // splits are whole tiles (multiples of 64 tokens)
+  const int tile0 = tile_first + wave;
+  const int n_tb = (p.S + TILE - 1) / TILE;
+  const int n_iter = max(0, ((ns + TILE - 1) / TILE - wave + WAVES - 1) / WAVES);
+  // table loads: lane (table l/16, token l%16) -> one 4-byte load per lane and tile
+  const int* tab_base;
+  int tab_ss;
+  {
+    const int tsel = lane >> 4;
+    const int* bases[4] = {p.lens_k + (long long)row * p.tk_sb, p.offs_k + (long long)row * p.tk_sb,
+                           p.lens_v + (long long)row * p.tv_sb, p.offs_v + (long long)row * p.tv_sb};
+    tab_base = tsel == 0 ? bases[0] : tsel == 1 ? bases[1] : tsel == 2 ? bases[2] : bases[3];
+    tab_ss = tsel < 2 ? (int)p.tk_ss : (int)p.tv_ss;
+  }
+  auto load_tab = [&](int j) {  // one load per lane into table slot j % TSLOT
+    const uint32_t t = (uint32_t)min((tile0 + WAVES * j) * TILE + n, s_end - 1);
+    lds_load4(tab_base + __umul24(t, (uint32_t)tab_ss), lds_addr(&sTabRing[wave][j % TSLOT][0][0]));
+  };
+  // the first two tiles' tables (the table ring does not alias the staging copy) are in
+  // flight during the prologue
+  load_tab(0);
+  load_tab(1);
+
   // ---- prologue: K basis, mask table, rotation step ---------------------------------------
   {
     // transpose to [dim][rank]: consecutive lanes take consecutive ranks, so each 2-byte LDS
-    // store of a wave covers 128 contiguous bytes (no bank conflicts). Dims 32..63 and 96..127
-    // go to their permanent place (sBH rows 0..31 and 32..63), the others to the staging copy.
+    // store of a wave covers 128 contiguous bytes (no bank conflicts). The dims of the block
+    // pairs past NREG_PP go to their permanent place in sBH (low blocks, then high blocks),
+    // the others to the staging copy.
     const uint16_t* kb = p.k_basis + (long long)kvh * p.k_unit;
     const int j = tid & 127, dq = tid >> 7;  // 4 groups of 8-dim slices
 #pragma unroll
@@ -364,8 +426,9 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
       for (int t = 0; t < 8; ++t) {
         const int d = d8 + t;
         const uint16_t x = (uint16_t)((e[t >> 1] >> (16 * (t & 1))) & 0xffffu);
-        if ((d & 32) != 0)
-          sBH[(((d >> 6) << 5) + (d & 31)) * BK_LD + j] = x;
+        const int pp = (d & 63) >> 4;
+        if (pp >= NREG_PP)
+          sBH[(((d >> 6) * (4 - NREG_PP) + pp - NREG_PP) * 16 + (d & 15)) * BK_LD + j] = x;
         else
           sBK[d * BK_LD + j] = x;
       }
@@ -426,30 +489,32 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
     q_wr = rb | (4u * (uint32_t)lane);
   }
 
-  const int tile_first = s_begin / TILE;  // splits are whole tiles (multiples of 64 tokens)
-  const int tile0 = tile_first + wave;
-  const int n_tb = (p.S + TILE - 1) / TILE;
-  const int n_iter = max(0, ((ns + TILE - 1) / TILE - wave + WAVES - 1) / WAVES);
   __syncthreads();  // staging copy, sBH, sMask ready
 
-  // recon A operands of blocks 0, 4, 1, 5 (dims 0..31 and 64..95; block blk = dims
-  // 16*blk + n, rank chunk c = ranks 32c + 8g .. +8), read straight into accumulation
-  // registers, which the MFMAs take as their A operand; blocks 2, 6, 3, 7 are read from sBH
-  // per tile.
-  dkv_u32x4 bA[4][4];  // [k][c], k -> block (k&1 ? 4 : 0) + (k >> 1)
+  // recon A operands of the block pairs pp < NREG_PP (blocks pp and pp + 4; block blk = dims
+  // 16*blk + n, rank chunk c = ranks 32c + 8g .. +8), read into the registers the MFMAs take
+  // as their A operand; the other pairs are read from sBH per tile.
+  dkv_u32x4 bA[2 * NREG_PP][4];  // [k][c], k -> block (k&1 ? 4 : 0) + (k >> 1)
   {
     const uint32_t a0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t*)(
         sBK + n * BK_LD + 8 * g);
+    // one statement per block: its four reads and the wait for them, so that the outputs
+    // hold their data when the statement ends (the compiler may copy or spill an asm output
+    // right after the statement)
 #pragma unroll
-    for (int k = 0; k < 4; ++k)
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int blk = (k & 1 ? 4 : 0) + (k >> 1);
-        asm volatile("ds_read_b128 %0, %1 offset:%2"
-                     : "=v"(bA[k][c])
-                     : "v"(a0), "i"((16 * blk * BK_LD + 32 * c) * 2));
-      }
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    for (int k = 0; k < 2 * NREG_PP; ++k) {
+      const int blk = (k & 1 ? 4 : 0) + (k >> 1);
+      asm volatile(
+          "ds_read_b128 %0, %4 offset:%5\n\t"
+          "ds_read_b128 %1, %4 offset:%6\n\t"
+          "ds_read_b128 %2, %4 offset:%7\n\t"
+          "ds_read_b128 %3, %4 offset:%8\n\t"
+          "s_waitcnt lgkmcnt(0)"
+          : "=&v"(bA[k][0]), "=&v"(bA[k][1]), "=&v"(bA[k][2]), "=&v"(bA[k][3])
+          : "v"(a0), "i"((16 * blk * BK_LD) * 2), "i"((16 * blk * BK_LD + 32) * 2),
+            "i"((16 * blk * BK_LD + 64) * 2), "i"((16 * blk * BK_LD + 96) * 2)
+          : "memory");
+    }
   }
   __syncthreads();  // every wave holds its operands: the rings may now be overwritten
 
@@ -459,20 +524,6 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
   const int k_row0 = row * p.k_ld, v_row0 = row * p.v_ld;
   // only the buffers' last row can hold a token whose 16-byte window crosses the end
   const bool last_row = row == p.B * p.G - 1;
-  // table loads: lane (table l/16, token l%16) -> one 4-byte load per lane and tile
-  const int* tab_base;
-  int tab_ss;
-  {
-    const int tsel = lane >> 4;
-    const int* bases[4] = {p.lens_k + (long long)row * p.tk_sb, p.offs_k + (long long)row * p.tk_sb,
-                           p.lens_v + (long long)row * p.tv_sb, p.offs_v + (long long)row * p.tv_sb};
-    tab_base = tsel == 0 ? bases[0] : tsel == 1 ? bases[1] : tsel == 2 ? bases[2] : bases[3];
-    tab_ss = tsel < 2 ? (int)p.tk_ss : (int)p.tv_ss;
-  }
-  auto load_tab = [&](int j) {  // one load per lane into table slot j % TSLOT
-    const uint32_t t = (uint32_t)min((tile0 + WAVES * j) * TILE + n, s_end - 1);
-    lds_load4(tab_base + __umul24(t, (uint32_t)tab_ss), lds_addr(&sTabRing[wave][j % TSLOT][0][0]));
-  };
   // token metadata of this lane's token in tile j (table slot must have arrived). A slot past
   // the split's end holds the entries of the split's last token (the table loads clamp): its
   // gathers read real data and its score is excluded in the softmax.
@@ -565,9 +616,9 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
 #pragma unroll
   for (int h = 0; h < QH; ++h) settle(qh[h]);
 
-  load_tab(0);
-  load_tab(1);
-  wait_vm<1>();  // T0
+  // T0 and T1 (a full wait: compiler-generated memory operations of the prologue, such as
+  // register spill stores, may lie between them and here and need not complete in order)
+  wait_vm<0>();
   issue(0);
 
   // one tile; par = j % NSLOT
@@ -606,7 +657,9 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
     dkv_u32x4 bq[4], bq_lo[4];
     {
       const float cb = bc, sb = bs;
-      const uint32_t wr = q_wr + (uint32_t)(par * GSLOT_BYTES);
+      // formed per tile (not hoisted as one register per row)
+      uint32_t wr = q_wr + (uint32_t)(par * GSLOT_BYTES);
+      settle(wr);
       auto rotate = [&](int h, uint32_t& hi, uint32_t& lo) {
         const float x = elt_to_f32<DT>(qh[h] & 0xffffu), y = elt_to_f32<DT>(qh[h] >> 16);
         split_f16x2(cb * x + sb * y, cb * y - sb * x, p.minus_one, hi, lo);
@@ -663,25 +716,35 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
 
     // ---- 1-3: K reconstruction, R(n) on the lane's token, fp16 K', scores -------------------
     dkv_f32x4 sc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int pp = 0; pp < 4; ++pp) {
-      dkv_f32x4 c0 = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
-      if (pp < 2) {
+    // blocks pp and pp+4 of K^T for the tile; pp < NREG_PP from the registers, the others
+    // from the streamed rows in sBH
+    auto recon = [&](int pp, dkv_f32x4& c0, dkv_f32x4& c1) {
+      c0 = dkv_f32x4{0.f, 0.f, 0.f, 0.f};
+      c1 = dkv_f32x4{0.f, 0.f, 0.f, 0.f};
+      if (pp < NREG_PP) {
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
           c0 = mfma_k<DT>(bA[2 * pp][c], xk[c], c0);
           c1 = mfma_k<DT>(bA[2 * pp + 1][c], xk[c], c1);
         }
       } else {
-        // blocks pp and pp+4 from the streamed half: sBH rows (pp-2)*16 + n and 32 + ...
-        const uint16_t* r0 = sBH + ((pp - 2) * 16 + n) * BK_LD + 8 * g;
-        const uint16_t* r1 = r0 + 32 * BK_LD;
+        const uint16_t* r0 = sBH + ((pp - NREG_PP) * 16 + n) * BK_LD + 8 * g;
+        const uint16_t* r1 = r0 + (4 - NREG_PP) * 16 * BK_LD;
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
           c0 = mfma_k<DT>(*(const dkv_u32x4*)(r0 + 32 * c), xk[c], c0);
           c1 = mfma_k<DT>(*(const dkv_u32x4*)(r1 + 32 * c), xk[c], c1);
         }
       }
+    };
+    // software-pipelined by one block pair: the products of pp+1 are issued before the
+    // rotation of pp, so the MFMA pipe and the VALU work of one wave overlap
+    dkv_f32x4 C0[2], C1[2];
+    recon(0, C0[0], C1[0]);
+#pragma unroll
+    for (int pp = 0; pp < 4; ++pp) {
+      if (pp + 1 < 4) recon(pp + 1, C0[(pp + 1) & 1], C1[(pp + 1) & 1]);
+      const dkv_f32x4 c0 = C0[pp & 1], c1 = C1[pp & 1];
       uint32_t k4[4];
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
@@ -822,6 +885,8 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
   float* sw = reinterpret_cast<float*>(sRing);  // [WAVES][16 m | 16 l | 16 x 128 acc]
   constexpr int WREC = 32 + 16 * DH;
   static_assert(WAVES * WREC * 4 <= WAVES * NSLOT * GSLOT_BYTES, "epilogue scratch fits");
+  static_assert(DH * DH * 2 + 16 * DH * 4 <= WAVES * NSLOT * GSLOT_BYTES, "merge scratch fits");
+  static_assert(WAVES * 16 == DH, "the merge projection gives each wave 16 output dims");
   float* my = sw + wave * WREC;
   if (g == 0) {
     my[n] = m_run;
