@@ -52,6 +52,9 @@ _SIGNATURES = {
     "dkv_selftest_layouts": (_i, [_vp, _vp]),
     "dkv_cutoff_workspace_bytes": (_ll, [_i, _i, _i]),
     "dkv_rope_dense": (_i, [_vp, _i, _vp, _ll, _ll, _i, _i, _i, _f]),
+    "dkv_add_rmsnorm": (_i, [_vp, _i, _vp, _ll, _vp, _ll, _vp, _vp, _ll, _i, _i, _f]),
+    "dkv_silu_mul": (_i, [_vp, _i, _vp, _ll, _vp, _ll, _i, _i]),
+    "dkv_gemv": (_i, [_vp, _i, _vp, _ll, _vp, _ll, _vp, _ll, _i, _i, _i]),
     "dkv_decode_layer": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i]),
     "dkv_prefill_attention": (_i, [_vp, _i, _vp, _ll, _ll, _ll, _vp, _ll, _ll, _ll, _ll,
                                    _vp, _ll, _ll, _ll, _ll, _vp, _i, _ll, _ll, _ll,

@@ -1,0 +1,88 @@
+"""Fused element-wise stages of the end-to-end decoder (host side of ``dkv_model.hip``).
+
+The reference runs DynaKV inside HF's Llama decoder layer (``custom_llama.py:93-323`` on
+transformers' ``LlamaDecoderLayer``): ``hidden = residual + sublayer(...)``, ``LlamaRMSNorm``
+(fp32 statistics, normalised value rounded to the model dtype, times the weight in that dtype)
+and ``LlamaMLP`` (``down(silu(gate(h)) * up(h))``). ``add_rmsnorm_`` is the residual add fused
+with the following norm, ``silu_mul`` the activation product of one concatenated gate/up GEMM,
+``linear`` the decoder's projections: a weight-streaming kernel for decode-sized inputs (at most
+8 rows), torch's library GEMM otherwise.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+
+
+def _rows(t: torch.Tensor) -> torch.Tensor:
+    if t.stride(-1) != 1:
+        raise ValueError("rows need a unit last stride")
+    r = t.reshape(-1, t.shape[-1])
+    if r.data_ptr() != t.data_ptr():
+        raise ValueError("leading dims must flatten without a copy")
+    return r
+
+
+def add_rmsnorm_(x: torch.Tensor, delta: torch.Tensor | None, w: torch.Tensor, eps: float,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
+    """``x += delta`` in place (rounded to x's dtype) when ``delta`` is given, then returns
+    ``rmsnorm(x) * w`` (a new tensor of x's shape, or ``out``)."""
+    xr = _rows(x)
+    H = xr.shape[1]
+    if out is None:
+        out = torch.empty_like(x)
+    orr = _rows(out)
+    dr = _rows(delta) if delta is not None else None
+    if dr is not None and dr.shape != xr.shape:
+        raise ValueError("delta must have x's shape")
+    if w.shape != (H,) or not w.is_contiguous() or w.dtype != x.dtype:
+        raise ValueError("w must be a contiguous (H,) vector of x's dtype")
+    lib = _lib.load()
+    rc = lib.dkv_add_rmsnorm(_lib.stream_of(x), _lib.dtype_code(x.dtype), xr.data_ptr(),
+                             xr.stride(0), dr.data_ptr() if dr is not None else None,
+                             dr.stride(0) if dr is not None else 0, w.data_ptr(), orr.data_ptr(),
+                             orr.stride(0), xr.shape[0], H, float(eps))
+    _lib.check(rc, "dkv_add_rmsnorm")
+    return out
+
+
+def silu_mul(gu: torch.Tensor) -> torch.Tensor:
+    """``gu`` (..., 2F) = [gate | up] -> silu(gate) * up (..., F)."""
+    gr = _rows(gu)
+    F2 = gr.shape[1]
+    if F2 % 2:
+        raise ValueError("gu must hold gate and up halves")
+    F = F2 // 2
+    out = torch.empty(gu.shape[:-1] + (F,), dtype=gu.dtype, device=gu.device)
+    orr = out.view(-1, F)
+    lib = _lib.load()
+    rc = lib.dkv_silu_mul(_lib.stream_of(gu), _lib.dtype_code(gu.dtype), gr.data_ptr(),
+                          gr.stride(0), orr.data_ptr(), orr.stride(0), gr.shape[0], F)
+    _lib.check(rc, "dkv_silu_mul")
+    return out
+
+
+def linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """``F.linear(x, w)`` (no bias): ``dkv_gemv`` when x has at most 8 rows and the weight is one
+    it streams faster than the library GEMM (measured on MI355X: the attention projections,
+    N <= 8192 with K <= 8192, about 12 us against 19 us; the output head, N >= 65536, 6.5 TB/s
+    against 5.7), the library GEMM otherwise (the MLP matrices, where it reaches 6.6 TB/s)."""
+    K = x.shape[-1]
+    M = x.numel() // K if K else 0
+    N = w.shape[0] if w.dim() == 2 else 0
+    if (1 <= M <= 8 and ((N <= 8192 and K <= 8192) or N >= 65536)
+            and x.dtype == w.dtype and x.dtype in (torch.bfloat16, torch.float16)
+            and w.dim() == 2 and w.shape[1] == K and w.stride(1) == 1 and K % 8 == 0
+            and M * K * 2 <= 96 * 1024 and x.is_cuda):
+        xr = x.reshape(M, K)
+        if xr.stride(1) == 1 and xr.data_ptr() % 16 == 0 and xr.stride(0) % 8 == 0 \
+                and w.data_ptr() % 16 == 0 and w.stride(0) % 8 == 0:
+            y = torch.empty(x.shape[:-1] + (N,), dtype=x.dtype, device=x.device)
+            rc = _lib.load().dkv_gemv(_lib.stream_of(x), _lib.dtype_code(x.dtype),
+                                      xr.data_ptr(), xr.stride(0), w.data_ptr(), w.stride(0),
+                                      y.data_ptr(), N, M, N, K)
+            _lib.check(rc, "dkv_gemv")
+            return y
+    return torch.nn.functional.linear(x, w)

@@ -15,8 +15,10 @@ only the forward math):
   ``compressed_attention.py:263-292``), and per-head cutoff heads whose bias ramps over the
   rank so that the retained fraction is close to a target (``retention``).
 * ``CompressedLlama.generate``: prefill (cutoff head, packed append, reconstruct-and-attend)
-  then greedy decode steps (cutoff head, decode append, routed decode attention), with
-  RMSNorm, rotary queries, SwiGLU MLP and the output head as plain library GEMMs.
+  then greedy decode steps (cutoff head, decode append, routed decode attention). The
+  projections and the output head are library GEMMs (gate and up as one concatenated GEMM);
+  the residual add with the following RMSNorm and the SwiGLU product are one fused kernel each
+  (``kernels/model_ops.py``), shared with the dense baseline.
 * ``DenseLlama.generate``: the uncompressed-cache baseline of the same weights (K/V kept in
   full in a preallocated cache, attention by torch's scaled_dot_product_attention).
 """
@@ -35,6 +37,7 @@ from .kernels.compressed_cache import CustomDynamicCache
 from .kernels.cutoff import CutoffHead
 from .kernels.decode import grouped_decode_attention
 from .kernels.layer import DecodeLayerPlan
+from .kernels.model_ops import add_rmsnorm_, linear, silu_mul
 from .kernels.prefill import compressed_prefill_attention, rope_dense_
 from .kernels.router import KernelPolicy
 
@@ -62,7 +65,8 @@ class LayerWeights:
     wv_c: torch.Tensor
     wo: torch.Tensor
     ln2: torch.Tensor
-    w_gate: torch.Tensor
+    w_gu: torch.Tensor     # (2 * ffn, hidden): gate rows, then up rows
+    w_gate: torch.Tensor   # views of w_gu
     w_up: torch.Tensor
     w_down: torch.Tensor
     k_basis: torch.Tensor  # (G, R, Dh) rank-major
@@ -122,23 +126,19 @@ class RandomLlama:
             wv_c = torch.matmul(Uv.transpose(1, 2), wv.float().view(G, Dh, H)).reshape(G * Dh, H)
             cut = [rnd(G, Dh, Dh) for _ in range(2)]
             bias = [ramp.expand(G, Dh).contiguous() for _ in range(2)]
+            w_gu = rnd(2 * s.ffn, H)
             self.layers.append(LayerWeights(
                 ln1=torch.ones(H, device=self.device, dtype=dtype), wq=rnd(H, H), wk=wk, wv=wv,
                 wk_c=wk_c.to(dtype), wv_c=wv_c.to(dtype), wo=rnd(H, H),
                 ln2=torch.ones(H, device=self.device, dtype=dtype),
-                w_gate=rnd(s.ffn, H), w_up=rnd(s.ffn, H), w_down=rnd(H, s.ffn),
+                w_gu=w_gu, w_gate=w_gu[:s.ffn], w_up=w_gu[s.ffn:], w_down=rnd(H, s.ffn),
                 k_basis=Uk.transpose(1, 2).contiguous().to(dtype),
                 v_basis=Uv.transpose(1, 2).contiguous().to(dtype),
                 cutoff=CutoffHead(cut[0], bias[0], cut[1], bias[1], groups=G)))
 
 
-def _rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
-    xf = x.float()
-    return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)).to(x.dtype) * w
-
-
 def _mlp(lw: LayerWeights, h: torch.Tensor) -> torch.Tensor:
-    return F.linear(F.silu(F.linear(h, lw.w_gate)) * F.linear(h, lw.w_up), lw.w_down)
+    return linear(silu_mul(linear(h, lw.w_gu)), lw.w_down)
 
 
 def _rope_q(q: torch.Tensor, pos0: int, theta: float) -> torch.Tensor:
@@ -153,7 +153,19 @@ class _Generator:
         self.s = model.shape
 
     def logits(self, x: torch.Tensor) -> torch.Tensor:
-        return F.linear(_rmsnorm(x, self.m.norm, self.s.eps), self.m.lm_head)
+        return linear(add_rmsnorm_(x, None, self.m.norm, self.s.eps), self.m.lm_head)
+
+    def _run(self, x: torch.Tensor, attn) -> torch.Tensor:
+        """The decoder layers over the residual stream ``x`` (B, S, hidden), owned and updated in
+        place; ``attn(i, lw, h)`` returns layer i's attention output (B, S, hidden) before the
+        output projection. Each residual add is fused with the norm that follows it."""
+        eps = self.s.eps
+        delta = None
+        for i, lw in enumerate(self.m.layers):
+            h = add_rmsnorm_(x, delta, lw.ln1, eps)
+            h2 = add_rmsnorm_(x, linear(attn(i, lw, h), lw.wo), lw.ln2, eps)
+            delta = _mlp(lw, h2)
+        return x.add_(delta)
 
     def generate(self, prompt: torch.Tensor, new_tokens: int) -> dict:
         """Greedy decode; returns tokens, timings and cache bytes."""
@@ -197,9 +209,9 @@ class CompressedLlama(_Generator):
     def _qkv(self, lw, h):
         B, S, _ = h.shape
         s = self.s
-        q = F.linear(h, lw.wq).view(B, S, s.heads, s.head_dim)
-        kc = F.linear(h, lw.wk_c)  # (B, S, G*Dh) coefficients
-        vc = F.linear(h, lw.wv_c)
+        q = linear(h, lw.wq).view(B, S, s.heads, s.head_dim)
+        kc = linear(h, lw.wk_c)  # (B, S, G*Dh) coefficients
+        vc = linear(h, lw.wv_c)
         k_out, v_out, len_k, len_v, _, _ = lw.cutoff.kv_process_fused(kc, vc)
         G, Dh = s.kv_heads, s.head_dim
         rows_k = k_out.view(B, S, G, Dh).transpose(1, 2).reshape(B * G, S, Dh)
@@ -214,30 +226,30 @@ class CompressedLlama(_Generator):
         self.plans = {}
         x = F.embedding(prompt, self.m.embed)
         B, S = prompt.shape
-        for i, lw in enumerate(self.m.layers):
-            h = _rmsnorm(x, lw.ln1, s.eps)
+
+        def attn(i, lw, h):
             q, rk, lk, rv, lv = self._qkv(lw, h)
             self.cache.update_sp(rk.contiguous(), lk, rv.contiguous(), lv, s.head_dim, i,
                                  s.head_dim)
             qh = _rope_q(q, 0, s.theta)
             a = compressed_prefill_attention(qh, self.cache, i, lw.k_basis, lw.v_basis,
                                              theta=s.theta)
-            x = x + F.linear(a.transpose(1, 2).reshape(B, S, s.hidden), lw.wo)
-            x = x + _mlp(lw, _rmsnorm(x, lw.ln2, s.eps))
-        return x
+            return a.transpose(1, 2).reshape(B, S, s.hidden)
+
+        return self._run(x, attn)
 
     def decode(self, tok: torch.Tensor, pos: int) -> torch.Tensor:
         s = self.s
         x = F.embedding(tok, self.m.embed)  # (B, 1, H)
         B = tok.shape[0]
-        for i, lw in enumerate(self.m.layers):
-            h = _rmsnorm(x, lw.ln1, s.eps)
+
+        def attn(i, lw, h):
             plan = self.plans.get(i)
             if plan is not None and plan.can_step():
                 # one call: cutoff head, K+V append, q RoPE, routed attention
-                q = F.linear(h, lw.wq).view(B, s.heads, s.head_dim)
-                kc = F.linear(h, lw.wk_c).view(B, -1)
-                vc = F.linear(h, lw.wv_c).view(B, -1)
+                q = linear(h, lw.wq).view(B, s.heads, s.head_dim)
+                kc = linear(h, lw.wk_c).view(B, -1)
+                vc = linear(h, lw.wv_c).view(B, -1)
                 a = plan.step(q, kc, vc, pos)
             else:
                 q, rk, lk, rv, lv = self._qkv(lw, h)
@@ -251,9 +263,9 @@ class CompressedLlama(_Generator):
                     self.plans[i] = DecodeLayerPlan(self.cache, i, lw.cutoff, lw.k_basis,
                                                     lw.v_basis, batch=B, heads=s.heads,
                                                     theta=s.theta, policy=self.policy)
-            x = x + F.linear(a.reshape(B, 1, s.hidden), lw.wo)
-            x = x + _mlp(lw, _rmsnorm(x, lw.ln2, s.eps))
-        return x
+            return a.reshape(B, 1, s.hidden)
+
+        return self._run(x, attn)
 
     def kv_bytes(self) -> int:
         """Stored bytes of the packed caches: the used part of each row plus 8 bytes of
@@ -285,9 +297,9 @@ class DenseLlama(_Generator):
     def _kv(self, lw, h, pos0):
         B, S, _ = h.shape
         s = self.s
-        q = F.linear(h, lw.wq).view(B, S, s.heads, s.head_dim)
-        k = F.linear(h, lw.wk).view(B, S, s.kv_heads, s.head_dim).transpose(1, 2).contiguous()
-        v = F.linear(h, lw.wv).view(B, S, s.kv_heads, s.head_dim).transpose(1, 2)
+        q = linear(h, lw.wq).view(B, S, s.heads, s.head_dim)
+        k = linear(h, lw.wk).view(B, S, s.kv_heads, s.head_dim).transpose(1, 2).contiguous()
+        v = linear(h, lw.wv).view(B, S, s.kv_heads, s.head_dim).transpose(1, 2)
         rope_dense_(k, theta=s.theta, pos0=pos0)
         return _rope_q(q, pos0, s.theta), k, v
 
@@ -300,8 +312,8 @@ class DenseLlama(_Generator):
         self.v = [torch.empty(shape, device=dev, dtype=dt) for _ in range(s.layers)]
         hpg = s.heads // s.kv_heads
         x = F.embedding(prompt, self.m.embed)
-        for i, lw in enumerate(self.m.layers):
-            h = _rmsnorm(x, lw.ln1, s.eps)
+
+        def attn(i, lw, h):
             qh, k, v = self._kv(lw, h, 0)
             self.k[i][:, :, :S] = k
             self.v[i][:, :, :S] = v
@@ -309,8 +321,9 @@ class DenseLlama(_Generator):
                 a = F.scaled_dot_product_attention(qh, k.repeat_interleave(hpg, dim=1),
                                                    v.repeat_interleave(hpg, dim=1),
                                                    is_causal=True)
-            x = x + F.linear(a.transpose(1, 2).reshape(B, S, s.hidden), lw.wo)
-            x = x + _mlp(lw, _rmsnorm(x, lw.ln2, s.eps))
+            return a.transpose(1, 2).reshape(B, S, s.hidden)
+
+        x = self._run(x, attn)
         self.len = S
         return x
 
@@ -322,8 +335,8 @@ class DenseLlama(_Generator):
         B = tok.shape[0]
         L = self.len
         hpg = s.heads // s.kv_heads
-        for i, lw in enumerate(self.m.layers):
-            h = _rmsnorm(x, lw.ln1, s.eps)
+
+        def attn(i, lw, h):
             qh, k, v = self._kv(lw, h, pos)
             self.k[i][:, :, L:L + 1] = k
             self.v[i][:, :, L:L + 1] = v
@@ -331,8 +344,9 @@ class DenseLlama(_Generator):
             with sdpa_kernel(_FAST_SDPA):
                 a = F.scaled_dot_product_attention(qg, self.k[i][:, :, :L + 1],
                                                    self.v[i][:, :, :L + 1])
-            x = x + F.linear(a.reshape(B, 1, s.hidden), lw.wo)
-            x = x + _mlp(lw, _rmsnorm(x, lw.ln2, s.eps))
+            return a.reshape(B, 1, s.hidden)
+
+        x = self._run(x, attn)
         self.len = L + 1
         return x
 

@@ -314,6 +314,36 @@ typedef struct DkvDecodeLayer {
 int dkv_decode_layer(void* stream, const DkvDecodeLayer* layer, void* q, const void* k_coef,
                      const void* v_coef, void* out, int seq, int pos);
 
+/*
+ * Element-wise stages of the end-to-end decoder around the attention (the HF Llama decoder
+ * layer the reference runs, custom_llama.py:93-323 on transformers' LlamaDecoderLayer and
+ * LlamaRMSNorm / LlamaMLP), one kernel each instead of torch's chains of element-wise kernels.
+ *
+ * dkv_add_rmsnorm: for each of rows rows (H <= 8192, H % 8 == 0): if delta is non-NULL,
+ * x = round(x + delta) in place (the residual add); then out = round(round(x * rsqrt(mean(x^2)
+ * + eps)) * w) (LlamaRMSNorm: fp32 statistics, the normalised value rounded to dtype, times the
+ * weight in dtype). Row strides x_ld / delta_ld / out_ld in elements; 16-byte aligned rows.
+ *
+ * dkv_silu_mul: out[r][j] = round(round(silu(g)) * u), g = gu[r][j], u = gu[r][F + j] (the
+ * gate and up projections of one concatenated GEMM), silu(g) = g / (1 + e^-g) in fp32 (LlamaMLP
+ * act_fn(gate_proj(x)) * up_proj(x)). F % 8 == 0, 16-byte aligned rows.
+ */
+int dkv_add_rmsnorm(void* stream, int dtype, void* x, long long x_ld, const void* delta,
+                    long long delta_ld, const void* w, void* out, long long out_ld, int rows,
+                    int H, float eps);
+int dkv_silu_mul(void* stream, int dtype, const void* gu, long long gu_ld, void* out,
+                 long long out_ld, int rows, int F);
+
+/*
+ * dkv_gemv: y[m][n] = sum_k x[m][k] W[n][k] for m < M <= 8 (the decode-time linear layers of
+ * the decoder, torch's F.linear(x, W) with W (N, K) row-major): fp32 accumulation, y rounded
+ * once to dtype. K % 8 == 0, M * K * 2 <= 96 KiB (x is staged in LDS), 16-byte aligned x and
+ * W rows; row strides x_ld, w_ld, y_ld in elements. DKV_E_UNSUPPORTED for other shapes (the
+ * caller uses a library GEMM then).
+ */
+int dkv_gemv(void* stream, int dtype, const void* x, long long x_ld, const void* W,
+             long long w_ld, void* y, long long y_ld, int M, int N, int K);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,98 @@
+"""Fused residual-add + RMSNorm and SwiGLU product (dkv_model.hip) against torch: the residual
+add is bit-exact (one fp32 add of two dtype values, rounded once); the normalised output and
+the activation product are within two units in the last place of the dtype, with almost all
+elements identical: each is rounded twice (the normalised value or silu(g), then its product
+with the weight or with up), and the first rounding can land on the neighbouring value (the
+kernel sums the squares in a different order than the reference's reduction, and evaluates
+e^-g with the device exp)."""
+import pytest
+import torch
+import torch.nn.functional as F
+
+from dynakv_amd.kernels.model_ops import add_rmsnorm_, silu_mul
+
+
+def _ulps(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """Distance in units in the last place between same-sign 16-bit floats."""
+    ai = a.view(torch.int16).to(torch.int32)
+    bi = b.view(torch.int16).to(torch.int32)
+    return (ai - bi).abs()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rows,H", [(1, 4096), (5, 4096), (3, 1024), (2, 8192), (300, 512)])
+def test_add_rmsnorm(dev, dtype, rows, H):
+    print(f"[gpu] add_rmsnorm {dtype} rows={rows} H={H}", flush=True)
+    g = torch.Generator(device="cpu").manual_seed(rows * 7919 + H)
+    x = torch.randn(rows, H, generator=g).to(dtype).to(dev)
+    d = torch.randn(rows, H, generator=g).to(dtype).to(dev)
+    w = (1 + 0.1 * torch.randn(H, generator=g)).to(dtype).to(dev)
+    eps = 1e-5
+    r = (x.float() + d.float()).to(dtype)
+    xs = x.clone()
+    out = add_rmsnorm_(xs, d, w, eps)
+    assert torch.equal(xs, r), "residual add"
+    rf = r.double()
+    ref = (rf * torch.rsqrt(rf.pow(2).mean(-1, keepdim=True) + eps)).to(dtype)
+    ref = (ref.double() * w.double()).to(dtype)
+    u = _ulps(out, ref)
+    print(f"[parity] add_rmsnorm: max ulp {int(u.max())}, differing {float((u > 0).float().mean()):.4f}",
+          flush=True)
+    assert int(u.max()) <= 2 and float((u > 0).float().mean()) < 0.02
+    # without the residual the input is left as it is
+    xs2 = r.clone()
+    out2 = add_rmsnorm_(xs2, None, w, eps)
+    assert torch.equal(xs2, r) and torch.equal(out2, out)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rows,Fdim", [(1, 14336), (4, 14336), (7, 1000), (3, 8)])
+def test_silu_mul(dev, dtype, rows, Fdim):
+    print(f"[gpu] silu_mul {dtype} rows={rows} F={Fdim}", flush=True)
+    g = torch.Generator(device="cpu").manual_seed(rows * 31 + Fdim)
+    gu = (3 * torch.randn(rows, 2 * Fdim, generator=g)).to(dtype).to(dev)
+    out = silu_mul(gu)
+    gate, up = gu[:, :Fdim].double(), gu[:, Fdim:].double()
+    ref = ((gate / (1 + torch.exp(-gate))).to(dtype).double() * up).to(dtype)
+    u = _ulps(out, ref)
+    print(f"[parity] silu_mul: max ulp {int(u.max())}, differing {float((u > 0).float().mean()):.4f}",
+          flush=True)
+    assert int(u.max()) <= 2 and float((u > 0).float().mean()) < 0.02
+    # the torch expression the model used before these kernels
+    t = F.silu(gu[:, :Fdim]) * gu[:, Fdim:]
+    assert int(_ulps(out, t).max()) <= 2
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (4, 1024, 4096), (3, 28672, 4096),
+                                   (2, 4096, 14336), (8, 130, 1024), (5, 7, 96)])
+def test_gemv(dev, dtype, M, N, K):
+    """Against a float64 product of the same inputs: error within fp32 accumulation plus one
+    rounding of y."""
+    from dynakv_amd import _lib
+    from dynakv_amd.kernels.model_ops import linear
+    print(f"[gpu] gemv {dtype} M={M} N={N} K={K}", flush=True)
+    g = torch.Generator(device="cpu").manual_seed(M * 1000003 + N * 31 + K)
+    x = torch.randn(M, K, generator=g).to(dtype).to(dev)
+    w = (0.02 * torch.randn(N, K, generator=g)).to(dtype).to(dev)
+    y = torch.empty(M, N, dtype=dtype, device=dev)
+    rc = _lib.load().dkv_gemv(_lib.stream_of(x), _lib.dtype_code(dtype), x.data_ptr(), K,
+                              w.data_ptr(), K, y.data_ptr(), N, M, N, K)
+    _lib.check(rc, "dkv_gemv")
+    ref = x.double() @ w.double().T
+    err = (y.double() - ref).abs()
+    bound = ref.abs() * 2.0 ** (-8 if dtype == torch.bfloat16 else -11) + 1e-5 * (
+        x.double().abs() @ w.double().abs().T)
+    print(f"[parity] gemv: max err {float(err.max()):.3e}, worst ratio "
+          f"{float((err / bound).max()):.3f}", flush=True)
+    assert bool((err <= bound).all())
+    # the model's entry point: this kernel where it is the faster one, the library GEMM else
+    y2 = linear(x, w)
+    if (N <= 8192 and K <= 8192) or N >= 65536:
+        assert torch.equal(y2, y)
+    else:
+        assert bool(((y2.double() - ref).abs() <= bound).all())
+
