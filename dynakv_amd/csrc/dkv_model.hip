@@ -168,10 +168,10 @@ extern "C" int dkv_silu_mul(void* stream, int dtype, const void* gu, long long g
 // ---------------------------------------------------------------------------------------
 // Skinny GEMM for decode: y[m][n] = sum_k x[m][k] W[n][k] (torch's F.linear with the weight
 // W (N, K) row-major), M <= 8 rows of x. The weights stream once from HBM. A workgroup of 4
-// waves stages x in LDS once; each wave then takes blocks of ROWS output columns n
-// grid-stride, each lane loading 16 contiguous bytes of each of the ROWS weight rows per step
-// (one wave: 1 KB per row, coalesced); products on v_dot2_f32_{bf16,f16}, lane partial sums
-// reduced per block, y rounded once to the dtype.
+// waves stages x in LDS once (when it fits; else each lane reads x from global memory) and
+// takes blocks of ROWS output columns grid-stride; each lane loads 16 contiguous bytes of each
+// of the ROWS weight rows per step (one wave: 1 KB per row, coalesced); products on
+// v_dot2_f32_{bf16,f16}, lane partial sums reduced per block, y rounded once to the dtype.
 // ---------------------------------------------------------------------------------------
 namespace {
 
@@ -193,20 +193,33 @@ __device__ __forceinline__ float dot8(const dkv_u32x4& a, const dkv_u32x4& b, fl
   return c;
 }
 
-template <int DT, int M>
+// XLDS: x staged in LDS (M * K * 2 bytes); otherwise each lane reads its x pieces from global
+// memory (cache hits after the first wave) -- for M * K too large to stage.
+// KSPLIT: the 4 waves of a workgroup share each block of ROWS columns, wave w taking the
+// quarter w of K, and add their partial sums through LDS -- four times the waves for a small
+// N; otherwise each wave owns its blocks.
+template <int DT, int M, bool XLDS, bool KSPLIT>
 __global__ __launch_bounds__(GV_WAVES * 64) void gemv_kernel(
     const uint16_t* __restrict__ x, long long x_ld, const uint16_t* __restrict__ W,
     long long w_ld, uint16_t* __restrict__ y, long long y_ld, int N, int K) {
-  extern __shared__ __attribute__((aligned(16))) uint16_t sx[];  // [M][K]
+  extern __shared__ __attribute__((aligned(16))) uint16_t sx[];  // [M][K] (XLDS)
+  __shared__ float sP[GV_WAVES][GV_ROWS][M];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  for (int c = tid; c < M * (K / 8); c += GV_WAVES * 64) {
-    const int m = c / (K / 8), kk = 8 * (c % (K / 8));
-    *(dkv_u32x4*)(sx + m * K + kk) = *(const dkv_u32x4*)(x + (long long)m * x_ld + kk);
+  if constexpr (XLDS) {
+    for (int c = tid; c < M * (K / 8); c += GV_WAVES * 64) {
+      const int m = c / (K / 8), kk = 8 * (c % (K / 8));
+      *(dkv_u32x4*)(sx + m * K + kk) = *(const dkv_u32x4*)(x + (long long)m * x_ld + kk);
+    }
+    __syncthreads();
   }
-  __syncthreads();
-  // wave-level blocks of GV_ROWS output columns, grid-stride over the waves of the grid
   const int nblk = (N + GV_ROWS - 1) / GV_ROWS;
-  for (int blk = blockIdx.x * GV_WAVES + wave; blk < nblk; blk += gridDim.x * GV_WAVES) {
+  // K range of this wave (multiples of 8)
+  const int kq = KSPLIT ? ((K / 8 + GV_WAVES - 1) / GV_WAVES) * 8 : K;
+  const int kb = KSPLIT ? min(wave * kq, K) : 0, ke = KSPLIT ? min(kb + kq, K) : K;
+  const int first = KSPLIT ? blockIdx.x : blockIdx.x * GV_WAVES + wave;
+  const int step = KSPLIT ? gridDim.x : gridDim.x * GV_WAVES;
+  // KSPLIT: every wave of the workgroup runs the same number of iterations (the barriers)
+  for (int blk = first; blk < nblk; blk += step) {
     const int n0 = blk * GV_ROWS;
     float acc[GV_ROWS][M];
 #pragma unroll
@@ -216,14 +229,15 @@ __global__ __launch_bounds__(GV_WAVES * 64) void gemv_kernel(
     const uint16_t* wr[GV_ROWS];
 #pragma unroll
     for (int r = 0; r < GV_ROWS; ++r) wr[r] = W + (long long)min(n0 + r, N - 1) * w_ld;
-    for (int k = 8 * lane; k < K; k += 512) {
+    for (int k = kb + 8 * lane; k < ke; k += 512) {
       dkv_u32x4 wv[GV_ROWS];
 #pragma unroll
       for (int r = 0; r < GV_ROWS; ++r)
         wv[r] = __builtin_nontemporal_load((const dkv_u32x4*)(wr[r] + k));
 #pragma unroll
       for (int m = 0; m < M; ++m) {
-        const dkv_u32x4 xv = *(const dkv_u32x4*)(sx + m * K + k);
+        const dkv_u32x4 xv = XLDS ? *(const dkv_u32x4*)(sx + m * K + k)
+                                  : *(const dkv_u32x4*)(x + (long long)m * x_ld + k);
 #pragma unroll
         for (int r = 0; r < GV_ROWS; ++r) acc[r][m] = dot8<DT>(wv[r], xv, acc[r][m]);
       }
@@ -235,10 +249,37 @@ __global__ __launch_bounds__(GV_WAVES * 64) void gemv_kernel(
         float v = acc[r][m];
 #pragma unroll
         for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-        if (lane == 0 && n0 + r < N) dkv_store_f32<DT>(y, (long long)m * y_ld + n0 + r, v);
+        acc[r][m] = v;
       }
+    if constexpr (KSPLIT) {
+      if (lane == 0)
+#pragma unroll
+        for (int r = 0; r < GV_ROWS; ++r)
+#pragma unroll
+          for (int m = 0; m < M; ++m) sP[wave][r][m] = acc[r][m];
+      __syncthreads();
+      if (tid < GV_ROWS * M) {
+        const int r = tid / M, m = tid % M;
+        if (n0 + r < N) {
+          float s = 0.f;
+#pragma unroll
+          for (int w = 0; w < GV_WAVES; ++w) s += sP[w][r][m];
+          dkv_store_f32<DT>(y, (long long)m * y_ld + n0 + r, s);
+        }
+      }
+      __syncthreads();  // sP is rewritten by the next block
+    } else {
+      if (lane == 0)
+#pragma unroll
+        for (int r = 0; r < GV_ROWS; ++r)
+#pragma unroll
+          for (int m = 0; m < M; ++m)
+            if (n0 + r < N) dkv_store_f32<DT>(y, (long long)m * y_ld + n0 + r, acc[r][m]);
+    }
   }
 }
+
+constexpr long long GV_XLDS_MAX = 64 * 1024;  // largest x staged in LDS (bytes)
 
 template <int DT, int M>
 void launch_gemv(const void* x, long long x_ld, const void* W, long long w_ld, void* y,
@@ -246,11 +287,28 @@ void launch_gemv(const void* x, long long x_ld, const void* W, long long w_ld, v
   // as many workgroups as can be resident at once (LDS bound, at most 8 per CU on 256 CUs);
   // each stages x once
   const int nblk = (N + GV_ROWS - 1) / GV_ROWS;
-  const int per_cu = max(1, min(8, (160 * 1024) / (M * K * 2 + 1024)));
-  const dim3 grid((unsigned)min((nblk + GV_WAVES - 1) / GV_WAVES, 256 * per_cu));
-  hipLaunchKernelGGL((gemv_kernel<DT, M>), grid, dim3(GV_WAVES * 64),
-                     (size_t)M * K * 2, st, (const uint16_t*)x, x_ld, (const uint16_t*)W, w_ld,
-                     (uint16_t*)y, y_ld, N, K);
+  const bool xlds = (long long)M * K * 2 <= GV_XLDS_MAX;
+  const int per_cu = xlds ? max(1, min(8, (160 * 1024) / (M * K * 2 + 1024))) : 8;
+  // fewer column blocks than twice the chip's wave slots at 8 waves per CU: split K
+  const bool ksplit = nblk < 2 * 256 * 8;
+  const int wg_blocks = ksplit ? nblk : (nblk + GV_WAVES - 1) / GV_WAVES;
+  const dim3 grid((unsigned)min(wg_blocks, 256 * per_cu));
+  const size_t lds = xlds ? (size_t)M * K * 2 : 0;
+  const uint16_t* xp = (const uint16_t*)x;
+  const uint16_t* wp = (const uint16_t*)W;
+  uint16_t* yp = (uint16_t*)y;
+  if (xlds && ksplit)
+    hipLaunchKernelGGL((gemv_kernel<DT, M, true, true>), grid, dim3(GV_WAVES * 64), lds, st, xp,
+                       x_ld, wp, w_ld, yp, y_ld, N, K);
+  else if (xlds)
+    hipLaunchKernelGGL((gemv_kernel<DT, M, true, false>), grid, dim3(GV_WAVES * 64), lds, st,
+                       xp, x_ld, wp, w_ld, yp, y_ld, N, K);
+  else if (ksplit)
+    hipLaunchKernelGGL((gemv_kernel<DT, M, false, true>), grid, dim3(GV_WAVES * 64), lds, st,
+                       xp, x_ld, wp, w_ld, yp, y_ld, N, K);
+  else
+    hipLaunchKernelGGL((gemv_kernel<DT, M, false, false>), grid, dim3(GV_WAVES * 64), lds, st,
+                       xp, x_ld, wp, w_ld, yp, y_ld, N, K);
 }
 
 template <int DT>
@@ -275,8 +333,7 @@ extern "C" int dkv_gemv(void* stream, int dtype, const void* x, long long x_ld, 
   if (dtype != DKV_BF16 && dtype != DKV_F16) return DKV_E_UNSUPPORTED;
   if (M < 0 || N < 0 || K <= 0) return DKV_E_ARG;
   if (M == 0 || N == 0) return DKV_OK;
-  if (M > 8 || K % 8 != 0 || (long long)M * K * 2 > 96 * 1024)
-    return DKV_E_UNSUPPORTED;
+  if (M > 8 || K % 8 != 0) return DKV_E_UNSUPPORTED;
   if (!x || !W || !y || x_ld < K || w_ld < K || y_ld < N) return DKV_E_ARG;
   if (!aligned16(x) || !aligned16(W) || (x_ld & 7) || (w_ld & 7)) return DKV_E_UNSUPPORTED;
   hipStream_t st = (hipStream_t)stream;

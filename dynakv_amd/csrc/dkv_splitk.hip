@@ -261,21 +261,35 @@ __device__ __forceinline__ void merge_unit_t(const SplitParams& p, int unit, uin
   for (int k = 0; k < VB_CHUNKS; ++k)  // 16-byte piece ch: rank ch / 16, dims 8 * (ch % 16)
     *(dkv_u32x4*)(sVB + (tid + k * NTHREADS) * 8) = vbr[k];
   // merged coefficient of (head slot hs, rank r): one pass over the splits with a running
-  // maximum (all loads of a thread are independent); slots past hpg are zero
+  // maximum, MB splits at a time (their record loads are all issued before any is used, so
+  // a call with many splits pays one load latency per MB splits); slots past hpg are zero
+  constexpr int MB = 8;
   for (int idx = tid; idx < 16 * DH; idx += NTHREADS) {
     const int hs = idx / DH, r = idx % DH;
     float a = 0.f;
     if (hs < p.hpg) {
       float M = -INFINITY, L = 0.f, A = 0.f;
-      for (int sp = 0; sp < p.n_splits; ++sp) {
-        const float* rec = base + sp * stride + hs * PREC;
-        const float m = rec[0], l = rec[1], x = r < p.R ? rec[2 + r] : 0.f;
-        const float Mn = fmaxf(M, m);
-        const float so = M == -INFINITY ? 0.f : exp2f(M - Mn);
-        const float sn = m == -INFINITY ? 0.f : exp2f(m - Mn);
-        L = L * so + l * sn;
-        A = A * so + x * sn;
-        M = Mn;
+      for (int sp0 = 0; sp0 < p.n_splits; sp0 += MB) {
+        float mb[MB], lb[MB], xb[MB];
+#pragma unroll
+        for (int u = 0; u < MB; ++u) {
+          const int sp = min(sp0 + u, p.n_splits - 1);
+          const float* rec = base + sp * stride + hs * PREC;
+          mb[u] = rec[0];
+          lb[u] = rec[1];
+          xb[u] = r < p.R ? rec[2 + r] : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < MB; ++u) {
+          if (sp0 + u >= p.n_splits) break;
+          const float m = mb[u];
+          const float Mn = fmaxf(M, m);
+          const float so = M == -INFINITY ? 0.f : exp2f(M - Mn);
+          const float sn = m == -INFINITY ? 0.f : exp2f(m - Mn);
+          L = L * so + lb[u] * sn;
+          A = A * so + xb[u] * sn;
+          M = Mn;
+        }
       }
       const float den = ROUTE == DKV_ROUTE_TWO_STAGE ? fmaxf(L, 1e-6f) : L;
       a = A / den;

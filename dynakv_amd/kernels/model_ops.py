@@ -65,17 +65,18 @@ def silu_mul(gu: torch.Tensor) -> torch.Tensor:
 
 
 def linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
-    """``F.linear(x, w)`` (no bias): ``dkv_gemv`` when x has at most 8 rows and the weight is one
-    it streams faster than the library GEMM (measured on MI355X: the attention projections,
-    N <= 8192 with K <= 8192, about 12 us against 19 us; the output head, N >= 65536, 6.5 TB/s
-    against 5.7), the library GEMM otherwise (the MLP matrices, where it reaches 6.6 TB/s)."""
+    """``F.linear(x, w)`` (no bias): ``dkv_gemv`` when x has at most 8 rows (decode), the
+    library GEMM otherwise. With weights streamed from HBM (as in a decode step, where no
+    matrix is reused before the others evict it) the kernel measured on MI355X: the Llama-3-8B
+    attention projections ~8-14 us against ~18 us, gate/up 5.9 TB/s against 3.7, down on par.
+    x larger than 64 KiB (down with 3+ rows) goes to the library GEMM: unstaged, the kernel is
+    slower there."""
     K = x.shape[-1]
     M = x.numel() // K if K else 0
     N = w.shape[0] if w.dim() == 2 else 0
-    if (1 <= M <= 8 and ((N <= 8192 and K <= 8192) or N >= 65536)
-            and x.dtype == w.dtype and x.dtype in (torch.bfloat16, torch.float16)
-            and w.dim() == 2 and w.shape[1] == K and w.stride(1) == 1 and K % 8 == 0
-            and M * K * 2 <= 96 * 1024 and x.is_cuda):
+    if (1 <= M <= 8 and M * K * 2 <= 64 * 1024 and x.dtype == w.dtype
+            and x.dtype in (torch.bfloat16, torch.float16) and w.dim() == 2 and w.shape[1] == K
+            and w.stride(1) == 1 and K % 8 == 0 and x.is_cuda):
         xr = x.reshape(M, K)
         if xr.stride(1) == 1 and xr.data_ptr() % 16 == 0 and xr.stride(0) % 8 == 0 \
                 and w.data_ptr() % 16 == 0 and w.stride(0) % 8 == 0:

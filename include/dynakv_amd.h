@@ -337,9 +337,8 @@ int dkv_silu_mul(void* stream, int dtype, const void* gu, long long gu_ld, void*
 /*
  * dkv_gemv: y[m][n] = sum_k x[m][k] W[n][k] for m < M <= 8 (the decode-time linear layers of
  * the decoder, torch's F.linear(x, W) with W (N, K) row-major): fp32 accumulation, y rounded
- * once to dtype. K % 8 == 0, M * K * 2 <= 96 KiB (x is staged in LDS), 16-byte aligned x and
- * W rows; row strides x_ld, w_ld, y_ld in elements. DKV_E_UNSUPPORTED for other shapes (the
- * caller uses a library GEMM then).
+ * once to dtype. K % 8 == 0, 16-byte aligned x and W rows; row strides x_ld, w_ld, y_ld in
+ * elements. DKV_E_UNSUPPORTED for other shapes (the caller uses a library GEMM then).
  */
 int dkv_gemv(void* stream, int dtype, const void* x, long long x_ld, const void* W,
              long long w_ld, void* y, long long y_ld, int M, int N, int K);
