@@ -107,3 +107,15 @@ __device__ __forceinline__ float dkv_inv_freq(int i, int Dh, float log_theta) {
   float f = (float)(2 * i) / (float)Dh;
   return expf(-f * log_theta);
 }
+
+// Rotate-half RoPE of the pair (i, i + 64) of one 128-element row in place: angle
+// float(pos) * inv_freq_i in fp32, the rotation in fp32, the results rounded to dtype DT.
+template <int DT>
+__device__ __forceinline__ void dkv_rope_pair(uint16_t* row, int i, int pos, float log_theta) {
+  const float inv = dkv_inv_freq(i, 128, log_theta);
+  const float ang = (float)pos * inv;
+  const float c = cosf(ang), sn = sinf(ang);
+  const float a = dkv_load_f32<DT>(row, i), b = dkv_load_f32<DT>(row, i + 64);
+  dkv_store_f32<DT>(row, i, a * c - b * sn);
+  dkv_store_f32<DT>(row, i + 64, b * c + a * sn);
+}

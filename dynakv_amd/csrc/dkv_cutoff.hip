@@ -25,7 +25,7 @@
 //                         compute dtype, the masked copy and the int32 length.
 // W is taken transposed, Wt[g][n][k] = W_g[k][n] (the input dimension contiguous), so both MFMA
 // operands are 16-byte row loads; the Python layer prepares that copy once per weight.
-#include "dkv_common.h"
+#include "dkv_internal.h"
 
 namespace {
 
@@ -113,17 +113,12 @@ __global__ __launch_bounds__(256) void cutoff_logits_kernel(CutoffParams p) {
   }
 }
 
-// One wave per (row m, group g, K|V). Lane l owns the E = D / 64 consecutive positions
-// l*E .. l*E + E - 1 of the row.
+// The retained count of one (row m, group g) of matrix mat, computed by one wave from the
+// rounded logits. Lane l owns the E = D / 64 consecutive positions l*E .. l*E + E - 1 of the
+// row.
 template <int DT, int E>
-__global__ __launch_bounds__(256) void cutoff_rows_kernel(CutoffParams p) {
-  const int lane = threadIdx.x & 63;
-  const long long task = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const long long n_rows = (long long)p.M * p.G;
-  if (task >= 2 * n_rows) return;
-  const int mat = (int)(task / n_rows);
-  const long long rg = task % n_rows;
-  const int m = (int)(rg / p.G), g = (int)(rg % p.G);
+__device__ __forceinline__ int cutoff_row_len(const CutoffParams& p, int mat, long long rg,
+                                              int lane) {
   const CutoffMat& cm = p.mat[mat];
   const int D = p.D;
   const uint16_t* lg = cm.logits + rg * D + lane * E;
@@ -161,7 +156,22 @@ __global__ __launch_bounds__(256) void cutoff_rows_kernel(CutoffParams p) {
   for (int e = 0; e < E; ++e) cnt += dkv_round_to<DT>(excl + x[e]) >= p.threshold ? 1 : 0;
 #pragma unroll
   for (int d = 32; d >= 1; d >>= 1) cnt += __shfl_xor(cnt, d, 64);
-  const int len = min(cnt, max(p.low_rank, 0));
+  return min(cnt, max(p.low_rank, 0));
+}
+
+// One wave per (row m, group g, K|V): the count and the masked copy of the row.
+template <int DT, int E>
+__global__ __launch_bounds__(256) void cutoff_rows_kernel(CutoffParams p) {
+  const int lane = threadIdx.x & 63;
+  const long long task = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const long long n_rows = (long long)p.M * p.G;
+  if (task >= 2 * n_rows) return;
+  const int mat = (int)(task / n_rows);
+  const long long rg = task % n_rows;
+  const int m = (int)(rg / p.G), g = (int)(rg % p.G);
+  const CutoffMat& cm = p.mat[mat];
+  const int D = p.D;
+  const int len = cutoff_row_len<DT, E>(p, mat, rg, lane);
 
   const uint16_t* xs = cm.x + (long long)m * p.x_ld + (long long)g * D + lane * E;
   uint16_t* xo = cm.out + (long long)m * p.out_ld + (long long)g * D + lane * E;
@@ -177,6 +187,55 @@ __global__ __launch_bounds__(256) void cutoff_rows_kernel(CutoffParams p) {
     xo[e] = lane * E + e < len ? xb : zb;
   }
   if (lane == 0) cm.lens[(long long)m * p.len_ld + g] = len;
+}
+
+// Decode step of the per-head layout, after the logits: for each (batch b, group g, K|V) the
+// count, then the decode append of that token to cache row b*G + g at position seq (the first
+// len coefficients -- exactly what the masked copy followed by the append stores); waves past
+// those tasks rotate the query rows (RoPE at position pos).
+struct TailParams {
+  CutoffParams cp;
+  void* flat[2];
+  long long flat_ld[2];
+  int* lens[2];
+  int* offs[2];
+  long long tab_sb[2], tab_ss[2];
+  int* ptr[2];
+  int seq;
+  uint16_t* q;
+  int q_rows;
+  int pos;
+  float log_theta;
+};
+
+template <int DT, int E>
+__global__ __launch_bounds__(256) void cutoff_append_rope_kernel(TailParams t) {
+  const int lane = threadIdx.x & 63;
+  const long long task = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const CutoffParams& p = t.cp;
+  const long long n_rows = (long long)p.M * p.G;
+  if (task < 2 * n_rows) {
+    const int mat = (int)(task / n_rows);
+    const long long rg = task % n_rows;  // = cache row b*G + g
+    const int m = (int)(rg / p.G), g = (int)(rg % p.G);
+    const int len = cutoff_row_len<DT, E>(p, mat, rg, lane);
+    int off = 0;
+    if (lane == 0) {
+      off = t.ptr[mat][rg];
+      t.ptr[mat][rg] = off + len;
+      t.lens[mat][rg * t.tab_sb[mat] + (long long)t.seq * t.tab_ss[mat]] = len;
+      t.offs[mat][rg * t.tab_sb[mat] + (long long)t.seq * t.tab_ss[mat]] = off;
+    }
+    off = __shfl(off, 0, 64);
+    const uint16_t* xs = p.mat[mat].x + (long long)m * p.x_ld + (long long)g * p.D + lane * E;
+    uint16_t* dst = (uint16_t*)t.flat[mat] + rg * t.flat_ld[mat] + off + lane * E;
+#pragma unroll
+    for (int e = 0; e < E; ++e)
+      if (lane * E + e < len) dst[e] = xs[e];
+    return;
+  }
+  const long long qr = task - 2 * n_rows;
+  if (qr < t.q_rows) dkv_rope_pair<DT>(t.q + qr * 128, lane, t.pos, t.log_theta);
 }
 
 template <int DT, int E>
@@ -260,6 +319,98 @@ extern "C" int dkv_cutoff_kv(void* stream, int dtype, const void* xk, const void
       return DKV_E_UNSUPPORTED;
   }
 #undef DKV_ROWS_CASE
+  DKV_HIP_CHECK_LAUNCH();
+  return DKV_OK;
+}
+
+// The decode step's cutoff head, K+V append and query RoPE in two launches (the logits, then
+// the counts with the appends and the rotation). Used by dkv_decode_layer; same checks as
+// dkv_cutoff_kv for the cutoff part. The per-row scratch (coef_k/v, len_k/v) of the layer's
+// argument block is not used.
+int dkv_layer_cutoff_append_rope(void* stream, const DkvDecodeLayer* L, const void* k_coef,
+                                 const void* v_coef, void* q, int seq, int pos) {
+  const int dtype = L->dtype, M = L->B, G = L->G, D = L->R;
+  if (dtype != DKV_F16 && dtype != DKV_BF16) return DKV_E_UNSUPPORTED;
+  if (M < 0 || G <= 0 || D <= 0 || L->Hq <= 0 || L->Dh != 128) return DKV_E_ARG;
+  if (M == 0) return DKV_OK;
+  if (!L->wt_k || !L->wt_v || !L->b_k || !L->b_v || !L->cut_ws || !L->flat_k || !L->flat_v ||
+      !L->lens_k || !L->offs_k || !L->lens_v || !L->offs_v || !L->ptr_k || !L->ptr_v)
+    return DKV_E_ARG;
+  if (D % 64 != 0 || D > 1024) return DKV_E_UNSUPPORTED;
+  const long long x_ld = (long long)G * D;
+  if (x_ld % 8 != 0 || ((uintptr_t)k_coef | (uintptr_t)v_coef | (uintptr_t)L->wt_k |
+                        (uintptr_t)L->wt_v) % 16)
+    return DKV_E_UNSUPPORTED;
+  if (L->cut_ws_bytes < dkv_cutoff_workspace_bytes(M, G, D)) return DKV_E_WORKSPACE;
+  if ((long long)M * G * D >= (1LL << 31) / 2) return DKV_E_UNSUPPORTED;
+  const int E = D / 64;
+  if (E != 1 && E != 2 && E != 4 && E != 8 && E != 16) return DKV_E_UNSUPPORTED;
+  TailParams t;
+  CutoffParams& p = t.cp;
+  const void* xs[2] = {k_coef, v_coef};
+  const void* ws[2] = {L->wt_k, L->wt_v};
+  const void* bs[2] = {L->b_k, L->b_v};
+  for (int m = 0; m < 2; ++m) {
+    p.mat[m].x = (const uint16_t*)xs[m];
+    p.mat[m].wt = (const uint16_t*)ws[m];
+    p.mat[m].b = (const uint16_t*)bs[m];
+    p.mat[m].out = nullptr;
+    p.mat[m].lens = nullptr;
+    p.mat[m].logits = (uint16_t*)L->cut_ws + (long long)m * M * G * D;
+  }
+  p.x_ld = x_ld;
+  p.out_ld = x_ld;
+  p.len_ld = G;
+  p.M = M;
+  p.G = G;
+  p.D = D;
+  p.low_rank = L->low_rank < 0 ? D : min(L->low_rank, D);
+  p.threshold = dtype == DKV_BF16 ? (float)(__bf16)L->threshold : (float)(_Float16)L->threshold;
+  t.flat[0] = L->flat_k;
+  t.flat[1] = L->flat_v;
+  t.flat_ld[0] = L->flat_k_ld;
+  t.flat_ld[1] = L->flat_v_ld;
+  t.lens[0] = L->lens_k;
+  t.lens[1] = L->lens_v;
+  t.offs[0] = L->offs_k;
+  t.offs[1] = L->offs_v;
+  t.tab_sb[0] = L->tab_k_sb;
+  t.tab_sb[1] = L->tab_v_sb;
+  t.tab_ss[0] = L->tab_k_ss;
+  t.tab_ss[1] = L->tab_v_ss;
+  t.ptr[0] = L->ptr_k;
+  t.ptr[1] = L->ptr_v;
+  t.seq = seq;
+  t.q = (uint16_t*)q;
+  t.q_rows = M * L->Hq;
+  t.pos = pos;
+  t.log_theta = L->log_theta;
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 lgrid(D / CT_COLS, (M + CT_ROWS - 1) / CT_ROWS, 2 * G);
+  if (dtype == DKV_BF16)
+    hipLaunchKernelGGL(cutoff_logits_kernel<DKV_BF16>, lgrid, dim3(256), 0, st, p);
+  else
+    hipLaunchKernelGGL(cutoff_logits_kernel<DKV_F16>, lgrid, dim3(256), 0, st, p);
+  DKV_HIP_CHECK_LAUNCH();
+  const long long tasks = 2LL * M * G + (long long)t.q_rows;
+  const dim3 grid((unsigned)((tasks + 3) / 4));
+#define DKV_TAIL_CASE(e)                                                                 \
+  case e:                                                                                \
+    if (dtype == DKV_BF16)                                                               \
+      hipLaunchKernelGGL((cutoff_append_rope_kernel<DKV_BF16, e>), grid, dim3(256), 0, st, t); \
+    else                                                                                 \
+      hipLaunchKernelGGL((cutoff_append_rope_kernel<DKV_F16, e>), grid, dim3(256), 0, st, t);  \
+    break;
+  switch (E) {
+    DKV_TAIL_CASE(1)
+    DKV_TAIL_CASE(2)
+    DKV_TAIL_CASE(4)
+    DKV_TAIL_CASE(8)
+    DKV_TAIL_CASE(16)
+    default:
+      return DKV_E_UNSUPPORTED;
+  }
+#undef DKV_TAIL_CASE
   DKV_HIP_CHECK_LAUNCH();
   return DKV_OK;
 }

@@ -1,5 +1,5 @@
-// One decode step of one attention layer in one host call: cutoff head, K+V append, RoPE of
-// the query, routed decode attention.
+// One decode step of one attention layer in one host call (three launches): cutoff head, K+V
+// append, RoPE of the query, routed decode attention.
 //
 // Reference behaviour: the decode branch of CustomAttention.forward
 // (src/dynakv/kernels/compressed_attention.py:312-357): q RoPE (:314), cutoff-head replay
@@ -10,25 +10,14 @@
 // only what changes per step. The host keeps the capacity bookkeeping: it calls this only when
 // the cache has room for one more token (seq + 1 <= table capacity, every row's upper bound +
 // R <= flat capacity) and the RoPE table covers seq + 1 positions.
-#include "dkv_common.h"
+#include "dkv_internal.h"
 
 extern "C" int dkv_decode_layer(void* stream, const DkvDecodeLayer* L, void* q,
                                 const void* k_coef, const void* v_coef, void* out, int seq,
                                 int pos) {
   if (!L || !q || !k_coef || !v_coef || !out || seq < 0 || pos < 0) return DKV_E_ARG;
-  const int rows = L->B * L->G;
-  const long long hid = (long long)L->G * L->R;
-  int rc = dkv_cutoff_kv(stream, L->dtype, k_coef, v_coef, hid, L->wt_k, L->wt_v, L->b_k, L->b_v,
-                         L->threshold, L->low_rank, L->coef_k, L->coef_v, hid, L->len_k,
-                         L->len_v, L->G, L->cut_ws, L->cut_ws_bytes, L->B, L->G, L->R);
-  if (rc != DKV_OK) return rc;
-  rc = dkv_append_decode_kv(stream, L->dtype, rows, L->R, seq, L->coef_k, L->R, L->len_k, 1,
-                            L->flat_k, L->flat_k_ld, L->lens_k, L->offs_k, L->tab_k_sb,
-                            L->tab_k_ss, L->ptr_k, L->coef_v, L->R, L->len_v, 1, L->flat_v,
-                            L->flat_v_ld, L->lens_v, L->offs_v, L->tab_v_sb, L->tab_v_ss,
-                            L->ptr_v);
-  if (rc != DKV_OK) return rc;
-  rc = dkv_rope_dense(stream, L->dtype, q, L->Dh, L->Dh, L->B * L->Hq, 1, pos, L->log_theta);
+  // cutoff logits; then counts, the K+V appends and the q rotation in one launch
+  int rc = dkv_layer_cutoff_append_rope(stream, L, k_coef, v_coef, q, seq, pos);
   if (rc != DKV_OK) return rc;
   const int S = seq + 1;
   const int route = S < L->switch_tokens ? DKV_ROUTE_FUSED : DKV_ROUTE_TWO_STAGE;

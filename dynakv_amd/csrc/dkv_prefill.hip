@@ -261,13 +261,7 @@ __global__ __launch_bounds__(256) void rope_dense_kernel(uint16_t* __restrict__ 
   const long long rs = idx / 64;
   const int s = (int)(rs % S);
   const long long r = rs / S;
-  const float inv = dkv_inv_freq(i, FA_DH, log_theta);
-  const float ang = (float)(pos0 + s) * inv;
-  const float c = cosf(ang), sn = sinf(ang);
-  uint16_t* row = x + r * r_ld + (long long)s * s_ld;
-  const float a = dkv_load_f32<DT>(row, i), bb = dkv_load_f32<DT>(row, i + 64);
-  dkv_store_f32<DT>(row, i, a * c - bb * sn);
-  dkv_store_f32<DT>(row, i + 64, bb * c + a * sn);
+  dkv_rope_pair<DT>(x + r * r_ld + (long long)s * s_ld, i, pos0 + s, log_theta);
 }
 
 }  // namespace

@@ -282,7 +282,9 @@ int dkv_prefill_attention(void* stream, int dtype, const void* q, long long q_sb
  * rotated in place, the layer's K/V coefficients (B, G*R) contiguous and the output
  * (B, Hq, Dh) contiguous in the cache dtype. The caller guarantees room for one more token:
  * seq + 1 <= the tables' capacity, every row's used length + R <= the flat capacity, and
- * rope_tiles * 16 >= seq + 1. Scratch: coef_k / coef_v (B, G*R) and len_k / len_v (B*G) int32.
+ * rope_tiles * 16 >= seq + 1. Three launches: the cutoff logits; the counts, the appends of
+ * the first len coefficients and the q rotation; the attention. coef_k / coef_v (B, G*R) and
+ * len_k / len_v (B*G) int32 are scratch the current implementation does not touch.
  */
 typedef struct DkvDecodeLayer {
   int dtype, B, G, Hq, R, Dh, low_rank, switch_tokens;
