@@ -79,6 +79,7 @@ class DecodeLayerArgs(C.Structure):
         ("k_basis", _vp), ("k_unit", _ll), ("k_sr", _ll),
         ("v_basis", _vp), ("v_unit", _ll), ("v_sr", _ll),
         ("rope", _vp), ("rope_tiles", _i), ("split_ws", _vp), ("split_ws_floats", _ll),
+        ("q_sb", _ll), ("coef_ld", _ll),
     ]
 
 

@@ -203,7 +203,8 @@ struct TailParams {
   int* ptr[2];
   int seq;
   uint16_t* q;
-  int q_rows;
+  long long q_sb;  // elements between batch rows of q (heads are contiguous 128-element rows)
+  int q_rows, Hq;
   int pos;
   float log_theta;
 };
@@ -235,7 +236,8 @@ __global__ __launch_bounds__(256) void cutoff_append_rope_kernel(TailParams t) {
     return;
   }
   const long long qr = task - 2 * n_rows;
-  if (qr < t.q_rows) dkv_rope_pair<DT>(t.q + qr * 128, lane, t.pos, t.log_theta);
+  if (qr < t.q_rows)
+    dkv_rope_pair<DT>(t.q + (qr / t.Hq) * t.q_sb + (qr % t.Hq) * 128, lane, t.pos, t.log_theta);
 }
 
 template <int DT, int E>
@@ -337,7 +339,9 @@ int dkv_layer_cutoff_append_rope(void* stream, const DkvDecodeLayer* L, const vo
       !L->lens_k || !L->offs_k || !L->lens_v || !L->offs_v || !L->ptr_k || !L->ptr_v)
     return DKV_E_ARG;
   if (D % 64 != 0 || D > 1024) return DKV_E_UNSUPPORTED;
-  const long long x_ld = (long long)G * D;
+  const long long x_ld = L->coef_ld ? L->coef_ld : (long long)G * D;
+  const long long q_sb = L->q_sb ? L->q_sb : (long long)L->Hq * 128;
+  if (x_ld < (long long)G * D || q_sb < (long long)L->Hq * 128) return DKV_E_ARG;
   if (x_ld % 8 != 0 || ((uintptr_t)k_coef | (uintptr_t)v_coef | (uintptr_t)L->wt_k |
                         (uintptr_t)L->wt_v) % 16)
     return DKV_E_UNSUPPORTED;
@@ -382,7 +386,9 @@ int dkv_layer_cutoff_append_rope(void* stream, const DkvDecodeLayer* L, const vo
   t.ptr[1] = L->ptr_v;
   t.seq = seq;
   t.q = (uint16_t*)q;
+  t.q_sb = q_sb;
   t.q_rows = M * L->Hq;
+  t.Hq = L->Hq;
   t.pos = pos;
   t.log_theta = L->log_theta;
   hipStream_t st = (hipStream_t)stream;

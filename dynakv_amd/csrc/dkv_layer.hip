@@ -21,7 +21,8 @@ extern "C" int dkv_decode_layer(void* stream, const DkvDecodeLayer* L, void* q,
   if (rc != DKV_OK) return rc;
   const int S = seq + 1;
   const int route = S < L->switch_tokens ? DKV_ROUTE_FUSED : DKV_ROUTE_TWO_STAGE;
-  return dkv_decode_splitk(stream, route, L->dtype, q, (long long)L->Hq * L->Dh, L->Dh,
+  const long long q_sb = L->q_sb ? L->q_sb : (long long)L->Hq * L->Dh;
+  return dkv_decode_splitk(stream, route, L->dtype, q, q_sb, L->Dh,
                            L->k_basis, L->k_unit, L->k_sr, L->v_basis, L->v_unit, L->v_sr,
                            L->flat_k, L->flat_k_ld, L->flat_v, L->flat_v_ld, L->lens_k,
                            L->offs_k, L->tab_k_sb, L->tab_k_ss, L->lens_v, L->offs_v,

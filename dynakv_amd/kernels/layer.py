@@ -105,11 +105,22 @@ class DecodeLayerPlan:
 
     def step(self, q: torch.Tensor, k_coef: torch.Tensor, v_coef: torch.Tensor,
              pos: int) -> torch.Tensor:
-        """q (B, Hq, Dh) contiguous, rotated in place; k/v_coef (B, G*R) contiguous.
-        Returns the attention output (B, Hq, Dh) in the cache dtype."""
+        """q (B, Hq, Dh) with contiguous heads (any batch stride), rotated in place; k/v_coef
+        (B, G*R) with unit element stride and one shared row stride (views into one projection
+        output are fine). Returns the attention output (B, Hq, Dh) contiguous in the cache
+        dtype."""
         ck, cv = self._slots
         seq = ck[4]
-        out = torch.empty_like(q)
+        B, Hq, Dh = self.B, self.Hq, self.Dh
+        if (q.shape != (B, Hq, Dh) or q.stride(2) != 1 or q.stride(1) != Dh
+                or k_coef.shape != (B, self.G * self.R) or v_coef.shape != k_coef.shape
+                or k_coef.stride(1) != 1 or v_coef.stride(1) != 1
+                or (B > 1 and k_coef.stride(0) != v_coef.stride(0))):
+            raise ValueError("q / coefficient layout not supported by the layer step")
+        a = self.args
+        a.q_sb = q.stride(0) if B > 1 else Hq * Dh
+        a.coef_ld = k_coef.stride(0) if B > 1 else self.G * self.R
+        out = torch.empty((B, Hq, Dh), dtype=q.dtype, device=q.device)
         rc = _lib.load().dkv_decode_layer(_lib.stream_of(q), self._ptr, q.data_ptr(),
                                           k_coef.data_ptr(), v_coef.data_ptr(), out.data_ptr(),
                                           seq, pos)

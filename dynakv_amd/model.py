@@ -58,10 +58,12 @@ class LlamaShape:
 @dataclass
 class LayerWeights:
     ln1: torch.Tensor
-    wq: torch.Tensor
-    wk: torch.Tensor      # dense K projection (the baseline)
+    w_qkv_c: torch.Tensor  # (H + 2 G Dh, H): q, then the merged K / V coefficient projections
+    w_qkv: torch.Tensor    # (H + 2 G Dh, H): q, K, V of the dense baseline
+    wq: torch.Tensor       # views of w_qkv_c (wq, wk_c, wv_c) and of w_qkv (wk, wv)
+    wk: torch.Tensor       # dense K projection (the baseline)
     wv: torch.Tensor
-    wk_c: torch.Tensor    # merged: emits per-head K coefficients
+    wk_c: torch.Tensor     # merged: emits per-head K coefficients
     wv_c: torch.Tensor
     wo: torch.Tensor
     ln2: torch.Tensor
@@ -127,9 +129,14 @@ class RandomLlama:
             cut = [rnd(G, Dh, Dh) for _ in range(2)]
             bias = [ramp.expand(G, Dh).contiguous() for _ in range(2)]
             w_gu = rnd(2 * s.ffn, H)
+            wq = rnd(H, H)
+            w_qkv_c = torch.cat([wq, wk_c.to(dtype), wv_c.to(dtype)])
+            w_qkv = torch.cat([wq, wk, wv])
+            GD = G * Dh
             self.layers.append(LayerWeights(
-                ln1=torch.ones(H, device=self.device, dtype=dtype), wq=rnd(H, H), wk=wk, wv=wv,
-                wk_c=wk_c.to(dtype), wv_c=wv_c.to(dtype), wo=rnd(H, H),
+                ln1=torch.ones(H, device=self.device, dtype=dtype), w_qkv_c=w_qkv_c, w_qkv=w_qkv,
+                wq=w_qkv_c[:H], wk=w_qkv[H:H + GD], wv=w_qkv[H + GD:],
+                wk_c=w_qkv_c[H:H + GD], wv_c=w_qkv_c[H + GD:], wo=rnd(H, H),
                 ln2=torch.ones(H, device=self.device, dtype=dtype),
                 w_gu=w_gu, w_gate=w_gu[:s.ffn], w_up=w_gu[s.ffn:], w_down=rnd(H, s.ffn),
                 k_basis=Uk.transpose(1, 2).contiguous().to(dtype),
@@ -151,6 +158,11 @@ class _Generator:
     def __init__(self, model: RandomLlama):
         self.m = model
         self.s = model.shape
+
+    def _split(self, y: torch.Tensor):
+        """The q, K and V column ranges of a fused projection output (views)."""
+        H, GD = self.s.hidden, self.s.kv_heads * self.s.head_dim
+        return y[..., :H], y[..., H:H + GD], y[..., H + GD:]
 
     def logits(self, x: torch.Tensor) -> torch.Tensor:
         return linear(add_rmsnorm_(x, None, self.m.norm, self.s.eps), self.m.lm_head)
@@ -209,9 +221,9 @@ class CompressedLlama(_Generator):
     def _qkv(self, lw, h):
         B, S, _ = h.shape
         s = self.s
-        q = linear(h, lw.wq).view(B, S, s.heads, s.head_dim)
-        kc = linear(h, lw.wk_c)  # (B, S, G*Dh) coefficients
-        vc = linear(h, lw.wv_c)
+        q, kc, vc = self._split(linear(h, lw.w_qkv_c))
+        q = q.reshape(B, S, s.heads, s.head_dim)
+        kc, vc = kc.contiguous(), vc.contiguous()  # (B, S, G*Dh) coefficients
         k_out, v_out, len_k, len_v, _, _ = lw.cutoff.kv_process_fused(kc, vc)
         G, Dh = s.kv_heads, s.head_dim
         rows_k = k_out.view(B, S, G, Dh).transpose(1, 2).reshape(B * G, S, Dh)
@@ -247,10 +259,9 @@ class CompressedLlama(_Generator):
             plan = self.plans.get(i)
             if plan is not None and plan.can_step():
                 # one call: cutoff head, K+V append, q RoPE, routed attention
-                q = linear(h, lw.wq).view(B, s.heads, s.head_dim)
-                kc = linear(h, lw.wk_c).view(B, -1)
-                vc = linear(h, lw.wv_c).view(B, -1)
-                a = plan.step(q, kc, vc, pos)
+                # one projection; q and the coefficients are views into its output
+                q, kc, vc = self._split(linear(h, lw.w_qkv_c).view(B, -1))
+                a = plan.step(q.view(B, s.heads, s.head_dim), kc, vc, pos)
             else:
                 q, rk, lk, rv, lv = self._qkv(lw, h)
                 fk, fv, tk, tv, ok, ov = self.cache.update_sp(rk, lk, rv, lv, s.head_dim, i,
@@ -297,9 +308,10 @@ class DenseLlama(_Generator):
     def _kv(self, lw, h, pos0):
         B, S, _ = h.shape
         s = self.s
-        q = linear(h, lw.wq).view(B, S, s.heads, s.head_dim)
-        k = linear(h, lw.wk).view(B, S, s.kv_heads, s.head_dim).transpose(1, 2).contiguous()
-        v = linear(h, lw.wv).view(B, S, s.kv_heads, s.head_dim).transpose(1, 2)
+        q, k, v = self._split(linear(h, lw.w_qkv))
+        q = q.reshape(B, S, s.heads, s.head_dim)
+        k = k.reshape(B, S, s.kv_heads, s.head_dim).transpose(1, 2).contiguous()
+        v = v.reshape(B, S, s.kv_heads, s.head_dim).transpose(1, 2)
         rope_dense_(k, theta=s.theta, pos0=pos0)
         return _rope_q(q, pos0, s.theta), k, v
 

@@ -278,9 +278,9 @@ int dkv_prefill_attention(void* stream, int dtype, const void* q, long long q_sb
  * of q at position pos (:314, dkv_rope_dense), decode attention over seq + 1 tokens routed at
  * switch_tokens (:335-348 and router.py:20-59, dkv_decode_splitk). The caller fills a
  * DkvDecodeLayer once per layer (and again after the cache grows or the RoPE table is
- * extended) and calls dkv_decode_layer per step with the step's q (B, Hq, Dh) contiguous,
- * rotated in place, the layer's K/V coefficients (B, G*R) contiguous and the output
- * (B, Hq, Dh) contiguous in the cache dtype. The caller guarantees room for one more token:
+ * extended) and calls dkv_decode_layer per step with the step's q (B, Hq, Dh) (batch stride
+ * q_sb, rotated in place), the layer's K/V coefficients (B, G*R) (row stride coef_ld) and the
+ * output (B, Hq, Dh) contiguous in the cache dtype. The caller guarantees room for one more token:
  * seq + 1 <= the tables' capacity, every row's used length + R <= the flat capacity, and
  * rope_tiles * 16 >= seq + 1. Three launches: the cutoff logits; the counts, the appends of
  * the first len coefficients and the q rotation; the attention. coef_k / coef_v (B, G*R) and
@@ -312,6 +312,9 @@ typedef struct DkvDecodeLayer {
   int rope_tiles;
   float* split_ws;
   long long split_ws_floats;
+  /* row strides in elements of q (per batch row; its heads are contiguous 128-element rows)
+   * and of k_coef / v_coef; 0 means contiguous (Hq * Dh, G * R) */
+  long long q_sb, coef_ld;
 } DkvDecodeLayer;
 int dkv_decode_layer(void* stream, const DkvDecodeLayer* layer, void* q, const void* k_coef,
                      const void* v_coef, void* out, int seq, int pos);
