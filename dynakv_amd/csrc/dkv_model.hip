@@ -198,14 +198,72 @@ __device__ __forceinline__ float dot8(const dkv_u32x4& a, const dkv_u32x4& b, fl
 // KSPLIT: the 4 waves of a workgroup share each block of ROWS columns, wave w taking the
 // quarter w of K, and add their partial sums through LDS -- four times the waves for a small
 // N; otherwise each wave owns its blocks.
-template <int DT, int M, bool XLDS, bool KSPLIT>
+// The RMSNorm folded into a GEMV's x staging (GemvNorm): x + delta (rounded; workgroup 0
+// stores it to r_out, the updated residual), then rmsnorm(.) * w with the roundings and the
+// per-thread / per-wave summation order of add_rmsnorm_kernel (same 256 threads, same chunk of
+// each row per thread), so the staged operand is bit-identical to that kernel's output.
+struct GemvNorm {
+  const uint16_t* delta;  // nullptr: no residual add
+  long long d_ld;
+  const uint16_t* w;      // (K,)
+  uint16_t* r_out;        // (M, K) rows, stride r_ld; written by workgroup 0 when delta is set
+  long long r_ld;
+  float eps;
+};
+
+template <int DT, int M, bool XLDS, bool KSPLIT, bool NORM>
 __global__ __launch_bounds__(GV_WAVES * 64) void gemv_kernel(
     const uint16_t* __restrict__ x, long long x_ld, const uint16_t* __restrict__ W,
-    long long w_ld, uint16_t* __restrict__ y, long long y_ld, int N, int K) {
+    long long w_ld, uint16_t* __restrict__ y, long long y_ld, int N, int K, GemvNorm nrm) {
   extern __shared__ __attribute__((aligned(16))) uint16_t sx[];  // [M][K] (XLDS)
   __shared__ float sP[GV_WAVES][GV_ROWS][M];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  if constexpr (XLDS) {
+  if constexpr (XLDS && NORM) {
+    static_assert(GV_WAVES * 64 == NORM_THREADS, "norm summation order of add_rmsnorm_kernel");
+    __shared__ float sRed[M][GV_WAVES];
+    const int nc = K / 8;
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      float ss = 0.f;
+      for (int c = tid; c < nc; c += NORM_THREADS) {
+        float v[8];
+        unpack8<DT>(*(const dkv_u32x4*)(x + (long long)m * x_ld + 8 * c), v);
+        if (nrm.delta) {
+          float d[8];
+          unpack8<DT>(*(const dkv_u32x4*)(nrm.delta + (long long)m * nrm.d_ld + 8 * c), d);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[e] = to_dt<DT>(v[e] + d[e]);
+          const dkv_u32x4 r = pack8<DT>(v);
+          if (blockIdx.x == 0) *(dkv_u32x4*)(nrm.r_out + (long long)m * nrm.r_ld + 8 * c) = r;
+          *(dkv_u32x4*)(sx + m * K + 8 * c) = r;
+        } else {
+          *(dkv_u32x4*)(sx + m * K + 8 * c) = pack8<DT>(v);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss = fmaf(v[e], v[e], ss);
+      }
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+      if (lane == 0) sRed[m][wave] = ss;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      float tot = 0.f;
+#pragma unroll
+      for (int i = 0; i < GV_WAVES; ++i) tot += sRed[m][i];
+      const float inv = 1.0f / sqrtf(tot / (float)K + nrm.eps);
+      for (int c = tid; c < nc; c += NORM_THREADS) {
+        float v[8], wv[8], o[8];
+        unpack8<DT>(*(const dkv_u32x4*)(sx + m * K + 8 * c), v);
+        unpack8<DT>(*(const dkv_u32x4*)(nrm.w + 8 * c), wv);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = to_dt<DT>(v[e] * inv) * wv[e];
+        *(dkv_u32x4*)(sx + m * K + 8 * c) = pack8<DT>(o);
+      }
+    }
+    __syncthreads();
+  } else if constexpr (XLDS) {
     for (int c = tid; c < M * (K / 8); c += GV_WAVES * 64) {
       const int m = c / (K / 8), kk = 8 * (c % (K / 8));
       *(dkv_u32x4*)(sx + m * K + kk) = *(const dkv_u32x4*)(x + (long long)m * x_ld + kk);
@@ -281,9 +339,9 @@ __global__ __launch_bounds__(GV_WAVES * 64) void gemv_kernel(
 
 constexpr long long GV_XLDS_MAX = 64 * 1024;  // largest x staged in LDS (bytes)
 
-template <int DT, int M>
+template <int DT, int M, bool NORM>
 void launch_gemv(const void* x, long long x_ld, const void* W, long long w_ld, void* y,
-                 long long y_ld, int N, int K, hipStream_t st) {
+                 long long y_ld, int N, int K, const GemvNorm& nrm, hipStream_t st) {
   // as many workgroups as can be resident at once (LDS bound, at most 8 per CU on 256 CUs);
   // each stages x once
   const int nblk = (N + GV_ROWS - 1) / GV_ROWS;
@@ -297,32 +355,40 @@ void launch_gemv(const void* x, long long x_ld, const void* W, long long w_ld, v
   const uint16_t* xp = (const uint16_t*)x;
   const uint16_t* wp = (const uint16_t*)W;
   uint16_t* yp = (uint16_t*)y;
-  if (xlds && ksplit)
-    hipLaunchKernelGGL((gemv_kernel<DT, M, true, true>), grid, dim3(GV_WAVES * 64), lds, st, xp,
-                       x_ld, wp, w_ld, yp, y_ld, N, K);
-  else if (xlds)
-    hipLaunchKernelGGL((gemv_kernel<DT, M, true, false>), grid, dim3(GV_WAVES * 64), lds, st,
-                       xp, x_ld, wp, w_ld, yp, y_ld, N, K);
-  else if (ksplit)
-    hipLaunchKernelGGL((gemv_kernel<DT, M, false, true>), grid, dim3(GV_WAVES * 64), lds, st,
-                       xp, x_ld, wp, w_ld, yp, y_ld, N, K);
-  else
-    hipLaunchKernelGGL((gemv_kernel<DT, M, false, false>), grid, dim3(GV_WAVES * 64), lds, st,
-                       xp, x_ld, wp, w_ld, yp, y_ld, N, K);
+  if constexpr (NORM) {  // the caller checked that x fits the LDS staging
+    if (ksplit)
+      hipLaunchKernelGGL((gemv_kernel<DT, M, true, true, true>), grid, dim3(GV_WAVES * 64), lds,
+                         st, xp, x_ld, wp, w_ld, yp, y_ld, N, K, nrm);
+    else
+      hipLaunchKernelGGL((gemv_kernel<DT, M, true, false, true>), grid, dim3(GV_WAVES * 64),
+                         lds, st, xp, x_ld, wp, w_ld, yp, y_ld, N, K, nrm);
+  } else if (xlds && ksplit) {
+    hipLaunchKernelGGL((gemv_kernel<DT, M, true, true, false>), grid, dim3(GV_WAVES * 64), lds,
+                       st, xp, x_ld, wp, w_ld, yp, y_ld, N, K, nrm);
+  } else if (xlds) {
+    hipLaunchKernelGGL((gemv_kernel<DT, M, true, false, false>), grid, dim3(GV_WAVES * 64), lds,
+                       st, xp, x_ld, wp, w_ld, yp, y_ld, N, K, nrm);
+  } else if (ksplit) {
+    hipLaunchKernelGGL((gemv_kernel<DT, M, false, true, false>), grid, dim3(GV_WAVES * 64), lds,
+                       st, xp, x_ld, wp, w_ld, yp, y_ld, N, K, nrm);
+  } else {
+    hipLaunchKernelGGL((gemv_kernel<DT, M, false, false, false>), grid, dim3(GV_WAVES * 64),
+                       lds, st, xp, x_ld, wp, w_ld, yp, y_ld, N, K, nrm);
+  }
 }
 
-template <int DT>
+template <int DT, bool NORM>
 void launch_gemv_m(int M, const void* x, long long x_ld, const void* W, long long w_ld,
-                   void* y, long long y_ld, int N, int K, hipStream_t st) {
+                   void* y, long long y_ld, int N, int K, const GemvNorm& nrm, hipStream_t st) {
   switch (M) {
-    case 1: launch_gemv<DT, 1>(x, x_ld, W, w_ld, y, y_ld, N, K, st); break;
-    case 2: launch_gemv<DT, 2>(x, x_ld, W, w_ld, y, y_ld, N, K, st); break;
-    case 3: launch_gemv<DT, 3>(x, x_ld, W, w_ld, y, y_ld, N, K, st); break;
-    case 4: launch_gemv<DT, 4>(x, x_ld, W, w_ld, y, y_ld, N, K, st); break;
-    case 5: launch_gemv<DT, 5>(x, x_ld, W, w_ld, y, y_ld, N, K, st); break;
-    case 6: launch_gemv<DT, 6>(x, x_ld, W, w_ld, y, y_ld, N, K, st); break;
-    case 7: launch_gemv<DT, 7>(x, x_ld, W, w_ld, y, y_ld, N, K, st); break;
-    default: launch_gemv<DT, 8>(x, x_ld, W, w_ld, y, y_ld, N, K, st); break;
+    case 1: launch_gemv<DT, 1, NORM>(x, x_ld, W, w_ld, y, y_ld, N, K, nrm, st); break;
+    case 2: launch_gemv<DT, 2, NORM>(x, x_ld, W, w_ld, y, y_ld, N, K, nrm, st); break;
+    case 3: launch_gemv<DT, 3, NORM>(x, x_ld, W, w_ld, y, y_ld, N, K, nrm, st); break;
+    case 4: launch_gemv<DT, 4, NORM>(x, x_ld, W, w_ld, y, y_ld, N, K, nrm, st); break;
+    case 5: launch_gemv<DT, 5, NORM>(x, x_ld, W, w_ld, y, y_ld, N, K, nrm, st); break;
+    case 6: launch_gemv<DT, 6, NORM>(x, x_ld, W, w_ld, y, y_ld, N, K, nrm, st); break;
+    case 7: launch_gemv<DT, 7, NORM>(x, x_ld, W, w_ld, y, y_ld, N, K, nrm, st); break;
+    default: launch_gemv<DT, 8, NORM>(x, x_ld, W, w_ld, y, y_ld, N, K, nrm, st); break;
   }
 }
 
@@ -337,10 +403,36 @@ extern "C" int dkv_gemv(void* stream, int dtype, const void* x, long long x_ld, 
   if (!x || !W || !y || x_ld < K || w_ld < K || y_ld < N) return DKV_E_ARG;
   if (!aligned16(x) || !aligned16(W) || (x_ld & 7) || (w_ld & 7)) return DKV_E_UNSUPPORTED;
   hipStream_t st = (hipStream_t)stream;
+  const GemvNorm none = {nullptr, 0, nullptr, nullptr, 0, 0.f};
   if (dtype == DKV_BF16)
-    launch_gemv_m<DKV_BF16>(M, x, x_ld, W, w_ld, y, y_ld, N, K, st);
+    launch_gemv_m<DKV_BF16, false>(M, x, x_ld, W, w_ld, y, y_ld, N, K, none, st);
   else
-    launch_gemv_m<DKV_F16>(M, x, x_ld, W, w_ld, y, y_ld, N, K, st);
+    launch_gemv_m<DKV_F16, false>(M, x, x_ld, W, w_ld, y, y_ld, N, K, none, st);
+  DKV_HIP_CHECK_LAUNCH();
+  return DKV_OK;
+}
+
+extern "C" int dkv_gemv_rmsnorm(void* stream, int dtype, const void* x, long long x_ld,
+                                const void* delta, long long delta_ld, const void* norm_w,
+                                float eps, void* r_out, long long r_ld, const void* W,
+                                long long w_ld, void* y, long long y_ld, int M, int N, int K) {
+  if (dtype != DKV_BF16 && dtype != DKV_F16) return DKV_E_UNSUPPORTED;
+  if (M < 0 || N < 0 || K <= 0) return DKV_E_ARG;
+  if (M == 0 || N == 0) return DKV_OK;
+  if (M > 8 || K % 8 != 0 || (long long)M * K * 2 > GV_XLDS_MAX) return DKV_E_UNSUPPORTED;
+  if (!x || !W || !y || !norm_w || x_ld < K || w_ld < K || y_ld < N) return DKV_E_ARG;
+  if (delta && (!r_out || delta_ld < K || r_ld < K)) return DKV_E_ARG;
+  if (delta && (r_out == x || r_out == delta)) return DKV_E_ARG;  // read while workgroup 0 writes
+  if (!aligned16(x) || !aligned16(W) || !aligned16(norm_w) || (x_ld & 7) || (w_ld & 7) ||
+      (delta && (!aligned16(delta) || !aligned16(r_out) || (delta_ld & 7) || (r_ld & 7))))
+    return DKV_E_UNSUPPORTED;
+  hipStream_t st = (hipStream_t)stream;
+  const GemvNorm nrm = {(const uint16_t*)delta, delta_ld, (const uint16_t*)norm_w,
+                        (uint16_t*)r_out, r_ld, eps};
+  if (dtype == DKV_BF16)
+    launch_gemv_m<DKV_BF16, true>(M, x, x_ld, W, w_ld, y, y_ld, N, K, nrm, st);
+  else
+    launch_gemv_m<DKV_F16, true>(M, x, x_ld, W, w_ld, y, y_ld, N, K, nrm, st);
   DKV_HIP_CHECK_LAUNCH();
   return DKV_OK;
 }

@@ -87,3 +87,33 @@ def linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
             _lib.check(rc, "dkv_gemv")
             return y
     return torch.nn.functional.linear(x, w)
+
+
+def rmsnorm_linear(x: torch.Tensor, delta: torch.Tensor | None, w_norm: torch.Tensor,
+                   eps: float, w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """``r = x + delta`` (or ``x``), ``y = F.linear(rmsnorm(r) * w_norm, w)``; returns
+    ``(y, r)``. ``x`` is consumed: it may be updated in place and returned as ``r``. One
+    ``dkv_gemv_rmsnorm`` launch for one or two rows (the normalised rows are bit-identical to
+    ``add_rmsnorm_``'s), else ``add_rmsnorm_`` and ``linear``: every workgroup of the fused
+    kernel normalises its own copy of the rows, which costs more than the saved launch from
+    about four rows on (measured on MI355X)."""
+    K = x.shape[-1]
+    M = x.numel() // K
+    if (M <= 2 and x.is_contiguous() and (delta is None or delta.is_contiguous())
+            and K % 8 == 0 and x.dtype == w.dtype == w_norm.dtype
+            and x.dtype in (torch.bfloat16, torch.float16) and w.dim() == 2 and w.shape[1] == K
+            and w.stride(1) == 1 and w.stride(0) % 8 == 0 and w.data_ptr() % 16 == 0
+            and x.data_ptr() % 16 == 0 and (delta is None or delta.data_ptr() % 16 == 0)
+            and x.is_cuda and M >= 1):
+        N = w.shape[0]
+        y = torch.empty(x.shape[:-1] + (N,), dtype=x.dtype, device=x.device)
+        r = torch.empty_like(x) if delta is not None else x
+        rc = _lib.load().dkv_gemv_rmsnorm(
+            _lib.stream_of(x), _lib.dtype_code(x.dtype), x.data_ptr(), K,
+            delta.data_ptr() if delta is not None else None, K, w_norm.data_ptr(), float(eps),
+            r.data_ptr() if delta is not None else None, K, w.data_ptr(), w.stride(0),
+            y.data_ptr(), N, M, N, K)
+        _lib.check(rc, "dkv_gemv_rmsnorm")
+        return y, r
+    h = add_rmsnorm_(x, delta, w_norm, eps)
+    return linear(h, w), x

@@ -15,10 +15,11 @@ only the forward math):
   ``compressed_attention.py:263-292``), and per-head cutoff heads whose bias ramps over the
   rank so that the retained fraction is close to a target (``retention``).
 * ``CompressedLlama.generate``: prefill (cutoff head, packed append, reconstruct-and-attend)
-  then greedy decode steps (cutoff head, decode append, routed decode attention). The
-  projections and the output head are library GEMMs (gate and up as one concatenated GEMM);
-  the residual add with the following RMSNorm and the SwiGLU product are one fused kernel each
-  (``kernels/model_ops.py``), shared with the dense baseline.
+  then greedy decode steps (cutoff head, decode append, routed decode attention). q/k/v and
+  gate/up are one concatenated projection each; at decode sizes the projections run on the
+  skinny GEMM (``kernels/model_ops.py``), with the residual add and the RMSNorm before them
+  folded into its x staging for one or two rows, and the SwiGLU product is one kernel --
+  the same stages serve the dense baseline.
 * ``DenseLlama.generate``: the uncompressed-cache baseline of the same weights (K/V kept in
   full in a preallocated cache, attention by torch's scaled_dot_product_attention).
 """
@@ -37,7 +38,7 @@ from .kernels.compressed_cache import CustomDynamicCache
 from .kernels.cutoff import CutoffHead
 from .kernels.decode import grouped_decode_attention
 from .kernels.layer import DecodeLayerPlan
-from .kernels.model_ops import add_rmsnorm_, linear, silu_mul
+from .kernels.model_ops import linear, rmsnorm_linear, silu_mul
 from .kernels.prefill import compressed_prefill_attention, rope_dense_
 from .kernels.router import KernelPolicy
 
@@ -144,8 +145,6 @@ class RandomLlama:
                 cutoff=CutoffHead(cut[0], bias[0], cut[1], bias[1], groups=G)))
 
 
-def _mlp(lw: LayerWeights, h: torch.Tensor) -> torch.Tensor:
-    return linear(silu_mul(linear(h, lw.w_gu)), lw.w_down)
 
 
 def _rope_q(q: torch.Tensor, pos0: int, theta: float) -> torch.Tensor:
@@ -165,19 +164,21 @@ class _Generator:
         return y[..., :H], y[..., H:H + GD], y[..., H + GD:]
 
     def logits(self, x: torch.Tensor) -> torch.Tensor:
-        return linear(add_rmsnorm_(x, None, self.m.norm, self.s.eps), self.m.lm_head)
+        return rmsnorm_linear(x, None, self.m.norm, self.s.eps, self.m.lm_head)[0]
 
-    def _run(self, x: torch.Tensor, attn) -> torch.Tensor:
-        """The decoder layers over the residual stream ``x`` (B, S, hidden), owned and updated in
-        place; ``attn(i, lw, h)`` returns layer i's attention output (B, S, hidden) before the
-        output projection. Each residual add is fused with the norm that follows it."""
+    def _run(self, x: torch.Tensor, attn, qkv: str) -> torch.Tensor:
+        """The decoder layers over the residual stream ``x`` (B, S, hidden); returns the final
+        residual stream. ``attn(i, lw, y)`` takes layer i's q/k/v projection output ``y``
+        (weight ``getattr(lw, qkv)``) and returns its attention output (B, S, hidden) before the
+        output projection. Each residual add and the norm after it are fused into the
+        projection that consumes them (decode), or one kernel before it (prefill)."""
         eps = self.s.eps
         delta = None
         for i, lw in enumerate(self.m.layers):
-            h = add_rmsnorm_(x, delta, lw.ln1, eps)
-            h2 = add_rmsnorm_(x, linear(attn(i, lw, h), lw.wo), lw.ln2, eps)
-            delta = _mlp(lw, h2)
-        return x.add_(delta)
+            y, x = rmsnorm_linear(x, delta, lw.ln1, eps, getattr(lw, qkv))
+            gu, x = rmsnorm_linear(x, linear(attn(i, lw, y), lw.wo), lw.ln2, eps, lw.w_gu)
+            delta = linear(silu_mul(gu), lw.w_down)
+        return x + delta
 
     def generate(self, prompt: torch.Tensor, new_tokens: int) -> dict:
         """Greedy decode; returns tokens, timings and cache bytes."""
@@ -219,9 +220,10 @@ class CompressedLlama(_Generator):
         self.plans: dict = {}
 
     def _qkv(self, lw, h):
+        """``h``: the layer's fused q/k/v projection output (B, S, H + 2 G Dh)."""
         B, S, _ = h.shape
         s = self.s
-        q, kc, vc = self._split(linear(h, lw.w_qkv_c))
+        q, kc, vc = self._split(h)
         q = q.reshape(B, S, s.heads, s.head_dim)
         kc, vc = kc.contiguous(), vc.contiguous()  # (B, S, G*Dh) coefficients
         k_out, v_out, len_k, len_v, _, _ = lw.cutoff.kv_process_fused(kc, vc)
@@ -239,8 +241,8 @@ class CompressedLlama(_Generator):
         x = F.embedding(prompt, self.m.embed)
         B, S = prompt.shape
 
-        def attn(i, lw, h):
-            q, rk, lk, rv, lv = self._qkv(lw, h)
+        def attn(i, lw, y):
+            q, rk, lk, rv, lv = self._qkv(lw, y)
             self.cache.update_sp(rk.contiguous(), lk, rv.contiguous(), lv, s.head_dim, i,
                                  s.head_dim)
             qh = _rope_q(q, 0, s.theta)
@@ -248,22 +250,22 @@ class CompressedLlama(_Generator):
                                              theta=s.theta)
             return a.transpose(1, 2).reshape(B, S, s.hidden)
 
-        return self._run(x, attn)
+        return self._run(x, attn, "w_qkv_c")
 
     def decode(self, tok: torch.Tensor, pos: int) -> torch.Tensor:
         s = self.s
         x = F.embedding(tok, self.m.embed)  # (B, 1, H)
         B = tok.shape[0]
 
-        def attn(i, lw, h):
+        def attn(i, lw, y):
             plan = self.plans.get(i)
             if plan is not None and plan.can_step():
                 # one call: cutoff head, K+V append, q RoPE, routed attention
                 # one projection; q and the coefficients are views into its output
-                q, kc, vc = self._split(linear(h, lw.w_qkv_c).view(B, -1))
+                q, kc, vc = self._split(y.view(B, -1))
                 a = plan.step(q.view(B, s.heads, s.head_dim), kc, vc, pos)
             else:
-                q, rk, lk, rv, lv = self._qkv(lw, h)
+                q, rk, lk, rv, lv = self._qkv(lw, y)
                 fk, fv, tk, tv, ok, ov = self.cache.update_sp(rk, lk, rv, lv, s.head_dim, i,
                                                               s.head_dim)
                 L = self.cache.get_seq_length_sp(i)
@@ -276,7 +278,7 @@ class CompressedLlama(_Generator):
                                                     theta=s.theta, policy=self.policy)
             return a.reshape(B, 1, s.hidden)
 
-        return self._run(x, attn)
+        return self._run(x, attn, "w_qkv_c")
 
     def kv_bytes(self) -> int:
         """Stored bytes of the packed caches: the used part of each row plus 8 bytes of
@@ -305,10 +307,11 @@ class DenseLlama(_Generator):
         self.k = self.v = None
         self.len = 0
 
-    def _kv(self, lw, h, pos0):
-        B, S, _ = h.shape
+    def _kv(self, lw, y, pos0):
+        """``y``: the layer's fused q/k/v projection output (B, S, H + 2 G Dh)."""
+        B, S, _ = y.shape
         s = self.s
-        q, k, v = self._split(linear(h, lw.w_qkv))
+        q, k, v = self._split(y)
         q = q.reshape(B, S, s.heads, s.head_dim)
         k = k.reshape(B, S, s.kv_heads, s.head_dim).transpose(1, 2).contiguous()
         v = v.reshape(B, S, s.kv_heads, s.head_dim).transpose(1, 2)
@@ -325,8 +328,8 @@ class DenseLlama(_Generator):
         hpg = s.heads // s.kv_heads
         x = F.embedding(prompt, self.m.embed)
 
-        def attn(i, lw, h):
-            qh, k, v = self._kv(lw, h, 0)
+        def attn(i, lw, y):
+            qh, k, v = self._kv(lw, y, 0)
             self.k[i][:, :, :S] = k
             self.v[i][:, :, :S] = v
             with sdpa_kernel(_FAST_SDPA):
@@ -335,7 +338,7 @@ class DenseLlama(_Generator):
                                                    is_causal=True)
             return a.transpose(1, 2).reshape(B, S, s.hidden)
 
-        x = self._run(x, attn)
+        x = self._run(x, attn, "w_qkv")
         self.len = S
         return x
 
@@ -348,8 +351,8 @@ class DenseLlama(_Generator):
         L = self.len
         hpg = s.heads // s.kv_heads
 
-        def attn(i, lw, h):
-            qh, k, v = self._kv(lw, h, pos)
+        def attn(i, lw, y):
+            qh, k, v = self._kv(lw, y, pos)
             self.k[i][:, :, L:L + 1] = k
             self.v[i][:, :, L:L + 1] = v
             qg = qh.view(B, s.kv_heads, hpg, s.head_dim)
@@ -358,7 +361,7 @@ class DenseLlama(_Generator):
                                                    self.v[i][:, :, :L + 1])
             return a.reshape(B, 1, s.hidden)
 
-        x = self._run(x, attn)
+        x = self._run(x, attn, "w_qkv")
         self.len = L + 1
         return x
 

@@ -348,6 +348,19 @@ int dkv_silu_mul(void* stream, int dtype, const void* gu, long long gu_ld, void*
 int dkv_gemv(void* stream, int dtype, const void* x, long long x_ld, const void* W,
              long long w_ld, void* y, long long y_ld, int M, int N, int K);
 
+/*
+ * dkv_gemv_rmsnorm: dkv_gemv of the normalised rows, h = rmsnorm(x + delta) * norm_w with the
+ * roundings and summation order of dkv_add_rmsnorm (h is bit-identical to its output), y = h
+ * W^T. With delta non-NULL the updated residual x + delta (rounded) is stored to r_out (a
+ * buffer other than x and delta: every workgroup reads x while one writes r_out). M * K * 2
+ * <= 64 KiB, K % 8 == 0; DKV_E_UNSUPPORTED otherwise (the caller runs dkv_add_rmsnorm and a
+ * GEMM then).
+ */
+int dkv_gemv_rmsnorm(void* stream, int dtype, const void* x, long long x_ld, const void* delta,
+                     long long delta_ld, const void* norm_w, float eps, void* r_out,
+                     long long r_ld, const void* W, long long w_ld, void* y, long long y_ld,
+                     int M, int N, int K);
+
 #ifdef __cplusplus
 }
 #endif

@@ -97,3 +97,39 @@ def test_gemv(dev, dtype, M, N, K):
     else:
         assert bool(((y2.double() - ref).abs() <= bound).all())
 
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M,N,K", [(1, 6144, 4096), (4, 28672, 4096), (2, 128256, 4096),
+                                   (8, 100, 512), (3, 40, 8192)])
+@pytest.mark.parametrize("with_delta", [True, False])
+def test_gemv_rmsnorm_is_norm_then_gemv(dev, dtype, M, N, K, with_delta):
+    """The fused norm + projection equals add_rmsnorm_ followed by dkv_gemv bit for bit, and
+    returns the updated residual; the kernel does not touch x."""
+    from dynakv_amd import _lib
+    from dynakv_amd.kernels.model_ops import rmsnorm_linear
+    print(f"[gpu] gemv_rmsnorm {dtype} M={M} N={N} K={K} delta={with_delta}", flush=True)
+    g = torch.Generator(device="cpu").manual_seed(M * 7 + N + K)
+    x = torch.randn(M, K, generator=g).to(dtype).to(dev)
+    d = torch.randn(M, K, generator=g).to(dtype).to(dev) if with_delta else None
+    wn = (1 + 0.1 * torch.randn(K, generator=g)).to(dtype).to(dev)
+    w = (0.02 * torch.randn(N, K, generator=g)).to(dtype).to(dev)
+    x0 = x.clone()
+    y, r = rmsnorm_linear(x.clone(), d, wn, 1e-5, w)
+    if M > 2:  # the model's entry point takes the unfused pair here; the kernel itself:
+        r = torch.empty_like(x) if with_delta else x
+        y = torch.empty(M, N, dtype=dtype, device=dev)
+        _lib.check(_lib.load().dkv_gemv_rmsnorm(
+            _lib.stream_of(x), _lib.dtype_code(dtype), x.data_ptr(), K,
+            d.data_ptr() if with_delta else None, K, wn.data_ptr(), 1e-5,
+            r.data_ptr() if with_delta else None, K, w.data_ptr(), K, y.data_ptr(), N, M, N, K),
+            "dkv_gemv_rmsnorm")
+    assert torch.equal(x, x0), "x untouched"
+    xs = x.clone()
+    h = add_rmsnorm_(xs, d, wn, 1e-5)
+    assert torch.equal(r, xs), "residual"
+    y_ref = torch.empty(M, N, dtype=dtype, device=dev)
+    _lib.check(_lib.load().dkv_gemv(_lib.stream_of(h), _lib.dtype_code(dtype), h.data_ptr(), K,
+                                    w.data_ptr(), K, y_ref.data_ptr(), N, M, N, K), "dkv_gemv")
+    assert torch.equal(y, y_ref), "projection of the normalised rows"
