@@ -245,11 +245,9 @@ __device__ __forceinline__ void wait_vm() {
 
 // LSE-merge the split records of one unit, normalise with the route's denominator, project
 // once through the unit's V basis and store the hpg output rows (all threads of the block).
-// vbr: this thread's share of the V basis, loaded by the caller (VB_CHUNKS 16-byte pieces, zero
-// past rank R); scratch: LDS for the basis ([128][DH] bf16/fp16) and 16 * DH floats.
+// scratch: LDS for the basis ([128][DH] bf16/fp16, zero past rank R) and 16 * DH floats.
 template <int DT, int ROUTE, int ODT>
-__device__ __forceinline__ void merge_unit_t(const SplitParams& p, int unit, uint8_t* scratch,
-                                             const dkv_u32x4 (&vbr)[VB_CHUNKS]) {
+__device__ __forceinline__ void merge_unit_t(const SplitParams& p, int unit, uint8_t* scratch) {
   const int b = unit / p.Hkv, kvh = unit % p.Hkv;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n = lane & 15, g = lane >> 4;
@@ -257,9 +255,19 @@ __device__ __forceinline__ void merge_unit_t(const SplitParams& p, int unit, uin
   const float* base = p.partials + (long long)unit * p.n_splits * stride;
   uint16_t* sVB = reinterpret_cast<uint16_t*>(scratch);          // [128][DH], rank-major
   float* sA = reinterpret_cast<float*>(scratch + DH * DH * 2);    // [16][DH] merged, normalised
+  // this thread's share of the V basis (16-byte piece ch: rank ch / 16, dims 8 * (ch % 16)),
+  // in flight while the records are read and merged
+  dkv_u32x4 vbr[VB_CHUNKS];
+  {
+    const uint16_t* vb = p.v_basis + (long long)kvh * p.v_unit;
 #pragma unroll
-  for (int k = 0; k < VB_CHUNKS; ++k)  // 16-byte piece ch: rank ch / 16, dims 8 * (ch % 16)
-    *(dkv_u32x4*)(sVB + (tid + k * NTHREADS) * 8) = vbr[k];
+    for (int k = 0; k < VB_CHUNKS; ++k) {
+      const int ch = tid + k * NTHREADS;
+      vbr[k] = dkv_u32x4{0u, 0u, 0u, 0u};
+      if (ch < p.R * (DH / 8))
+        vbr[k] = *(const dkv_u32x4*)(vb + (long long)(ch >> 4) * p.v_sr + 8 * (ch & 15));
+    }
+  }
   // merged coefficient of (head slot hs, rank r): one pass over the splits with a running
   // maximum, MB splits at a time (their record loads are all issued before any is used, so
   // a call with many splits pays one load latency per MB splits); slots past hpg are zero
@@ -296,6 +304,8 @@ __device__ __forceinline__ void merge_unit_t(const SplitParams& p, int unit, uin
     }
     sA[idx] = a;
   }
+#pragma unroll
+  for (int k = 0; k < VB_CHUNKS; ++k) *(dkv_u32x4*)(sVB + (tid + k * NTHREADS) * 8) = vbr[k];
   __syncthreads();
   // out[hs][d] = sum_r a[hs][r] VB[r][d] on 16x16x32 MFMA: wave w takes dims 16w..16w+15.
   // A: the merged coefficients of head slot n, ranks 32c + 8g..+7, as hi + lo parts in the
@@ -347,12 +357,11 @@ __device__ __forceinline__ void merge_unit_t(const SplitParams& p, int unit, uin
   }
 }
 template <int DT, int ROUTE>
-__device__ __forceinline__ void merge_unit(const SplitParams& p, int unit, uint8_t* scratch,
-                                           const dkv_u32x4 (&vbr)[VB_CHUNKS]) {
+__device__ __forceinline__ void merge_unit(const SplitParams& p, int unit, uint8_t* scratch) {
   if (p.out_f32)
-    merge_unit_t<DT, ROUTE, DKV_F32>(p, unit, scratch, vbr);
+    merge_unit_t<DT, ROUTE, DKV_F32>(p, unit, scratch);
   else
-    merge_unit_t<DT, ROUTE, DT>(p, unit, scratch, vbr);
+    merge_unit_t<DT, ROUTE, DT>(p, unit, scratch);
 }
 
 // WIDE: more than 8 query heads per unit (up to 16). The query operand then carries the heads'
@@ -933,20 +942,9 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
 
   // ---- fused merge: the last split of the unit to finish combines the unit's records -------
   // Every wave's record stores are released at agent scope before the arrival is counted; the
-  // last arrival acquires them (the splits of a unit may run on different XCDs). The V basis
-  // loads are issued first so their latency overlaps the arrival round trip.
+  // last arrival acquires them (the splits of a unit may run on different XCDs) and only it
+  // loads the V basis, together with the records.
   __shared__ int sLast;
-  dkv_u32x4 vbr[VB_CHUNKS];
-  {
-    const uint16_t* vb = p.v_basis + (long long)kvh * p.v_unit;
-#pragma unroll
-    for (int k = 0; k < VB_CHUNKS; ++k) {
-      const int ch = tid + k * NTHREADS;
-      vbr[k] = dkv_u32x4{0u, 0u, 0u, 0u};
-      if (ch < R * (DH / 8))
-        vbr[k] = *(const dkv_u32x4*)(vb + (long long)(ch >> 4) * p.v_sr + 8 * (ch & 15));
-    }
-  }
   // Each wave waits until its record stores have reached the XCD's L2; after the barrier one
   // wave releases them at agent scope (one L2 write-back covers every wave of the block: they
   // share the L2) and counts the arrival. The last arrival acquires once (L1 and L2
@@ -966,7 +964,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
   }
   __syncthreads();
   if (!sLast) return;
-  merge_unit<DT, ROUTE>(p, unit, sRing, vbr);
+  merge_unit<DT, ROUTE>(p, unit, sRing);
   if (tid == 0) p.counters[unit] = 0;  // ready for the next call (calls are stream-ordered)
 }
 
