@@ -246,33 +246,12 @@ __device__ __forceinline__ void wait_vm() {
 // LSE-merge the split records of one unit, normalise with the route's denominator, project
 // once through the unit's V basis and store the hpg output rows (all threads of the block).
 // scratch: LDS for the basis ([128][DH] bf16/fp16, zero past rank R) and 16 * DH floats.
-template <int DT, int ROUTE, int ODT>
-__device__ __forceinline__ void merge_unit_t(const SplitParams& p, int unit, uint8_t* scratch) {
-  const int b = unit / p.Hkv, kvh = unit % p.Hkv;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int n = lane & 15, g = lane >> 4;
-  const long long stride = (long long)p.hpg * PREC;  // between splits of one head
-  const float* base = p.partials + (long long)unit * p.n_splits * stride;
-  uint16_t* sVB = reinterpret_cast<uint16_t*>(scratch);          // [128][DH], rank-major
-  float* sA = reinterpret_cast<float*>(scratch + DH * DH * 2);    // [16][DH] merged, normalised
-  // this thread's share of the V basis (16-byte piece ch: rank ch / 16, dims 8 * (ch % 16)),
-  // in flight while the records are read and merged
-  dkv_u32x4 vbr[VB_CHUNKS];
-  {
-    const uint16_t* vb = p.v_basis + (long long)kvh * p.v_unit;
-#pragma unroll
-    for (int k = 0; k < VB_CHUNKS; ++k) {
-      const int ch = tid + k * NTHREADS;
-      vbr[k] = dkv_u32x4{0u, 0u, 0u, 0u};
-      if (ch < p.R * (DH / 8))
-        vbr[k] = *(const dkv_u32x4*)(vb + (long long)(ch >> 4) * p.v_sr + 8 * (ch & 15));
-    }
-  }
-  // merged coefficient of (head slot hs, rank r): one pass over the splits with a running
-  // maximum, MB splits at a time (their record loads are all issued before any is used, so
-  // a call with many splits pays one load latency per MB splits); slots past hpg are zero
-  constexpr int MB = 8;
-  for (int idx = tid; idx < 16 * DH; idx += NTHREADS) {
+// The LSE merge of one unit's split records into sA[16][DH] (merged, normalised coefficients;
+// head slots past hpg zero), MB splits per batch of loads.
+template <int MB, int ROUTE>
+__device__ __forceinline__ void merge_records(const SplitParams& p, const float* base,
+                                              long long stride, float* sA) {
+  for (int idx = threadIdx.x; idx < 16 * DH; idx += NTHREADS) {
     const int hs = idx / DH, r = idx % DH;
     float a = 0.f;
     if (hs < p.hpg) {
@@ -304,8 +283,114 @@ __device__ __forceinline__ void merge_unit_t(const SplitParams& p, int unit, uin
     }
     sA[idx] = a;
   }
+}
+
+// The same merge with the weights formed once per (head, split) for up to MERGE_WSPLITS
+// splits: w = 2^(m - M) / den from the head's maximum M and denominator, then each (head,
+// rank) thread only loads its coefficient of every split and sums the weighted values (a third
+// of the loads and none of the exponentials of merge_records per thread).
+constexpr int MERGE_WSPLITS = 64;
+template <int MB, int ROUTE>
+__device__ __forceinline__ void merge_records_w(const SplitParams& p, const float* base,
+                                                long long stride, float* sA, float* sM,
+                                                float* sL, float* sW) {
+  const int tid = threadIdx.x, ns = p.n_splits;
+  // this thread's (head, rank) pairs: idx = tid + k * NTHREADS. For the first (head slots
+  // 0..3) the coefficients of the first MB splits are loaded here, in flight with the (m, l)
+  // loads below; the others are loaded once the weights are known.
+  constexpr int NIDX = 16 * DH / NTHREADS;
+  float x0[MB];
+  {
+    const int hsc = min(tid / DH, p.hpg - 1), rc = min(tid % DH, p.R - 1);
 #pragma unroll
-  for (int k = 0; k < VB_CHUNKS; ++k) *(dkv_u32x4*)(sVB + (tid + k * NTHREADS) * 8) = vbr[k];
+    for (int u = 0; u < MB; ++u) x0[u] = base[min(u, ns - 1) * stride + hsc * PREC + 2 + rc];
+  }
+  for (int t = tid; t < p.hpg * ns; t += NTHREADS) {
+    const int hs = t / ns, sp = t % ns;
+    const float* rec = base + sp * stride + hs * PREC;
+    sM[hs * MERGE_WSPLITS + sp] = rec[0];
+    sL[hs * MERGE_WSPLITS + sp] = rec[1];
+  }
+  __syncthreads();
+  for (int t = tid; t < p.hpg * ns; t += NTHREADS) {
+    const int hs = t / ns, sp = t % ns;
+    const float* mh = sM + hs * MERGE_WSPLITS;
+    const float* lh = sL + hs * MERGE_WSPLITS;
+    float M = -INFINITY;
+    for (int u = 0; u < ns; ++u) M = fmaxf(M, mh[u]);
+    float L = 0.f;
+    for (int u = 0; u < ns; ++u) L += mh[u] == -INFINITY ? 0.f : lh[u] * exp2f(mh[u] - M);
+    const float den = ROUTE == DKV_ROUTE_TWO_STAGE ? fmaxf(L, 1e-6f) : L;
+    sW[hs * MERGE_WSPLITS + sp] = mh[sp] == -INFINITY ? 0.f : exp2f(mh[sp] - M) / den;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < NIDX; ++k) {
+    const int idx = tid + k * NTHREADS, hs = idx / DH, r = idx % DH;
+    float a = 0.f;
+    if (hs < p.hpg && r < p.R) {
+      int sp0 = 0;
+      if (k == 0) {
+#pragma unroll
+        for (int u = 0; u < MB; ++u)
+          if (u < ns) a += sW[hs * MERGE_WSPLITS + u] * x0[u];
+        sp0 = MB;
+      }
+      for (; sp0 < ns; sp0 += MB) {
+        float xb[MB];
+#pragma unroll
+        for (int u = 0; u < MB; ++u) xb[u] = base[min(sp0 + u, ns - 1) * stride + hs * PREC + 2 + r];
+#pragma unroll
+        for (int u = 0; u < MB; ++u)
+          if (sp0 + u < ns) a += sW[hs * MERGE_WSPLITS + sp0 + u] * xb[u];
+      }
+    }
+    sA[idx] = a;
+  }
+}
+
+template <int DT, int ROUTE, int ODT>
+__device__ __forceinline__ void merge_unit_t(const SplitParams& p, int unit, uint8_t* scratch) {
+  const int b = unit / p.Hkv, kvh = unit % p.Hkv;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n = lane & 15, g = lane >> 4;
+  const long long stride = (long long)p.hpg * PREC;  // between splits of one head
+  const float* base = p.partials + (long long)unit * p.n_splits * stride;
+  uint16_t* sVB = reinterpret_cast<uint16_t*>(scratch);          // [128][DH], rank-major
+  float* sA = reinterpret_cast<float*>(scratch + DH * DH * 2);    // [16][DH] merged, normalised
+  // this thread's share of the V basis (16-byte piece ch: rank ch / 16, dims 8 * (ch % 16)),
+  // in flight while the records are read and merged
+  dkv_u32x4 vbr[VB_CHUNKS];
+  {
+    const uint16_t* vb = p.v_basis + (long long)kvh * p.v_unit;
+    // unconditional loads (pieces of ranks past R read rank R-1's and are zeroed after use
+    // is known), so that none waits for another
+#pragma unroll
+    for (int k = 0; k < VB_CHUNKS; ++k) {
+      const int ch = min(tid + k * NTHREADS, p.R * (DH / 8) - 1);
+      vbr[k] = *(const dkv_u32x4*)(vb + (long long)(ch >> 4) * p.v_sr + 8 * (ch & 15));
+    }
+  }
+  // merged coefficient of (head slot hs, rank r); slots past hpg are zero. A batch of MB
+  // splits' record loads is issued before any is used, so a call pays one load latency per
+  // MB splits (MB the smallest of 8, 16, 32 that covers the splits). Up to 8 splits merge
+  // in one pass of running maxima; from 9 on the weights are formed once per (head, split)
+  // (measured on MI355X: ~1 us less at 32 splits, ~0.5 us more at 2).
+  float* sM = sA + 16 * DH;
+  float* sL = sM + 16 * MERGE_WSPLITS;
+  float* sW = sL + 16 * MERGE_WSPLITS;
+  if (p.n_splits <= 8)
+    merge_records<8, ROUTE>(p, base, stride, sA);
+  else if (p.n_splits <= 16)
+    merge_records_w<16, ROUTE>(p, base, stride, sA, sM, sL, sW);
+  else if (p.n_splits <= MERGE_WSPLITS)
+    merge_records_w<32, ROUTE>(p, base, stride, sA, sM, sL, sW);
+  else
+    merge_records<32, ROUTE>(p, base, stride, sA);
+#pragma unroll
+  for (int k = 0; k < VB_CHUNKS; ++k)
+    *(dkv_u32x4*)(sVB + (tid + k * NTHREADS) * 8) =
+        tid + k * NTHREADS < p.R * (DH / 8) ? vbr[k] : dkv_u32x4{0u, 0u, 0u, 0u};
   __syncthreads();
   // out[hs][d] = sum_r a[hs][r] VB[r][d] on 16x16x32 MFMA: wave w takes dims 16w..16w+15.
   // A: the merged coefficients of head slot n, ranks 32c + 8g..+7, as hi + lo parts in the
@@ -472,11 +557,13 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
   uint32_t qh[QH];
   {
     const long long qo = (long long)b * p.q_sb + (long long)kvh * p.hpg * p.q_sh + lane;
+    // unconditional loads (slots past the heads read head 0), so that they are all in flight
+    // at once rather than one round trip per head
 #pragma unroll
     for (int h = 0; h < QH; ++h) {
-      qh[h] = 0u;
-      if (h < p.hpg)
-        qh[h] = (uint32_t)p.q[qo + h * p.q_sh] | ((uint32_t)p.q[qo + h * p.q_sh + 64] << 16);
+      const long long o = qo + (h < p.hpg ? h : 0) * p.q_sh;
+      const uint32_t v = (uint32_t)p.q[o] | ((uint32_t)p.q[o + 64] << 16);
+      qh[h] = h < p.hpg ? v : 0u;
     }
   }
   // R(n) of this lane's token slot for its 16 frequencies i = 16*pp + 4*g + w
@@ -762,6 +849,8 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
     };
     // software-pipelined by one block pair: the products of pp+1 are issued before the
     // rotation of pp, so the MFMA pipe and the VALU work of one wave overlap
+    // a wave in its reconstruction yields issue priority to a wave in the other phases
+    __builtin_amdgcn_s_setprio(0);
     dkv_f32x4 C0[2], C1[2];
     recon(0, C0[0], C1[0]);
 #pragma unroll
@@ -786,6 +875,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
                                                             DPP_ROW_SHL8, 0xf, 0xf, false));
     }
 
+    __builtin_amdgcn_s_setprio(1);
     // scores of lane (head slot n, tokens 4g+u) with the route's masking: the fused route in
     // log2 units, the two-stage route as the rounded scores (natural units; the factor log2(e)
     // is applied to their maximum and inside the exponent's fma)
@@ -908,7 +998,8 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
   float* sw = reinterpret_cast<float*>(sRing);  // [WAVES][16 m | 16 l | 16 x 128 acc]
   constexpr int WREC = 32 + 16 * DH;
   static_assert(WAVES * WREC * 4 <= WAVES * NSLOT * GSLOT_BYTES, "epilogue scratch fits");
-  static_assert(DH * DH * 2 + 16 * DH * 4 <= WAVES * NSLOT * GSLOT_BYTES, "merge scratch fits");
+  static_assert(DH * DH * 2 + 16 * DH * 4 + 3 * 16 * MERGE_WSPLITS * 4 <= WAVES * NSLOT * GSLOT_BYTES,
+                "merge scratch fits");
   static_assert(WAVES * 16 == DH, "the merge projection gives each wave 16 output dims");
   float* my = sw + wave * WREC;
   if (g == 0) {
