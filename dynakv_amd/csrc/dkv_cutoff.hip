@@ -79,14 +79,11 @@ __device__ __forceinline__ uint16_t f32_elt(float v) {
 // B = Wt rows (lane: output n = lane % 16, the same inputs); the result lane holds rows
 // 4*(lane/16) + u of output column lane % 16.
 template <int DT>
-__global__ __launch_bounds__(256) void cutoff_logits_kernel(CutoffParams p) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+__device__ __forceinline__ void logits_tile(const CutoffParams& p, int mat, int g, int row0,
+                                            int n0, int lane) {
   const int i = lane & 15, kg = lane >> 4;
-  const int mat = blockIdx.z & 1, g = blockIdx.z >> 1;
   const CutoffMat& cm = p.mat[mat];
   const int D = p.D;
-  const int row0 = blockIdx.y * CT_ROWS;
-  const int n0 = blockIdx.x * CT_COLS + wave * 16;
   const int xrow = min(row0 + i, p.M - 1);  // rows past M compute a copy of the last row
   const uint16_t* xa = cm.x + (long long)xrow * p.x_ld + (long long)g * D + 8 * kg;
   const uint16_t* wb = cm.wt + ((long long)g * D + n0 + i) * D + 8 * kg;
@@ -111,6 +108,12 @@ __global__ __launch_bounds__(256) void cutoff_logits_kernel(CutoffParams p) {
     if (m < p.M)
       cm.logits[((long long)m * p.G + g) * D + n0 + i] = f32_elt<DT>(acc[u] + bias);
   }
+}
+template <int DT>
+__global__ __launch_bounds__(256) void cutoff_logits_kernel(CutoffParams p) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  logits_tile<DT>(p, blockIdx.z & 1, blockIdx.z >> 1, blockIdx.y * CT_ROWS,
+                  blockIdx.x * CT_COLS + wave * 16, lane);
 }
 
 // The retained count of one (row m, group g) of matrix mat, computed by one wave from the
@@ -209,15 +212,11 @@ struct TailParams {
   float log_theta;
 };
 
+// count, table entries and append of cache row rg = b*G + g of matrix mat (one wave)
 template <int DT, int E>
-__global__ __launch_bounds__(256) void cutoff_append_rope_kernel(TailParams t) {
-  const int lane = threadIdx.x & 63;
-  const long long task = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+__device__ __forceinline__ void append_row(const TailParams& t, int mat, long long rg, int lane) {
   const CutoffParams& p = t.cp;
-  const long long n_rows = (long long)p.M * p.G;
-  if (task < 2 * n_rows) {
-    const int mat = (int)(task / n_rows);
-    const long long rg = task % n_rows;  // = cache row b*G + g
+  {
     const int m = (int)(rg / p.G), g = (int)(rg % p.G);
     const int len = cutoff_row_len<DT, E>(p, mat, rg, lane);
     int off = 0;
@@ -233,9 +232,29 @@ __global__ __launch_bounds__(256) void cutoff_append_rope_kernel(TailParams t) {
 #pragma unroll
     for (int e = 0; e < E; ++e)
       if (lane * E + e < len) dst[e] = xs[e];
+  }
+}
+
+// One launch for the whole tail of a decode step's cutoff head: workgroup 2g + mat computes the
+// logits of group g of matrix mat (K or V) for 16 rows at a time (wave w: columns 16w + 64c, as
+// cutoff_logits_kernel computes them), then its waves take those rows' counts and appends;
+// the workgroups past 2G rotate the query rows (RoPE at position pos), one per wave.
+template <int DT, int E>
+__global__ __launch_bounds__(256) void cutoff_layer_kernel(TailParams t) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const CutoffParams& p = t.cp;
+  const int n_cut = 2 * p.G;
+  if ((int)blockIdx.x < n_cut) {
+    const int mat = blockIdx.x & 1, g = blockIdx.x >> 1;
+    for (int row0 = 0; row0 < p.M; row0 += CT_ROWS) {
+      for (int c0 = 0; c0 < p.D; c0 += CT_COLS) logits_tile<DT>(p, mat, g, row0, c0 + 16 * wave, lane);
+      __syncthreads();  // the rows' logits (global workspace) are visible to the workgroup
+      for (int m = row0 + wave; m < min(row0 + CT_ROWS, p.M); m += 4)
+        append_row<DT, E>(t, mat, (long long)m * p.G + g, lane);
+    }
     return;
   }
-  const long long qr = task - 2 * n_rows;
+  const long long qr = (long long)(blockIdx.x - n_cut) * 4 + wave;
   if (qr < t.q_rows)
     dkv_rope_pair<DT>(t.q + (qr / t.Hq) * t.q_sb + (qr % t.Hq) * 128, lane, t.pos, t.log_theta);
 }
@@ -325,8 +344,8 @@ extern "C" int dkv_cutoff_kv(void* stream, int dtype, const void* xk, const void
   return DKV_OK;
 }
 
-// The decode step's cutoff head, K+V append and query RoPE in two launches (the logits, then
-// the counts with the appends and the rotation). Used by dkv_decode_layer; same checks as
+// The decode step's cutoff head, K+V append and query RoPE in one launch
+// (cutoff_layer_kernel). Used by dkv_decode_layer; same checks as
 // dkv_cutoff_kv for the cutoff part. The per-row scratch (coef_k/v, len_k/v) of the layer's
 // argument block is not used.
 int dkv_layer_cutoff_append_rope(void* stream, const DkvDecodeLayer* L, const void* k_coef,
@@ -392,20 +411,13 @@ int dkv_layer_cutoff_append_rope(void* stream, const DkvDecodeLayer* L, const vo
   t.pos = pos;
   t.log_theta = L->log_theta;
   hipStream_t st = (hipStream_t)stream;
-  const dim3 lgrid(D / CT_COLS, (M + CT_ROWS - 1) / CT_ROWS, 2 * G);
-  if (dtype == DKV_BF16)
-    hipLaunchKernelGGL(cutoff_logits_kernel<DKV_BF16>, lgrid, dim3(256), 0, st, p);
-  else
-    hipLaunchKernelGGL(cutoff_logits_kernel<DKV_F16>, lgrid, dim3(256), 0, st, p);
-  DKV_HIP_CHECK_LAUNCH();
-  const long long tasks = 2LL * M * G + (long long)t.q_rows;
-  const dim3 grid((unsigned)((tasks + 3) / 4));
+  const dim3 grid((unsigned)(2 * G + (t.q_rows + 3) / 4));
 #define DKV_TAIL_CASE(e)                                                                 \
   case e:                                                                                \
     if (dtype == DKV_BF16)                                                               \
-      hipLaunchKernelGGL((cutoff_append_rope_kernel<DKV_BF16, e>), grid, dim3(256), 0, st, t); \
+      hipLaunchKernelGGL((cutoff_layer_kernel<DKV_BF16, e>), grid, dim3(256), 0, st, t);       \
     else                                                                                 \
-      hipLaunchKernelGGL((cutoff_append_rope_kernel<DKV_F16, e>), grid, dim3(256), 0, st, t);  \
+      hipLaunchKernelGGL((cutoff_layer_kernel<DKV_F16, e>), grid, dim3(256), 0, st, t);        \
     break;
   switch (E) {
     DKV_TAIL_CASE(1)

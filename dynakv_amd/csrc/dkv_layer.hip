@@ -1,4 +1,4 @@
-// One decode step of one attention layer in one host call (three launches): cutoff head, K+V
+// One decode step of one attention layer in one host call (two launches): cutoff head, K+V
 // append, RoPE of the query, routed decode attention.
 //
 // Reference behaviour: the decode branch of CustomAttention.forward
@@ -16,7 +16,7 @@ extern "C" int dkv_decode_layer(void* stream, const DkvDecodeLayer* L, void* q,
                                 const void* k_coef, const void* v_coef, void* out, int seq,
                                 int pos) {
   if (!L || !q || !k_coef || !v_coef || !out || seq < 0 || pos < 0) return DKV_E_ARG;
-  // cutoff logits; then counts, the K+V appends and the q rotation in one launch
+  // cutoff logits, counts, the K+V appends and the q rotation in one launch
   int rc = dkv_layer_cutoff_append_rope(stream, L, k_coef, v_coef, q, seq, pos);
   if (rc != DKV_OK) return rc;
   const int S = seq + 1;
