@@ -68,70 +68,118 @@ __global__ __launch_bounds__(256) void append_decode_kv_kernel(AppendSlot k, App
                 s.flat_ld, s.lens, s.offs, s.tab_sb, s.tab_ss, s.ptr, seq_pos, row, max_dim);
 }
 
-// Block-wide inclusive scan of one long long per thread (256 threads).
-__device__ __forceinline__ long long block_scan_incl(long long v, long long* s_tmp) {
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    long long o = __shfl_up(v, d, 64);
-    if (lane >= d) v += o;
-  }
-  if (lane == 63) s_tmp[wave] = v;
-  __syncthreads();
-  long long add = 0;
-  for (int w = 0; w < wave; ++w) add += s_tmp[w];
-  __syncthreads();
-  return v + add;
-}
-
-// One 256-thread block per row; tokens processed in chunks of 256.
+// Prefill append, workgroup (chunk, row): AP_CHUNK tokens of one row. The row's offsets before
+// the chunk come from a reduction over the earlier tokens' counts (every workgroup reads the
+// row's old pointer, so the pointer itself is advanced by append_prefill_ptr_kernel, launched
+// after); wave 0 scans the chunk, then each wave copies its tokens four at a time (all loads
+// of a group issued before its stores). Offsets follow the unclipped counts, the coefficients
+// are stored at the clipped ones (min(len, max_dim)), as in the one-token append.
+constexpr int AP_CHUNK = 64;
 template <typename T>
 __global__ __launch_bounds__(256) void append_prefill_kernel(
     const T* __restrict__ states, long long states_sb, long long states_ss,
     const int* __restrict__ new_len, long long len_sb, long long len_ss, T* __restrict__ flat,
     long long flat_ld, int* __restrict__ lens, int* __restrict__ offs, long long tab_sb,
-    long long tab_ss, int* __restrict__ ptr, int seq_pos, int n_new, int max_dim) {
-  __shared__ long long s_tmp[4];
-  __shared__ long long s_dst[256];
-  __shared__ int s_clen[256];
-  const int row = blockIdx.x;
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+    long long tab_ss, const int* __restrict__ ptr, int seq_pos, int n_new, int max_dim) {
+  __shared__ long long s_red[2][4];
+  __shared__ long long s_dst[AP_CHUNK];
+  __shared__ int s_clen[AP_CHUNK];
+  const int row = blockIdx.y, c0 = blockIdx.x * AP_CHUNK;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const long long start = ptr[row];
-  long long carry_u = 0, carry_c = 0;
-  T* frow = flat + (long long)row * flat_ld;
-  const T* srow = states + (long long)row * states_sb;
-  for (int base = 0; base < n_new; base += 256) {
-    const int t = base + tid;
-    const int len = t < n_new ? new_len[(long long)row * len_sb + (long long)t * len_ss] : 0;
+  const int* lrow = new_len + (long long)row * len_sb;
+  // counts of the tokens before the chunk
+  long long pu = 0, pc = 0;
+  for (int t = tid; t < c0; t += 256) {
+    const int len = lrow[(long long)t * len_ss];
+    pu += len;
+    pc += max(0, min(len, max_dim));
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    pu += __shfl_xor(pu, o, 64);
+    pc += __shfl_xor(pc, o, 64);
+  }
+  if (lane == 0) {
+    s_red[0][wave] = pu;
+    s_red[1][wave] = pc;
+  }
+  __syncthreads();
+  if (wave == 0) {
+    const long long bu = s_red[0][0] + s_red[0][1] + s_red[0][2] + s_red[0][3];
+    const long long bc = s_red[1][0] + s_red[1][1] + s_red[1][2] + s_red[1][3];
+    const int t = c0 + lane;
+    const int len = t < n_new ? lrow[(long long)t * len_ss] : 0;
     const int clen = max(0, min(len, max_dim));
-    const long long inc_u = block_scan_incl((long long)len, s_tmp);
-    const long long inc_c = block_scan_incl((long long)clen, s_tmp);
+    long long iu = len, ic = clen;  // inclusive scans over the chunk
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const long long ou = __shfl_up(iu, d, 64), oc = __shfl_up(ic, d, 64);
+      if (lane >= d) {
+        iu += ou;
+        ic += oc;
+      }
+    }
     if (t < n_new) {
       const long long ti = (long long)row * tab_sb + (long long)(seq_pos + t) * tab_ss;
       lens[ti] = len;
-      offs[ti] = (int)(start + carry_u + inc_u - len);
+      offs[ti] = (int)(start + bu + iu - len);
     }
-    s_dst[tid] = start + carry_c + inc_c - clen;
-    s_clen[tid] = clen;
-    // chunk totals, identical in every thread after the broadcast
-    if (tid == 255) {
-      s_tmp[0] = inc_u;
-      s_tmp[1] = inc_c;
-    }
-    __syncthreads();
-    carry_u += s_tmp[0];
-    carry_c += s_tmp[1];
-    for (int tt = wave; tt < 256 && base + tt < n_new; tt += 4) {
-      const T* src = srow + (long long)(base + tt) * states_ss;
-      T* dst = frow + s_dst[tt];
-      const int c = s_clen[tt];
-      for (int j = lane; j < c; j += 64) dst[j] = src[j];
-    }
-    __syncthreads();
+    s_dst[lane] = start + bc + ic - clen;
+    s_clen[lane] = clen;
   }
-  if (tid == 0) ptr[row] = (int)(start + carry_c);
+  __syncthreads();
+  T* frow = flat + (long long)row * flat_ld;
+  const T* srow = states + (long long)row * states_sb;
+  const int nt = min(AP_CHUNK, n_new - c0);
+  for (int t0 = 4 * wave; t0 < nt; t0 += 16) {
+    // tokens t0 .. t0+3 of the chunk: lane j copies element j (and j + 64) of each
+    T v[4][2];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int tt = t0 + u;
+      const int c = tt < nt ? s_clen[tt] : 0;
+      const T* src = srow + (long long)(c0 + tt) * states_ss;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) v[u][h] = lane + 64 * h < c ? src[lane + 64 * h] : T(0);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int tt = t0 + u;
+      const int c = tt < nt ? s_clen[tt] : 0;
+      T* dst = frow + s_dst[tt < nt ? tt : 0];
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        if (lane + 64 * h < c) dst[lane + 64 * h] = v[u][h];
+    }
+    // counts above 128 (max_dim past the per-head rank): the rest element by element
+    for (int u = 0; u < 4; ++u) {
+      const int tt = t0 + u;
+      if (tt >= nt) break;
+      const int c = s_clen[tt];
+      const T* src = srow + (long long)(c0 + tt) * states_ss;
+      T* dst = frow + s_dst[tt];
+      for (int j = 128 + lane; j < c; j += 64) dst[j] = src[j];
+    }
+  }
+}
+
+// ptr[row] += sum over the appended tokens of min(len, max_dim)
+__global__ __launch_bounds__(256) void append_prefill_ptr_kernel(const int* __restrict__ new_len,
+                                                                long long len_sb,
+                                                                long long len_ss,
+                                                                int* __restrict__ ptr, int n_new,
+                                                                int max_dim) {
+  __shared__ long long s_red[4];
+  const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  long long pc = 0;
+  for (int t = tid; t < n_new; t += 256)
+    pc += max(0, min(new_len[(long long)row * len_sb + (long long)t * len_ss], max_dim));
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) pc += __shfl_xor(pc, o, 64);
+  if (lane == 0) s_red[wave] = pc;
+  __syncthreads();
+  if (tid == 0) ptr[row] = (int)(ptr[row] + s_red[0] + s_red[1] + s_red[2] + s_red[3]);
 }
 
 // out[b, t, j] = flat[b, offs[b,t] + j] for j < min(lens, max_dim), else 0.
@@ -233,7 +281,8 @@ extern "C" int dkv_append_prefill(void* stream, int dtype, const void* states,
   if (!states || !new_len || !flat || !lens || !offs || !ptr) return DKV_E_ARG;
   const int es = dkv_elt_size(dtype);
   if (es == 0) return DKV_E_ARG;
-  dim3 grid(rows), block(256);
+  if (rows > 65535) return DKV_E_UNSUPPORTED;
+  const dim3 grid((unsigned)((n_new + AP_CHUNK - 1) / AP_CHUNK), (unsigned)rows), block(256);
   hipStream_t s = (hipStream_t)stream;
   if (es == 4)
     hipLaunchKernelGGL(append_prefill_kernel<uint32_t>, grid, block, 0, s, (const uint32_t*)states,
@@ -243,6 +292,9 @@ extern "C" int dkv_append_prefill(void* stream, int dtype, const void* states,
     hipLaunchKernelGGL(append_prefill_kernel<uint16_t>, grid, block, 0, s, (const uint16_t*)states,
                        states_sb, states_ss, new_len, len_sb, len_ss, (uint16_t*)flat, flat_ld,
                        lens, offs, tab_sb, tab_ss, ptr, seq_pos, n_new, max_dim);
+  DKV_HIP_CHECK_LAUNCH();
+  hipLaunchKernelGGL(append_prefill_ptr_kernel, dim3((unsigned)rows), block, 0, s, new_len, len_sb,
+                     len_ss, ptr, n_new, max_dim);
   DKV_HIP_CHECK_LAUNCH();
   return DKV_OK;
 }

@@ -97,9 +97,12 @@ class CustomDynamicCache(_CacheBase):
         while len(cache_list) <= layer_idx:
             cache_list.append(None)
         B, new_s = new_len.shape
+        added = None
         if cache_list[layer_idx] is None:
             init_flat = int(new_len.sum(dim=1).max().item())
             self.device_syncs += 1
+            if not is_decode:
+                added = init_flat  # the same reduction sizes the append below
             flat = new_states.new_zeros(B, init_flat)
             lens = torch.zeros(B, new_s, dtype=torch.int32, device=new_len.device)
             offs = torch.zeros(B, new_s, dtype=torch.int32, device=new_len.device)
@@ -118,7 +121,7 @@ class CustomDynamicCache(_CacheBase):
 
         if is_decode:
             added = new_s * max_dim
-        else:
+        elif added is None:
             added = int(new_len.sum(dim=1).max().item())
             self.device_syncs += 1
         if max(ub) + added > flat.shape[1]:
