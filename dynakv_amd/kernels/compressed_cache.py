@@ -92,15 +92,21 @@ class CustomDynamicCache(_CacheBase):
         return self.get_seq_length_sp(layer_idx)
 
     # ------------------------------------------------------------------ updates
-    def _prepare_slot(self, cache_list, layer_idx, new_states, new_len, max_dim, is_decode):
-        """Host-side bookkeeping of one slot; returns ``(cache, added)`` ready for the kernel."""
+    def _prepare_slot(self, cache_list, layer_idx, new_states, new_len, max_dim, is_decode,
+                      row_max=None):
+        """Host-side bookkeeping of one slot; returns ``(cache, added)`` ready for the kernel.
+        ``row_max``: max over rows of the summed new lengths when the caller already has it
+        (a prefill append then needs no device synchronisation of its own)."""
         while len(cache_list) <= layer_idx:
             cache_list.append(None)
         B, new_s = new_len.shape
-        added = None
+        added = None if row_max is None else int(row_max)
         if cache_list[layer_idx] is None:
-            init_flat = int(new_len.sum(dim=1).max().item())
-            self.device_syncs += 1
+            if added is None:
+                init_flat = int(new_len.sum(dim=1).max().item())
+                self.device_syncs += 1
+            else:
+                init_flat = added
             if not is_decode:
                 added = init_flat  # the same reduction sizes the append below
             flat = new_states.new_zeros(B, init_flat)
@@ -142,7 +148,9 @@ class CustomDynamicCache(_CacheBase):
         if is_decode:
             cache[5] = [p + added for p in cache[5]]
 
-    def _launch_prefill(self, cache, new_states, new_len, max_dim):
+    def _launch_prefill(self, cache, new_states, new_len, max_dim, ub=None):
+        """``ub``: the rows' pointers after the append when the caller knows them (a slot
+        that started empty); otherwise they are read back from the device."""
         flat, lens, offs, ptr, seq, _ = cache
         B, new_s = new_len.shape
         st = _lib.stream_of(flat)
@@ -154,8 +162,11 @@ class CustomDynamicCache(_CacheBase):
             lens.data_ptr(), offs.data_ptr(), lens.stride(0), lens.stride(1),
             ptr.data_ptr(), seq, B, new_s, max_dim)
         _lib.check(rc, "dkv_append_prefill")
-        cache[5] = ptr.cpu().tolist()
-        self.device_syncs += 1
+        if ub is not None:
+            cache[5] = [int(v) for v in ub]
+        else:
+            cache[5] = ptr.cpu().tolist()
+            self.device_syncs += 1
 
     @staticmethod
     def _decode_view(new_states, new_len):
@@ -182,6 +193,38 @@ class CustomDynamicCache(_CacheBase):
         else:
             self._launch_prefill(cache, new_states, new_len, max_dim)
         self._finish_slot(cache, new_len.shape[1], added, is_decode)
+
+    def update_sp_prefill_many(self, items, tensor_d):
+        """Prefill appends of several layers, ``items`` = [(layer_idx, key_states, key_len,
+        value_states, value_len), ...] (each as ``update_sp`` takes them, S > 1): the same
+        cache state as one ``update_sp`` per layer, with one device synchronisation for all
+        of them (the per-row length totals that size each slot's buffer) instead of one per
+        slot."""
+        if not items:
+            return
+        max_dim = _max_dim_of(tensor_d)
+        lens = [l for it in items for l in (it[2], it[4])]
+        if any(it[1].shape[1] == 1 for it in items):
+            raise ValueError("update_sp_prefill_many takes prefill appends (S > 1)")
+        # per slot and row: the summed counts (buffer sizing) and the clipped sums (the row's
+        # pointer after the append, for a slot that starts empty), in one transfer
+        host = torch.cat([l.sum(dim=1) for l in lens] +
+                         [l.clamp(0, max_dim).sum(dim=1) for l in lens]).tolist()
+        self.device_syncs += 1
+        rows = [l.shape[0] for l in lens]
+        starts = [sum(rows[:k]) for k in range(len(lens))]
+        half = sum(rows)
+        for n, (layer_idx, ks, kl, vs, vl) in enumerate(items):
+            for j, (cache_list, st, ln) in enumerate(((self.key_cache_sp, ks, kl),
+                                                      (self.value_cache_sp, vs, vl))):
+                k = 2 * n + j
+                su = host[starts[k]:starts[k] + rows[k]]
+                sc = host[half + starts[k]:half + starts[k] + rows[k]]
+                fresh = len(cache_list) <= layer_idx or cache_list[layer_idx] is None
+                cache, added = self._prepare_slot(cache_list, layer_idx, st, ln, max_dim, False,
+                                                  row_max=max(su))
+                self._launch_prefill(cache, st, ln, max_dim, ub=sc if fresh else None)
+                self._finish_slot(cache, ln.shape[1], added, False)
 
     def update_sp(self, key_states, key_len, value_states, value_len, max_dim, layer_idx,
                   tensor_d, k_scalar=None, v_scalar=None):

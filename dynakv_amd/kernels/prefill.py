@@ -103,3 +103,20 @@ def compressed_prefill_attention(q: torch.Tensor, cache, layer_idx: int, k_basis
     already RoPE'd at its positions (the last ``Sq`` of the cache)."""
     k, v = reconstruct_kv(cache, layer_idx, k_basis, v_basis, batch=q.shape[0], theta=theta)
     return prefill_attention(q, k, v, causal=True, out_dtype=out_dtype)
+
+
+def coef_prefill_attention(q: torch.Tensor, ck: torch.Tensor, cv: torch.Tensor,
+                           k_basis: torch.Tensor, v_basis: torch.Tensor, *, theta: float,
+                           out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """``compressed_prefill_attention`` from the masked coefficient rows themselves, ``ck`` /
+    ``cv`` (B*G, S, R) zero past each token's count -- exactly what decompressing the packed
+    cache returns -- so a prefill can attend before (or without) its appends."""
+    G, R, Dh = k_basis.shape
+    rows, S, _ = ck.shape
+    batch = q.shape[0]
+    if rows != batch * G or cv.shape != ck.shape:
+        raise ValueError(f"coefficient rows {tuple(ck.shape)}, expected ({batch * G}, S, {R})")
+    k = torch.matmul(ck.view(batch, G, S, R), k_basis.contiguous())
+    v = torch.matmul(cv.view(batch, G, S, R), v_basis.contiguous())
+    rope_dense_(k, theta=theta, pos0=0)
+    return prefill_attention(q, k, v, causal=True, out_dtype=out_dtype)

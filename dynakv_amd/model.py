@@ -39,7 +39,7 @@ from .kernels.cutoff import CutoffHead
 from .kernels.decode import grouped_decode_attention
 from .kernels.layer import DecodeLayerPlan
 from .kernels.model_ops import linear, rmsnorm_linear, silu_mul
-from .kernels.prefill import compressed_prefill_attention, rope_dense_
+from .kernels.prefill import coef_prefill_attention, rope_dense_
 from .kernels.router import KernelPolicy
 
 
@@ -241,16 +241,21 @@ class CompressedLlama(_Generator):
         x = F.embedding(prompt, self.m.embed)
         B, S = prompt.shape
 
+        pending = []
+
         def attn(i, lw, y):
             q, rk, lk, rv, lv = self._qkv(lw, y)
-            self.cache.update_sp(rk.contiguous(), lk, rv.contiguous(), lv, s.head_dim, i,
-                                 s.head_dim)
+            rk, rv = rk.contiguous(), rv.contiguous()
+            pending.append((i, rk, lk, rv, lv))
             qh = _rope_q(q, 0, s.theta)
-            a = compressed_prefill_attention(qh, self.cache, i, lw.k_basis, lw.v_basis,
-                                             theta=s.theta)
+            # the masked coefficients are what the packed cache returns once appended
+            a = coef_prefill_attention(qh, rk, rv, lw.k_basis, lw.v_basis, theta=s.theta)
             return a.transpose(1, 2).reshape(B, S, s.hidden)
 
-        return self._run(x, attn, "w_qkv_c")
+        x = self._run(x, attn, "w_qkv_c")
+        # every layer's appends after the forward pass: one host synchronisation in all
+        self.cache.update_sp_prefill_many(pending, s.head_dim)
+        return x
 
     def decode(self, tok: torch.Tensor, pos: int) -> torch.Tensor:
         s = self.s

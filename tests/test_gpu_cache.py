@@ -105,3 +105,41 @@ def test_single_slot_append_path(dev):
                                   is_decode=True)
         ref.append_decode(x.float().numpy(), l, D)
     _cmp_slot(cache.key_cache_sp[0], ref, "K single")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_bulk_prefill_append_equals_per_layer(dev, dtype):
+    """update_sp_prefill_many (one host synchronisation for all layers) leaves the caches
+    exactly as one update_sp per layer does, and attention from the masked coefficient rows
+    equals attention from the packed cache."""
+    from dynakv_amd.kernels.prefill import coef_prefill_attention, compressed_prefill_attention
+    print(f"[gpu] bulk prefill append {dtype}", flush=True)
+    g = torch.Generator(device="cpu").manual_seed(77)
+    B, G, R, S, layers = 2, 4, 128, 300, 3
+    items = []
+    for i in range(layers):
+        lk = torch.randint(1, R + 1, (B * G, S), generator=g, dtype=torch.int32)
+        lv = torch.randint(1, R + 1, (B * G, S), generator=g, dtype=torch.int32)
+        ks = torch.randn(B * G, S, R, generator=g) * (torch.arange(R) < lk[..., None])
+        vs = torch.randn(B * G, S, R, generator=g) * (torch.arange(R) < lv[..., None])
+        items.append((i, ks.to(dtype).to(dev), lk.to(dev), vs.to(dtype).to(dev), lv.to(dev)))
+    a, b = CustomDynamicCache(), CustomDynamicCache()
+    for i, ks, lk, vs, lv in items:
+        a.update_sp(ks, lk, vs, lv, R, i, R)
+    b.update_sp_prefill_many(items, R)
+    assert b.device_syncs == 1
+    for i in range(layers):
+        for sa, sb in ((a.key_cache_sp[i], b.key_cache_sp[i]),
+                       (a.value_cache_sp[i], b.value_cache_sp[i])):
+            assert tuple(sa[0].shape) == tuple(sb[0].shape)
+            for t in range(4):
+                assert torch.equal(sa[t], sb[t]), (i, t)
+            assert sa[4] == sb[4] and list(sa[5]) == list(sb[5])
+    kb = torch.linalg.qr(torch.randn(G, R, R, generator=g))[0].to(dtype).to(dev)
+    vb = torch.linalg.qr(torch.randn(G, R, R, generator=g))[0].to(dtype).to(dev)
+    q = torch.randn(B, 2 * G, S, 128, generator=g).to(dtype).to(dev)
+    i, ks, _, vs, _ = items[1]
+    o1 = compressed_prefill_attention(q, a, 1, kb, vb, theta=500000.0)
+    o2 = coef_prefill_attention(q, ks, vs, kb, vb, theta=500000.0)
+    assert torch.equal(o1, o2)
