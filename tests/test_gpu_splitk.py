@@ -152,3 +152,18 @@ def test_output_is_rounded_fp32_result(dev, dtype):
         low = _run(p, case, route, out_dtype=None)
         assert low.dtype == dtype
         assert torch.equal(low, f32.to(dtype)), route
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("route", ROUTES)
+def test_more_units_than_merge_counters(dev, route):
+    """16400 units (batch 2050 x 8 KV groups) exceed the fused merge's 16384 arrival
+    counters: the split records are merged by the separate merge kernel instead. Rows spread
+    over the batch against the oracle."""
+    print(f"[gpu] splitk standalone merge route={route}", flush=True)
+    case = make_case(B=2050, G=8, Hq=8, S=70, R=16, uniform=(0, 16), seed=41)
+    p = packed_from_case(case, torch.float16, dev)
+    got = _run(p, case, route, split_len=64)
+    rows = [0, 1, 1024, 2049]
+    ref = oracle_grouped(case, p["host"], route, "float16", batches=rows)
+    assert_close(got[rows], ref, f"standalone merge {route}")
