@@ -430,6 +430,11 @@ def main():
     ap.add_argument("--no-e2e", action="store_true",
                     help="skip config 5 (greedy generation with a random Llama-3-8B, compressed "
                          "against uncompressed cache; about 10 s)")
+    ap.add_argument("--e2e-only", action="store_true",
+                    help="run config 5 alone (for a kernel trace of the decoder) and print its "
+                         "JSON object")
+    ap.add_argument("--e2e-batches", default="1,2,4", help="config 5 batch sizes")
+    ap.add_argument("--e2e-tokens", type=int, default=100, help="config 5 new tokens")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="run one device copy of this many MiB first (counter calibration)")
     args = ap.parse_args()
@@ -443,6 +448,11 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
     dev = torch.device("cuda:0")
+    e2e_batches = tuple(int(b) for b in args.e2e_batches.split(","))
+    if args.e2e_only:
+        print(json.dumps({"e2e": bench_e2e(dev, batches=e2e_batches, new_tokens=args.e2e_tokens)}),
+              flush=True)
+        return
     cfg = Config3 if args.workload == "config3" else Config2
     if args.copy_probe_mib > 0:
         # a plain device copy of known size: the reference point that scales the FETCH_SIZE and
@@ -513,7 +523,7 @@ def main():
         line["prefill_attention"] = bench_prefill(dev)
     if not args.no_e2e:
         _log("end-to-end generation (config 5)")
-        line["e2e"] = bench_e2e(dev)
+        line["e2e"] = bench_e2e(dev, batches=e2e_batches, new_tokens=args.e2e_tokens)
     if not args.no_cpu_baseline:
         _log("cpu baseline")
         line["cpu_baseline"] = cpu_baseline(cfg, r["workload"], r["cache"], args.cpu_baseline_seconds)
