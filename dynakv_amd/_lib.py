@@ -57,6 +57,8 @@ _SIGNATURES = {
     "dkv_gemv": (_i, [_vp, _i, _vp, _ll, _vp, _ll, _vp, _ll, _i, _i, _i]),
     "dkv_gemv_rmsnorm": (_i, [_vp, _i, _vp, _ll, _vp, _ll, _vp, _f, _vp, _ll, _vp, _ll, _vp,
                               _ll, _i, _i, _i]),
+    "dkv_gemv_glu": (_i, [_vp, _i, _vp, _ll, _vp, _ll, _vp, _f, _vp, _ll, _vp, _ll, _vp, _ll,
+                          _i, _i, _i]),
     "dkv_decode_layer": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i]),
     "dkv_prefill_attention": (_i, [_vp, _i, _vp, _ll, _ll, _ll, _vp, _ll, _ll, _ll, _ll,
                                    _vp, _ll, _ll, _ll, _ll, _vp, _i, _ll, _ll, _ll,

@@ -202,6 +202,13 @@ __device__ __forceinline__ float dot8(const dkv_u32x4& a, const dkv_u32x4& b, fl
 // stores it to r_out, the updated residual), then rmsnorm(.) * w with the roundings and the
 // per-thread / per-wave summation order of add_rmsnorm_kernel (same 256 threads, same chunk of
 // each row per thread), so the staged operand is bit-identical to that kernel's output.
+// silu(g) * u of two fp32 projections, with silu_mul_kernel's roundings
+template <int DT>
+__device__ __forceinline__ float glu_of(float acc_g, float acc_u) {
+  const float g = to_dt<DT>(acc_g), u = to_dt<DT>(acc_u);
+  return to_dt<DT>(g / (1.0f + expf(-g))) * u;
+}
+
 struct GemvNorm {
   const uint16_t* delta;  // nullptr: no residual add
   long long d_ld;
@@ -211,7 +218,11 @@ struct GemvNorm {
   float eps;
 };
 
-template <int DT, int M, bool XLDS, bool KSPLIT, bool NORM>
+// GLU: W holds gate and up rows interleaved (row 2j gate j, row 2j + 1 up j) and the kernel
+// stores h[j] = silu(gate_j) * up_j instead of the 2F projections (y of F columns), each
+// projection rounded to the dtype first and silu rounded before the product, as
+// silu_mul_kernel computes it from the stored projections.
+template <int DT, int M, bool XLDS, bool KSPLIT, bool NORM, bool GLU = false>
 __global__ __launch_bounds__(GV_WAVES * 64) void gemv_kernel(
     const uint16_t* __restrict__ x, long long x_ld, const uint16_t* __restrict__ W,
     long long w_ld, uint16_t* __restrict__ y, long long y_ld, int N, int K, GemvNorm nrm) {
@@ -316,7 +327,20 @@ __global__ __launch_bounds__(GV_WAVES * 64) void gemv_kernel(
 #pragma unroll
           for (int m = 0; m < M; ++m) sP[wave][r][m] = acc[r][m];
       __syncthreads();
-      if (tid < GV_ROWS * M) {
+      if constexpr (GLU) {
+        if (tid < GV_ROWS / 2 * M) {
+          const int r = 2 * (tid / M), m = tid % M;
+          if (n0 + r + 1 < N) {
+            float sg = 0.f, su = 0.f;
+#pragma unroll
+            for (int w = 0; w < GV_WAVES; ++w) {
+              sg += sP[w][r][m];
+              su += sP[w][r + 1][m];
+            }
+            dkv_store_f32<DT>(y, (long long)m * y_ld + (n0 + r) / 2, glu_of<DT>(sg, su));
+          }
+        }
+      } else if (tid < GV_ROWS * M) {
         const int r = tid / M, m = tid % M;
         if (n0 + r < N) {
           float s = 0.f;
@@ -326,6 +350,15 @@ __global__ __launch_bounds__(GV_WAVES * 64) void gemv_kernel(
         }
       }
       __syncthreads();  // sP is rewritten by the next block
+    } else if constexpr (GLU) {
+      if (lane == 0)
+#pragma unroll
+        for (int r = 0; r < GV_ROWS; r += 2)
+#pragma unroll
+          for (int m = 0; m < M; ++m)
+            if (n0 + r + 1 < N)
+              dkv_store_f32<DT>(y, (long long)m * y_ld + (n0 + r) / 2,
+                                glu_of<DT>(acc[r][m], acc[r + 1][m]));
     } else {
       if (lane == 0)
 #pragma unroll
@@ -339,7 +372,7 @@ __global__ __launch_bounds__(GV_WAVES * 64) void gemv_kernel(
 
 constexpr long long GV_XLDS_MAX = 64 * 1024;  // largest x staged in LDS (bytes)
 
-template <int DT, int M, bool NORM>
+template <int DT, int M, bool NORM, bool GLU>
 void launch_gemv(const void* x, long long x_ld, const void* W, long long w_ld, void* y,
                  long long y_ld, int N, int K, const GemvNorm& nrm, hipStream_t st) {
   // as many workgroups as can be resident at once (LDS bound, at most 8 per CU on 256 CUs);
@@ -357,38 +390,38 @@ void launch_gemv(const void* x, long long x_ld, const void* W, long long w_ld, v
   uint16_t* yp = (uint16_t*)y;
   if constexpr (NORM) {  // the caller checked that x fits the LDS staging
     if (ksplit)
-      hipLaunchKernelGGL((gemv_kernel<DT, M, true, true, true>), grid, dim3(GV_WAVES * 64), lds,
+      hipLaunchKernelGGL((gemv_kernel<DT, M, true, true, true, GLU>), grid, dim3(GV_WAVES * 64), lds,
                          st, xp, x_ld, wp, w_ld, yp, y_ld, N, K, nrm);
     else
-      hipLaunchKernelGGL((gemv_kernel<DT, M, true, false, true>), grid, dim3(GV_WAVES * 64),
+      hipLaunchKernelGGL((gemv_kernel<DT, M, true, false, true, GLU>), grid, dim3(GV_WAVES * 64),
                          lds, st, xp, x_ld, wp, w_ld, yp, y_ld, N, K, nrm);
   } else if (xlds && ksplit) {
-    hipLaunchKernelGGL((gemv_kernel<DT, M, true, true, false>), grid, dim3(GV_WAVES * 64), lds,
+    hipLaunchKernelGGL((gemv_kernel<DT, M, true, true, false, GLU>), grid, dim3(GV_WAVES * 64), lds,
                        st, xp, x_ld, wp, w_ld, yp, y_ld, N, K, nrm);
   } else if (xlds) {
-    hipLaunchKernelGGL((gemv_kernel<DT, M, true, false, false>), grid, dim3(GV_WAVES * 64), lds,
+    hipLaunchKernelGGL((gemv_kernel<DT, M, true, false, false, GLU>), grid, dim3(GV_WAVES * 64), lds,
                        st, xp, x_ld, wp, w_ld, yp, y_ld, N, K, nrm);
   } else if (ksplit) {
-    hipLaunchKernelGGL((gemv_kernel<DT, M, false, true, false>), grid, dim3(GV_WAVES * 64), lds,
+    hipLaunchKernelGGL((gemv_kernel<DT, M, false, true, false, GLU>), grid, dim3(GV_WAVES * 64), lds,
                        st, xp, x_ld, wp, w_ld, yp, y_ld, N, K, nrm);
   } else {
-    hipLaunchKernelGGL((gemv_kernel<DT, M, false, false, false>), grid, dim3(GV_WAVES * 64),
+    hipLaunchKernelGGL((gemv_kernel<DT, M, false, false, false, GLU>), grid, dim3(GV_WAVES * 64),
                        lds, st, xp, x_ld, wp, w_ld, yp, y_ld, N, K, nrm);
   }
 }
 
-template <int DT, bool NORM>
+template <int DT, bool NORM, bool GLU = false>
 void launch_gemv_m(int M, const void* x, long long x_ld, const void* W, long long w_ld,
                    void* y, long long y_ld, int N, int K, const GemvNorm& nrm, hipStream_t st) {
   switch (M) {
-    case 1: launch_gemv<DT, 1, NORM>(x, x_ld, W, w_ld, y, y_ld, N, K, nrm, st); break;
-    case 2: launch_gemv<DT, 2, NORM>(x, x_ld, W, w_ld, y, y_ld, N, K, nrm, st); break;
-    case 3: launch_gemv<DT, 3, NORM>(x, x_ld, W, w_ld, y, y_ld, N, K, nrm, st); break;
-    case 4: launch_gemv<DT, 4, NORM>(x, x_ld, W, w_ld, y, y_ld, N, K, nrm, st); break;
-    case 5: launch_gemv<DT, 5, NORM>(x, x_ld, W, w_ld, y, y_ld, N, K, nrm, st); break;
-    case 6: launch_gemv<DT, 6, NORM>(x, x_ld, W, w_ld, y, y_ld, N, K, nrm, st); break;
-    case 7: launch_gemv<DT, 7, NORM>(x, x_ld, W, w_ld, y, y_ld, N, K, nrm, st); break;
-    default: launch_gemv<DT, 8, NORM>(x, x_ld, W, w_ld, y, y_ld, N, K, nrm, st); break;
+    case 1: launch_gemv<DT, 1, NORM, GLU>(x, x_ld, W, w_ld, y, y_ld, N, K, nrm, st); break;
+    case 2: launch_gemv<DT, 2, NORM, GLU>(x, x_ld, W, w_ld, y, y_ld, N, K, nrm, st); break;
+    case 3: launch_gemv<DT, 3, NORM, GLU>(x, x_ld, W, w_ld, y, y_ld, N, K, nrm, st); break;
+    case 4: launch_gemv<DT, 4, NORM, GLU>(x, x_ld, W, w_ld, y, y_ld, N, K, nrm, st); break;
+    case 5: launch_gemv<DT, 5, NORM, GLU>(x, x_ld, W, w_ld, y, y_ld, N, K, nrm, st); break;
+    case 6: launch_gemv<DT, 6, NORM, GLU>(x, x_ld, W, w_ld, y, y_ld, N, K, nrm, st); break;
+    case 7: launch_gemv<DT, 7, NORM, GLU>(x, x_ld, W, w_ld, y, y_ld, N, K, nrm, st); break;
+    default: launch_gemv<DT, 8, NORM, GLU>(x, x_ld, W, w_ld, y, y_ld, N, K, nrm, st); break;
   }
 }
 
@@ -433,6 +466,41 @@ extern "C" int dkv_gemv_rmsnorm(void* stream, int dtype, const void* x, long lon
     launch_gemv_m<DKV_BF16, true>(M, x, x_ld, W, w_ld, y, y_ld, N, K, nrm, st);
   else
     launch_gemv_m<DKV_F16, true>(M, x, x_ld, W, w_ld, y, y_ld, N, K, nrm, st);
+  DKV_HIP_CHECK_LAUNCH();
+  return DKV_OK;
+}
+
+extern "C" int dkv_gemv_glu(void* stream, int dtype, const void* x, long long x_ld,
+                            const void* delta, long long delta_ld, const void* norm_w, float eps,
+                            void* r_out, long long r_ld, const void* W, long long w_ld, void* h,
+                            long long h_ld, int M, int F, int K) {
+  if (dtype != DKV_BF16 && dtype != DKV_F16) return DKV_E_UNSUPPORTED;
+  if (M < 0 || F < 0 || K <= 0) return DKV_E_ARG;
+  if (M == 0 || F == 0) return DKV_OK;
+  if (M > 8 || K % 8 != 0) return DKV_E_UNSUPPORTED;
+  if (norm_w && (long long)M * K * 2 > GV_XLDS_MAX) return DKV_E_UNSUPPORTED;
+  if (!x || !W || !h || x_ld < K || w_ld < K || h_ld < F) return DKV_E_ARG;
+  if (delta && (!norm_w || !r_out || delta_ld < K || r_ld < K)) return DKV_E_ARG;
+  if (delta && (r_out == x || r_out == delta)) return DKV_E_ARG;  // read while workgroup 0 writes
+  if (!aligned16(x) || !aligned16(W) || (x_ld & 7) || (w_ld & 7) ||
+      (norm_w && !aligned16(norm_w)) ||
+      (delta && (!aligned16(delta) || !aligned16(r_out) || (delta_ld & 7) || (r_ld & 7))))
+    return DKV_E_UNSUPPORTED;
+  hipStream_t st = (hipStream_t)stream;
+  const GemvNorm nrm = {(const uint16_t*)delta, delta_ld, (const uint16_t*)norm_w,
+                        (uint16_t*)r_out, r_ld, eps};
+  const int N = 2 * F;
+  if (norm_w) {
+    if (dtype == DKV_BF16)
+      launch_gemv_m<DKV_BF16, true, true>(M, x, x_ld, W, w_ld, h, h_ld, N, K, nrm, st);
+    else
+      launch_gemv_m<DKV_F16, true, true>(M, x, x_ld, W, w_ld, h, h_ld, N, K, nrm, st);
+  } else {
+    if (dtype == DKV_BF16)
+      launch_gemv_m<DKV_BF16, false, true>(M, x, x_ld, W, w_ld, h, h_ld, N, K, nrm, st);
+    else
+      launch_gemv_m<DKV_F16, false, true>(M, x, x_ld, W, w_ld, h, h_ld, N, K, nrm, st);
+  }
   DKV_HIP_CHECK_LAUNCH();
   return DKV_OK;
 }

@@ -117,3 +117,43 @@ def rmsnorm_linear(x: torch.Tensor, delta: torch.Tensor | None, w_norm: torch.Te
         return y, r
     h = add_rmsnorm_(x, delta, w_norm, eps)
     return linear(h, w), x
+
+
+def rmsnorm_glu(x: torch.Tensor, delta: torch.Tensor | None, w_norm: torch.Tensor, eps: float,
+                w_gu: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """``r = x + delta`` (or ``x``), ``h = silu(g) * u`` with ``g``/``u`` the gate/up
+    projections of ``rmsnorm(r) * w_norm`` by ``w_gu``, whose rows interleave them (row 2j gate
+    j, row 2j + 1 up j); returns ``(h, r)`` like ``rmsnorm_linear``. One ``dkv_gemv_glu``
+    launch for one or two rows (norm folded in as well), ``add_rmsnorm_`` and one
+    ``dkv_gemv_glu`` up to eight rows, else ``add_rmsnorm_``, the library GEMM and the product
+    of the de-interleaved halves (torch's ``silu(g) * u``, the same roundings)."""
+    K = x.shape[-1]
+    M = x.numel() // K
+    N = w_gu.shape[0]
+    F = N // 2
+    ok_w = (w_gu.dim() == 2 and w_gu.shape[1] == K and N % 2 == 0 and w_gu.stride(1) == 1
+            and w_gu.stride(0) % 8 == 0 and w_gu.data_ptr() % 16 == 0 and w_gu.dtype == x.dtype
+            and x.dtype in (torch.bfloat16, torch.float16) and K % 8 == 0 and x.is_cuda)
+    lib = _lib.load()
+    if ok_w and M <= 2 and x.is_contiguous() and (delta is None or delta.is_contiguous()) \
+            and w_norm.dtype == x.dtype and x.data_ptr() % 16 == 0 \
+            and (delta is None or delta.data_ptr() % 16 == 0) and M >= 1:
+        h = torch.empty(x.shape[:-1] + (F,), dtype=x.dtype, device=x.device)
+        r = torch.empty_like(x) if delta is not None else x
+        rc = lib.dkv_gemv_glu(_lib.stream_of(x), _lib.dtype_code(x.dtype), x.data_ptr(), K,
+                              delta.data_ptr() if delta is not None else None, K,
+                              w_norm.data_ptr(), float(eps),
+                              r.data_ptr() if delta is not None else None, K, w_gu.data_ptr(),
+                              w_gu.stride(0), h.data_ptr(), F, M, F, K)
+        _lib.check(rc, "dkv_gemv_glu")
+        return h, r
+    y = add_rmsnorm_(x, delta, w_norm, eps)
+    if ok_w and 1 <= M <= 8 and y.is_contiguous():
+        h = torch.empty(y.shape[:-1] + (F,), dtype=y.dtype, device=y.device)
+        rc = lib.dkv_gemv_glu(_lib.stream_of(y), _lib.dtype_code(y.dtype), y.data_ptr(), K,
+                              None, 0, None, 0.0, None, 0, w_gu.data_ptr(), w_gu.stride(0),
+                              h.data_ptr(), F, M, F, K)
+        _lib.check(rc, "dkv_gemv_glu")
+        return h, x
+    gu = torch.nn.functional.linear(y, w_gu)
+    return torch.nn.functional.silu(gu[..., 0::2]) * gu[..., 1::2], x

@@ -38,7 +38,7 @@ from .kernels.compressed_cache import CustomDynamicCache
 from .kernels.cutoff import CutoffHead
 from .kernels.decode import grouped_decode_attention
 from .kernels.layer import DecodeLayerPlan
-from .kernels.model_ops import linear, rmsnorm_linear, silu_mul
+from .kernels.model_ops import linear, rmsnorm_glu, rmsnorm_linear
 from .kernels.prefill import coef_prefill_attention, rope_dense_
 from .kernels.router import KernelPolicy
 
@@ -68,7 +68,7 @@ class LayerWeights:
     wv_c: torch.Tensor
     wo: torch.Tensor
     ln2: torch.Tensor
-    w_gu: torch.Tensor     # (2 * ffn, hidden): gate rows, then up rows
+    w_gu: torch.Tensor     # (2 * ffn, hidden): gate and up rows interleaved (2j gate, 2j+1 up)
     w_gate: torch.Tensor   # views of w_gu
     w_up: torch.Tensor
     w_down: torch.Tensor
@@ -139,7 +139,7 @@ class RandomLlama:
                 wq=w_qkv_c[:H], wk=w_qkv[H:H + GD], wv=w_qkv[H + GD:],
                 wk_c=w_qkv_c[H:H + GD], wv_c=w_qkv_c[H + GD:], wo=rnd(H, H),
                 ln2=torch.ones(H, device=self.device, dtype=dtype),
-                w_gu=w_gu, w_gate=w_gu[:s.ffn], w_up=w_gu[s.ffn:], w_down=rnd(H, s.ffn),
+                w_gu=w_gu, w_gate=w_gu[0::2], w_up=w_gu[1::2], w_down=rnd(H, s.ffn),
                 k_basis=Uk.transpose(1, 2).contiguous().to(dtype),
                 v_basis=Uv.transpose(1, 2).contiguous().to(dtype),
                 cutoff=CutoffHead(cut[0], bias[0], cut[1], bias[1], groups=G)))
@@ -176,8 +176,8 @@ class _Generator:
         delta = None
         for i, lw in enumerate(self.m.layers):
             y, x = rmsnorm_linear(x, delta, lw.ln1, eps, getattr(lw, qkv))
-            gu, x = rmsnorm_linear(x, linear(attn(i, lw, y), lw.wo), lw.ln2, eps, lw.w_gu)
-            delta = linear(silu_mul(gu), lw.w_down)
+            h, x = rmsnorm_glu(x, linear(attn(i, lw, y), lw.wo), lw.ln2, eps, lw.w_gu)
+            delta = linear(h, lw.w_down)
         return x + delta
 
     def generate(self, prompt: torch.Tensor, new_tokens: int) -> dict:

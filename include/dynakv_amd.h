@@ -361,6 +361,20 @@ int dkv_gemv_rmsnorm(void* stream, int dtype, const void* x, long long x_ld, con
                      long long r_ld, const void* W, long long w_ld, void* y, long long y_ld,
                      int M, int N, int K);
 
+/*
+ * dkv_gemv_glu: the LlamaMLP gate/up projection and SwiGLU product of a decode step in one
+ * launch (reference: transformers' LlamaMLP under custom_llama.py:93-323): W holds the gate and
+ * up weight rows interleaved (row 2j gate row j, row 2j + 1 up row j; 2F rows of K), and
+ * h[m][j] = silu(g) * u with g, u the two projections of x row m each rounded to dtype and
+ * silu(g) rounded before the product (bit-identical to dkv_gemv then dkv_silu_mul of the
+ * de-interleaved halves). With norm_w the rows are first normalised as in dkv_gemv_rmsnorm
+ * (delta / r_out as there; M * K * 2 <= 64 KiB), without it x is used as it is. M <= 8,
+ * K % 8 == 0; DKV_E_UNSUPPORTED otherwise.
+ */
+int dkv_gemv_glu(void* stream, int dtype, const void* x, long long x_ld, const void* delta,
+                 long long delta_ld, const void* norm_w, float eps, void* r_out, long long r_ld,
+                 const void* W, long long w_ld, void* h, long long h_ld, int M, int F, int K);
+
 #ifdef __cplusplus
 }
 #endif

@@ -133,3 +133,47 @@ def test_gemv_rmsnorm_is_norm_then_gemv(dev, dtype, M, N, K, with_delta):
     _lib.check(_lib.load().dkv_gemv(_lib.stream_of(h), _lib.dtype_code(dtype), h.data_ptr(), K,
                                     w.data_ptr(), K, y_ref.data_ptr(), N, M, N, K), "dkv_gemv")
     assert torch.equal(y, y_ref), "projection of the normalised rows"
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M,F,K,norm", [(1, 14336, 4096, True), (2, 14336, 4096, True),
+                                        (4, 14336, 4096, False), (1, 136, 512, True),
+                                        (3, 1000, 1024, False), (8, 64, 256, False)])
+def test_gemv_glu_is_gemv_then_silu_mul(dev, dtype, M, F, K, norm):
+    """The gate/up projection with the SwiGLU product in its epilogue (interleaved gate/up
+    rows) equals dkv_gemv of the de-interleaved weights followed by silu_mul, bit for bit, with
+    the norm folded in (one or two rows) or not."""
+    from dynakv_amd import _lib
+    from dynakv_amd.kernels.model_ops import rmsnorm_glu
+    print(f"[gpu] gemv_glu {dtype} M={M} F={F} K={K} norm={norm}", flush=True)
+    g = torch.Generator(device="cpu").manual_seed(M * 5 + F + K)
+    x = torch.randn(M, K, generator=g).to(dtype).to(dev)
+    d = torch.randn(M, K, generator=g).to(dtype).to(dev)
+    wn = (1 + 0.1 * torch.randn(K, generator=g)).to(dtype).to(dev)
+    w = (0.05 * torch.randn(2 * F, K, generator=g)).to(dtype).to(dev)  # rows interleaved
+    lib = _lib.load()
+    # reference: normalised rows, then the [gate | up] projection and silu_mul
+    xs = x.clone()
+    hn = add_rmsnorm_(xs, d, wn, 1e-5)
+    w_halves = torch.cat([w[0::2], w[1::2]]).contiguous()
+    gu = torch.empty(M, 2 * F, dtype=dtype, device=dev)
+    _lib.check(lib.dkv_gemv(_lib.stream_of(hn), _lib.dtype_code(dtype), hn.data_ptr(), K,
+                            w_halves.data_ptr(), K, gu.data_ptr(), 2 * F, M, 2 * F, K), "dkv_gemv")
+    ref = silu_mul(gu)
+    h = torch.empty(M, F, dtype=dtype, device=dev)
+    if norm:
+        r = torch.empty_like(x)
+        rc = lib.dkv_gemv_glu(_lib.stream_of(x), _lib.dtype_code(dtype), x.data_ptr(), K,
+                              d.data_ptr(), K, wn.data_ptr(), 1e-5, r.data_ptr(), K, w.data_ptr(),
+                              K, h.data_ptr(), F, M, F, K)
+        _lib.check(rc, "dkv_gemv_glu")
+        assert torch.equal(r, xs), "residual"
+    else:
+        rc = lib.dkv_gemv_glu(_lib.stream_of(hn), _lib.dtype_code(dtype), hn.data_ptr(), K, None,
+                              0, None, 0.0, None, 0, w.data_ptr(), K, h.data_ptr(), F, M, F, K)
+        _lib.check(rc, "dkv_gemv_glu")
+    assert torch.equal(h, ref), "silu(gate) * up in the epilogue"
+    # the model's entry point agrees with the launch it makes
+    h2, r2 = rmsnorm_glu(x.clone(), d, wn, 1e-5, w)
+    assert torch.equal(h2, ref) and torch.equal(r2, xs)
