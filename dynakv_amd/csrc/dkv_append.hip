@@ -68,7 +68,7 @@ __global__ __launch_bounds__(256) void append_decode_kv_kernel(AppendSlot k, App
                 s.flat_ld, s.lens, s.offs, s.tab_sb, s.tab_ss, s.ptr, seq_pos, row, max_dim);
 }
 
-// Prefill append, workgroup (chunk, row): AP_CHUNK tokens of one row. The row's offsets before
+// Prefill append, workgroup (row, chunk): AP_CHUNK tokens of one row. The row's offsets before
 // the chunk come from a reduction over the earlier tokens' counts (every workgroup reads the
 // row's old pointer, so the pointer itself is advanced by append_prefill_ptr_kernel, launched
 // after); wave 0 scans the chunk, then each wave copies its tokens four at a time (all loads
@@ -84,7 +84,7 @@ __global__ __launch_bounds__(256) void append_prefill_kernel(
   __shared__ long long s_red[2][4];
   __shared__ long long s_dst[AP_CHUNK];
   __shared__ int s_clen[AP_CHUNK];
-  const int row = blockIdx.y, c0 = blockIdx.x * AP_CHUNK;
+  const int row = blockIdx.x, c0 = blockIdx.y * AP_CHUNK;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const long long start = ptr[row];
   const int* lrow = new_len + (long long)row * len_sb;
@@ -281,8 +281,8 @@ extern "C" int dkv_append_prefill(void* stream, int dtype, const void* states,
   if (!states || !new_len || !flat || !lens || !offs || !ptr) return DKV_E_ARG;
   const int es = dkv_elt_size(dtype);
   if (es == 0) return DKV_E_ARG;
-  if (rows > 65535) return DKV_E_UNSUPPORTED;
-  const dim3 grid((unsigned)((n_new + AP_CHUNK - 1) / AP_CHUNK), (unsigned)rows), block(256);
+  if ((n_new + AP_CHUNK - 1) / AP_CHUNK > 65535) return DKV_E_UNSUPPORTED;
+  const dim3 grid((unsigned)rows, (unsigned)((n_new + AP_CHUNK - 1) / AP_CHUNK)), block(256);
   hipStream_t s = (hipStream_t)stream;
   if (es == 4)
     hipLaunchKernelGGL(append_prefill_kernel<uint32_t>, grid, block, 0, s, (const uint32_t*)states,

@@ -216,23 +216,21 @@ struct TailParams {
 template <int DT, int E>
 __device__ __forceinline__ void append_row(const TailParams& t, int mat, long long rg, int lane) {
   const CutoffParams& p = t.cp;
-  {
-    const int m = (int)(rg / p.G), g = (int)(rg % p.G);
-    const int len = cutoff_row_len<DT, E>(p, mat, rg, lane);
-    int off = 0;
-    if (lane == 0) {
-      off = t.ptr[mat][rg];
-      t.ptr[mat][rg] = off + len;
-      t.lens[mat][rg * t.tab_sb[mat] + (long long)t.seq * t.tab_ss[mat]] = len;
-      t.offs[mat][rg * t.tab_sb[mat] + (long long)t.seq * t.tab_ss[mat]] = off;
-    }
-    off = __shfl(off, 0, 64);
-    const uint16_t* xs = p.mat[mat].x + (long long)m * p.x_ld + (long long)g * p.D + lane * E;
-    uint16_t* dst = (uint16_t*)t.flat[mat] + rg * t.flat_ld[mat] + off + lane * E;
-#pragma unroll
-    for (int e = 0; e < E; ++e)
-      if (lane * E + e < len) dst[e] = xs[e];
+  const int m = (int)(rg / p.G), g = (int)(rg % p.G);
+  const int len = cutoff_row_len<DT, E>(p, mat, rg, lane);
+  int off = 0;
+  if (lane == 0) {
+    off = t.ptr[mat][rg];
+    t.ptr[mat][rg] = off + len;
+    t.lens[mat][rg * t.tab_sb[mat] + (long long)t.seq * t.tab_ss[mat]] = len;
+    t.offs[mat][rg * t.tab_sb[mat] + (long long)t.seq * t.tab_ss[mat]] = off;
   }
+  off = __shfl(off, 0, 64);
+  const uint16_t* xs = p.mat[mat].x + (long long)m * p.x_ld + (long long)g * p.D + lane * E;
+  uint16_t* dst = (uint16_t*)t.flat[mat] + rg * t.flat_ld[mat] + off + lane * E;
+#pragma unroll
+  for (int e = 0; e < E; ++e)
+    if (lane * E + e < len) dst[e] = xs[e];
 }
 
 // One launch for the whole tail of a decode step's cutoff head: workgroup 2g + mat computes the
