@@ -134,7 +134,10 @@ class SplitKRunner:
         self.cfg = cfg
         self.dev = dev
         st = torch.cuda.current_stream(dev).cuda_stream
-        nfl = self.lib.dkv_splitk_workspace_floats(cfg.B, cfg.Hq, cfg.G, max_S, cfg.R, 0)
+        # the automatic split length changes with S (fewer, longer splits as the cache grows),
+        # so the workspace is sized for the largest need over the lengths the run visits
+        nfl = max(self.lib.dkv_splitk_workspace_floats(cfg.B, cfg.Hq, cfg.G, S, cfg.R, 0)
+                  for S in range(cfg.S0, max_S + 1))
         self.ws = workspace(dev, st, int(nfl))
         self.rope, self.rope_tiles = rope_table(dev, st, cfg.theta, max_S)
         self.out = torch.empty((cfg.B, cfg.Hq, cfg.Dh), dtype=cfg.dtype, device=dev)
@@ -475,6 +478,14 @@ def main():
     achieved = launch_bytes / split_avg_s / 1e9
     layer_step_s = attn_s / calls
     traffic = load_traffic(cfg.name)
+    dt_name = "bf16" if cfg.dtype == torch.bfloat16 else "fp16"
+    # KernelPolicy(switch_tokens=500): the fused route below 500 tokens, two-stage from 500 on
+    if cfg.S0 >= 500:
+        route_label = "long_two_stage"
+    elif r["final_len"] < 500:
+        route_label = "short_fused"
+    else:
+        route_label = "short_fused below 500 tokens, long_two_stage from 500 (router)"
     line = {
         "metric": "decode-attn GB/s (% HBM peak) + decode tokens/s, Llama-3-8B shape, 1 GPU",
         "value": round(gbs, 2),
@@ -492,7 +503,8 @@ def main():
             "workload": cfg.name,
             "batch": cfg.B, "q_heads": cfg.Hq, "kv_heads": cfg.G, "head_dim": cfg.Dh,
             "rank": cfg.R, "cache_len_start": cfg.S0, "cache_len_end": r["final_len"],
-            "mean_retention": cfg.mean, "route": "long_two_stage", "layout": "per-head (G=8, R=128)",
+            "mean_retention": cfg.mean, "route": route_label,
+            "layout": "per-head (G=8, R=128)",
         },
         "pct_hbm_peak": round(100.0 * gbs / HBM_PEAK_GBS, 2),
         "layers_per_step": args.layers,
@@ -502,7 +514,7 @@ def main():
         "decode_tokens_per_s_step_wall": round(cfg.B * args.steps / r["wall_s"], 1),
         "host_syncs_total": r["syncs"],
         "roofline": {
-            "kernel": "splitk_kernel<bf16, two_stage>",
+            "kernel": f"splitk_kernel<{dt_name}, {'two_stage' if cfg.S0 >= 500 else 'fused / two_stage'}>",
             "bound": "hbm",
             "achieved": round(achieved, 2),
             "peak": HBM_PEAK_GBS,

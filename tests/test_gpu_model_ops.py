@@ -177,3 +177,26 @@ def test_gemv_glu_is_gemv_then_silu_mul(dev, dtype, M, F, K, norm):
     # the model's entry point agrees with the launch it makes
     h2, r2 = rmsnorm_glu(x.clone(), d, wn, 1e-5, w)
     assert torch.equal(h2, ref) and torch.equal(r2, xs)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_rmsnorm_glu_many_rows_fallback(dev, dtype):
+    """More than eight rows (a prompt) take the library GEMM and torch's silu * up of the
+    de-interleaved halves: within two units in the last place of the kernel path's result
+    (the same roundings; silu evaluated by a different formula)."""
+    from dynakv_amd.kernels.model_ops import rmsnorm_glu
+    print(f"[gpu] rmsnorm_glu fallback {dtype}", flush=True)
+    g = torch.Generator(device="cpu").manual_seed(99)
+    M, F, K = 40, 512, 1024
+    x = torch.randn(M, K, generator=g).to(dtype).to(dev)
+    d = torch.randn(M, K, generator=g).to(dtype).to(dev)
+    wn = (1 + 0.1 * torch.randn(K, generator=g)).to(dtype).to(dev)
+    w = (0.05 * torch.randn(2 * F, K, generator=g)).to(dtype).to(dev)
+    h, r = rmsnorm_glu(x.clone(), d, wn, 1e-5, w)
+    xs = x.clone()
+    hn = add_rmsnorm_(xs, d, wn, 1e-5)
+    assert torch.equal(r, xs)
+    gu = torch.nn.functional.linear(hn, w)
+    ref = silu_mul(torch.cat([gu[:, 0::2], gu[:, 1::2]], dim=1).contiguous())
+    assert int(_ulps(h, ref).max()) <= 2
