@@ -383,7 +383,11 @@ void launch_gemv(const void* x, long long x_ld, const void* W, long long w_ld, v
   // fewer column blocks than twice the chip's wave slots at 8 waves per CU: split K
   const bool ksplit = nblk < 2 * 256 * 8;
   const int wg_blocks = ksplit ? nblk : (nblk + GV_WAVES - 1) / GV_WAVES;
-  const dim3 grid((unsigned)min(wg_blocks, 256 * per_cu));
+  // with the norm folded in, every workgroup normalises its own copy of x: at most 4 per CU
+  // for the K-split shapes (the q/k/v projection: 11.4 against 12.2 us at 8 per CU, measured
+  // on MI355X with cold weights)
+  const int cap = (NORM && ksplit) ? 4 : 8;
+  const dim3 grid((unsigned)min(wg_blocks, 256 * min(per_cu, cap)));
   const size_t lds = xlds ? (size_t)M * K * 2 : 0;
   const uint16_t* xp = (const uint16_t*)x;
   const uint16_t* wp = (const uint16_t*)W;
