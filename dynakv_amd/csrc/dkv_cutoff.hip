@@ -212,15 +212,19 @@ struct TailParams {
   float log_theta;
 };
 
-// count, table entries and append of cache row rg = b*G + g of matrix mat (one wave)
+// count, table entries and append of cache row rg = b*G + g of matrix mat (one wave). pre:
+// the row's pointer (lane 0) and this lane's E coefficients when the caller loaded them
+// ahead (have_pre), else they are loaded here.
 template <int DT, int E>
-__device__ __forceinline__ void append_row(const TailParams& t, int mat, long long rg, int lane) {
+__device__ __forceinline__ void append_row(const TailParams& t, int mat, long long rg, int lane,
+                                           bool have_pre = false, int pre_off = 0,
+                                           const uint16_t* pre_x = nullptr) {
   const CutoffParams& p = t.cp;
   const int m = (int)(rg / p.G), g = (int)(rg % p.G);
   const int len = cutoff_row_len<DT, E>(p, mat, rg, lane);
   int off = 0;
   if (lane == 0) {
-    off = t.ptr[mat][rg];
+    off = have_pre ? pre_off : t.ptr[mat][rg];
     t.ptr[mat][rg] = off + len;
     t.lens[mat][rg * t.tab_sb[mat] + (long long)t.seq * t.tab_ss[mat]] = len;
     t.offs[mat][rg * t.tab_sb[mat] + (long long)t.seq * t.tab_ss[mat]] = off;
@@ -230,7 +234,7 @@ __device__ __forceinline__ void append_row(const TailParams& t, int mat, long lo
   uint16_t* dst = (uint16_t*)t.flat[mat] + rg * t.flat_ld[mat] + off + lane * E;
 #pragma unroll
   for (int e = 0; e < E; ++e)
-    if (lane * E + e < len) dst[e] = xs[e];
+    if (lane * E + e < len) dst[e] = have_pre ? pre_x[e] : xs[e];
 }
 
 // One launch for the whole tail of a decode step's cutoff head: workgroup 2g + mat computes the
@@ -244,11 +248,22 @@ __global__ __launch_bounds__(256) void cutoff_layer_kernel(TailParams t) {
   const int n_cut = 2 * p.G;
   if ((int)blockIdx.x < n_cut) {
     const int mat = blockIdx.x & 1, g = blockIdx.x >> 1;
+    // the first row of each wave: its pointer and coefficients loaded before the logits, so
+    // that their latency overlaps the products
+    int off0 = 0;
+    uint16_t x0[E];
+    if (wave < p.M) {
+      const long long rg = (long long)wave * p.G + g;
+      if (lane == 0) off0 = t.ptr[mat][rg];
+      const uint16_t* xs = p.mat[mat].x + (long long)wave * p.x_ld + (long long)g * p.D + lane * E;
+#pragma unroll
+      for (int e = 0; e < E; ++e) x0[e] = xs[e];
+    }
     for (int row0 = 0; row0 < p.M; row0 += CT_ROWS) {
       for (int c0 = 0; c0 < p.D; c0 += CT_COLS) logits_tile<DT>(p, mat, g, row0, c0 + 16 * wave, lane);
       __syncthreads();  // the rows' logits (global workspace) are visible to the workgroup
       for (int m = row0 + wave; m < min(row0 + CT_ROWS, p.M); m += 4)
-        append_row<DT, E>(t, mat, (long long)m * p.G + g, lane);
+        append_row<DT, E>(t, mat, (long long)m * p.G + g, lane, m == wave, off0, x0);
     }
     return;
   }
