@@ -739,6 +739,10 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
     if (last_row) regather_if_needed(cur, slot);
     load_tab(j + 2);
     issue(j + 1);
+    // issue priority by phase (measured on MI355X, ~3% at config 3 over one level): the tile's
+    // front (masks, K windows, query rotation) 2, the reconstruction products 0, scores,
+    // softmax and P.V 1
+    __builtin_amdgcn_s_setprio(2);
     // ---- masks: elements past a token's count belong to the next tokens. Pieces wholly past
     //      the count were loaded as zeros, so only the partial piece of each token needs one:
     //      the lane masks its own partial K and V piece in place, then reads the K windows ----
@@ -849,7 +853,6 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
     };
     // software-pipelined by one block pair: the products of pp+1 are issued before the
     // rotation of pp, so the MFMA pipe and the VALU work of one wave overlap
-    // a wave in its reconstruction yields issue priority to a wave in the other phases
     __builtin_amdgcn_s_setprio(0);
     dkv_f32x4 C0[2], C1[2];
     recon(0, C0[0], C1[0]);
