@@ -164,13 +164,7 @@ __device__ __forceinline__ int cutoff_row_len(const CutoffParams& p, int mat, lo
 
 // One wave per (row m, group g, K|V): the count and the masked copy of the row.
 template <int DT, int E>
-__global__ __launch_bounds__(256) void cutoff_rows_kernel(CutoffParams p) {
-  const int lane = threadIdx.x & 63;
-  const long long task = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const long long n_rows = (long long)p.M * p.G;
-  if (task >= 2 * n_rows) return;
-  const int mat = (int)(task / n_rows);
-  const long long rg = task % n_rows;
+__device__ __forceinline__ void row_task(const CutoffParams& p, int mat, long long rg, int lane) {
   const int m = (int)(rg / p.G), g = (int)(rg % p.G);
   const CutoffMat& cm = p.mat[mat];
   const int D = p.D;
@@ -190,6 +184,27 @@ __global__ __launch_bounds__(256) void cutoff_rows_kernel(CutoffParams p) {
     xo[e] = lane * E + e < len ? xb : zb;
   }
   if (lane == 0) cm.lens[(long long)m * p.len_ld + g] = len;
+}
+template <int DT, int E>
+__global__ __launch_bounds__(256) void cutoff_rows_kernel(CutoffParams p) {
+  const int lane = threadIdx.x & 63;
+  const long long task = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const long long n_rows = (long long)p.M * p.G;
+  if (task >= 2 * n_rows) return;
+  row_task<DT, E>(p, (int)(task / n_rows), task % n_rows, lane);
+}
+
+// Both steps in one launch for a few rows (M <= 16, D <= 128: a decode step): workgroup
+// 2g + mat computes the logits of group g of matrix mat for the rows (wave w: columns
+// 16w + 64c, as cutoff_logits_kernel computes them), then its waves take the rows' counts and
+// masked copies.
+template <int DT, int E>
+__global__ __launch_bounds__(256) void cutoff_small_kernel(CutoffParams p) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int mat = blockIdx.x & 1, g = blockIdx.x >> 1;
+  for (int c0 = 0; c0 < p.D; c0 += CT_COLS) logits_tile<DT>(p, mat, g, 0, c0 + 16 * wave, lane);
+  __syncthreads();  // the rows' logits (global workspace) are visible to the workgroup
+  for (int m = wave; m < p.M; m += 4) row_task<DT, E>(p, mat, (long long)m * p.G + g, lane);
 }
 
 // Decode step of the per-head layout, after the logits: for each (batch b, group g, K|V) the
@@ -330,6 +345,21 @@ extern "C" int dkv_cutoff_kv(void* stream, int dtype, const void* xk, const void
   const int E = D / 64;
   if (E != 1 && E != 2 && E != 4 && E != 8 && E != 16) return DKV_E_UNSUPPORTED;
   hipStream_t st = (hipStream_t)stream;
+  if (M <= CT_ROWS && D <= 128) {
+    if (dtype == DKV_BF16) {
+      if (E == 1)
+        hipLaunchKernelGGL((cutoff_small_kernel<DKV_BF16, 1>), dim3(2 * G), dim3(256), 0, st, p);
+      else
+        hipLaunchKernelGGL((cutoff_small_kernel<DKV_BF16, 2>), dim3(2 * G), dim3(256), 0, st, p);
+    } else {
+      if (E == 1)
+        hipLaunchKernelGGL((cutoff_small_kernel<DKV_F16, 1>), dim3(2 * G), dim3(256), 0, st, p);
+      else
+        hipLaunchKernelGGL((cutoff_small_kernel<DKV_F16, 2>), dim3(2 * G), dim3(256), 0, st, p);
+    }
+    DKV_HIP_CHECK_LAUNCH();
+    return DKV_OK;
+  }
   const dim3 lgrid(D / CT_COLS, (M + CT_ROWS - 1) / CT_ROWS, 2 * G);
   if (dtype == DKV_BF16)
     hipLaunchKernelGGL(cutoff_logits_kernel<DKV_BF16>, lgrid, dim3(256), 0, st, p);
