@@ -54,6 +54,10 @@ constexpr int ROPE_FIXED_ROWS = TILE + 1;  // rows 0..15: in-tile deltas; row 16
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float RESCALE_THRESH = 11.5f;  // log2 units
 constexpr int OOB = 0x7ffffff0;          // buffer offset that reads as zero
+// elements a flat-buffer resource covers at most (its byte size stays below OOB), and the
+// largest row stride the kernel accepts (a row's last 16-byte window stays inside that range)
+constexpr int FLAT_ELEM_CAP = 0x3ffffff0;
+constexpr int FLAT_LD_MAX = FLAT_ELEM_CAP - 8;
 constexpr int DPP_ROW_SHL8 = 0x108;      // DPP row_shl:8: lane i of a 16-lane row reads lane i+8
 
 struct SplitParams {
@@ -66,7 +70,7 @@ struct SplitParams {
   const uint16_t* k_flat;
   const uint16_t* v_flat;
   int k_ld, v_ld;
-  uint32_t k_end, v_end;  // elements covered by the buffer resources: rows * ld
+  int rows;               // cache rows of the flat buffers (B * G)
   const int* lens_k;
   const int* offs_k;
   long long tk_sb, tk_ss;
@@ -629,9 +633,15 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
   __syncthreads();  // every wave holds its operands: the rings may now be overwritten
 
   // one resource per buffer, ranges [flat, flat + rows * ld); row offsets go in the voffset
-  const __amdgpu_buffer_rsrc_t rk_src = dkv_make_rsrc(p.k_flat, p.k_end * 2u);
-  const __amdgpu_buffer_rsrc_t rv_src = dkv_make_rsrc(p.v_flat, p.v_end * 2u);
-  const int k_row0 = row * p.k_ld, v_row0 = row * p.v_ld;
+  // one resource per buffer, based at this workgroup's row (a workgroup reads one row only),
+  // covering the rest of the buffer up to FLAT_ELEM_CAP elements; token offsets go in the
+  // voffset. Row strides are at most FLAT_LD_MAX, so a row's last window stays in range unless
+  // the row is the buffer's last.
+  const uint32_t k_end = (uint32_t)min((long long)(p.rows - row) * p.k_ld, (long long)FLAT_ELEM_CAP);
+  const uint32_t v_end = (uint32_t)min((long long)(p.rows - row) * p.v_ld, (long long)FLAT_ELEM_CAP);
+  const __amdgpu_buffer_rsrc_t rk_src = dkv_make_rsrc(p.k_flat + (long long)row * p.k_ld, k_end * 2u);
+  const __amdgpu_buffer_rsrc_t rv_src = dkv_make_rsrc(p.v_flat + (long long)row * p.v_ld, v_end * 2u);
+  constexpr int k_row0 = 0, v_row0 = 0;
   // only the buffers' last row can hold a token whose 16-byte window crosses the end
   const bool last_row = row == p.B * p.G - 1;
   // token metadata of this lane's token in tile j (table slot must have arrived). A slot past
@@ -671,15 +681,15 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
   // tokens of the last row can need one. Such a tile is gathered again with element loads
   // once its slot has landed.
   auto regather_if_needed = [&](const Tok& d, uint8_t* slot) {
-    const bool risky = (d.rkc > 0 && (uint32_t)(d.ko + d.rkc + 7) > p.k_end) ||
-                       (d.rvc > 0 && (uint32_t)(d.vo + d.rvc + 7) > p.v_end);
+    const bool risky = (d.rkc > 0 && (uint32_t)(d.ko + d.rkc + 7) > k_end) ||
+                       (d.rvc > 0 && (uint32_t)(d.vo + d.rvc + 7) > v_end);
     if (__builtin_expect(__ballot(risky) != 0ull, 0)) {
       // one chunk at a time: this cold path must not raise the loop's register pressure
 #pragma unroll 1
       for (int c = 0; c < 8; ++c) {
         const bool isv = c >= 4;
         *(dkv_u32x4*)(slot + c * 1024 + 16 * lane) =
-            gather_chunk(isv ? rv_src : rk_src, isv ? p.v_end : p.k_end, isv ? d.vo : d.ko,
+            gather_chunk(isv ? rv_src : rk_src, isv ? v_end : k_end, isv ? d.vo : d.ko,
                          isv ? d.rvc : d.rkc, c & 3, g);
       }
     }
@@ -1351,18 +1361,17 @@ extern "C" int dkv_profile_end(double* split_ms, double* merge_ms, int* calls) {
   return rc;
 }
 
-extern "C" int dkv_decode_splitk(void* stream, int route, int dtype, const void* q, long long q_sb,
-                                 long long q_sh, const void* k_basis, long long k_unit_stride,
-                                 long long k_basis_sr, const void* v_basis,
-                                 long long v_unit_stride, long long v_basis_sr,
-                                 const void* k_flat, long long k_ld, const void* v_flat,
-                                 long long v_ld, const int* lens_k, const int* offs_k,
-                                 long long tk_sb, long long tk_ss, const int* lens_v,
-                                 const int* offs_v, long long tv_sb, long long tv_ss,
-                                 const float* rope, int rope_tiles, float* workspace,
-                                 long long workspace_floats, void* out, long long out_sb,
-                                 long long out_sh, int out_dtype, int B, int Hq, int Hkv, int G,
-                                 int S, int R, int Dh, int split_len) {
+// Argument checks shared by both entry points; 0 when the call is valid, or a status.
+// On success *n_floats receives the workspace size the call needs (0 when nothing is launched).
+static int splitk_check(int route, int dtype, const void* q, const void* k_basis,
+                        long long k_unit_stride, long long k_basis_sr, const void* v_basis,
+                        long long v_unit_stride, long long v_basis_sr, const void* k_flat,
+                        long long k_ld, const void* v_flat, long long v_ld, const int* lens_k,
+                        const int* offs_k, long long tk_ss, const int* lens_v,
+                        const int* offs_v, long long tv_ss, const float* rope, int rope_tiles,
+                        const void* out, int out_dtype, int B, int Hq, int Hkv, int G, int S,
+                        int R, int Dh, int* split_len, long long* n_floats) {
+  *n_floats = 0;
   if (route != DKV_ROUTE_FUSED && route != DKV_ROUTE_TWO_STAGE) return DKV_E_ARG;
   if (dtype != DKV_F16 && dtype != DKV_BF16) return DKV_E_UNSUPPORTED;
   if (out_dtype != dtype && out_dtype != DKV_F32) return DKV_E_ARG;
@@ -1372,7 +1381,7 @@ extern "C" int dkv_decode_splitk(void* stream, int route, int dtype, const void*
   if (B == 0) return DKV_OK;
   if (S == 0) return DKV_E_UNSUPPORTED;  // empty cache: the vector path defines the result
   if (!q || !k_basis || !v_basis || !k_flat || !v_flat || !lens_k || !offs_k || !lens_v ||
-      !offs_v || !rope || !workspace || !out)
+      !offs_v || !rope || !out)
     return DKV_E_ARG;
   // 16-byte aligned K basis rows for the vector LDS staging
   if (((uintptr_t)k_basis & 15) || (k_basis_sr & 7) || (k_unit_stride & 7))
@@ -1381,21 +1390,38 @@ extern "C" int dkv_decode_splitk(void* stream, int route, int dtype, const void*
   if (((uintptr_t)v_basis & 15) || (v_basis_sr & 7) || (v_unit_stride & 7))
     return DKV_E_UNSUPPORTED;
   if (k_ld <= 0 || v_ld <= 0) return DKV_E_ARG;
-  // buffer offsets are 32-bit byte offsets from the first row
+  // buffer offsets are 32-bit byte offsets from the start of a row
   const long long rows = (long long)B * G;
-  if (rows * k_ld >= (1LL << 30) || rows * v_ld >= (1LL << 30)) return DKV_E_UNSUPPORTED;
+  if (k_ld > FLAT_LD_MAX || v_ld > FLAT_LD_MAX || rows > 0x7fffffffLL) return DKV_E_UNSUPPORTED;
   if (rope_tiles < (S + TILE - 1) / TILE) return DKV_E_ARG;
-  if (split_len <= 0) split_len = dkv_splitk_choose_split(B, Hkv, S);
-  if (split_len % 64 != 0) return DKV_E_ARG;
+  if (*split_len <= 0) *split_len = dkv_splitk_choose_split(B, Hkv, S);
+  if (*split_len % 64 != 0) return DKV_E_ARG;
   // token indices times table strides stay 32-bit inside the kernel, both factors 24-bit
   if ((long long)S * tk_ss >= (1LL << 31) || (long long)S * tv_ss >= (1LL << 31) || tk_ss < 0 ||
       tv_ss < 0 || S >= (1 << 24) || tk_ss >= (1 << 24) || tv_ss >= (1 << 24))
     return DKV_E_UNSUPPORTED;
-  const long long n_splits = ((long long)S + split_len - 1) / split_len;
+  const long long n_splits = ((long long)S + *split_len - 1) / *split_len;
   const long long units = (long long)B * Hkv;
   if (units * n_splits > 0x7fffffffLL) return DKV_E_UNSUPPORTED;
-  if (workspace_floats < dkv_splitk_workspace_floats(B, Hq, Hkv, S, R, split_len))
-    return DKV_E_WORKSPACE;
+  *n_floats = dkv_splitk_workspace_floats(B, Hq, Hkv, S, R, *split_len);
+  return DKV_OK;
+}
+
+// Launch the split kernel (and the merge kernel when one is needed) of a call that passed
+// splitk_check, with `workspace` holding at least the floats splitk_check asked for.
+static int splitk_launch(void* stream, int route, int dtype, const void* q, long long q_sb,
+                         long long q_sh, const void* k_basis, long long k_unit_stride,
+                         long long k_basis_sr, const void* v_basis, long long v_unit_stride,
+                         long long v_basis_sr, const void* k_flat, long long k_ld,
+                         const void* v_flat, long long v_ld, const int* lens_k,
+                         const int* offs_k, long long tk_sb, long long tk_ss,
+                         const int* lens_v, const int* offs_v, long long tv_sb, long long tv_ss,
+                         const float* rope, float* workspace, void* out, long long out_sb,
+                         long long out_sh, int out_dtype, int B, int Hq, int Hkv, int G, int S,
+                         int R, int Dh, int split_len) {
+  const long long rows = (long long)B * G;
+  const long long n_splits = ((long long)S + split_len - 1) / split_len;
+  const long long units = (long long)B * Hkv;
   SplitParams p;
   p.q = (const uint16_t*)q;
   p.q_sb = q_sb;
@@ -1410,8 +1436,7 @@ extern "C" int dkv_decode_splitk(void* stream, int route, int dtype, const void*
   p.v_flat = (const uint16_t*)v_flat;
   p.k_ld = (int)k_ld;
   p.v_ld = (int)v_ld;
-  p.k_end = (uint32_t)(rows * k_ld);
-  p.v_end = (uint32_t)(rows * v_ld);
+  p.rows = (int)rows;
   p.lens_k = lens_k;
   p.offs_k = offs_k;
   p.tk_sb = tk_sb;
@@ -1457,6 +1482,32 @@ extern "C" int dkv_decode_splitk(void* stream, int route, int dtype, const void*
   }
   DKV_HIP_CHECK_LAUNCH();
   return DKV_OK;
+}
+
+extern "C" int dkv_decode_splitk(void* stream, int route, int dtype, const void* q, long long q_sb,
+                                 long long q_sh, const void* k_basis, long long k_unit_stride,
+                                 long long k_basis_sr, const void* v_basis,
+                                 long long v_unit_stride, long long v_basis_sr,
+                                 const void* k_flat, long long k_ld, const void* v_flat,
+                                 long long v_ld, const int* lens_k, const int* offs_k,
+                                 long long tk_sb, long long tk_ss, const int* lens_v,
+                                 const int* offs_v, long long tv_sb, long long tv_ss,
+                                 const float* rope, int rope_tiles, float* workspace,
+                                 long long workspace_floats, void* out, long long out_sb,
+                                 long long out_sh, int out_dtype, int B, int Hq, int Hkv, int G,
+                                 int S, int R, int Dh, int split_len) {
+  long long need = 0;
+  const int rc = splitk_check(route, dtype, q, k_basis, k_unit_stride, k_basis_sr, v_basis,
+                              v_unit_stride, v_basis_sr, k_flat, k_ld, v_flat, v_ld, lens_k,
+                              offs_k, tk_ss, lens_v, offs_v, tv_ss, rope, rope_tiles, out,
+                              out_dtype, B, Hq, Hkv, G, S, R, Dh, &split_len, &need);
+  if (rc != DKV_OK || need == 0) return rc;
+  if (!workspace) return DKV_E_ARG;
+  if (workspace_floats < need) return DKV_E_WORKSPACE;
+  return splitk_launch(stream, route, dtype, q, q_sb, q_sh, k_basis, k_unit_stride, k_basis_sr,
+                       v_basis, v_unit_stride, v_basis_sr, k_flat, k_ld, v_flat, v_ld, lens_k,
+                       offs_k, tk_sb, tk_ss, lens_v, offs_v, tv_sb, tv_ss, rope, workspace, out,
+                       out_sb, out_sh, out_dtype, B, Hq, Hkv, G, S, R, Dh, split_len);
 }
 
 extern "C" int dkv_selftest_layouts(void* stream, int* mismatches) {

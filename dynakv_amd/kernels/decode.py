@@ -68,6 +68,19 @@ class UnitLayout:
     v_basis: torch.Tensor
 
 
+# Largest row stride (elements) of a flat buffer the split kernel addresses: each workgroup's
+# buffer resource starts at its own row and covers at most 0x3ffffff0 elements, of which a row
+# needs its stride plus one 16-byte window (dkv_splitk.hip FLAT_LD_MAX).
+FLAT_LD_MAX = 0x3FFFFFE8
+
+
+def flat_ok(t: torch.Tensor) -> bool:
+    """A packed flat buffer the split kernel can read: 2-D, unit element stride, row stride at
+    most ``FLAT_LD_MAX`` (the limit is per row; the number of rows is free up to 2^31 - 1)."""
+    return (t.dim() == 2 and t.stride(1) == 1 and 0 < t.stride(0) <= FLAT_LD_MAX
+            and t.shape[0] < 2**31)
+
+
 def _basis_ok(t: torch.Tensor) -> bool:
     return (t.dim() == 3 and t.stride(2) == 1 and t.stride(1) % 8 == 0
             and t.stride(0) % 8 == 0 and t.data_ptr() % 16 == 0)
@@ -92,9 +105,7 @@ def splitk_layout(q3: torch.Tensor, k_up: torch.Tensor, v_up: torch.Tensor,
     B, hq, qdh = q3.shape
     if dh != SPLITK_HEAD_DIM or qdh != dh or r > SPLITK_MAX_RANK or r <= 0 or hq % hb:
         return None
-    if k_flat.dim() != 2 or v_flat.dim() != 2 or k_flat.stride(1) != 1 or v_flat.stride(1) != 1:
-        return None
-    if k_flat.stride(0) * 2 >= 2**31 or v_flat.stride(0) * 2 >= 2**31:
+    if not (flat_ok(k_flat) and flat_ok(v_flat)):
         return None
     if hb == hq and k_up.stride(0) == 0 and v_up.stride(0) == 0:
         n_kv = 1

@@ -184,8 +184,9 @@ int dkv_rope_table(void* stream, float* rope, int from_tile, int to_tile, float 
  *   out: (B, Hq, Dh) strides (out_sb, out_sh), dtype out_dtype = the cache dtype (what the
  *        reference returns) or DKV_F32 (the merged result before rounding).
  * Requirements: q and cache dtype f16 or bf16 (same), Dh == 128, R <= 128, hpg <= 16,
- * Hkv % G == 0, (B*G) * row stride < 2^30 elements for each flat buffer, S and the table
- * token strides < 2^24 with S * table token stride < 2^31. split_len is a multiple of 64
+ * Hkv % G == 0, flat row strides k_ld, v_ld <= 0x3fffffe8 elements (each workgroup addresses
+ * the buffer from its own row, so the number of rows is not limited), S and the table token
+ * strides < 2^24 with S * table token stride < 2^31. split_len is a multiple of 64
  * (0 = dkv_splitk_choose_split: about one workgroup per CU).
  */
 long long dkv_splitk_workspace_floats(int B, int Hq, int Hkv, int S, int R, int split_len);

@@ -90,11 +90,15 @@ def test_config4_ragged_batch(dev):
         cache.update_sp(torch.from_numpy(kc).to(dev, dtype), torch.from_numpy(case.k_len).to(dev),
                         torch.from_numpy(vc).to(dev, dtype), torch.from_numpy(case.v_len).to(dev),
                         R, 0, R)
+        # K and V of the new token are independent (coefficients and retained counts), as the
+        # reference's cutoff head produces them (compressed_cache.py:222-223)
         kx = cast_np(rng.standard_normal((G, 1, R)), dtype)
         kl = beta_lengths((G, 1), 0.20, R, rng)
+        vx = cast_np(rng.standard_normal((G, 1, R)), dtype)
+        vl = beta_lengths((G, 1), 0.20, R, rng)
         fk, fv, lk, lv, okk, ovv = cache.update_sp(
             torch.from_numpy(kx).to(dev, dtype), torch.from_numpy(kl).to(dev),
-            torch.from_numpy(kx).to(dev, dtype), torch.from_numpy(kl).to(dev), R, 0, R)
+            torch.from_numpy(vx).to(dev, dtype), torch.from_numpy(vl).to(dev), R, 0, R)
         L = cache.get_seq_length_sp(0)
         assert L == S0 + 1
         route = policy.select(L)
@@ -109,12 +113,16 @@ def test_config4_ragged_batch(dev):
         sk.append_prefill(kc, case.k_len, R)
         sv.append_prefill(vc, case.v_len, R)
         sk.append_decode(kx, kl, R)
-        sv.append_decode(kx, kl, R)
+        sv.append_decode(vx, vl, R)
         hk, ho = sk.tables()
         hv, hov = sv.tables()
-        np.testing.assert_array_equal(okk.cpu().numpy(), ho)
-        np.testing.assert_array_equal(fk[:, : int(sk.ptr.max())].float().cpu().numpy(),
-                                      sk.flat[:, : int(sk.ptr.max())].astype(np.float32))
+        for got_t, want_t, what in ((lk, hk, "K lens"), (okk, ho, "K offsets"),
+                                    (lv, hv, "V lens"), (ovv, hov, "V offsets")):
+            np.testing.assert_array_equal(got_t.cpu().numpy(), want_t, err_msg=what)
+        for got_f, slot, what in ((fk, sk, "K flat"), (fv, sv, "V flat")):
+            n = int(slot.ptr.max())
+            np.testing.assert_array_equal(got_f[:, :n].float().cpu().numpy(),
+                                          slot.flat[:, :n].astype(np.float32), err_msg=what)
         ref = A.decode_attention(q, sk.flat, cast_np(case.k_basis, dtype), sv.flat,
                                  cast_np(case.v_basis, dtype), hk, ho, hv, hov, case.theta,
                                  route=route, q_dtype="float16",

@@ -167,3 +167,32 @@ def test_more_units_than_merge_counters(dev, route):
     rows = [0, 1, 1024, 2049]
     ref = oracle_grouped(case, p["host"], route, "float16", batches=rows)
     assert_close(got[rows], ref, f"standalone merge {route}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("route", ROUTES)
+def test_flat_buffers_beyond_32bit_range(dev, route):
+    """Flat buffers of 3 rows with a row stride of 0x16000000 elements (2.06 GiB per buffer,
+    rows * stride >= 2^30): each workgroup addresses its own row, so the fast path takes them.
+    Results equal the same cache in compact buffers, and match the oracle."""
+    print(f"[gpu] splitk flat buffers past 2^30 elements route={route}", flush=True)
+    from dynakv_amd.kernels.decode import splitk_layout
+
+    case = make_case(B=3, G=1, Hq=4, S=300, uniform=(1, 128), seed=42)
+    p = packed_from_case(case, torch.bfloat16, dev)
+    LD = 0x16000000
+    big = {}
+    for name in ("k_flat", "v_flat"):
+        t = torch.empty((3, LD), dtype=torch.bfloat16, device=dev)
+        t[:, : p[name].shape[1]] = p[name]
+        big[name] = t
+    assert big["k_flat"].shape[0] * big["k_flat"].stride(0) >= 2**30
+    assert splitk_layout(p["q"], p["k_basis"], p["v_basis"], big["k_flat"], big["v_flat"]) is not None
+    compact = _run(p, case, route)
+    pb = dict(p, **big)
+    got = _run(pb, case, route)
+    assert torch.equal(got, compact)
+    ref = oracle_grouped(case, p["host"], route, "bfloat16")
+    assert_close(got, ref, f"large buffers {route}")
+    del big, pb
+    torch.cuda.empty_cache()
