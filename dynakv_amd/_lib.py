@@ -16,7 +16,8 @@ import torch
 LIB_PATH = Path(__file__).resolve().parent / "lib" / "libdynakv_amd.so"
 
 DKV_F32, DKV_F16, DKV_BF16 = 0, 1, 2
-DKV_OK, DKV_E_ARG, DKV_E_UNSUPPORTED, DKV_E_WORKSPACE = 0, -1, -2, -3
+DKV_OK, DKV_E_ARG, DKV_E_UNSUPPORTED, DKV_E_WORKSPACE, DKV_E_SCRATCH = 0, -1, -2, -3, -4
+DKV_NOALLOC_SCRATCH_FLOATS = 1 << 20
 DKV_E_HIP_BASE = 1000
 DKV_ROUTE_FUSED, DKV_ROUTE_TWO_STAGE = 0, 1
 
@@ -47,6 +48,10 @@ _SIGNATURES = {
                                _vp, _ll, _vp, _ll, _vp, _vp, _ll, _ll, _vp, _vp, _ll, _ll,
                                _vp, _i, _vp, _ll, _vp, _ll, _ll, _i,
                                _i, _i, _i, _i, _i, _i, _i, _i]),
+    "dkv_decode_splitk_noalloc": (_i, [_vp, _i, _i, _vp, _ll, _ll, _vp, _ll, _ll, _vp, _ll, _ll,
+                                       _vp, _ll, _vp, _ll, _vp, _vp, _ll, _ll, _vp, _vp, _ll, _ll,
+                                       _vp, _i, _vp, _ll, _ll, _i,
+                                       _i, _i, _i, _i, _i, _i, _i, _i]),
     "dkv_profile_begin": (_i, [_i]),
     "dkv_profile_end": (_i, [_vp, _vp, _vp]),
     "dkv_selftest_layouts": (_i, [_vp, _vp]),
@@ -125,7 +130,7 @@ def check(status: int, what: str) -> None:
     if status == DKV_OK:
         return
     msg = load().dkv_status_string(status).decode()
-    if status in (DKV_E_ARG, DKV_E_WORKSPACE):
+    if status in (DKV_E_ARG, DKV_E_WORKSPACE, DKV_E_SCRATCH):
         raise ValueError(f"{what}: {msg}")
     if status == DKV_E_UNSUPPORTED:
         raise NotImplementedError(f"{what}: {msg}")

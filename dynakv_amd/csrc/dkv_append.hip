@@ -212,6 +212,7 @@ extern "C" const char* dkv_status_string(int status) {
     case DKV_E_ARG: return "invalid argument";
     case DKV_E_UNSUPPORTED: return "unsupported configuration";
     case DKV_E_WORKSPACE: return "workspace too small";
+    case DKV_E_SCRATCH: return "call needs more than the fixed no-allocation scratch";
     default: break;
   }
   if (status <= -DKV_E_HIP_BASE) return hipGetErrorString((hipError_t)(-status - DKV_E_HIP_BASE));

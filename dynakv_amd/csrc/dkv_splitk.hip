@@ -27,6 +27,7 @@
 // the V basis (merge_kernel does this instead when a call has more units than counters).
 #include "dkv_common.h"
 
+#include <mutex>
 #include <type_traits>
 
 namespace {
@@ -1508,6 +1509,78 @@ extern "C" int dkv_decode_splitk(void* stream, int route, int dtype, const void*
                        v_basis, v_unit_stride, v_basis_sr, k_flat, k_ld, v_flat, v_ld, lens_k,
                        offs_k, tk_sb, tk_ss, lens_v, offs_v, tv_sb, tv_ss, rope, workspace, out,
                        out_sb, out_sh, out_dtype, B, Hq, Hkv, G, S, R, Dh, split_len);
+}
+
+// ---------------------------------------------------------------------------------------
+// The entry point that allocates nothing: the split workspace lives in a fixed device array.
+// ---------------------------------------------------------------------------------------
+// One copy per GPU (each device that loads the code object gets its own, at its own address),
+// held until the process ends. Host code never passes `scratch` itself to a kernel: on the host
+// the name only stands in for the symbol; the device address comes from hipGetSymbolAddress.
+__device__ __align__(256) float scratch[DKV_NOALLOC_SCRATCH_FLOATS];
+
+namespace {
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[MAX_DEVICES] = {};
+
+__global__ __launch_bounds__(256) void zero_ints_kernel(int* __restrict__ p, int n) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
+// Device address of this GPU's scratch array (the device of `stream`, or the current device for
+// the null stream). The first call on a device looks the address up with that device current
+// and zeroes the arrival counters with a fill kernel on `stream`; later calls reuse the address.
+int noalloc_scratch(hipStream_t stream, float** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return -(DKV_E_HIP_BASE + (int)e);
+  if (stream) {
+    int sdev = -1;
+    e = hipStreamGetDevice(stream, &sdev);
+    if (e != hipSuccess) return -(DKV_E_HIP_BASE + (int)e);
+    if (sdev != dev) return DKV_E_ARG;  // the stream must belong to the current device
+  }
+  if (dev < 0 || dev >= MAX_DEVICES) return DKV_E_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return -(DKV_E_HIP_BASE + (int)e);
+    if (!ptr) return -(DKV_E_HIP_BASE + (int)hipErrorInvalidSymbol);
+    hipLaunchKernelGGL(zero_ints_kernel, dim3((MERGE_COUNTERS + 255) / 256), dim3(256), 0,
+                       stream, reinterpret_cast<int*>(ptr), MERGE_COUNTERS);
+    DKV_HIP_CHECK_LAUNCH();
+    g_scratch_ptr[dev] = static_cast<float*>(ptr);
+  }
+  *out = g_scratch_ptr[dev];
+  return DKV_OK;
+}
+}  // namespace
+
+extern "C" int dkv_decode_splitk_noalloc(
+    void* stream, int route, int dtype, const void* q, long long q_sb, long long q_sh,
+    const void* k_basis, long long k_unit_stride, long long k_basis_sr, const void* v_basis,
+    long long v_unit_stride, long long v_basis_sr, const void* k_flat, long long k_ld,
+    const void* v_flat, long long v_ld, const int* lens_k, const int* offs_k, long long tk_sb,
+    long long tk_ss, const int* lens_v, const int* offs_v, long long tv_sb, long long tv_ss,
+    const float* rope, int rope_tiles, void* out, long long out_sb, long long out_sh,
+    int out_dtype, int B, int Hq, int Hkv, int G, int S, int R, int Dh, int split_len) {
+  long long need = 0;
+  int rc = splitk_check(route, dtype, q, k_basis, k_unit_stride, k_basis_sr, v_basis,
+                        v_unit_stride, v_basis_sr, k_flat, k_ld, v_flat, v_ld, lens_k, offs_k,
+                        tk_ss, lens_v, offs_v, tv_ss, rope, rope_tiles, out, out_dtype, B, Hq,
+                        Hkv, G, S, R, Dh, &split_len, &need);
+  if (rc != DKV_OK || need == 0) return rc;
+  if (need > DKV_NOALLOC_SCRATCH_FLOATS) return DKV_E_SCRATCH;
+  float* ws = nullptr;
+  rc = noalloc_scratch((hipStream_t)stream, &ws);
+  if (rc != DKV_OK) return rc;
+  return splitk_launch(stream, route, dtype, q, q_sb, q_sh, k_basis, k_unit_stride, k_basis_sr,
+                       v_basis, v_unit_stride, v_basis_sr, k_flat, k_ld, v_flat, v_ld, lens_k,
+                       offs_k, tk_sb, tk_ss, lens_v, offs_v, tv_sb, tv_ss, rope, ws, out, out_sb,
+                       out_sh, out_dtype, B, Hq, Hkv, G, S, R, Dh, split_len);
 }
 
 extern "C" int dkv_selftest_layouts(void* stream, int* mismatches) {

@@ -36,6 +36,7 @@ extern "C" {
 #define DKV_E_ARG (-1)       /* invalid argument (shape, stride, dtype, null pointer) */
 #define DKV_E_UNSUPPORTED (-2) /* valid arguments outside what the kernel implements */
 #define DKV_E_WORKSPACE (-3) /* caller workspace too small */
+#define DKV_E_SCRATCH (-4)   /* call needs more than the fixed scratch of dkv_decode_splitk_noalloc */
 #define DKV_E_HIP_BASE 1000  /* -(1000 + hipError_t) for HIP runtime failures */
 
 /* decode-attention semantics ("route") */
@@ -202,6 +203,30 @@ int dkv_decode_splitk(void* stream, int route, int dtype,
                       float* workspace, long long workspace_floats,
                       void* out, long long out_sb, long long out_sh, int out_dtype,
                       int B, int Hq, int Hkv, int G, int S, int R, int Dh, int split_len);
+
+/*
+ * dkv_decode_splitk without a workspace argument, for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). It has no
+ * counterpart in the reference. Same arguments, semantics and results as dkv_decode_splitk; the
+ * split records and arrival counters live in a fixed device array of DKV_NOALLOC_SCRATCH_FLOATS
+ * floats (4 MiB) per GPU, held until the process ends. The call allocates nothing: a call whose
+ * dkv_splitk_workspace_floats(...) exceeds that size returns DKV_E_SCRATCH. The first call on a
+ * device looks the array up and zeroes its counters with a fill kernel on `stream`; every call
+ * leaves the counters zero. All calls on one GPU share the array: calls that overlap in time
+ * (different streams without ordering, or different host threads) race and give wrong results.
+ * `stream` must belong to the current device (DKV_E_ARG otherwise).
+ */
+#define DKV_NOALLOC_SCRATCH_FLOATS (1 << 20)
+int dkv_decode_splitk_noalloc(void* stream, int route, int dtype,
+                              const void* q, long long q_sb, long long q_sh,
+                              const void* k_basis, long long k_unit_stride, long long k_basis_sr,
+                              const void* v_basis, long long v_unit_stride, long long v_basis_sr,
+                              const void* k_flat, long long k_ld, const void* v_flat, long long v_ld,
+                              const int* lens_k, const int* offs_k, long long tk_sb, long long tk_ss,
+                              const int* lens_v, const int* offs_v, long long tv_sb, long long tv_ss,
+                              const float* rope, int rope_tiles,
+                              void* out, long long out_sb, long long out_sh, int out_dtype,
+                              int B, int Hq, int Hkv, int G, int S, int R, int Dh, int split_len);
 
 /*
  * Launch timing hooks (measurement only, no reference counterpart). Between
