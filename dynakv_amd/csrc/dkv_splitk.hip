@@ -6,19 +6,20 @@
 // and one contiguous token range ("split", a multiple of 64 tokens); waves take 16-token tiles
 // round-robin.
 //
-// Prologue: half of the K basis goes to registers (MFMA A operands), the other half to LDS
-// ([dim][rank], read per tile), plus the mask table; each lane keeps its token slot's fixed
-// rotation R(n) and the query pairs of its frequency. Each wave then runs a software pipeline
+// Prologue: the K basis goes to registers (MFMA A operands; NREG_PP < 4 keeps part of it in
+// LDS instead, [dim][rank], read per tile), the mask table and the table of every lane's fixed
+// token-slot rotation R(n) to LDS; each lane keeps the query pairs of its frequency. Each wave then runs a software pipeline
 // over its tiles: the length/offset tables of tile j+2 and the coefficient windows of tile j+1
 // (direct-to-LDS buffer loads, one lane = one token x 8 ranks, empty pieces read from an
 // out-of-range offset as zeros) are in flight while tile j computes:
 //   1. the partial piece of each token is masked in place; the K windows go to registers;
 //   2. the query rotated back by the tile's base position, R(-16T) q (RoPE by angle addition:
-//      q . R(16T+n) k = (R(-16T) q) . (R(n) k)), split into fp16 hi/lo and staged through LDS
+//      q . R(16T+n) k = (R(-16T) q) . (R(n) k)), split into bf16 hi/lo and staged through LDS
 //      into the B operand of the score MFMA;
 //   3. K^T[128 x 16] = BK^T . X^T on v_mfma_f32_16x16x32_{bf16,f16}, two 16-dim blocks at a
-//      time ((i, i+64) rotate-half pairs), R(n) per lane and fp16 conversion, scores on
-//      16x16x32 f16 MFMA (hi and lo query columns added by one DPP step);
+//      time ((i, i+64) rotate-half pairs), R(n) per lane in fp32, K' split into bf16 hi + lo,
+//      scores on 16x16x32 bf16 MFMA (K'hi and K'lo products; hi and lo query columns added by
+//      one DPP step);
 //   4. online softmax in the log2 domain, lazily rescaled (only when the running max grows by
 //      more than 2^11.5);
 //   5. P.X^V in coefficient space on MFMA, the X^V operand read transposed from the windows.
@@ -39,7 +40,7 @@ constexpr int NTHREADS = WAVES * 64;
 constexpr int BK_LD = 136;    // LDS row pitch (elements) of the transposed K basis
 // K^T is formed as 4 pairs pp of 16-dim blocks (pp, pp + 4); the basis rows of the first
 // NREG_PP pairs stay in registers, the others are read from LDS per tile
-constexpr int NREG_PP = 3;
+constexpr int NREG_PP = 4;
 constexpr int SBH_ROWS = 32 * (4 - NREG_PP);
 constexpr int VT_LD = 136;    // LDS row pitch (elements) of a wave's V tile
 constexpr int PREC = DH + 2;  // floats per partial record: m, l, acc[128]
@@ -146,6 +147,24 @@ __device__ __forceinline__ void split_f16x2(float x0, float x1, float minus_one,
   const _Float16 l1 = (_Float16)__builtin_fmaf((float)hv[1], minus_one, x1);
   hi = __builtin_bit_cast(uint32_t, hv);
   lo = __builtin_bit_cast(uint32_t, dkv_f16x2{l0, l1});
+}
+
+__device__ __forceinline__ dkv_f32x4 mfma_bf16(const dkv_u32x4& a, const dkv_u32x4& b,
+                                               dkv_f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(dkv_bf16x8, a),
+                                                 __builtin_bit_cast(dkv_bf16x8, b), c, 0, 0, 0);
+}
+
+// x ~= hi + lo in bf16 for two values packed per dword: hi = RNE(x), lo = RNE(x - hi). x - hi is
+// exact in fp32 (a bf16 value as fp32 is its bits in the upper half of a dword), so the pair
+// carries 16 significant bits over fp32's exponent range (no overflow where fp32 has none).
+__device__ __forceinline__ void split_bf16x2(float x0, float x1, uint32_t& hi, uint32_t& lo) {
+  typedef __attribute__((ext_vector_type(2))) float f32x2;
+  const uint32_t h = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{x0, x1}, dkv_bf16x2));
+  const float l0 = x0 - __uint_as_float(h << 16);
+  const float l1 = x1 - __uint_as_float(h & 0xffff0000u);
+  hi = h;
+  lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{l0, l1}, dkv_bf16x2));
 }
 
 // Element-wise gather of the first nv (1..8) 16-bit values at element offset e, the rest zero:
@@ -460,12 +479,16 @@ __device__ __forceinline__ void merge_unit(const SplitParams& p, int unit, uint8
 template <int DT, int ROUTE, bool WIDE>
 __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
   // LDS: per-wave rings (NSLOT gather slots: K then V, 4 chunks x 64 lanes x 16 bytes each;
-  // TSLOT table slots: lens_k, offs_k, lens_v, offs_v x 16 tokens), the streamed half of the
-  // K basis ([dim][rank] rows of dims 32..63 and 96..127) and the mask table. The full basis
+  // TSLOT table slots: lens_k, offs_k, lens_v, offs_v x 16 tokens), the part of the K basis not
+  // held in registers ([dim][rank] rows; none with NREG_PP = 4), the R(n) table and the mask
+  // table. The full basis
   // staging copy, the per-tile query operand and the epilogue scratch alias the rings.
   __shared__ __attribute__((aligned(16))) uint32_t sMask[MASK_ROWS][4];
   __shared__ __attribute__((aligned(16))) int sTabRing[WAVES][TSLOT][4][TILE];
-  __shared__ __attribute__((aligned(16))) uint16_t sBH[SBH_ROWS * BK_LD];
+  __shared__ __attribute__((aligned(16))) uint16_t sBH[(SBH_ROWS > 0 ? SBH_ROWS : 1) * BK_LD];
+  // R(n) of every lane's token slot, in lane order: entry [2*pp + k][lane] holds (cos, sin) of
+  // the lane's frequencies 16*pp + 4*g + 2k and + 1 (one conflict-free 16-byte read per lane)
+  __shared__ __attribute__((aligned(16))) dkv_f32x4 sRn[8][64];
   // 256-byte aligned: the query operand's row swizzle XORs bits 4..7 of ring addresses
   __shared__ __attribute__((aligned(256))) uint8_t sRing[WAVES * NSLOT * GSLOT_BYTES];
   static_assert(DH * BK_LD * 2 <= WAVES * NSLOT * GSLOT_BYTES, "basis staging fits the rings");
@@ -571,18 +594,12 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
       qh[h] = h < p.hpg ? v : 0u;
     }
   }
-  // R(n) of this lane's token slot for its 16 frequencies i = 16*pp + 4*g + w
-  float rc[16], rs[16];
+  // R(n) table in LDS (see sRn): thread t fills entry t (8 x 64 entries, 512 threads)
   {
-    const float* delt = p.rope + (long long)n * 128;
-#pragma unroll
-    for (int pp = 0; pp < 4; ++pp)
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const int i = 16 * pp + 4 * g + w, f = pp * 4 + w;
-        rc[f] = delt[2 * i];
-        rs[f] = delt[2 * i + 1];
-      }
+    const int k = tid >> 6, ln = tid & 63;
+    const int nn = ln & 15, gg = ln >> 4, i0 = 16 * (k >> 1) + 4 * gg + 2 * (k & 1);
+    const float* delt = p.rope + (long long)nn * 128 + 2 * i0;
+    sRn[k][ln] = dkv_f32x4{delt[0], delt[1], delt[2], delt[3]};
   }
   // The per-tile query operand lives in the K half of the tile's gather slot once the K
   // coefficients are in registers: row r (one per operand column), chunk c (16 bytes: dwords
@@ -730,11 +747,6 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
   settle(stc);
   settle(sts);
 #pragma unroll
-  for (int f = 0; f < 16; ++f) {
-    settle(rc[f]);
-    settle(rs[f]);
-  }
-#pragma unroll
   for (int h = 0; h < QH; ++h) settle(qh[h]);
 
   // T0 and T1 (a full wait: compiler-generated memory operations of the prologue, such as
@@ -776,7 +788,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-    // ---- query of this tile: R(-16T) q times the score scale, as fp16 hi + lo, written to the
+    // ---- query of this tile: R(-16T) q times the score scale, as bf16 hi + lo, written to the
     //      K half of the slot (its coefficients are in xk; LDS accesses of a wave run in order)
     //      and read back as the B operand of the score MFMAs (lane: column n, k-group g) ----
     dkv_u32x4 bq[4], bq_lo[4];
@@ -787,7 +799,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
       settle(wr);
       auto rotate = [&](int h, uint32_t& hi, uint32_t& lo) {
         const float x = elt_to_f32<DT>(qh[h] & 0xffffu), y = elt_to_f32<DT>(qh[h] >> 16);
-        split_f16x2(cb * x + sb * y, cb * y - sb * x, p.minus_one, hi, lo);
+        split_bf16x2(cb * x + sb * y, cb * y - sb * x, hi, lo);
       };
       // the next tile's base rotation
       bc = cb * stc - sb * sts;
@@ -839,7 +851,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
       }
     }
 
-    // ---- 1-3: K reconstruction, R(n) on the lane's token, fp16 K', scores -------------------
+    // ---- 1-3: K reconstruction, R(n) on the lane's token, K' as bf16 hi + lo, scores -------
     dkv_f32x4 sc = {0.f, 0.f, 0.f, 0.f};
     // blocks pp and pp+4 of K^T for the tile; pp < NREG_PP from the registers, the others
     // from the streamed rows in sBH
@@ -871,15 +883,19 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
     for (int pp = 0; pp < 4; ++pp) {
       if (pp + 1 < 4) recon(pp + 1, C0[(pp + 1) & 1], C1[(pp + 1) & 1]);
       const dkv_f32x4 c0 = C0[pp & 1], c1 = C1[pp & 1];
-      uint32_t k4[4];
+      // K' rotated in fp32 and split into bf16 hi + lo parts: the score products are
+      // (K'hi + K'lo) . (q hi + q lo) to ~16 bits per factor, with fp32's range
+      uint32_t kh[4], kl[4];
+      const dkv_f32x4 r01 = sRn[2 * pp][lane], r23 = sRn[2 * pp + 1][lane];
+      const float rc[4] = {r01.x, r01.z, r23.x, r23.z}, rs[4] = {r01.y, r01.w, r23.y, r23.w};
 #pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const int f = pp * 4 + w;
-        k4[w] = pack_f16x2(c0[w] * rc[f] - c1[w] * rs[f], c1[w] * rc[f] + c0[w] * rs[f]);
-      }
-      const dkv_u32x4 ka = dkv_u32x4{k4[0], k4[1], k4[2], k4[3]};
-      sc = mfma_f16(ka, bq[pp], sc);
-      if constexpr (WIDE) sc = mfma_f16(ka, bq_lo[pp], sc);
+      for (int w = 0; w < 4; ++w)
+        split_bf16x2(c0[w] * rc[w] - c1[w] * rs[w], c1[w] * rc[w] + c0[w] * rs[w], kh[w], kl[w]);
+      const dkv_u32x4 ka = dkv_u32x4{kh[0], kh[1], kh[2], kh[3]};
+      const dkv_u32x4 kal = dkv_u32x4{kl[0], kl[1], kl[2], kl[3]};
+      sc = mfma_bf16(ka, bq[pp], sc);
+      sc = mfma_bf16(kal, bq[pp], sc);
+      if constexpr (WIDE) sc = mfma_bf16(ka, bq_lo[pp], sc);
     }
     if constexpr (!WIDE) {
       // column n += column n + 8 (the lo part of head n) within each row of 16 lanes
