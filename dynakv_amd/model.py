@@ -34,6 +34,7 @@ import torch
 import torch.nn.functional as F
 from torch.nn.attention import SDPBackend, sdpa_kernel
 
+from .formats import merge_projection
 from .kernels.compressed_cache import CustomDynamicCache
 from .kernels.cutoff import CutoffHead
 from .kernels.decode import grouped_decode_attention
@@ -124,9 +125,11 @@ class RandomLlama:
             wk, wv = rnd(G * Dh, H), rnd(G * Dh, H)
             Uk = _orthogonal(Dh, G, g, self.device)  # (G, d, r): K_g = U_g c_g
             Uv = _orthogonal(Dh, G, g, self.device)
-            # coefficients c_g = U_g^T k_g: the projection merged with the basis transpose
-            wk_c = torch.matmul(Uk.transpose(1, 2), wk.float().view(G, Dh, H)).reshape(G * Dh, H)
-            wv_c = torch.matmul(Uv.transpose(1, 2), wv.float().view(G, Dh, H)).reshape(G * Dh, H)
+            # coefficients c_g = U_g^T k_g: the projection merged with the basis transpose (the
+            # reference's one-time merge, k_proj <- k_down @ k_proj, per KV group)
+            wk_c = merge_projection(wk.float().view(G, Dh, H), Uk.transpose(1, 2))[0]
+            wv_c = merge_projection(wv.float().view(G, Dh, H), Uv.transpose(1, 2))[0]
+            wk_c, wv_c = wk_c.reshape(G * Dh, H), wv_c.reshape(G * Dh, H)
             cut = [rnd(G, Dh, Dh) for _ in range(2)]
             bias = [ramp.expand(G, Dh).contiguous() for _ in range(2)]
             w_gu = rnd(2 * s.ffn, H)

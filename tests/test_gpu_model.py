@@ -22,17 +22,18 @@ def _rope(x, pos0, theta):
     import numpy as np
 
     c, s = rope_cos_sin(np.arange(pos0, pos0 + S), 128, theta)
-    c = torch.from_numpy(c).float()
-    s = torch.from_numpy(s).float()
+    c = torch.from_numpy(c).float().to(x.device)
+    s = torch.from_numpy(s).float().to(x.device)
     x0, x1 = x[..., :64], x[..., 64:]
     return torch.cat([x0 * c - x1 * s, x1 * c + x0 * s], dim=-1)
 
 
-def _reference_logits(model, tokens, lens_k=None, lens_v=None):
-    """float32 CPU forward over all positions; lens_*: per layer (B*G, S) retained dims or None
-    (keep all)."""
+def _reference_logits(model, tokens, lens_k=None, lens_v=None, device="cpu"):
+    """float32 forward over all positions (on the CPU, or on ``device`` for the full shape);
+    lens_*: per layer (B*G, S) retained dims or None (keep all)."""
     s = model.shape
-    f = lambda t: t.detach().float().cpu()  # noqa: E731
+    f = lambda t: t.detach().to(device).float()  # noqa: E731
+    tokens = tokens.to(device)
     x = f(model.embed)[tokens]
     B, S = tokens.shape
     G, Dh, hpg = s.kv_heads, s.head_dim, s.heads // s.kv_heads
@@ -42,7 +43,7 @@ def _reference_logits(model, tokens, lens_k=None, lens_v=None):
         kc = (h @ f(lw.wk_c).T).view(B, S, G, Dh).transpose(1, 2)  # (B, G, S, R)
         vc = (h @ f(lw.wv_c).T).view(B, S, G, Dh).transpose(1, 2)
         if lens_k is not None:
-            ar = torch.arange(Dh)
+            ar = torch.arange(Dh, device=device)
             kc = kc * (ar < lens_k[i].view(B, G, S, 1)).float()
             vc = vc * (ar < lens_v[i].view(B, G, S, 1)).float()
         k = torch.einsum("bgsr,grd->bgsd", kc, f(lw.k_basis))
@@ -52,7 +53,8 @@ def _reference_logits(model, tokens, lens_k=None, lens_v=None):
         k = k.repeat_interleave(hpg, dim=1)
         v = v.repeat_interleave(hpg, dim=1)
         sc = q @ k.transpose(-1, -2) / math.sqrt(Dh)
-        sc = sc.masked_fill(torch.ones(S, S, dtype=torch.bool).triu(1), float("-inf"))
+        sc = sc.masked_fill(torch.ones(S, S, dtype=torch.bool, device=device).triu(1),
+                            float("-inf"))
         a = torch.softmax(sc, -1) @ v
         x = x + a.transpose(1, 2).reshape(B, S, s.hidden) @ f(lw.wo).T
         h2 = _rms(x, f(lw.ln2), s.eps)
@@ -97,3 +99,57 @@ def test_model_matches_float32_forward(dev, kind):
         assert 0.3 < frac < 0.65  # the cutoff heads aim at 0.47
     ref = _reference_logits(model, tokens, lk, lv)
     _close(got, ref, kind)
+
+
+@pytest.mark.gpu
+def test_full_shape_keep_all_dims_matches_dense(dev):
+    """Config 5 at its full Llama-3-8B shape (hidden 4096, 32 layers, 32/8 heads, FFN 14336,
+    vocab 128256, bf16 weights N(0, 0.02)). With every layer's cutoff heads set to keep all 128
+    dims the compressed model computes the dense model's function (orthogonal bases: k = U U^T k)
+    and differs only by rounding (bf16 coefficients instead of bf16 keys, fp32-reconstructed K
+    and V in the kernels). Its logits at the prompt's last position and over three decode steps
+    must match the dense model's."""
+    from dynakv_amd.kernels.cutoff import CutoffHead
+
+    print("[gpu] model full shape, r = 128 everywhere, against the dense model", flush=True)
+    shape = LlamaShape()
+    model = RandomLlama(shape, device=dev, seed=11)
+    G, Dh = shape.kv_heads, shape.head_dim
+    zero = torch.zeros(G, Dh, Dh, device=dev, dtype=model.dtype)
+    bias = torch.zeros(G, Dh, device=dev, dtype=model.dtype)
+    # softmax mass on index 0: every prefix sum is ~1, so flip(cumsum) >= 0.1 keeps all dims
+    bias[:, 0] = 30.0
+    for lw in model.layers:
+        lw.cutoff = CutoffHead(zero, bias, zero, bias, groups=G)
+    g = torch.Generator(device="cpu").manual_seed(5)
+    B, S = 2, 64
+    tokens = torch.randint(0, shape.vocab, (B, S + 3), generator=g)
+    outs = {}
+    for kind in ("compressed", "dense"):
+        gen = CompressedLlama(model) if kind == "compressed" else DenseLlama(model, max_len=128)
+        x = gen.prefill(tokens[:, :S].to(dev))
+        lg = [gen.logits(x[:, -1:]).float()]
+        for j in range(3):
+            x = gen.decode(tokens[:, S + j:S + j + 1].to(dev), S + j)
+            lg.append(gen.logits(x).float())
+        outs[kind] = torch.cat(lg, dim=1).cpu()  # (B, 4, vocab)
+        if kind == "compressed":
+            for slots in (gen.cache.key_cache_sp, gen.cache.value_cache_sp):
+                for c in slots:
+                    assert int(c[1][:, : S + 3].min()) == Dh  # every dim retained
+        del gen
+        torch.cuda.empty_cache()
+    # float32 forward of the same weights over all S + 3 positions (compressed form, all dims
+    # kept); positions S-1 .. S+2 are the prompt's last and the three decoded ones
+    with torch.no_grad():
+        ref = _reference_logits(model, tokens, device=dev)[:, S - 1:].float().cpu()
+    scale = ref.abs().amax().item()
+    errs = {k: (v - ref).abs().amax().item() for k, v in outs.items()}
+    top1 = {k: (v.argmax(-1) == ref.argmax(-1)).float().mean().item() for k, v in outs.items()}
+    between = (outs["compressed"] - outs["dense"]).abs().amax().item()
+    print(f"[parity] full shape r=128 against float32: compressed max_abs={errs['compressed']:.3e} "
+          f"dense max_abs={errs['dense']:.3e} (|ref|max={scale:.3f}); compressed vs dense "
+          f"{between:.3e}; top-1 agreement with float32 {top1}", flush=True)
+    # the compressed cache adds no error beyond the dense bf16 model's own rounding
+    assert errs["compressed"] <= 1.25 * errs["dense"] + 0.01 * scale, errs
+    assert errs["compressed"] <= 0.1 * scale, errs
