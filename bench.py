@@ -369,31 +369,39 @@ def bench_prefill(dev, iters=10, B=4, S=2048, Hq=32, Hkv=8, dtype=torch.bfloat16
     }
 
 
-def bench_e2e(dev, batches=(1, 2, 4), prompt_len=2048, new_tokens=100):
+def bench_e2e(dev, batches=(1, 2, 4), prompt_len=2048, new_tokens=100, models="both"):
     """Config 5: greedy generation with a random-init Llama-3-8B (bf16 N(0, 0.02) weights,
     per-head random orthogonal bases, cutoff heads set for mean retention 0.47) over the
-    compressed cache, against the same weights with an uncompressed cache (torch's fused
-    attention kernels). tokens/s = batch * new tokens / wall time with prefill, as the
-    reference's benchmark_throughput.py:73 counts it; decode-only tokens/s beside it. Both
-    models run eagerly (one launch per op, no graph capture)."""
+    compressed cache, against the same weights with an uncompressed cache (decode attention by
+    the same split kernel over the full cache, every token at 128 dims with an identity basis;
+    prefill attention by torch's fused attention). tokens/s = batch * new tokens / wall time
+    with prefill, as the reference's benchmark_throughput.py:73 counts it; decode-only tokens/s
+    beside it. Both models run eagerly (one launch per op, no graph capture). ``models``:
+    "both", "compressed" or "dense" (one model alone, for a kernel trace of it)."""
     from dynakv_amd.model import CompressedLlama, DenseLlama, LlamaShape, RandomLlama
 
     shape = LlamaShape()
     model = RandomLlama(shape, device=dev, seed=5)
-    comp, dense = CompressedLlama(model), DenseLlama(model, max_len=prompt_len + new_tokens + 8)
+    comp = CompressedLlama(model) if models in ("both", "compressed") else None
+    dense = (DenseLlama(model, max_len=prompt_len + new_tokens + 8)
+             if models in ("both", "dense") else None)
     g = torch.Generator(device="cpu").manual_seed(11)
     res = {"model": "random-init Llama-3-8B shape (32 layers, 4096 hidden, 32/8 heads, FFN "
                     "14336, vocab 128256), bf16", "prompt_len": prompt_len,
            "new_tokens": new_tokens, "runs": []}
     # one short warm-up of each path (kernel loading, library handles)
     warm = torch.randint(0, shape.vocab, (1, 64), generator=g).to(dev)
-    comp.generate(warm, 4)
-    dense.generate(warm, 4)
+    for m in (comp, dense):
+        if m is not None:
+            m.generate(warm, 4)
+    empty = {"tokens_per_s": 0.0, "decode_tokens_per_s": 0.0, "prefill_s": 0.0, "kv_bytes": 0,
+             "tokens": None}
     for B in batches:
         prompt = torch.randint(0, shape.vocab, (B, prompt_len), generator=g).to(dev)
-        rc = comp.generate(prompt, new_tokens)
-        rd = dense.generate(prompt, new_tokens)
-        lens = [int(c[1][:, :c[4]].float().mean().item()) for c in comp.cache.key_cache_sp[:1]]
+        rc = comp.generate(prompt, new_tokens) if comp is not None else empty
+        rd = dense.generate(prompt, new_tokens) if dense is not None else empty
+        lens = ([int(c[1][:, :c[4]].float().mean().item()) for c in comp.cache.key_cache_sp[:1]]
+                if comp is not None else [])
         res["runs"].append({
             "batch": B,
             "compressed_tokens_per_s": round(rc["tokens_per_s"], 1),
@@ -405,7 +413,8 @@ def bench_e2e(dev, batches=(1, 2, 4), prompt_len=2048, new_tokens=100):
             "compressed_kv_bytes": rc["kv_bytes"],
             "dense_kv_bytes": rd["kv_bytes"],
             "mean_retained_dims_layer0_k": lens[0] if lens else None,
-            "same_tokens_frac": round(float((rc["tokens"] == rd["tokens"]).float().mean()), 3),
+            "same_tokens_frac": (round(float((rc["tokens"] == rd["tokens"]).float().mean()), 3)
+                                 if comp is not None and dense is not None else None),
         })
     del comp, dense, model
     torch.cuda.empty_cache()
@@ -447,6 +456,8 @@ def main():
                     help="run config 5 alone (for a kernel trace of the decoder) and print its "
                          "JSON object")
     ap.add_argument("--e2e-batches", default="1,2,4", help="config 5 batch sizes")
+    ap.add_argument("--e2e-model", default="both", choices=["both", "compressed", "dense"],
+                    help="config 5 models to run (one alone for a kernel trace of it)")
     ap.add_argument("--e2e-tokens", type=int, default=100, help="config 5 new tokens")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="run one device copy of this many MiB first (counter calibration)")
@@ -463,7 +474,8 @@ def main():
     dev = torch.device("cuda:0")
     e2e_batches = tuple(int(b) for b in args.e2e_batches.split(","))
     if args.e2e_only:
-        print(json.dumps({"e2e": bench_e2e(dev, batches=e2e_batches, new_tokens=args.e2e_tokens)}),
+        print(json.dumps({"e2e": bench_e2e(dev, batches=e2e_batches, new_tokens=args.e2e_tokens,
+                                           models=args.e2e_model)}),
               flush=True)
         return
     cfg = Config3 if args.workload == "config3" else Config2

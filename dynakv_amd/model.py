@@ -21,7 +21,9 @@ only the forward math):
   folded into its x staging for one or two rows, and the SwiGLU product is one kernel --
   the same stages serve the dense baseline.
 * ``DenseLlama.generate``: the uncompressed-cache baseline of the same weights (K/V kept in
-  full in a preallocated cache, attention by torch's scaled_dot_product_attention).
+  full in a preallocated cache; decode attention by the same split kernel over that cache read
+  as a packed cache with all 128 dims per token and an identity basis, prefill attention by
+  torch's scaled_dot_product_attention).
 """
 
 from __future__ import annotations
@@ -307,7 +309,12 @@ _FAST_SDPA = [SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]
 
 
 class DenseLlama(_Generator):
-    """The same weights with an uncompressed cache (K/V of every layer kept in full)."""
+    """The same weights with an uncompressed cache: every token's K and V kept in full (head dim
+    128 per KV head, K before RoPE). Decode attention runs the compressed path's split kernel on
+    that cache read as a packed cache with every token retaining all 128 dims and an identity
+    basis -- dense GQA decode attention in the packed format (fused-route semantics: fp32
+    scores, no rounding) -- so the two models differ in the bytes their caches hold, not in the
+    attention implementation. Prefill attention is torch's fused attention on the rotated keys."""
 
     def __init__(self, model: RandomLlama, max_len: int = 4096):
         super().__init__(model)
@@ -316,32 +323,42 @@ class DenseLlama(_Generator):
         self.len = 0
 
     def _kv(self, lw, y, pos0):
-        """``y``: the layer's fused q/k/v projection output (B, S, H + 2 G Dh)."""
+        """``y``: the layer's fused q/k/v projection output (B, S, H + 2 G Dh). Returns the
+        rotated q (B, Hq, S, Dh) and K (before RoPE) / V as (B, G, S, Dh)."""
         B, S, _ = y.shape
         s = self.s
         q, k, v = self._split(y)
         q = q.reshape(B, S, s.heads, s.head_dim)
-        k = k.reshape(B, S, s.kv_heads, s.head_dim).transpose(1, 2).contiguous()
+        k = k.reshape(B, S, s.kv_heads, s.head_dim).transpose(1, 2)
         v = v.reshape(B, S, s.kv_heads, s.head_dim).transpose(1, 2)
-        rope_dense_(k, theta=s.theta, pos0=pos0)
         return _rope_q(q, pos0, s.theta), k, v
 
     def prefill(self, prompt: torch.Tensor) -> torch.Tensor:
         s = self.s
         B, S = prompt.shape
         dev, dt = self.m.device, self.m.dtype
-        shape = (B, s.kv_heads, self.max_len, s.head_dim)
-        self.k = [torch.empty(shape, device=dev, dtype=dt) for _ in range(s.layers)]
-        self.v = [torch.empty(shape, device=dev, dtype=dt) for _ in range(s.layers)]
+        G, Dh = s.kv_heads, s.head_dim
+        rows = B * G
+        # per layer: K and V rows (b*G + g) of max_len tokens x Dh, tokens back to back, and the
+        # shared tables of the packed view (128 dims per token, token t at offset 128 t)
+        self.k = [torch.empty((rows, self.max_len * Dh), device=dev, dtype=dt)
+                  for _ in range(s.layers)]
+        self.v = [torch.empty((rows, self.max_len * Dh), device=dev, dtype=dt)
+                  for _ in range(s.layers)]
+        self.lens = torch.full((rows, self.max_len), Dh, device=dev, dtype=torch.int32)
+        self.offs = (torch.arange(self.max_len, device=dev, dtype=torch.int32) * Dh).expand(
+            rows, -1).contiguous()
+        self.eye = torch.eye(Dh, device=dev, dtype=dt).expand(G, Dh, Dh).contiguous()
         hpg = s.heads // s.kv_heads
         x = F.embedding(prompt, self.m.embed)
 
         def attn(i, lw, y):
             qh, k, v = self._kv(lw, y, 0)
-            self.k[i][:, :, :S] = k
-            self.v[i][:, :, :S] = v
+            self.k[i][:, :S * Dh] = k.reshape(rows, S * Dh)
+            self.v[i][:, :S * Dh] = v.reshape(rows, S * Dh)
+            kr = rope_dense_(k.contiguous(), theta=s.theta, pos0=0)
             with sdpa_kernel(_FAST_SDPA):
-                a = F.scaled_dot_product_attention(qh, k.repeat_interleave(hpg, dim=1),
+                a = F.scaled_dot_product_attention(qh, kr.repeat_interleave(hpg, dim=1),
                                                    v.repeat_interleave(hpg, dim=1),
                                                    is_causal=True)
             return a.transpose(1, 2).reshape(B, S, s.hidden)
@@ -351,22 +368,22 @@ class DenseLlama(_Generator):
         return x
 
     def decode(self, tok: torch.Tensor, pos: int) -> torch.Tensor:
-        """One token: K/V appended at position len, then the query heads of each KV group
-        attend as that group's queries (no copy of the cache per step)."""
+        """One token: K/V written at position len, then decode attention over len + 1 tokens."""
         s = self.s
         x = F.embedding(tok, self.m.embed)
         B = tok.shape[0]
         L = self.len
-        hpg = s.heads // s.kv_heads
+        Dh = s.head_dim
+        rows = B * s.kv_heads
+        lens, offs = self.lens[:, :L + 1], self.offs[:, :L + 1]
 
         def attn(i, lw, y):
             qh, k, v = self._kv(lw, y, pos)
-            self.k[i][:, :, L:L + 1] = k
-            self.v[i][:, :, L:L + 1] = v
-            qg = qh.view(B, s.kv_heads, hpg, s.head_dim)
-            with sdpa_kernel(_FAST_SDPA):
-                a = F.scaled_dot_product_attention(qg, self.k[i][:, :, :L + 1],
-                                                   self.v[i][:, :, :L + 1])
+            self.k[i][:, L * Dh:(L + 1) * Dh] = k.reshape(rows, Dh)
+            self.v[i][:, L * Dh:(L + 1) * Dh] = v.reshape(rows, Dh)
+            a = grouped_decode_attention(qh[:, :, 0], self.k[i], self.v[i], lens, offs, lens,
+                                         offs, self.eye, self.eye, theta=s.theta,
+                                         route="short_fused")
             return a.reshape(B, 1, s.hidden)
 
         x = self._run(x, attn, "w_qkv")
@@ -374,6 +391,7 @@ class DenseLlama(_Generator):
         return x
 
     def kv_bytes(self) -> int:
+        """Stored K and V payload: every token of every (batch, KV head) row at 128 dims."""
         s = self.s
-        B = self.k[0].shape[0] if self.k else 0
-        return 2 * s.layers * B * s.kv_heads * self.len * s.head_dim * self.m.embed.element_size()
+        rows = self.k[0].shape[0] if self.k else 0
+        return 2 * s.layers * rows * self.len * s.head_dim * self.m.embed.element_size()
