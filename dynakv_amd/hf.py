@@ -1,0 +1,335 @@
+"""Hugging Face model classes over the compressed cache (transformers 5.x).
+
+The reference's model-level surface for its physical path:
+
+* ``get_model_class(model_type)`` (reference ``src/dynakv/__init__.py:6-17``) returns
+  ``CustomLlamaForCausalLM`` for ``"llama"``; the reference picks its physical attention and
+  cache classes when ``DYNAKV_PHYSICAL_KERNELS=1`` (``custom_llama.py:11-16``), which is the only
+  path this build implements -- the research (masked-dimension, trainable) classes and Qwen3 are
+  not part of it, and asking for them raises;
+* ``CustomAttention`` (``kernels/compressed_attention.py:204-357``): a ``LlamaAttention`` with the
+  reference's DynaKV parameters under the reference's names (``Wk, bk, Wv, bv`` -- the cutoff
+  heads -- and ``k_down, k_up, v_down, v_up``, identity unless a checkpoint or the
+  ``DYNAKV_PCA_DIR`` files provide them), the reference's one-time merge of ``k_down`` / ``v_down``
+  into the K/V projections on the first forward pass, and a forward that appends the cutoff head's
+  masked coefficients to a ``CustomDynamicCache`` and attends over it;
+* ``CustomLlamaModel`` / ``CustomLlamaForCausalLM`` (``custom_llama.py:93-323``): Llama with
+  ``CustomAttention`` in every layer, a ``CustomDynamicCache`` created for ``use_cache``, and
+  ``generate`` handing that cache to transformers' generation loop.
+
+Layouts. When ``k_up``, ``v_up``, ``Wk`` and ``Wv`` are block-diagonal per KV head (the per-head
+layout of the benchmark configurations), the layer keeps one 128 x 128 basis and cutoff head per
+KV head and one packed cache row per (batch, KV head): decode steps run ``DecodeLayerPlan`` (one
+call: cutoff, appends, q RoPE, split-K attention), prefill attends from the masked coefficients
+(``coef_prefill_attention``, or from the cache when it already holds tokens). Otherwise the
+reference's joint layout is used (one ``D x D`` basis and cutoff head, rank up to ``D``, one row
+per batch element) through ``compressed_decode_attention`` and a reconstruct-and-attend prefill.
+
+Position handling: q is rotated by the kernels' RoPE (angles ``float32(pos) * inv_freq`` in
+fp32, rounded once), the same rotation the kernels apply to the reconstructed keys; the
+``position_embeddings`` the HF decoder passes are not used.
+"""
+
+from __future__ import annotations
+
+import os
+import sys
+
+import torch
+from torch import nn
+from transformers.models.llama.modeling_llama import (LlamaAttention, LlamaForCausalLM,
+                                                      LlamaModel, LlamaPreTrainedModel)
+from transformers.modeling_outputs import BaseModelOutputWithPast
+
+from . import formats as F
+from .kernels.compressed_cache import CustomDynamicCache
+from .kernels.cutoff import CutoffHead
+from .kernels.decode import grouped_decode_attention
+from .kernels.layer import DecodeLayerPlan
+from .kernels.prefill import (coef_prefill_attention, compressed_prefill_attention,
+                              prefill_attention, rope_dense_)
+from .kernels.router import KernelPolicy, compressed_decode_attention
+
+PHYSICAL_ENV = "DYNAKV_PHYSICAL_KERNELS"
+
+
+def get_model_class(model_type: str):
+    """The model class of a backbone (reference ``__init__.py:6-17``): ``"llama"`` (also
+    ``llama3`` / ``llama-3``) -> ``CustomLlamaForCausalLM`` over the physical compressed cache.
+    Requires ``DYNAKV_PHYSICAL_KERNELS=1`` (the reference's switch to its physical classes,
+    which ``benchmark_throughput.py --implementation physical`` sets)."""
+    normalized = model_type.lower().replace("_", "-")
+    if normalized in {"qwen", "qwen3", "qwen-3"}:
+        raise ValueError("Qwen3 is not part of this build (its decode path is the Llama one with "
+                         "q/k norms); use model_type 'llama'")
+    if normalized not in {"llama", "llama3", "llama-3"}:
+        raise ValueError(f"Unsupported model type: {model_type!r}; choose llama or qwen.")
+    if os.environ.get(PHYSICAL_ENV) != "1":
+        raise ValueError(f"this build implements the physical compressed-cache path only: set "
+                         f"{PHYSICAL_ENV}=1 (the research masked-dimension classes are not part "
+                         f"of it)")
+    return CustomLlamaForCausalLM
+
+
+def _block_diagonal(W: torch.Tensor, G: int, n: int) -> bool:
+    """True when the (G*n, G*n) matrix has no entry outside its G diagonal n x n blocks."""
+    blocks = W.detach().reshape(G, n, G, n)
+    idx = torch.arange(G, device=W.device)
+    off = blocks.clone()
+    off[idx, :, idx, :] = 0
+    return bool((off == 0).all())
+
+
+def _diag_blocks(W: torch.Tensor, G: int, n: int) -> torch.Tensor:
+    """(G, n, n): the diagonal blocks of a (G*n, G*n) matrix."""
+    idx = torch.arange(G, device=W.device)
+    return W.detach().reshape(G, n, G, n)[idx, :, idx, :].contiguous()
+
+
+class CustomAttention(LlamaAttention):
+    """``LlamaAttention`` over the compressed cache (reference
+    ``kernels/compressed_attention.py:204-357``)."""
+
+    def __init__(self, config, layer_idx: int, original_attn: LlamaAttention | None = None):
+        super().__init__(config, layer_idx)
+        self.n_kv = config.num_key_value_heads
+        self.n_q = config.num_attention_heads
+        D = self.n_kv * self.head_dim
+        self.d = D
+        if original_attn is not None:  # keep a loaded layer's projections
+            for name in ("q_proj", "k_proj", "v_proj", "o_proj"):
+                setattr(self, name, getattr(original_attn, name))
+        dt = self.q_proj.weight.dtype
+        # the reference reads config.rope_theta (default 10000) and applies plain RoPE
+        rp = getattr(config, "rope_parameters", None) or {}
+        self.theta = float(getattr(config, "rope_theta", None) or rp.get("rope_theta", 10000.0))
+        # cutoff heads and bases under the reference's names (KVProcessor): random heads and
+        # identity bases (or the DYNAKV_PCA_DIR files) until a checkpoint provides them
+        self.Wk = nn.Parameter(torch.randn(D, D, dtype=dt))
+        self.bk = nn.Parameter(torch.randn(1, D, dtype=dt))
+        self.Wv = nn.Parameter(torch.randn(D, D, dtype=dt))
+        self.bv = nn.Parameter(torch.randn(1, D, dtype=dt))
+        self.k_down = nn.Parameter(self._initial_basis("k_Ut", dt))
+        self.k_up = nn.Parameter(self._initial_basis("k_U", dt))
+        self.v_down = nn.Parameter(self._initial_basis("v_Ut", dt))
+        self.v_up = nn.Parameter(self._initial_basis("v_U", dt))
+        self.low_rank = D
+        self.policy = KernelPolicy()
+        self.merged = False
+        self.per_head = None
+        self._plan = None
+
+    def _initial_basis(self, suffix: str, dtype) -> torch.Tensor:
+        pca_dir = os.environ.get("DYNAKV_PCA_DIR", "")
+        path = os.path.join(pca_dir, f"L{self.layer_idx}_{suffix}.pt") if pca_dir else ""
+        if path and os.path.isfile(path):
+            return F.load_basis_file(path, dtype)
+        return torch.eye(self.d, dtype=dtype)
+
+    def init_dynakv_parameters(self) -> None:
+        """The constructor's values for the DynaKV parameters a checkpoint did not provide
+        (transformers' guarded initialisers leave loaded tensors alone)."""
+        from transformers import initialization as init
+
+        for p in (self.Wk, self.bk, self.Wv, self.bv):
+            init.normal_(p, 0.0, 1.0)
+        for p, suffix in ((self.k_down, "k_Ut"), (self.k_up, "k_U"), (self.v_down, "v_Ut"),
+                          (self.v_up, "v_U")):
+            init.copy_(p, self._initial_basis(suffix, p.dtype).to(p.device))
+
+    # -- one-time merge (reference compressed_attention.py:263-292) ------------------------
+    @torch.no_grad()
+    def _merge(self):
+        dt = self.q_proj.weight.dtype
+        for proj, down in ((self.k_proj, self.k_down), (self.v_proj, self.v_down)):
+            w, b = F.merge_projection(proj.weight.data.float(), down.data.float(),
+                                      None if proj.bias is None else proj.bias.data.float())
+            proj.weight.data = w.to(dt)
+            if b is not None:
+                proj.bias.data = b.to(dt)
+        G, Dh = self.n_kv, self.head_dim
+        self.per_head = all(_block_diagonal(W, G, Dh) for W in (self.k_up, self.v_up,
+                                                                self.Wk, self.Wv))
+        if self.per_head:
+            self.k_basis = F.per_head_bases(self.k_up.data, G, Dh).to(dt)
+            self.v_basis = F.per_head_bases(self.v_up.data, G, Dh).to(dt)
+            self.cutoff = CutoffHead(_diag_blocks(self.Wk, G, Dh), self.bk.data.view(G, Dh),
+                                     _diag_blocks(self.Wv, G, Dh), self.bv.data.view(G, Dh),
+                                     groups=G)
+        else:
+            R = int(self.low_rank)
+            self.k_basis = F.kernel_basis(self.k_up.data, G, Dh, R).to(dt)
+            self.v_basis = F.kernel_basis(self.v_up.data, G, Dh, R).to(dt)
+            self.k_rep = F.repeat_for_query_heads(self.k_basis, self.n_q)
+            self.v_rep = F.repeat_for_query_heads(self.v_basis, self.n_q)
+            self.cutoff = CutoffHead(self.Wk.data, self.bk.data, self.Wv.data, self.bv.data,
+                                     groups=1, low_rank=R)
+        self.k_down.data = torch.eye(self.d, dtype=dt, device=self.k_down.device)
+        self.v_down.data = torch.eye(self.d, dtype=dt, device=self.v_down.device)
+        self.merged = True
+
+    def forward(self, hidden_states: torch.Tensor, position_embeddings=None, attention_mask=None,
+                past_key_values=None, **kwargs):
+        if not self.merged:
+            self._merge()
+        B, S, _ = hidden_states.shape
+        q = self.q_proj(hidden_states).view(B, S, self.n_q, self.head_dim)
+        kc = self.k_proj(hidden_states)
+        vc = self.v_proj(hidden_states)
+        cache = past_key_values if isinstance(past_key_values, CustomDynamicCache) else None
+        if past_key_values is not None and cache is None:
+            raise TypeError("CustomAttention needs a CustomDynamicCache as past_key_values")
+        pos0 = cache.get_seq_length_sp(self.layer_idx) if cache is not None else 0
+        if self.per_head:
+            a = self._per_head(q, kc, vc, cache, pos0)
+        else:
+            a = self._joint(q, kc, vc, cache, pos0)
+        return self.o_proj(a.reshape(B, S, self.n_q * self.head_dim)), None
+
+    def _rows(self, x, B, S):
+        G, Dh = self.n_kv, self.head_dim
+        return x.view(B, S, G, Dh).transpose(1, 2).reshape(B * G, S, Dh).contiguous()
+
+    def _per_head(self, q, kc, vc, cache, pos0):
+        B, S = q.shape[:2]
+        G, Dh = self.n_kv, self.head_dim
+        if cache is not None and S == 1 and pos0 > 0:
+            plan = self._plan
+            if (plan is not None and plan.cache is cache and plan.B == B and plan.can_step()):
+                # one call: cutoff head, K+V appends, q RoPE, routed split-K attention
+                a = plan.step(q.view(B, self.n_q, Dh), kc.view(B, G * Dh), vc.view(B, G * Dh),
+                              pos0)
+                return a.view(B, 1, self.n_q, Dh)
+            k_out, v_out, len_k, len_v, _, _ = self.cutoff.kv_process_fused(kc, vc)
+            lk = len_k.view(B, 1, G).transpose(1, 2).reshape(B * G, 1).contiguous()
+            lv = len_v.view(B, 1, G).transpose(1, 2).reshape(B * G, 1).contiguous()
+            fk, fv, tk, tv, ok, ov = cache.update_sp(self._rows(k_out, B, 1), lk,
+                                                     self._rows(v_out, B, 1), lv, Dh,
+                                                     self.layer_idx, Dh)
+            L = cache.get_seq_length_sp(self.layer_idx)
+            qh = rope_dense_(q.transpose(1, 2).contiguous(), theta=self.theta, pos0=pos0)[:, :, 0]
+            a = grouped_decode_attention(qh, fk, fv, tk, ok, tv, ov, self.k_basis, self.v_basis,
+                                         theta=self.theta, route=self.policy.select(L))
+            self._plan = DecodeLayerPlan(cache, self.layer_idx, self.cutoff, self.k_basis,
+                                         self.v_basis, batch=B, heads=self.n_q, theta=self.theta,
+                                         policy=self.policy)
+            return a.view(B, 1, self.n_q, Dh)
+        # prefill (or a cache-less forward): masked coefficients, appended, then attended
+        k_out, v_out, len_k, len_v, _, _ = self.cutoff.kv_process_fused(kc, vc)
+        rk, rv = self._rows(k_out, B, S), self._rows(v_out, B, S)
+        qh = rope_dense_(q.transpose(1, 2).contiguous(), theta=self.theta, pos0=pos0)
+        if cache is not None:
+            lk = len_k.view(B, S, G).transpose(1, 2).reshape(B * G, S).contiguous()
+            lv = len_v.view(B, S, G).transpose(1, 2).reshape(B * G, S).contiguous()
+            cache.update_sp(rk, lk, rv, lv, Dh, self.layer_idx, Dh)
+            self._plan = None
+            if pos0 > 0:  # attend over the cached tokens too
+                a = compressed_prefill_attention(qh, cache, self.layer_idx, self.k_basis,
+                                                 self.v_basis, theta=self.theta)
+                return a.transpose(1, 2)
+        a = coef_prefill_attention(qh, rk, rv, self.k_basis, self.v_basis, theta=self.theta)
+        return a.transpose(1, 2)
+
+    def _joint(self, q, kc, vc, cache, pos0):
+        B, S = q.shape[:2]
+        D, Dh, G = self.d, self.head_dim, self.n_kv
+        R = int(self.low_rank)
+        k_out, v_out, len_k, len_v, _, _ = self.cutoff.kv_process_fused(kc, vc)
+        qh = rope_dense_(q.transpose(1, 2).contiguous(), theta=self.theta, pos0=pos0)
+        if cache is not None and S == 1 and pos0 > 0:
+            fk, fv, lk, lv, ok, ov = cache.update_sp(k_out, len_k, v_out, len_v, D,
+                                                     self.layer_idx, R)
+            L = cache.get_seq_length_sp(self.layer_idx)
+            a = compressed_decode_attention(q=qh, k_flat=fk, k_up=self.k_rep, v_flat=fv,
+                                            v_up=self.v_rep, key_lengths=lk, key_offsets=ok,
+                                            value_lengths=lv, value_offsets=ov, theta=self.theta,
+                                            cache_length=L, policy=self.policy)
+            return a.view(B, 1, self.n_q, Dh)
+        if cache is not None:
+            cache.update_sp(k_out, len_k, v_out, len_v, D, self.layer_idx, R)
+            ck, cv = cache.get_origin_states(R, self.layer_idx)  # (B, L, R)
+        else:
+            ck, cv = k_out[..., :R], v_out[..., :R]
+        # K / V in head space (B, G, L, Dh): coefficients through the basis, K rotated at its
+        # positions 0..L-1
+        k = torch.matmul(ck.unsqueeze(1), self.k_basis).contiguous()
+        v = torch.matmul(cv.unsqueeze(1), self.v_basis).contiguous()
+        rope_dense_(k, theta=self.theta, pos0=0)
+        a = prefill_attention(qh, k, v, causal=True)
+        return a.transpose(1, 2)
+
+
+class CustomLlamaModel(LlamaModel):
+    """``LlamaModel`` with ``CustomAttention`` in every layer (reference ``custom_llama.py:93-248``).
+    The attention is causal by construction (prefill) or over the whole cache (decode), so no
+    attention mask is built."""
+
+    def __init__(self, config):
+        super().__init__(config)
+        for i, layer in enumerate(self.layers):
+            layer.self_attn = CustomAttention(config, i, original_attn=layer.self_attn)
+
+    def _init_weights(self, module):
+        super()._init_weights(module)
+        if isinstance(module, CustomAttention):
+            module.init_dynakv_parameters()
+
+    def forward(self, input_ids=None, attention_mask=None, position_ids=None, past_key_values=None,
+                inputs_embeds=None, use_cache=None, cache_position=None, **kwargs):
+        if (input_ids is None) ^ (inputs_embeds is not None):
+            raise ValueError("You must specify exactly one of input_ids or inputs_embeds")
+        use_cache = use_cache if use_cache is not None else self.config.use_cache
+        if inputs_embeds is None:
+            inputs_embeds = self.embed_tokens(input_ids)
+        if use_cache and past_key_values is None:
+            past_key_values = CustomDynamicCache()
+        h = inputs_embeds
+        for layer in self.layers[: self.config.num_hidden_layers]:
+            h = layer(h, attention_mask=None, position_ids=position_ids,
+                      past_key_values=past_key_values, use_cache=use_cache,
+                      position_embeddings=None, **kwargs)
+        h = self.norm(h)
+        return BaseModelOutputWithPast(last_hidden_state=h,
+                                       past_key_values=past_key_values if use_cache else None)
+
+
+class CustomLlamaForCausalLM(LlamaForCausalLM):
+    """``LlamaForCausalLM`` over the compressed cache (reference ``custom_llama.py:250-323``,
+    inference part)."""
+
+    def __init__(self, config):
+        LlamaPreTrainedModel.__init__(self, config)
+        self.model = CustomLlamaModel(config)
+        self.vocab_size = config.vocab_size
+        self.lm_head = nn.Linear(config.hidden_size, config.vocab_size, bias=False)
+        self.post_init()
+
+    def _init_weights(self, module):
+        super()._init_weights(module)
+        if isinstance(module, CustomAttention):
+            module.init_dynakv_parameters()
+
+    def generate(self, *args, **kwargs):
+        if kwargs.get("past_key_values") is None:
+            kwargs["past_key_values"] = CustomDynamicCache()
+        return super().generate(*args, **kwargs)
+
+
+def install_reference_alias() -> None:
+    """Make the reference's import paths resolve to this build (no source edit of the caller):
+    ``dynakv`` (with ``get_model_class``), ``dynakv.custom_llama``, ``dynakv.kernels`` and its
+    ``router``, ``fused``, ``two_stage``, ``compressed_cache`` and ``compressed_attention``."""
+    import dynakv_amd
+    import dynakv_amd.kernels as kernels
+    import dynakv_amd.kernels.compressed_cache  # noqa: F401
+    import dynakv_amd.kernels.fused  # noqa: F401
+    import dynakv_amd.kernels.router  # noqa: F401
+    import dynakv_amd.kernels.two_stage  # noqa: F401
+
+    mod = sys.modules[__name__]
+    sys.modules["dynakv"] = dynakv_amd
+    sys.modules["dynakv.custom_llama"] = mod
+    sys.modules["dynakv.kernels"] = kernels
+    for name in ("router", "fused", "two_stage", "compressed_cache"):
+        sys.modules[f"dynakv.kernels.{name}"] = getattr(kernels, name)
+    sys.modules["dynakv.kernels.compressed_attention"] = mod
