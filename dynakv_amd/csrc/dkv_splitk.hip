@@ -267,6 +267,18 @@ __device__ __forceinline__ void wait_vm() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// Split records are exchanged between the workgroups of a unit with relaxed agent-scope atomic
+// accesses: such loads and stores are coherent across the XCDs' L2 caches by themselves, so
+// publishing a record needs only the wait for its stores before the arrival is counted, and
+// the last arrival reads the records without an L2 write-back or invalidation (the fences an
+// acquire/release pair at agent scope would add for ordinary accesses).
+__device__ __forceinline__ float rec_load(const float* a) {
+  return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void rec_store(float* a, float v) {
+  __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // LSE-merge the split records of one unit, normalise with the route's denominator, project
 // once through the unit's V basis and store the hpg output rows (all threads of the block).
 // scratch: LDS for the basis ([128][DH] bf16/fp16, zero past rank R) and 16 * DH floats.
@@ -286,9 +298,9 @@ __device__ __forceinline__ void merge_records(const SplitParams& p, const float*
         for (int u = 0; u < MB; ++u) {
           const int sp = min(sp0 + u, p.n_splits - 1);
           const float* rec = base + sp * stride + hs * PREC;
-          mb[u] = rec[0];
-          lb[u] = rec[1];
-          xb[u] = r < p.R ? rec[2 + r] : 0.f;
+          mb[u] = rec_load(rec);
+          lb[u] = rec_load(rec + 1);
+          xb[u] = r < p.R ? rec_load(rec + 2 + r) : 0.f;
         }
 #pragma unroll
         for (int u = 0; u < MB; ++u) {
@@ -327,13 +339,13 @@ __device__ __forceinline__ void merge_records_w(const SplitParams& p, const floa
   {
     const int hsc = min(tid / DH, p.hpg - 1), rc = min(tid % DH, p.R - 1);
 #pragma unroll
-    for (int u = 0; u < MB; ++u) x0[u] = base[min(u, ns - 1) * stride + hsc * PREC + 2 + rc];
+    for (int u = 0; u < MB; ++u) x0[u] = rec_load(base + min(u, ns - 1) * stride + hsc * PREC + 2 + rc);
   }
   for (int t = tid; t < p.hpg * ns; t += NTHREADS) {
     const int hs = t / ns, sp = t % ns;
     const float* rec = base + sp * stride + hs * PREC;
-    sM[hs * MERGE_WSPLITS + sp] = rec[0];
-    sL[hs * MERGE_WSPLITS + sp] = rec[1];
+    sM[hs * MERGE_WSPLITS + sp] = rec_load(rec);
+    sL[hs * MERGE_WSPLITS + sp] = rec_load(rec + 1);
   }
   __syncthreads();
   for (int t = tid; t < p.hpg * ns; t += NTHREADS) {
@@ -363,7 +375,7 @@ __device__ __forceinline__ void merge_records_w(const SplitParams& p, const floa
       for (; sp0 < ns; sp0 += MB) {
         float xb[MB];
 #pragma unroll
-        for (int u = 0; u < MB; ++u) xb[u] = base[min(sp0 + u, ns - 1) * stride + hs * PREC + 2 + r];
+        for (int u = 0; u < MB; ++u) xb[u] = rec_load(base + min(sp0 + u, ns - 1) * stride + hs * PREC + 2 + r);
 #pragma unroll
         for (int u = 0; u < MB; ++u)
           if (sp0 + u < ns) a += sW[hs * MERGE_WSPLITS + sp0 + u] * xb[u];
@@ -1057,31 +1069,22 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
       const float x = e == 1 ? sw[w * WREC + 16 + hs] : (e >= 2 ? sw[w * WREC + 32 + hs * DH + (e - 2)] : 0.f);
       v += wt * x;
     }
-    prec[hs * PREC + e] = e == 0 ? M : v;
+    rec_store(prec + hs * PREC + e, e == 0 ? M : v);
   }
   if (!p.fused_merge) return;
 
   // ---- fused merge: the last split of the unit to finish combines the unit's records -------
-  // Every wave's record stores are released at agent scope before the arrival is counted; the
-  // last arrival acquires them (the splits of a unit may run on different XCDs) and only it
-  // loads the V basis, together with the records.
+  // The records are written with device-coherent stores (rec_store); each wave waits until its
+  // stores have completed, then one thread counts the arrival. The last arrival reads the
+  // records with device-coherent loads (rec_load) issued after it has seen the count (the
+  // splits of a unit may run on different XCDs), and only it loads the V basis.
   __shared__ int sLast;
-  // Each wave waits until its record stores have reached the XCD's L2; after the barrier one
-  // wave releases them at agent scope (one L2 write-back covers every wave of the block: they
-  // share the L2) and counts the arrival. The last arrival acquires once (L1 and L2
-  // invalidation are per CU / per XCD, so one wave's acquire serves the whole block).
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  if (tid < 64) {
-    int last = 0;
-    if (tid == 0) {
-      const int old = __hip_atomic_fetch_add(p.counters + unit, 1, __ATOMIC_RELEASE,
-                                             __HIP_MEMORY_SCOPE_AGENT);
-      last = old == p.n_splits - 1;
-    }
-    last = __shfl(last, 0, 64);
-    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    if (tid == 0) sLast = last;
+  if (tid == 0) {
+    const int old = __hip_atomic_fetch_add(p.counters + unit, 1, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+    sLast = old == p.n_splits - 1;
   }
   __syncthreads();
   if (!sLast) return;
