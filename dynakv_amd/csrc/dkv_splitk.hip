@@ -485,11 +485,14 @@ __device__ __forceinline__ void merge_unit(const SplitParams& p, int unit, uint8
     merge_unit_t<DT, ROUTE, DT>(p, unit, scratch);
 }
 
-// WIDE: more than 8 query heads per unit (up to 16). The query operand then carries the heads'
-// hi parts in its 16 columns and a second product takes the lo parts; with up to 8 heads the
-// hi parts sit in columns 0..7 and the lo parts in columns 8..15 of one product.
-template <int DT, int ROUTE, bool WIDE>
+// HMAX: the most query heads per unit the instance handles (4, 8 or 16); each lane keeps HMAX
+// query registers, so the common 4-head groups carry no registers for absent heads. Past 8
+// heads (WIDE) the query operand carries the heads' hi parts in its 16 columns and a second
+// product takes the lo parts; with up to 8 heads the hi parts sit in columns 0..7 and the lo
+// parts in columns 8..15 of one product.
+template <int DT, int ROUTE, int HMAX>
 __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
+  constexpr bool WIDE = HMAX > 8;
   // LDS: per-wave rings (NSLOT gather slots: K then V, 4 chunks x 64 lanes x 16 bytes each;
   // TSLOT table slots: lens_k, offs_k, lens_v, offs_v x 16 tokens), the part of the K basis not
   // held in registers ([dim][rank] rows; none with NREG_PP = 4), the R(n) table and the mask
@@ -505,7 +508,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
   __shared__ __attribute__((aligned(256))) uint8_t sRing[WAVES * NSLOT * GSLOT_BYTES];
   static_assert(DH * BK_LD * 2 <= WAVES * NSLOT * GSLOT_BYTES, "basis staging fits the rings");
   static_assert(16 * QROW_BYTES <= GSLOT_BYTES / 2, "query operand fits a slot's K half");
-  constexpr int QH = WIDE ? 16 : 8;  // head registers per lane
+  constexpr int QH = HMAX;  // head registers per lane
   uint16_t* sBK = reinterpret_cast<uint16_t*>(sRing);
 
   // XCD-aware mapping: consecutive workgroup ids land on different XCDs (id % 8), so give
@@ -1320,9 +1323,11 @@ static void launch_splitk_t(const SplitParams& p, int out_dtype, dim3 grid, dim3
   hipEvent_t* ev = slot >= 0 ? g_prof.ev + 3 * slot : nullptr;
   if (ev) (void)hipEventRecord(ev[0], st);
   if (p.hpg > 8)
-    hipLaunchKernelGGL((splitk_kernel<DT, RT, true>), grid, dim3(NTHREADS), 0, st, p);
+    hipLaunchKernelGGL((splitk_kernel<DT, RT, 16>), grid, dim3(NTHREADS), 0, st, p);
+  else if (p.hpg > 4)
+    hipLaunchKernelGGL((splitk_kernel<DT, RT, 8>), grid, dim3(NTHREADS), 0, st, p);
   else
-    hipLaunchKernelGGL((splitk_kernel<DT, RT, false>), grid, dim3(NTHREADS), 0, st, p);
+    hipLaunchKernelGGL((splitk_kernel<DT, RT, 4>), grid, dim3(NTHREADS), 0, st, p);
   if (ev) (void)hipEventRecord(ev[1], st);
   if (!p.fused_merge) {
     if (out_dtype == DKV_F32)
