@@ -40,6 +40,13 @@ _SIGNATURES = {
                         _vp, _ll, _ll, _vp, _ll, _ll, _vp, _ll, _ll, _ll, _i, _i, _i, _i, _i, _f]),
     "dkv_av": (_i, [_vp, _i, _i, _i, _i, _vp, _ll, _ll, _ll, _vp, _ll, _ll, _i, _vp, _ll,
                     _vp, _ll, _ll, _vp, _ll, _ll, _vp, _ll, _ll, _i, _i, _i, _i, _i]),
+    "dkv_joint_scores": (_i, [_vp, _i, _i, _i, _vp, _ll, _ll, _vp, _ll, _ll, _i, _vp, _ll,
+                              _vp, _ll, _ll, _vp, _ll, _ll, _vp, _i, _vp, _ll, _ll, _ll,
+                              _i, _i, _i, _i, _i]),
+    "dkv_joint_av_workspace_floats": (_ll, [_i, _i, _i, _i]),
+    "dkv_joint_av": (_i, [_vp, _i, _i, _i, _i, _vp, _ll, _ll, _ll, _vp, _ll, _ll, _i, _vp, _ll,
+                          _vp, _ll, _ll, _vp, _ll, _ll, _vp, _ll, _vp, _ll, _ll,
+                          _i, _i, _i, _i, _i]),
     "dkv_splitk_workspace_floats": (_ll, [_i, _i, _i, _i, _i, _i]),
     "dkv_splitk_choose_split": (_i, [_i, _i, _i]),
     "dkv_rope_table_floats": (_ll, [_i]),

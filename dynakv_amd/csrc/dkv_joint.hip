@@ -1,0 +1,675 @@
+// Decode attention for the reference's joint layout on MFMA: one packed coefficient row per batch
+// element with ranks up to 1024 shared by every KV head, one (R, 128) basis per KV head (or per
+// query head, as the reference's repeated k_up).
+//
+// Reference behaviour: abx_sparse / _abx_sparse_fwd (src/dynakv/kernels/two_stage.py:48-189) and
+// avx / _avx_proj_fwd (:207-324), the router's long route for this layout; the fused route
+// (fused.py:28-170) is the same scores with -inf masking and the V pass without the 1e-6 clamp.
+// The entry points take what dkv_scores / dkv_av take for these shapes (the K basis transposed
+// to [dim][rank], a RoPE table, a workspace for the V pass) and compute the same results to fp32
+// accuracy:
+//
+// joint_scores_kernel -- workgroup = (512 tokens, basis head h, batch row b); wave w takes 64
+//   tokens (4 column blocks of 16). K^T[128 x 64] = B_h^T . X^T accumulates on 16x16x32 MFMA over
+//   the rank chunks of 32 that the block's longest token needs. Each basis chunk ([128 dims][32
+//   ranks], 8 KB) is loaded once per workgroup into LDS (two buffers) and every A operand read
+//   from it serves the wave's 4 column blocks; the coefficients go straight into B operand
+//   registers (lane = one token x 8 ranks, elements past the token's count zeroed), two chunks
+//   ahead. Then per 16-token tile T: R(n) applied to the lane's token (n = its slot in the tile,
+//   LDS table) in fp32, K' split into bf16 hi + lo, scores on MFMA against R(-16T) q (hi and lo
+//   parts in separate operand columns), the route's masking and rounding.
+// joint_av_kernel -- workgroup = (token split, 16 query heads, batch row b); wave w takes ranks
+//   [128w, 128w + 128). Per 16-token tile: the 16 heads' scores through an online softmax in the
+//   log2 domain (every wave computes the same values), P as bf16 hi + lo (fp16 for fp16 caches),
+//   the wave's V coefficients of the tile staged in LDS and read transposed (ds_read_b64_tr_b16)
+//   as the B operand of P.X^V. Each split writes (m, l, acc[R]) per head.
+// joint_merge_kernel -- workgroup = (query head, batch row b): LSE merge of the split records,
+//   the route's denominator, the projection through the V basis, the output rounding.
+#include "dkv_common.h"
+#include "dkv_mfma_ops.h"
+
+namespace {
+
+constexpr int JDH = 128;
+constexpr int JWAVES = 8;
+constexpr int JTHREADS = JWAVES * 64;
+constexpr int JCB = 4;                   // 16-token column blocks per wave (scores)
+constexpr int JTOK = JWAVES * JCB * 16;  // tokens per scores workgroup
+constexpr int JCH = 32;                  // ranks per basis chunk
+constexpr int JRMAX = 1024;
+constexpr int JPREC = 2 + JRMAX;         // split record: m (log2 units), l, acc[R]
+constexpr int JROPE_FIXED = 17;          // rows of the RoPE table before the per-tile rows
+constexpr int JFLAT_CAP = 0x3ffffff0;    // elements one buffer resource covers
+constexpr int JMAX_SPLITS = 1024;
+constexpr float JLOG2E = 1.4426950408889634f;
+constexpr float JRESCALE = 11.5f;        // log2 units: rescale when the running max grows more
+
+__device__ __forceinline__ dkv_f32x4 mfma_bf16x32(const dkv_u32x4& a, const dkv_u32x4& b,
+                                                  dkv_f32x4 c) {
+  return dkv_mfma32<DKV_BF16>(a, b, c);
+}
+
+struct JScoresParams {
+  const uint16_t* q;
+  long long q_sb, q_sh;
+  const uint16_t* bt;  // K basis [n_basis][Dh][R-stride]
+  long long bt_sh, bt_sd;
+  const uint16_t* flat;
+  long long flat_ld;
+  const int* lens;
+  long long lens_sb, lens_ss;
+  const int* offs;
+  long long offs_sb, offs_ss;
+  const float* rope;
+  void* out;
+  long long out_sb, out_sh, out_ss;
+  int B, S, R, hpg;
+  float scale;
+};
+
+template <int DT, int MODE, int ODT>
+__global__ __launch_bounds__(JTHREADS, 1) void joint_scores_kernel(JScoresParams p) {
+  // basis chunk buffers: piece (dim d, ranks 8k..8k+7) at index 4d + (k ^ ((d >> 2) & 3)), so the
+  // 16 rows one k-group reads land in 16 different bank groups
+  __shared__ __attribute__((aligned(16))) dkv_u32x4 sB[2][JDH * JCH / 8];
+  // R(n) of every lane's token slot: [2*pp + k][lane] holds (cos, sin) of frequencies
+  // 16pp + 4g + 2k and + 1
+  __shared__ __attribute__((aligned(16))) dkv_f32x4 sRn[8][64];
+  // per-wave query operand: row r (column r of the score product: head r's hi part for r < 8,
+  // head r-8's lo part), dword i = frequency i, 16-byte chunk c stored at chunk position c ^ r
+  __shared__ __attribute__((aligned(16))) uint32_t sQ[JWAVES][16 * 64];
+  __shared__ int sLen[JTOK], sOff[JTOK];
+  __shared__ int sMax[JWAVES];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n = lane & 15, g = lane >> 4;
+  const int t0 = blockIdx.x * JTOK, h = blockIdx.y, b = blockIdx.z;
+
+  {
+    const int t = t0 + tid;
+    int len = 0, off = 0;
+    if (t < p.S) {
+      len = p.lens[(long long)b * p.lens_sb + (long long)t * p.lens_ss];
+      off = p.offs[(long long)b * p.offs_sb + (long long)t * p.offs_ss];
+    }
+    len = min(max(len, 0), p.R);
+    sLen[tid] = len;
+    sOff[tid] = off;
+    const int m = dkv_wave_max_i(len);
+    if (lane == 0) sMax[wave] = m;
+  }
+  {
+    const int k = tid >> 6;
+    const int i0 = 16 * (k >> 1) + 4 * g + 2 * (k & 1);
+    const float* delt = p.rope + n * 128 + 2 * i0;
+    sRn[k][lane] = dkv_f32x4{delt[0], delt[1], delt[2], delt[3]};
+  }
+  // (q_i, q_{i+64}) of the group's heads for frequency i = lane, as 16-bit values
+  uint32_t qh[8];
+  {
+    const long long qo = (long long)b * p.q_sb + (long long)h * p.hpg * p.q_sh + lane;
+#pragma unroll
+    for (int hh = 0; hh < 8; ++hh) {
+      const long long o = qo + (hh < p.hpg ? hh : 0) * p.q_sh;
+      const uint32_t v = (uint32_t)p.q[o] | ((uint32_t)p.q[o + 64] << 16);
+      qh[hh] = hh < p.hpg ? v : 0u;
+    }
+  }
+  __syncthreads();
+  int maxlen = 0;
+#pragma unroll
+  for (int w = 0; w < JWAVES; ++w) maxlen = max(maxlen, sMax[w]);
+  const int nch = (maxlen + JCH - 1) / JCH;
+
+  const uint32_t end =
+      (uint32_t)min((long long)(p.B - b) * p.flat_ld, (long long)JFLAT_CAP);
+  const __amdgpu_buffer_rsrc_t rs = dkv_make_rsrc(p.flat + (long long)b * p.flat_ld, end * 2u);
+  // this thread's basis piece of every chunk: dim bd, ranks 8*bk .. +8 of the chunk
+  const int bd = tid >> 2, bk = (tid & 3) ^ ((bd >> 2) & 3);
+  const uint16_t* bsrc = p.bt + (long long)h * p.bt_sh + (long long)bd * p.bt_sd + 8 * bk;
+
+  int tlen[JCB], toff[JCB];
+#pragma unroll
+  for (int cb = 0; cb < JCB; ++cb) {
+    const int tl = 64 * wave + 16 * cb + n;
+    tlen[cb] = sLen[tl];
+    toff[cb] = sOff[tl];
+  }
+  auto load_x = [&](int c, dkv_u32x4(&x)[JCB]) {
+#pragma unroll
+    for (int cb = 0; cb < JCB; ++cb) {
+      const int j0 = JCH * c + 8 * g;
+      x[cb] = dkv_load8_prefix(rs, end, toff[cb] + j0, tlen[cb] - j0);
+    }
+  };
+
+  dkv_f32x4 acc[8][JCB];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int cb = 0; cb < JCB; ++cb) acc[i][cb] = dkv_f32x4{0.f, 0.f, 0.f, 0.f};
+
+  dkv_u32x4 xa[JCB], xb[JCB];
+  dkv_u32x4 bnext = dkv_u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int cb = 0; cb < JCB; ++cb) xa[cb] = xb[cb] = dkv_u32x4{0u, 0u, 0u, 0u};
+  if (nch > 0) {
+    sB[0][tid] = *(const dkv_u32x4*)bsrc;
+    if (nch > 1) bnext = *(const dkv_u32x4*)(bsrc + JCH);
+    load_x(0, xa);
+    if (nch > 1) load_x(1, xb);
+  }
+  __syncthreads();
+  // chunk c: its basis sits in sB[c & 1] (written before the previous barrier); the basis of
+  // chunk c+1 (loaded one iteration ago) goes to the other buffer, whose readers finished before
+  // that barrier; the coefficients run two chunks ahead
+  for (int c = 0; c < nch; ++c) {
+    if (c + 1 < nch) sB[(c + 1) & 1][tid] = bnext;
+    if (c + 2 < nch) bnext = *(const dkv_u32x4*)(bsrc + JCH * (c + 2));
+    dkv_u32x4 xn[JCB];
+#pragma unroll
+    for (int cb = 0; cb < JCB; ++cb) xn[cb] = dkv_u32x4{0u, 0u, 0u, 0u};
+    if (c + 2 < nch) load_x(c + 2, xn);
+    const dkv_u32x4* buf = sB[c & 1];
+#pragma unroll
+    for (int blk = 0; blk < 8; ++blk) {
+      const int d = 16 * blk + n;
+      const dkv_u32x4 a = buf[4 * d + (g ^ ((d >> 2) & 3))];
+#pragma unroll
+      for (int cb = 0; cb < JCB; ++cb) acc[blk][cb] = dkv_mfma32<DT>(a, xa[cb], acc[blk][cb]);
+    }
+#pragma unroll
+    for (int cb = 0; cb < JCB; ++cb) {
+      xa[cb] = xb[cb];
+      xb[cb] = xn[cb];
+    }
+    __syncthreads();
+  }
+
+  // ---- per 16-token tile: rotation, K' hi + lo, scores, masking, store ---------------------
+  const int hn = n & 7;
+  const int qrow = (n & 8) + (hn < p.hpg ? hn : hn % p.hpg);
+  uint32_t* qw = sQ[wave];
+#pragma unroll
+  for (int cb = 0; cb < JCB; ++cb) {
+    const int tbase = t0 + 64 * wave + 16 * cb;
+    if (tbase >= p.S) break;  // wave-uniform
+    const int tile = tbase / 16;
+    {
+      // R(-16T) q times the score scale for frequency i = lane, as bf16 hi + lo
+      const float* row = p.rope + (long long)(JROPE_FIXED + tile) * 128 + 2 * lane;
+      const float cs = row[0] * p.scale, sn = row[1] * p.scale;
+#pragma unroll
+      for (int hh = 0; hh < 8; ++hh)
+        if (hh < p.hpg) {
+          const float x = dkv_elt_to_f32<DT>(qh[hh] & 0xffffu);
+          const float y = dkv_elt_to_f32<DT>(qh[hh] >> 16);
+          uint32_t hi, lo;
+          dkv_split_bf16x2(cs * x + sn * y, cs * y - sn * x, hi, lo);
+          qw[hh * 64 + 4 * ((lane >> 2) ^ hh) + (lane & 3)] = hi;
+          qw[(8 + hh) * 64 + 4 * ((lane >> 2) ^ (8 + hh)) + (lane & 3)] = lo;
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    dkv_u32x4 bq[4];
+#pragma unroll
+    for (int pp = 0; pp < 4; ++pp)
+      bq[pp] = *(const dkv_u32x4*)&qw[qrow * 64 + 4 * ((4 * pp + g) ^ qrow)];
+
+    dkv_f32x4 sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int pp = 0; pp < 4; ++pp) {
+      const dkv_f32x4 c0 = acc[pp][cb], c1 = acc[pp + 4][cb];
+      const dkv_f32x4 r01 = sRn[2 * pp][lane], r23 = sRn[2 * pp + 1][lane];
+      const float rc[4] = {r01.x, r01.z, r23.x, r23.z}, rsn[4] = {r01.y, r01.w, r23.y, r23.w};
+      uint32_t kh[4], kl[4];
+#pragma unroll
+      for (int w = 0; w < 4; ++w)
+        dkv_split_bf16x2(c0[w] * rc[w] - c1[w] * rsn[w], c1[w] * rc[w] + c0[w] * rsn[w], kh[w],
+                         kl[w]);
+      sc = mfma_bf16x32(dkv_u32x4{kh[0], kh[1], kh[2], kh[3]}, bq[pp], sc);
+      sc = mfma_bf16x32(dkv_u32x4{kl[0], kl[1], kl[2], kl[3]}, bq[pp], sc);
+    }
+    // column n += column n + 8 (the lo part of head n) within each row of 16 lanes
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      sc[u] += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sc[u]),
+                                                          DKV_DPP_ROW_SHL8, 0xf, 0xf, false));
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (n < p.hpg) {
+      const long long ob = (long long)b * p.out_sb + (long long)(h * p.hpg + n) * p.out_sh;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int tl = 64 * wave + 16 * cb + 4 * g + u;
+        const int t = t0 + tl;
+        if (t < p.S) {
+          const int len = sLen[tl];
+          float z;
+          if constexpr (MODE == 0)
+            z = len > 0 ? sc[u] : -1.0e4f * p.scale;
+          else
+            z = len > 0 ? sc[u] : -INFINITY;
+          dkv_store_f32<ODT>(p.out, ob + (long long)t * p.out_ss, z);
+        }
+      }
+    }
+  }
+}
+
+struct JAvParams {
+  const void* scores;
+  long long sc_sb, sc_sh, sc_ss;
+  const uint16_t* flat;
+  long long flat_ld;
+  const int* lens;
+  long long lens_sb, lens_ss;
+  const int* offs;
+  long long offs_sb, offs_ss;
+  float* rec;  // [B][Hq][n_splits][JPREC]
+  int B, Hq, S, R, n_splits, split_len;
+};
+
+template <int DT, int SDT>
+__global__ __launch_bounds__(JTHREADS, 1) void joint_av_kernel(JAvParams p) {
+  // per wave: its rank slice of the current tile's V coefficients, the split kernel's V-window
+  // layout: rank r of token t in chunk r/32 at lane slot 16*((r%32)/8) + t, element r%8
+  __shared__ __attribute__((aligned(16))) dkv_u32x4 sV[JWAVES][4 * 64];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n = lane & 15, g = lane >> 4;
+  const int split = blockIdx.x, hset = blockIdx.y, b = blockIdx.z;
+  const int s_begin = split * p.split_len;
+  const int s_end = min(p.S, s_begin + p.split_len);
+  const int ntiles = s_end > s_begin ? (s_end - s_begin + 15) / 16 : 0;
+  const int r0 = 128 * wave;
+  const int hq = 16 * hset + n;  // head slot n of this lane's softmax values
+  const bool hq_ok = hq < p.Hq;
+
+  const uint32_t end =
+      (uint32_t)min((long long)(p.B - b) * p.flat_ld, (long long)JFLAT_CAP);
+  const __amdgpu_buffer_rsrc_t rs = dkv_make_rsrc(p.flat + (long long)b * p.flat_ld, end * 2u);
+  const long long sbase = (long long)b * p.sc_sb + (long long)(hq_ok ? hq : 0) * p.sc_sh;
+
+  // tile j's inputs: the V pieces of token n (ranks r0 + 32c + 8g .. +8) and the scores of head
+  // slot n for tokens 4g .. 4g+3
+  auto load_tile = [&](int j, dkv_u32x4(&x)[4], float(&z)[4]) {
+    const int t = s_begin + 16 * j + n;
+    int len = 0, off = 0;
+    if (t < s_end) {
+      len = min(max(p.lens[(long long)b * p.lens_sb + (long long)t * p.lens_ss], 0), p.R);
+      off = p.offs[(long long)b * p.offs_sb + (long long)t * p.offs_ss];
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int j0 = r0 + 32 * c + 8 * g;
+      x[c] = dkv_load8_prefix(rs, end, off + j0, len - j0);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int tt = s_begin + 16 * j + 4 * g + u;
+      z[u] = (hq_ok && tt < s_end) ? dkv_load_f32<SDT>(p.scores, sbase + (long long)tt * p.sc_ss)
+                                   : -INFINITY;
+    }
+  };
+
+  dkv_f32x4 acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = dkv_f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -1.0e30f;  // finite floor: excluded tokens give exp2(-inf) = 0
+  float l_run = 0.f;
+
+  dkv_u32x4 xc[4];
+  float zc[4];
+  if (ntiles > 0) load_tile(0, xc, zc);
+  dkv_u32x4* slot = sV[wave];
+  for (int j = 0; j < ntiles; ++j) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) slot[c * 64 + lane] = xc[c];
+    float z[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) z[u] = zc[u] * JLOG2E;
+    if (j + 1 < ntiles) load_tile(j + 1, xc, zc);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // online softmax of head slot n (its 16 tokens sit in lanes n, n+16, n+32, n+48)
+    float tmax = dkv_max3(dkv_max3(z[0], z[1], z[2]), z[3], z[3]);
+    tmax = dkv_lane_max32(tmax);
+    tmax = dkv_lane_max16(tmax);
+    if (__ballot(tmax > m_run + JRESCALE)) {
+      const float m_new = fmaxf(m_run, tmax);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      l_run *= alpha;
+      m_run = m_new;
+      float au[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) au[u] = __shfl(alpha, 4 * g + u, 64);
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc[i][u] *= au[u];
+    }
+    float pu[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      pu[u] = __builtin_amdgcn_exp2f(z[u] - m_run);
+      l_run += pu[u];
+    }
+    // P.X^V in coefficient space (A: P of head slot n, tokens 4g..4g+3; B: the transposed V reads)
+    dkv_u32x2 pa_hi, pa_lo;
+    if constexpr (DT == DKV_F16) {
+      pa_hi = dkv_u32x2{dkv_pack_f16x2(pu[0], pu[1]), dkv_pack_f16x2(pu[2], pu[3])};
+      pa_lo = pa_hi;
+    } else {
+      uint32_t h01, l01, h23, l23;
+      dkv_split_bf16x2(pu[0], pu[1], h01, l01);
+      dkv_split_bf16x2(pu[2], pu[3], h23, l23);
+      pa_hi = dkv_u32x2{h01, h23};
+      pa_lo = dkv_u32x2{l01, l23};
+    }
+    {
+      const int u = n >> 2, q = n & 3;
+      const uint8_t* vbase =
+          (const uint8_t*)slot + 16 * (16 * (q >> 1) + 4 * g + u) + 8 * (q & 1);
+#pragma unroll
+      for (int blk = 0; blk < 8; ++blk) {
+        const uint8_t* src = vbase + (blk >> 1) * 1024 + (blk & 1) * 512;
+        const dkv_u32x2 xv = __builtin_bit_cast(
+            dkv_u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                           (__attribute__((address_space(3))) dkv_i16x4*)(
+                               (__attribute__((address_space(3))) uint8_t*)src)));
+        if constexpr (DT == DKV_BF16)
+          acc[blk] = dkv_mfma32<DT>(
+              dkv_u32x4{pa_hi.x, pa_hi.y, pa_lo.x, pa_lo.y},
+              __builtin_bit_cast(dkv_u32x4, dkv_u64x2{__builtin_bit_cast(uint64_t, xv),
+                                                      __builtin_bit_cast(uint64_t, xv)}),
+              acc[blk]);
+        else
+          acc[blk] = __builtin_amdgcn_mfma_f32_16x16x16f16(
+              __builtin_bit_cast(dkv_f16x4, pa_hi), __builtin_bit_cast(dkv_f16x4, xv), acc[blk],
+              0, 0, 0);
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+
+  // the split's record per head: m and l (identical in every wave: wave 0 writes them), the
+  // wave's rank slice of acc (head slot 4g+u, rank r0 + 16*blk + n)
+  float l_tot = l_run;
+  l_tot += __shfl_xor(l_tot, 16, 64);
+  l_tot += __shfl_xor(l_tot, 32, 64);
+  if (wave == 0 && g == 0 && hq_ok) {
+    float* rec = p.rec + (((long long)b * p.Hq + hq) * p.n_splits + split) * JPREC;
+    rec[0] = m_run;
+    rec[1] = l_tot;
+  }
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int hs = 16 * hset + 4 * g + u;
+    if (hs < p.Hq) {
+      float* rec = p.rec + (((long long)b * p.Hq + hs) * p.n_splits + split) * JPREC + 2;
+#pragma unroll
+      for (int blk = 0; blk < 8; ++blk) {
+        const int r = r0 + 16 * blk + n;
+        if (r < p.R) rec[r] = acc[blk][u];
+      }
+    }
+  }
+}
+
+struct JMergeParams {
+  const float* rec;
+  const uint16_t* vb;  // V basis [n_basis][R][Dh] with strides (vb_sh, vb_sr)
+  long long vb_sh, vb_sr;
+  void* out;
+  long long out_sb, out_sh;
+  int Hq, R, n_splits, hpg;
+};
+
+template <int DT, int MODE, int ODT>
+__global__ __launch_bounds__(256) void joint_merge_kernel(JMergeParams p) {
+  __shared__ float sW[JMAX_SPLITS];
+  __shared__ float sA[JRMAX];
+  __shared__ float sOut[2][JDH];
+  __shared__ float sRed[8];
+  const int hq = blockIdx.x, b = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const float* base = p.rec + ((long long)b * p.Hq + hq) * p.n_splits * JPREC;
+  // maximum over the splits
+  float M = -INFINITY;
+  for (int s = tid; s < p.n_splits; s += 256) M = fmaxf(M, base[(long long)s * JPREC]);
+  M = dkv_wave_max(M);
+  if (lane == 0) sRed[wave] = M;
+  __syncthreads();
+  M = fmaxf(fmaxf(sRed[0], sRed[1]), fmaxf(sRed[2], sRed[3]));
+  __syncthreads();
+  float L = 0.f;
+  for (int s = tid; s < p.n_splits; s += 256) {
+    const float w = __builtin_amdgcn_exp2f(base[(long long)s * JPREC] - M);
+    sW[s] = w;
+    L += w * base[(long long)s * JPREC + 1];
+  }
+  L = dkv_wave_sum(L);
+  if (lane == 0) sRed[4 + wave] = L;
+  __syncthreads();
+  L = sRed[4] + sRed[5] + sRed[6] + sRed[7];
+  const float den = MODE == 0 ? fmaxf(L, 1e-6f) : L;
+  for (int r = tid; r < p.R; r += 256) {
+    float a = 0.f;
+    for (int s = 0; s < p.n_splits; ++s) a += sW[s] * base[(long long)s * JPREC + 2 + r];
+    sA[r] = a / den;
+  }
+  __syncthreads();
+  // out[d] = sum_r a[r] VB[r][d]: two halves of the rank range, then added
+  const int d = tid & 127, half = tid >> 7;
+  const uint16_t* vb = p.vb + (long long)(hq / p.hpg) * p.vb_sh + d;
+  float o = 0.f;
+  for (int r = half; r < p.R; r += 2) o = fmaf(sA[r], dkv_elt_to_f32<DT>(vb[(long long)r * p.vb_sr]), o);
+  sOut[half][d] = o;
+  __syncthreads();
+  if (half == 0)
+    dkv_store_f32<ODT>(p.out, (long long)b * p.out_sb + (long long)hq * p.out_sh + d,
+                       sOut[0][d] + sOut[1][d]);
+}
+
+int joint_av_split_len(int B, int Hq, int S) {
+  const long long groups = (long long)B * ((Hq + 15) / 16);
+  long long ns = (512 + groups - 1) / groups;
+  const long long max_ns = (S + 15) / 16;
+  if (ns > max_ns) ns = max_ns;
+  if (ns > JMAX_SPLITS) ns = JMAX_SPLITS;
+  if (ns < 1) ns = 1;
+  long long sl = (S + ns - 1) / ns;
+  sl = ((sl + 15) / 16) * 16;
+  return (int)(sl < 16 ? 16 : sl);
+}
+
+bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
+
+}  // namespace
+
+extern "C" int dkv_joint_scores(void* stream, int mode, int dtype, int out_dtype, const void* q,
+                                long long q_sb, long long q_sh, const void* basis_t,
+                                long long bt_sh, long long bt_sd, int n_basis, const void* flat,
+                                long long flat_ld, const int* lens, long long lens_sb,
+                                long long lens_ss, const int* offs, long long offs_sb,
+                                long long offs_ss, const float* rope, int rope_tiles, void* out,
+                                long long out_sb, long long out_sh, long long out_ss, int B,
+                                int Hq, int S, int R, int Dh) {
+  if (mode != 0 && mode != 1) return DKV_E_ARG;
+  if (dtype != DKV_BF16 && dtype != DKV_F16) return DKV_E_UNSUPPORTED;
+  if (out_dtype != DKV_F32 && out_dtype != DKV_F16 && out_dtype != DKV_BF16) return DKV_E_ARG;
+  if (mode == 1 && out_dtype != DKV_F32) return DKV_E_ARG;
+  if (B < 0 || Hq < 0 || S < 0 || R <= 0 || n_basis <= 0) return DKV_E_ARG;
+  if (Dh != JDH || R % JCH != 0 || R > JRMAX) return DKV_E_UNSUPPORTED;
+  if (Hq % n_basis != 0 || Hq / n_basis > 8) return DKV_E_UNSUPPORTED;
+  if (B == 0 || Hq == 0 || S == 0) return DKV_OK;
+  if (!q || !basis_t || !flat || !lens || !offs || !rope || !out) return DKV_E_ARG;
+  if (!aligned16(basis_t) || bt_sd < R || bt_sd % 8 != 0 || bt_sh % 8 != 0) return DKV_E_UNSUPPORTED;
+  if (flat_ld <= 0 || flat_ld > JFLAT_CAP - 8) return DKV_E_UNSUPPORTED;
+  if (rope_tiles < (S + 15) / 16) return DKV_E_ARG;
+  if (B > 65535 || n_basis > 65535) return DKV_E_UNSUPPORTED;
+  JScoresParams p;
+  p.q = (const uint16_t*)q;
+  p.q_sb = q_sb;
+  p.q_sh = q_sh;
+  p.bt = (const uint16_t*)basis_t;
+  p.bt_sh = bt_sh;
+  p.bt_sd = bt_sd;
+  p.flat = (const uint16_t*)flat;
+  p.flat_ld = flat_ld;
+  p.lens = lens;
+  p.lens_sb = lens_sb;
+  p.lens_ss = lens_ss;
+  p.offs = offs;
+  p.offs_sb = offs_sb;
+  p.offs_ss = offs_ss;
+  p.rope = rope;
+  p.out = out;
+  p.out_sb = out_sb;
+  p.out_sh = out_sh;
+  p.out_ss = out_ss;
+  p.B = B;
+  p.S = S;
+  p.R = R;
+  p.hpg = Hq / n_basis;
+  p.scale = 1.0f / sqrtf((float)Dh);
+  const dim3 grid((unsigned)((S + JTOK - 1) / JTOK), (unsigned)n_basis, (unsigned)B);
+  hipStream_t st = (hipStream_t)stream;
+#define DKV_JS_LAUNCH(DT_, MODE_, ODT_) \
+  hipLaunchKernelGGL((joint_scores_kernel<DT_, MODE_, ODT_>), grid, dim3(JTHREADS), 0, st, p)
+  if (mode == 1) {
+    if (dtype == DKV_BF16) DKV_JS_LAUNCH(DKV_BF16, 1, DKV_F32);
+    else DKV_JS_LAUNCH(DKV_F16, 1, DKV_F32);
+  } else if (dtype == DKV_BF16) {
+    if (out_dtype == DKV_BF16) DKV_JS_LAUNCH(DKV_BF16, 0, DKV_BF16);
+    else if (out_dtype == DKV_F16) DKV_JS_LAUNCH(DKV_BF16, 0, DKV_F16);
+    else DKV_JS_LAUNCH(DKV_BF16, 0, DKV_F32);
+  } else {
+    if (out_dtype == DKV_BF16) DKV_JS_LAUNCH(DKV_F16, 0, DKV_BF16);
+    else if (out_dtype == DKV_F16) DKV_JS_LAUNCH(DKV_F16, 0, DKV_F16);
+    else DKV_JS_LAUNCH(DKV_F16, 0, DKV_F32);
+  }
+#undef DKV_JS_LAUNCH
+  DKV_HIP_CHECK_LAUNCH();
+  return DKV_OK;
+}
+
+extern "C" long long dkv_joint_av_workspace_floats(int B, int Hq, int S, int R) {
+  (void)R;
+  if (B <= 0 || Hq <= 0 || S <= 0) return 0;
+  const int sl = joint_av_split_len(B, Hq, S);
+  const long long ns = (S + sl - 1) / sl;
+  return (long long)B * Hq * ns * JPREC;
+}
+
+extern "C" int dkv_joint_av(void* stream, int mode, int scores_dtype, int dtype, int out_dtype,
+                            const void* scores, long long sc_sb, long long sc_sh, long long sc_ss,
+                            const void* basis, long long basis_sh, long long basis_sr, int n_basis,
+                            const void* flat, long long flat_ld, const int* lens, long long lens_sb,
+                            long long lens_ss, const int* offs, long long offs_sb,
+                            long long offs_ss, float* workspace, long long workspace_floats,
+                            void* out, long long out_sb, long long out_sh, int B, int Hq, int S,
+                            int R, int Dh) {
+  if (mode != 0 && mode != 1) return DKV_E_ARG;
+  if (dtype != DKV_BF16 && dtype != DKV_F16) return DKV_E_UNSUPPORTED;
+  if (scores_dtype != DKV_F32 && scores_dtype != DKV_F16 && scores_dtype != DKV_BF16)
+    return DKV_E_ARG;
+  if (out_dtype != DKV_F32 && out_dtype != DKV_F16 && out_dtype != DKV_BF16) return DKV_E_ARG;
+  if (B < 0 || Hq < 0 || S < 0 || R <= 0 || n_basis <= 0) return DKV_E_ARG;
+  if (Dh != JDH || R > JRMAX) return DKV_E_UNSUPPORTED;
+  if (Hq % n_basis != 0) return DKV_E_ARG;
+  if (B == 0 || Hq == 0) return DKV_OK;
+  if (S == 0) return DKV_E_UNSUPPORTED;  // the reference's empty-cache result: generic path
+  if (!scores || !basis || !flat || !lens || !offs || !out || !workspace) return DKV_E_ARG;
+  if (flat_ld <= 0 || flat_ld > JFLAT_CAP - 8) return DKV_E_UNSUPPORTED;
+  if (B > 65535 || Hq > 65535) return DKV_E_UNSUPPORTED;
+  const int sl = joint_av_split_len(B, Hq, S);
+  const int ns = (S + sl - 1) / sl;
+  if (workspace_floats < (long long)B * Hq * ns * JPREC) return DKV_E_WORKSPACE;
+  hipStream_t st = (hipStream_t)stream;
+
+  JAvParams a;
+  a.scores = scores;
+  a.sc_sb = sc_sb;
+  a.sc_sh = sc_sh;
+  a.sc_ss = sc_ss;
+  a.flat = (const uint16_t*)flat;
+  a.flat_ld = flat_ld;
+  a.lens = lens;
+  a.lens_sb = lens_sb;
+  a.lens_ss = lens_ss;
+  a.offs = offs;
+  a.offs_sb = offs_sb;
+  a.offs_ss = offs_ss;
+  a.rec = workspace;
+  a.B = B;
+  a.Hq = Hq;
+  a.S = S;
+  a.R = R;
+  a.n_splits = ns;
+  a.split_len = sl;
+  const dim3 agrid((unsigned)ns, (unsigned)((Hq + 15) / 16), (unsigned)B);
+#define DKV_JA_LAUNCH(DT_, SDT_) \
+  hipLaunchKernelGGL((joint_av_kernel<DT_, SDT_>), agrid, dim3(JTHREADS), 0, st, a)
+  if (dtype == DKV_BF16) {
+    if (scores_dtype == DKV_F32) DKV_JA_LAUNCH(DKV_BF16, DKV_F32);
+    else if (scores_dtype == DKV_BF16) DKV_JA_LAUNCH(DKV_BF16, DKV_BF16);
+    else DKV_JA_LAUNCH(DKV_BF16, DKV_F16);
+  } else {
+    if (scores_dtype == DKV_F32) DKV_JA_LAUNCH(DKV_F16, DKV_F32);
+    else if (scores_dtype == DKV_BF16) DKV_JA_LAUNCH(DKV_F16, DKV_BF16);
+    else DKV_JA_LAUNCH(DKV_F16, DKV_F16);
+  }
+#undef DKV_JA_LAUNCH
+  DKV_HIP_CHECK_LAUNCH();
+
+  JMergeParams m;
+  m.rec = workspace;
+  m.vb = (const uint16_t*)basis;
+  m.vb_sh = basis_sh;
+  m.vb_sr = basis_sr;
+  m.out = out;
+  m.out_sb = out_sb;
+  m.out_sh = out_sh;
+  m.Hq = Hq;
+  m.R = R;
+  m.n_splits = ns;
+  m.hpg = Hq / n_basis;
+  const dim3 mgrid((unsigned)Hq, (unsigned)B);
+#define DKV_JM_LAUNCH(DT_, MODE_, ODT_) \
+  hipLaunchKernelGGL((joint_merge_kernel<DT_, MODE_, ODT_>), mgrid, dim3(256), 0, st, m)
+  if (dtype == DKV_BF16) {
+    if (mode == 0) {
+      if (out_dtype == DKV_BF16) DKV_JM_LAUNCH(DKV_BF16, 0, DKV_BF16);
+      else if (out_dtype == DKV_F16) DKV_JM_LAUNCH(DKV_BF16, 0, DKV_F16);
+      else DKV_JM_LAUNCH(DKV_BF16, 0, DKV_F32);
+    } else {
+      if (out_dtype == DKV_BF16) DKV_JM_LAUNCH(DKV_BF16, 1, DKV_BF16);
+      else if (out_dtype == DKV_F16) DKV_JM_LAUNCH(DKV_BF16, 1, DKV_F16);
+      else DKV_JM_LAUNCH(DKV_BF16, 1, DKV_F32);
+    }
+  } else {
+    if (mode == 0) {
+      if (out_dtype == DKV_BF16) DKV_JM_LAUNCH(DKV_F16, 0, DKV_BF16);
+      else if (out_dtype == DKV_F16) DKV_JM_LAUNCH(DKV_F16, 0, DKV_F16);
+      else DKV_JM_LAUNCH(DKV_F16, 0, DKV_F32);
+    } else {
+      if (out_dtype == DKV_BF16) DKV_JM_LAUNCH(DKV_F16, 1, DKV_BF16);
+      else if (out_dtype == DKV_F16) DKV_JM_LAUNCH(DKV_F16, 1, DKV_F16);
+      else DKV_JM_LAUNCH(DKV_F16, 1, DKV_F32);
+    }
+  }
+#undef DKV_JM_LAUNCH
+  DKV_HIP_CHECK_LAUNCH();
+  return DKV_OK;
+}

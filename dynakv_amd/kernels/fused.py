@@ -15,6 +15,7 @@ import math
 import torch
 
 from .. import _lib
+from . import joint as _joint
 from .decode import splitk_attention, splitk_layout
 
 
@@ -25,6 +26,10 @@ def fused_attention_dispatch(q, k_flat, k_up, v_flat, v_up, l_k, o_k, l_v, o_v, 
     if layout is not None:
         return splitk_attention(q, k_flat, v_flat, layout, l_k, o_k, l_v, o_v,
                                 theta=theta, route=_lib.DKV_ROUTE_FUSED)
+    out = _joint.joint_attention(q, k_flat, k_up, v_flat, v_up, l_k, o_k, l_v, o_v,
+                                 theta=theta, route=_lib.DKV_ROUTE_FUSED)
+    if out is not None:
+        return out
     return _fused_vector(q, k_flat, k_up, v_flat, v_up, l_k, o_k, l_v, o_v, theta)
 
 

@@ -20,6 +20,7 @@ import math
 import torch
 
 from .. import _lib
+from . import joint as _joint
 from .decode import splitk_attention, splitk_layout
 
 
@@ -30,6 +31,9 @@ def abx_sparse(a: torch.Tensor, b: torch.Tensor, x_flat: torch.Tensor, l_vec: to
     rank_per_head_groups = b.shape[1]
     if offsets is None:
         raise ValueError("offsets are required for the variable-length key cache")
+    if seq_len > 0 and _joint.scores_eligible(a, b, x_flat):
+        return _joint.joint_scores(a, b, x_flat, l_vec, offsets, theta=theta, mode=0,
+                                   out_dtype=a.dtype)
     lib = _lib.load()
     if a.stride(2) != 1:
         a = a.contiguous()
@@ -58,6 +62,8 @@ def avx(a: torch.Tensor, x_flat: torch.Tensor, v_up: torch.Tensor, l_vec: torch.
     num_kv_heads, rank_total, head_dim = v_up.shape
     if offsets is None:
         raise ValueError("offsets are required for the variable-length value cache")
+    if _joint.av_eligible(v_up, x_flat, num_heads, seq_len):
+        return _joint.joint_av(a, v_up, x_flat, l_vec, offsets, mode=0, out_dtype=a.dtype)
     lib = _lib.load()
     if v_up.stride(2) != 1:
         v_up = v_up.contiguous()
@@ -85,5 +91,10 @@ def two_stage_attention(*, q, k_flat, k_up, v_flat, v_up, key_lengths, key_offse
         return splitk_attention(q3, k_flat, v_flat, layout, key_lengths, key_offsets,
                                 value_lengths, value_offsets, theta=theta,
                                 route=_lib.DKV_ROUTE_TWO_STAGE)
+    out = _joint.joint_attention(q3, k_flat, k_up, v_flat, v_up, key_lengths, key_offsets,
+                                 value_lengths, value_offsets, theta=theta,
+                                 route=_lib.DKV_ROUTE_TWO_STAGE)
+    if out is not None:
+        return out
     scores = abx_sparse(q3, k_up, k_flat, key_lengths, offsets=key_offsets, theta=theta)
     return avx(scores, v_flat, v_up, value_lengths, value_offsets)

@@ -156,6 +156,47 @@ int dkv_av(void* stream, int mode, int scores_dtype, int cache_dtype, int out_dt
            int B, int Hq, int S, int R, int Dh);
 
 /*
+ * dkv_scores on MFMA for the reference's joint layout and any 16-bit cache with ranks up to 1024
+ * (abx_sparse / _abx_sparse_fwd, reference two_stage.py:48-189; with mode 1 the scores of the
+ * fused route, fused.py:28-140). Same semantics and outputs as dkv_scores (mode, masking,
+ * rounding to out_dtype), with the K basis given transposed: basis_t (n_basis, Dh, R-stride),
+ * element [h][d][r] at h*bt_sh + d*bt_sd + r, 16-byte aligned, bt_sd >= R, bt_sh and bt_sd
+ * multiples of 8. RoPE: the rope table of dkv_rope_table with rope_tiles >= ceil(S/16).
+ * q: (B, Hq, Dh) strides (q_sb, q_sh), unit dim stride; dtype (q and cache) DKV_BF16 or DKV_F16.
+ * DKV_E_UNSUPPORTED unless Dh == 128, R % 32 == 0, R <= 1024, Hq / n_basis <= 8,
+ * flat_ld <= 0x3fffffe8 (the caller then uses dkv_scores).
+ */
+int dkv_joint_scores(void* stream, int mode, int dtype, int out_dtype,
+                     const void* q, long long q_sb, long long q_sh,
+                     const void* basis_t, long long bt_sh, long long bt_sd, int n_basis,
+                     const void* flat, long long flat_ld,
+                     const int* lens, long long lens_sb, long long lens_ss,
+                     const int* offs, long long offs_sb, long long offs_ss,
+                     const float* rope, int rope_tiles,
+                     void* out, long long out_sb, long long out_sh, long long out_ss,
+                     int B, int Hq, int S, int R, int Dh);
+
+/* fp32 workspace dkv_joint_av needs for these sizes (split records). */
+long long dkv_joint_av_workspace_floats(int B, int Hq, int S, int R);
+
+/*
+ * dkv_av on MFMA (avx / _avx_proj_fwd, reference two_stage.py:207-324; mode 1: the fused route's V
+ * pass): the same inputs and outputs as dkv_av plus a caller workspace of
+ * dkv_joint_av_workspace_floats(B, Hq, S, R) floats. Token splits write (m, l, acc[R]) records,
+ * merged by LSE and projected through the V basis by a second launch. dtype (cache) DKV_BF16 or
+ * DKV_F16, Dh == 128, R <= 1024; S == 0 returns DKV_E_UNSUPPORTED (dkv_av covers it).
+ */
+int dkv_joint_av(void* stream, int mode, int scores_dtype, int dtype, int out_dtype,
+                 const void* scores, long long sc_sb, long long sc_sh, long long sc_ss,
+                 const void* basis, long long basis_sh, long long basis_sr, int n_basis,
+                 const void* flat, long long flat_ld,
+                 const int* lens, long long lens_sb, long long lens_ss,
+                 const int* offs, long long offs_sb, long long offs_ss,
+                 float* workspace, long long workspace_floats,
+                 void* out, long long out_sb, long long out_sh,
+                 int B, int Hq, int S, int R, int Dh);
+
+/*
  * RoPE cos/sin table for the split-K kernel, (17 + n_tiles) rows of 64 (cos, sin) fp32 pairs:
  * rows 0..15 the in-tile offsets (angle = d * inv_freq), row 16 the rotation by 128 positions (8 waves x 16),
  * row 17 + T the base of 16-token tile T (angle = 16T * inv_freq); inv_freq_i =

@@ -1,0 +1,175 @@
+"""The joint-layout MFMA kernels (dkv_joint_scores / dkv_joint_av, dynakv_amd/kernels/joint.py)
+against the vector kernels of the same semantics (dkv_scores / dkv_av, themselves checked against
+the oracle in test_gpu_generic.py) and against the oracle directly.
+
+Reference: abx_sparse / avx (two_stage.py:48-324) and the fused route (fused.py:28-170) on the
+reference's shipped layout: one packed row per batch element, ranks up to 1024, k_up / v_up
+repeated over query heads. Cases cover every rank chunk count (token counts 0..R), token counts
+not a multiple of the 512-token scores block or the 16-token V tile, a packed buffer that ends
+exactly at the last coefficient (the last window read past the end), repeated and distinct
+bases (1, 4 and 8 query heads per basis), fp16 and bf16.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from dynakv_amd import _lib
+from dynakv_amd.kernels import joint as J
+from oracle import attention as A
+from oracle.packing import pack_rows
+
+from helpers import assert_close, cast_np
+
+THETA = 500000.0
+
+
+def _case(B, S, R, n_basis, Hq=32, dtype=torch.bfloat16, seed=0, len_lo=0, exact_end=False):
+    rng = np.random.default_rng(seed)
+    coef_k = cast_np(rng.standard_normal((B, S, R)), dtype)
+    coef_v = cast_np(rng.standard_normal((B, S, R)), dtype)
+    lk = rng.integers(len_lo, R + 1, size=(B, S)).astype(np.int32)
+    lv = rng.integers(len_lo, R + 1, size=(B, S)).astype(np.int32)
+    if S > 2:
+        lk[:, 0], lk[:, 1], lv[:, 0], lv[:, 1] = R, 0, 0, R
+    if exact_end:  # the longest rows last, so the buffer can end at the last row's last value
+        lk = lk[np.argsort(lk.sum(1), kind="stable")]
+        lv = lv[np.argsort(lv.sum(1), kind="stable")]
+    fk, lk, ok, _ = pack_rows(coef_k, lk, R)
+    fv, lv, ov, _ = pack_rows(coef_v, lv, R)
+    if exact_end:
+        fk = np.ascontiguousarray(fk[:, : int(lk[-1].sum())])
+        fv = np.ascontiguousarray(fv[:, : int(lv[-1].sum())])
+    kb = cast_np(rng.standard_normal((n_basis, R, 128)) / math.sqrt(R), dtype)
+    vb = cast_np(rng.standard_normal((n_basis, R, 128)) / math.sqrt(R), dtype)
+    q = cast_np(rng.standard_normal((B, Hq, 128)), dtype)
+    return dict(q=q, fk=fk, lk=lk, ok=ok, fv=fv, lv=lv, ov=ov, kb=kb, vb=vb)
+
+
+def _dev(h, dev, dtype):
+    t = lambda x, dt=dtype: torch.from_numpy(np.ascontiguousarray(x)).to(dev, dt)  # noqa: E731
+    return {k: t(v, torch.int32 if k in ("lk", "ok", "lv", "ov") else dtype) for k, v in h.items()}
+
+
+def _generic_scores(d, k_up, mode, out_dtype):
+    q = d["q"]
+    B, Hq, _ = q.shape
+    S = d["lk"].shape[1]
+    out = torch.empty((B, Hq, S), dtype=out_dtype, device=q.device)
+    rc = _lib.load().dkv_scores(
+        _lib.stream_of(q), mode, _lib.dtype_code(q.dtype), _lib.dtype_code(d["fk"].dtype),
+        _lib.dtype_code(out_dtype), q.data_ptr(), q.stride(0), q.stride(1),
+        k_up.data_ptr(), k_up.stride(0), k_up.stride(1), k_up.shape[0],
+        d["fk"].data_ptr(), d["fk"].stride(0),
+        d["lk"].data_ptr(), d["lk"].stride(0), d["lk"].stride(1),
+        d["ok"].data_ptr(), d["ok"].stride(0), d["ok"].stride(1),
+        out.data_ptr(), out.stride(0), out.stride(1), out.stride(2),
+        B, Hq, S, k_up.shape[1], 128, math.log(THETA))
+    _lib.check(rc, "dkv_scores")
+    return out
+
+
+def _generic_av(sc, d, v_up, mode, out_dtype):
+    B, Hq, S = sc.shape
+    out = torch.empty((B, Hq, 128), dtype=out_dtype, device=sc.device)
+    rc = _lib.load().dkv_av(
+        _lib.stream_of(sc), mode, _lib.dtype_code(sc.dtype), _lib.dtype_code(d["fv"].dtype),
+        _lib.dtype_code(out_dtype), sc.data_ptr(), sc.stride(0), sc.stride(1), sc.stride(2),
+        v_up.data_ptr(), v_up.stride(0), v_up.stride(1), v_up.shape[0],
+        d["fv"].data_ptr(), d["fv"].stride(0),
+        d["lv"].data_ptr(), d["lv"].stride(0), d["lv"].stride(1),
+        d["ov"].data_ptr(), d["ov"].stride(0), d["ov"].stride(1),
+        out.data_ptr(), out.stride(0), out.stride(1), B, Hq, S, v_up.shape[1], 128)
+    _lib.check(rc, "dkv_av")
+    return out
+
+
+ULP = {torch.float16: 2.0 ** -10, torch.bfloat16: 2.0 ** -7}
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("B,S,R,n_basis,repeat", [
+    (2, 777, 1024, 8, 4),   # the reference's repeated k_up (32 bases -> 8 distinct)
+    (3, 513, 512, 4, 1),    # 8 query heads per basis
+    (1, 40, 32, 32, 1),     # one rank chunk, one query head per basis
+    (2, 1100, 1024, 8, 1),  # 4 query heads per basis, three 512-token blocks
+])
+def test_scores_match_vector_kernel(dev, dtype, B, S, R, n_basis, repeat):
+    print(f"[gpu] joint scores {dtype} B={B} S={S} R={R} nb={n_basis} rep={repeat}", flush=True)
+    h = _case(B, S, R, n_basis, dtype=dtype, seed=S + R, exact_end=True)
+    d = _dev(h, dev, dtype)
+    k_up = d["kb"].repeat_interleave(repeat, dim=0).contiguous() if repeat > 1 else d["kb"]
+    for mode, odt in ((0, dtype), (1, torch.float32)):
+        got = J.joint_scores(d["q"], k_up, d["fk"], d["lk"], d["ok"], theta=THETA, mode=mode,
+                             out_dtype=odt)
+        ref = _generic_scores(d, k_up, mode, odt)
+        g, r = got.float(), ref.float()
+        fin = torch.isfinite(r)
+        assert torch.equal(torch.isfinite(g), fin)
+        err = (g[fin] - r[fin]).abs()
+        # fp32-faithful K' and products: mode 0 results are the same rounding target (allow two
+        # units in the last place), mode 1 agrees to fp32 accumulation-order differences
+        tol = (2 * ULP[dtype] * r[fin].abs() + 1e-4) if mode == 0 else (1e-4 * r[fin].abs() + 1e-4)
+        print(f"[parity] scores mode {mode}: max_abs={err.max().item():.3e}", flush=True)
+        assert (err <= tol).all(), float(err.max())
+        masked = d["lk"] == 0
+        if mode == 0:
+            assert torch.equal(g.masked_select(masked[:, None, :]), r.masked_select(masked[:, None, :]))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("B,S,R,n_basis", [(2, 1000, 1024, 8), (1, 17, 1024, 32), (3, 1, 256, 4),
+                                           (2, 300, 1024, 8)])
+def test_av_matches_vector_kernel(dev, dtype, B, S, R, n_basis):
+    print(f"[gpu] joint av {dtype} B={B} S={S} R={R} nb={n_basis}", flush=True)
+    h = _case(B, S, R, n_basis, dtype=dtype, seed=7 * S + R, exact_end=True)
+    d = _dev(h, dev, dtype)
+    rng = np.random.default_rng(S)
+    for mode in (0, 1):
+        sdt = dtype if mode == 0 else torch.float32
+        z = rng.standard_normal((B, 32, S)) * 2
+        if mode == 1:
+            z[:, :, rng.random(S) < 0.3] = -np.inf  # the fused route's masked tokens
+            z[:, :, 0] = 0.5
+        sc = torch.from_numpy(cast_np(z, sdt)).to(dev, sdt)
+        got = J.joint_av(sc, d["vb"], d["fv"], d["lv"], d["ov"], mode=mode, out_dtype=torch.float32)
+        ref = _generic_av(sc, d, d["vb"], mode, torch.float32)
+        # bf16 caches: P as bf16 hi + lo (fp32-faithful); fp16 caches: P in fp16 (2^-11 per term)
+        ta = 2e-4 if dtype == torch.bfloat16 else 1e-3
+        assert_close(got, ref.cpu().numpy(), f"av mode {mode}", tol_abs=ta, tol_rel=2e-3)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("route", ["short_fused", "long_two_stage"])
+def test_joint_attention_against_oracle(dev, route):
+    """The router's joint path end to end against the oracle (two rows, 700 tokens)."""
+    print(f"[gpu] joint attention {route}", flush=True)
+    dtype = torch.bfloat16
+    h = _case(2, 700, 1024, 8, dtype=dtype, seed=11, len_lo=0)
+    d = _dev(h, dev, dtype)
+    k_up = d["kb"].repeat_interleave(4, dim=0).contiguous()
+    v_up = d["vb"].repeat_interleave(4, dim=0).contiguous()
+    rt = _lib.DKV_ROUTE_FUSED if route == "short_fused" else _lib.DKV_ROUTE_TWO_STAGE
+    got = J.joint_attention(d["q"], d["fk"], k_up, d["fv"], v_up, d["lk"], d["ok"], d["lv"],
+                            d["ov"], theta=THETA, route=rt)
+    assert got is not None and got.dtype == dtype
+    ref = A.decode_attention(h["q"], h["fk"], np.repeat(h["kb"], 4, axis=0), h["fv"],
+                             np.repeat(h["vb"], 4, axis=0), h["lk"], h["ok"], h["lv"], h["ov"],
+                             THETA, route=route, q_dtype="bfloat16")
+    assert_close(got, ref, f"joint {route}")
+
+
+@pytest.mark.gpu
+def test_distinct_basis_detection(dev):
+    """A k_up repeated over query heads is reduced to its distinct bases (once per tensor and
+    in-place version); a basis whose copies differ is kept whole."""
+    kb = torch.randn(8, 64, 128, device=dev, dtype=torch.bfloat16)
+    rep = kb.repeat_interleave(4, dim=0).contiguous()
+    got = J._distinct(rep, 32)
+    assert got.shape == (8, 64, 128) and torch.equal(got, kb)
+    assert J._distinct(rep, 32) is got
+    rep[5, 0, 0] += 1  # in place: the copies differ now
+    assert J._distinct(rep, 32).shape[0] == 32
