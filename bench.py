@@ -43,6 +43,7 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 
 
 def _log(msg):
@@ -369,6 +370,109 @@ def bench_prefill(dev, iters=10, B=4, S=2048, Hq=32, Hkv=8, dtype=torch.bfloat16
     }
 
 
+def bench_joint(dev, iters=5, B=16, S=8192, R=1024, Hq=32, Hkv=8, mean=0.29,
+                dtype=torch.bfloat16):
+    """The reference's joint layout at the config-3 shape: one packed row per batch element with
+    ranks up to 1024 shared by the 8 KV heads, k_up / v_up repeated to the 32 query heads as the
+    reference ships them (compressed_attention.py:278-286), the router's long route
+    (abx_sparse + avx semantics) through the MFMA kernels of ``kernels/joint.py``. GPU time from
+    events around ``iters`` back-to-back calls; the scores kernel's MFMA work counted as
+    launched (2 * 128 * 32 flop per rank chunk, token slot and KV head, chunks up to each
+    512-token block's longest token). The vector kernels (dkv_scores / dkv_av, what a joint
+    layout ran on before) are timed on a 2 x 512-token slice of the same data."""
+    import math as _m
+
+    from dynakv_amd import _lib
+    from dynakv_amd.kernels import joint as J
+    from dynakv_amd.synthetic import device_lengths
+
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(99)
+    lk = device_lengths(B, S, R, mean, gen, dev, 4, 0.05)
+    lv = device_lengths(B, S, R, mean, gen, dev, 4, 0.05)
+
+    def packed(lens):
+        offs = torch.zeros_like(lens)
+        offs[:, 1:] = torch.cumsum(lens, dim=1)[:, :-1]
+        cap = int(lens.sum(dim=1).max().item())
+        flat = torch.randn((B, cap), generator=gen, device=dev, dtype=torch.float32).to(dtype)
+        return flat, offs.to(torch.int32).contiguous()
+
+    fk, ok = packed(lk)
+    fv, ov = packed(lv)
+    kb = (torch.randn((Hkv, R, 128), generator=gen, device=dev) / _m.sqrt(R)).to(dtype)
+    vb = (torch.randn((Hkv, R, 128), generator=gen, device=dev) / _m.sqrt(R)).to(dtype)
+    k_up = kb.repeat_interleave(Hq // Hkv, dim=0).contiguous()
+    v_up = vb.repeat_interleave(Hq // Hkv, dim=0).contiguous()
+    q = torch.randn((B, Hq, 128), generator=gen, device=dev).to(dtype)
+    theta = 500000.0
+
+    def timed(fn, n):
+        for _ in range(2):
+            fn()
+        torch.cuda.synchronize(dev)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(n):
+            fn()
+        e1.record()
+        torch.cuda.synchronize(dev)
+        return e0.elapsed_time(e1) / n * 1e3  # us
+
+    route = _lib.DKV_ROUTE_TWO_STAGE
+    full = timed(lambda: J.joint_attention(q, fk, k_up, fv, v_up, lk, ok, lv, ov, theta=theta,
+                                           route=route), iters)
+    sc = J.joint_scores(q, k_up, fk, lk, ok, theta=theta, mode=0, out_dtype=dtype)
+    t_sc = timed(lambda: J.joint_scores(q, k_up, fk, lk, ok, theta=theta, mode=0,
+                                        out_dtype=dtype), iters)
+    t_av = timed(lambda: J.joint_av(sc, v_up, fv, lv, ov, mode=0, out_dtype=dtype), iters)
+    flops = J.joint_flops(lk, R, Hkv, B)
+    dense_flops = 2.0 * B * S * Hkv * 128 * R
+    coef_bytes = 2 * int(lk.clamp(0, R).sum().item() + lv.clamp(0, R).sum().item())
+
+    # the vector kernels on a slice: 2 rows x 512 tokens
+    b2, s2 = 2, 512
+    lib = _lib.load()
+    lk2, ok2, lv2, ov2 = (t[:b2, :s2].contiguous() for t in (lk, ok, lv, ov))
+    q2 = q[:b2].contiguous()
+    st = _lib.stream_of(q2)
+    sc2 = torch.empty((b2, Hq, s2), dtype=dtype, device=dev)
+    out2 = torch.empty((b2, Hq, 128), dtype=dtype, device=dev)
+
+    def vector_pass():
+        lib.dkv_scores(st, 0, _lib.dtype_code(dtype), _lib.dtype_code(dtype), _lib.dtype_code(dtype),
+                       q2.data_ptr(), q2.stride(0), q2.stride(1), k_up.data_ptr(), k_up.stride(0),
+                       k_up.stride(1), Hq, fk.data_ptr(), fk.stride(0), lk2.data_ptr(),
+                       lk2.stride(0), lk2.stride(1), ok2.data_ptr(), ok2.stride(0), ok2.stride(1),
+                       sc2.data_ptr(), sc2.stride(0), sc2.stride(1), sc2.stride(2),
+                       b2, Hq, s2, R, 128, _m.log(theta))
+        lib.dkv_av(st, 0, _lib.dtype_code(dtype), _lib.dtype_code(dtype), _lib.dtype_code(dtype),
+                   sc2.data_ptr(), sc2.stride(0), sc2.stride(1), sc2.stride(2), v_up.data_ptr(),
+                   v_up.stride(0), v_up.stride(1), Hq, fv.data_ptr(), fv.stride(0),
+                   lv2.data_ptr(), lv2.stride(0), lv2.stride(1), ov2.data_ptr(), ov2.stride(0),
+                   ov2.stride(1), out2.data_ptr(), out2.stride(0), out2.stride(1),
+                   b2, Hq, s2, R, 128)
+
+    t_vec = timed(vector_pass, 2)
+    t_mfma_slice = timed(lambda: J.joint_attention(q2, fk, k_up, fv, v_up, lk2, ok2, lv2, ov2,
+                                                   theta=theta, route=route), 5)
+    return {
+        "shape": (f"B={B}, S={S}, joint rank {R} shared by {Hkv} KV heads, k_up/v_up repeated "
+                  f"to {Hq} query heads, mean retention {mean}, {str(dtype).split('.')[-1]}, "
+                  "long route"),
+        "us_per_call": round(full, 1),
+        "scores_us": round(t_sc, 1),
+        "av_us": round(t_av, 1),
+        "scores_mfma_tflops": round(flops / (t_sc * 1e-6) / 1e12, 1),
+        "scores_mfma_peak_frac": round(flops / (t_sc * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+        "scores_flop_as_launched": flops,
+        "reconstruction_flop_dense": dense_flops,
+        "coefficient_bytes": coef_bytes,
+        "vector_kernels_slice": {"slice": f"B={b2}, S={s2}", "us_per_call": round(t_vec, 1),
+                                 "mfma_us_per_call": round(t_mfma_slice, 1)},
+    }
+
+
 def bench_e2e(dev, batches=(1, 2, 4), prompt_len=2048, new_tokens=100, models="both"):
     """Config 5: greedy generation with a random-init Llama-3-8B (bf16 N(0, 0.02) weights,
     per-head random orthogonal bases, cutoff heads set for mean retention 0.47) over the
@@ -449,6 +553,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-cutoff", action="store_true", help="skip the cutoff-head timing")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill-attention timing")
+    ap.add_argument("--no-joint", action="store_true",
+                    help="skip the joint-layout (rank 1024) attention timing")
     ap.add_argument("--no-e2e", action="store_true",
                     help="skip config 5 (greedy generation with a random Llama-3-8B, compressed "
                          "against uncompressed cache; about 10 s)")
@@ -553,6 +659,9 @@ def main():
     if not args.no_cutoff:
         _log("cutoff head")
         line["cutoff_head"] = bench_cutoff(cfg, dev)
+    if not args.no_joint:
+        _log("joint layout")
+        line["joint_layout"] = bench_joint(dev)
     if not args.no_prefill:
         _log("prefill attention")
         line["prefill_attention"] = bench_prefill(dev)

@@ -23,8 +23,11 @@
 //   log2 domain (every wave computes the same values), P as bf16 hi + lo (fp16 for fp16 caches),
 //   the wave's V coefficients of the tile staged in LDS and read transposed (ds_read_b64_tr_b16)
 //   as the B operand of P.X^V. Each split writes (m, l, acc[R]) per head.
-// joint_merge_kernel -- workgroup = (query head, batch row b): LSE merge of the split records,
-//   the route's denominator, the projection through the V basis, the output rounding.
+// joint_merge_kernel -- workgroup = (V basis and up to 8 of its query heads, batch row b): LSE
+//   merge of the split records, the route's denominator, the projection through the V basis
+//   (each basis value loaded once for the group's heads), the output rounding.
+#include <type_traits>
+
 #include "dkv_common.h"
 #include "dkv_mfma_ops.h"
 
@@ -40,7 +43,7 @@ constexpr int JRMAX = 1024;
 constexpr int JPREC = 2 + JRMAX;         // split record: m (log2 units), l, acc[R]
 constexpr int JROPE_FIXED = 17;          // rows of the RoPE table before the per-tile rows
 constexpr int JFLAT_CAP = 0x3ffffff0;    // elements one buffer resource covers
-constexpr int JMAX_SPLITS = 1024;
+constexpr int JMAX_SPLITS = 1024;  // token splits of the V pass
 constexpr float JLOG2E = 1.4426950408889634f;
 constexpr float JRESCALE = 11.5f;        // log2 units: rescale when the running max grows more
 
@@ -136,56 +139,74 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_scores_kernel(JScoresParams
     tlen[cb] = sLen[tl];
     toff[cb] = sOff[tl];
   }
-  auto load_x = [&](int c, dkv_u32x4(&x)[JCB]) {
-#pragma unroll
-    for (int cb = 0; cb < JCB; ++cb) {
-      const int j0 = JCH * c + 8 * g;
-      x[cb] = dkv_load8_prefix(rs, end, toff[cb] + j0, tlen[cb] - j0);
-    }
-  };
-
   dkv_f32x4 acc[8][JCB];
 #pragma unroll
   for (int i = 0; i < 8; ++i)
 #pragma unroll
     for (int cb = 0; cb < JCB; ++cb) acc[i][cb] = dkv_f32x4{0.f, 0.f, 0.f, 0.f};
 
-  dkv_u32x4 xa[JCB], xb[JCB];
-  dkv_u32x4 bnext = dkv_u32x4{0u, 0u, 0u, 0u};
+  // The rank loop. The coefficient loads are not waited for where they are issued (their masks
+  // are applied where the values are used), so each wave keeps two chunks of loads in flight.
+  // Only the last batch row can hold a window that crosses the end of the buffer; its
+  // workgroups run the loop with element-wise gathers for such windows.
+  auto rank_loop = [&](auto safe_tag) {
+    constexpr bool SAFE = decltype(safe_tag)::value;
+    auto load_x = [&](int c, dkv_u32x4(&x)[JCB]) {
 #pragma unroll
-  for (int cb = 0; cb < JCB; ++cb) xa[cb] = xb[cb] = dkv_u32x4{0u, 0u, 0u, 0u};
-  if (nch > 0) {
-    sB[0][tid] = *(const dkv_u32x4*)bsrc;
-    if (nch > 1) bnext = *(const dkv_u32x4*)(bsrc + JCH);
-    load_x(0, xa);
-    if (nch > 1) load_x(1, xb);
-  }
-  __syncthreads();
-  // chunk c: its basis sits in sB[c & 1] (written before the previous barrier); the basis of
-  // chunk c+1 (loaded one iteration ago) goes to the other buffer, whose readers finished before
-  // that barrier; the coefficients run two chunks ahead
-  for (int c = 0; c < nch; ++c) {
-    if (c + 1 < nch) sB[(c + 1) & 1][tid] = bnext;
-    if (c + 2 < nch) bnext = *(const dkv_u32x4*)(bsrc + JCH * (c + 2));
-    dkv_u32x4 xn[JCB];
+      for (int cb = 0; cb < JCB; ++cb) {
+        const int j0 = JCH * c + 8 * g;
+        if constexpr (SAFE)
+          x[cb] = dkv_load8_safe(rs, end, toff[cb] + j0, tlen[cb] - j0);
+        else
+          x[cb] = dkv_load8_raw(rs, toff[cb] + j0, tlen[cb] - j0);
+      }
+    };
+    dkv_u32x4 xa[JCB], xb[JCB];
+    dkv_u32x4 bnext = dkv_u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
-    for (int cb = 0; cb < JCB; ++cb) xn[cb] = dkv_u32x4{0u, 0u, 0u, 0u};
-    if (c + 2 < nch) load_x(c + 2, xn);
-    const dkv_u32x4* buf = sB[c & 1];
-#pragma unroll
-    for (int blk = 0; blk < 8; ++blk) {
-      const int d = 16 * blk + n;
-      const dkv_u32x4 a = buf[4 * d + (g ^ ((d >> 2) & 3))];
-#pragma unroll
-      for (int cb = 0; cb < JCB; ++cb) acc[blk][cb] = dkv_mfma32<DT>(a, xa[cb], acc[blk][cb]);
-    }
-#pragma unroll
-    for (int cb = 0; cb < JCB; ++cb) {
-      xa[cb] = xb[cb];
-      xb[cb] = xn[cb];
+    for (int cb = 0; cb < JCB; ++cb) xa[cb] = xb[cb] = dkv_u32x4{0u, 0u, 0u, 0u};
+    if (nch > 0) {
+      sB[0][tid] = *(const dkv_u32x4*)bsrc;
+      bnext = *(const dkv_u32x4*)(bsrc + JCH * min(1, nch - 1));
+      load_x(0, xa);
+      load_x(1, xb);
     }
     __syncthreads();
-  }
+    // Chunk c: its basis sits in sB[c & 1] (written before the previous barrier); the basis of
+    // chunk c+1 (loaded one chunk ago, before that chunk's coefficients) goes to the other
+    // buffer, whose readers finished before that barrier; the coefficients run two chunks ahead
+    // and are reloaded into the registers they were used from (x: xa for even c, xb for odd c),
+    // so no loaded value is ever copied and the waits cover only the values being used. Loads
+    // past the last chunk clamp the basis index and have coefficient counts <= 0 (no traffic).
+    auto step = [&](int c, dkv_u32x4(&x)[JCB]) {
+      dkv_u32x4 xm[JCB];
+#pragma unroll
+      for (int cb = 0; cb < JCB; ++cb) xm[cb] = dkv_mask8(x[cb], tlen[cb] - (JCH * c + 8 * g));
+      sB[(c + 1) & 1][tid] = bnext;
+      bnext = *(const dkv_u32x4*)(bsrc + JCH * min(c + 2, nch - 1));
+      load_x(c + 2, x);
+      const dkv_u32x4* buf = sB[c & 1];
+#pragma unroll
+      for (int blk = 0; blk < 8; ++blk) {
+        const int d = 16 * blk + n;
+        const dkv_u32x4 a = buf[4 * d + (g ^ ((d >> 2) & 3))];
+#pragma unroll
+        for (int cb = 0; cb < JCB; ++cb) acc[blk][cb] = dkv_mfma32<DT>(a, xm[cb], acc[blk][cb]);
+      }
+      __syncthreads();
+    };
+    // whole pairs in the loop (every path back to its head has issued both steps' loads)
+    int c = 0;
+    for (; c + 1 < nch; c += 2) {
+      step(c, xa);
+      step(c + 1, xb);
+    }
+    if (c < nch) step(c, xa);
+  };
+  if (b == p.B - 1)
+    rank_loop(std::integral_constant<bool, true>{});
+  else
+    rank_loop(std::integral_constant<bool, false>{});
 
   // ---- per 16-token tile: rotation, K' hi + lo, scores, masking, store ---------------------
   const int hn = n & 7;
@@ -296,26 +317,34 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_av_kernel(JAvParams p) {
   const __amdgpu_buffer_rsrc_t rs = dkv_make_rsrc(p.flat + (long long)b * p.flat_ld, end * 2u);
   const long long sbase = (long long)b * p.sc_sb + (long long)(hq_ok ? hq : 0) * p.sc_sh;
 
-  // tile j's inputs: the V pieces of token n (ranks r0 + 32c + 8g .. +8) and the scores of head
-  // slot n for tokens 4g .. 4g+3
-  auto load_tile = [&](int j, dkv_u32x4(&x)[4], float(&z)[4]) {
-    const int t = s_begin + 16 * j + n;
-    int len = 0, off = 0;
-    if (t < s_end) {
-      len = min(max(p.lens[(long long)b * p.lens_sb + (long long)t * p.lens_ss], 0), p.R);
-      off = p.offs[(long long)b * p.offs_sb + (long long)t * p.offs_ss];
-    }
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int j0 = r0 + 32 * c + 8 * g;
-      x[c] = dkv_load8_prefix(rs, end, off + j0, len - j0);
-    }
+  // Tile j's inputs for this lane: the metadata (count, offset) of token n, its V pieces (ranks
+  // r0 + 32c + 8g .. +8) and the scores of head slot n for tokens 4g .. 4g+3. Every lane issues
+  // every load (indices past the split clamp to its last token) and keeps the raw value; counts
+  // are clamped, pieces masked and excluded scores replaced where the values are used, two tiles
+  // later, so no load is waited for where it is issued.
+  auto load_meta = [&](int j, int& l, int& o) {
+    const int tc = min(s_begin + 16 * j + n, s_end - 1);
+    l = p.lens[(long long)b * p.lens_sb + (long long)tc * p.lens_ss];
+    o = p.offs[(long long)b * p.offs_sb + (long long)tc * p.offs_ss];
+  };
+  auto count = [&](int j, int l) { return s_begin + 16 * j + n < s_end ? min(max(l, 0), p.R) : 0; };
+  auto load_z = [&](int j, uint32_t(&z)[4]) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const int tt = s_begin + 16 * j + 4 * g + u;
-      z[u] = (hq_ok && tt < s_end) ? dkv_load_f32<SDT>(p.scores, sbase + (long long)tt * p.sc_ss)
-                                   : -INFINITY;
+      const long long i = sbase + (long long)min(s_begin + 16 * j + 4 * g + u, s_end - 1) * p.sc_ss;
+      if constexpr (SDT == DKV_F32)
+        z[u] = ((const uint32_t*)p.scores)[i];
+      else
+        z[u] = ((const uint16_t*)p.scores)[i];
     }
+  };
+  auto score = [&](int j, int u, uint32_t raw) {
+    float v;
+    if constexpr (SDT == DKV_F32)
+      v = __uint_as_float(raw);
+    else
+      v = dkv_elt_to_f32<SDT>(raw);
+    return (hq_ok && s_begin + 16 * j + 4 * g + u < s_end) ? v * JLOG2E : -INFINITY;
   };
 
   dkv_f32x4 acc[8];
@@ -323,83 +352,128 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_av_kernel(JAvParams p) {
   for (int i = 0; i < 8; ++i) acc[i] = dkv_f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = -1.0e30f;  // finite floor: excluded tokens give exp2(-inf) = 0
   float l_run = 0.f;
-
-  dkv_u32x4 xc[4];
-  float zc[4];
-  if (ntiles > 0) load_tile(0, xc, zc);
   dkv_u32x4* slot = sV[wave];
-  for (int j = 0; j < ntiles; ++j) {
-#pragma unroll
-    for (int c = 0; c < 4; ++c) slot[c * 64 + lane] = xc[c];
-    float z[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) z[u] = zc[u] * JLOG2E;
-    if (j + 1 < ntiles) load_tile(j + 1, xc, zc);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-    // online softmax of head slot n (its 16 tokens sit in lanes n, n+16, n+32, n+48)
-    float tmax = dkv_max3(dkv_max3(z[0], z[1], z[2]), z[3], z[3]);
-    tmax = dkv_lane_max32(tmax);
-    tmax = dkv_lane_max16(tmax);
-    if (__ballot(tmax > m_run + JRESCALE)) {
-      const float m_new = fmaxf(m_run, tmax);
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-      l_run *= alpha;
-      m_run = m_new;
-      float au[4];
+  auto tile_loop = [&](auto safe_tag) {
+    constexpr bool SAFE = decltype(safe_tag)::value;
+    auto load_v = [&](int len, int off, dkv_u32x4(&x)[4]) {
 #pragma unroll
-      for (int u = 0; u < 4; ++u) au[u] = __shfl(alpha, 4 * g + u, 64);
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-#pragma unroll
-        for (int u = 0; u < 4; ++u) acc[i][u] *= au[u];
-    }
-    float pu[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      pu[u] = __builtin_amdgcn_exp2f(z[u] - m_run);
-      l_run += pu[u];
-    }
-    // P.X^V in coefficient space (A: P of head slot n, tokens 4g..4g+3; B: the transposed V reads)
-    dkv_u32x2 pa_hi, pa_lo;
-    if constexpr (DT == DKV_F16) {
-      pa_hi = dkv_u32x2{dkv_pack_f16x2(pu[0], pu[1]), dkv_pack_f16x2(pu[2], pu[3])};
-      pa_lo = pa_hi;
-    } else {
-      uint32_t h01, l01, h23, l23;
-      dkv_split_bf16x2(pu[0], pu[1], h01, l01);
-      dkv_split_bf16x2(pu[2], pu[3], h23, l23);
-      pa_hi = dkv_u32x2{h01, h23};
-      pa_lo = dkv_u32x2{l01, l23};
-    }
-    {
-      const int u = n >> 2, q = n & 3;
-      const uint8_t* vbase =
-          (const uint8_t*)slot + 16 * (16 * (q >> 1) + 4 * g + u) + 8 * (q & 1);
-#pragma unroll
-      for (int blk = 0; blk < 8; ++blk) {
-        const uint8_t* src = vbase + (blk >> 1) * 1024 + (blk & 1) * 512;
-        const dkv_u32x2 xv = __builtin_bit_cast(
-            dkv_u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                           (__attribute__((address_space(3))) dkv_i16x4*)(
-                               (__attribute__((address_space(3))) uint8_t*)src)));
-        if constexpr (DT == DKV_BF16)
-          acc[blk] = dkv_mfma32<DT>(
-              dkv_u32x4{pa_hi.x, pa_hi.y, pa_lo.x, pa_lo.y},
-              __builtin_bit_cast(dkv_u32x4, dkv_u64x2{__builtin_bit_cast(uint64_t, xv),
-                                                      __builtin_bit_cast(uint64_t, xv)}),
-              acc[blk]);
+      for (int c = 0; c < 4; ++c) {
+        const int j0 = r0 + 32 * c + 8 * g;
+        if constexpr (SAFE)
+          x[c] = dkv_load8_safe(rs, end, off + j0, len - j0);
         else
-          acc[blk] = __builtin_amdgcn_mfma_f32_16x16x16f16(
-              __builtin_bit_cast(dkv_f16x4, pa_hi), __builtin_bit_cast(dkv_f16x4, xv), acc[blk],
-              0, 0, 0);
+          x[c] = dkv_load8_raw(rs, off + j0, len - j0);
       }
+    };
+    // Set A holds even tiles, set B odd ones: the V pieces x and raw scores z of its current
+    // tile, that tile's count, and the raw metadata (ml, mo) of the tile two ahead. A tile's
+    // loads go into the registers its set just used, so no loaded value is ever copied.
+    dkv_u32x4 xA[4], xB[4];
+    uint32_t zA[4], zB[4];
+    int cA, cB, mlA, moA, mlB, moB;
+    {
+      int l0, o0, l1, o1;
+      load_meta(0, l0, o0);
+      load_meta(1, l1, o1);
+      load_meta(2, mlA, moA);
+      load_meta(3, mlB, moB);
+      cA = count(0, l0);
+      cB = count(1, l1);
+      load_v(cA, o0, xA);
+      load_z(0, zA);
+      load_v(cB, o1, xB);
+      load_z(1, zB);
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    auto step = [&](int j, dkv_u32x4(&x)[4], uint32_t(&zr)[4], int& cnt, int& ml, int& mo) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) slot[c * 64 + lane] = dkv_mask8(x[c], cnt - (r0 + 32 * c + 8 * g));
+      float z[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) z[u] = score(j, u, zr[u]);
+      cnt = count(j + 2, ml);
+      load_v(cnt, mo, x);
+      load_z(j + 2, zr);
+      load_meta(j + 4, ml, mo);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+      // online softmax of head slot n (its 16 tokens sit in lanes n, n+16, n+32, n+48)
+      float tmax = dkv_max3(dkv_max3(z[0], z[1], z[2]), z[3], z[3]);
+      tmax = dkv_lane_max32(tmax);
+      tmax = dkv_lane_max16(tmax);
+      if (__ballot(tmax > m_run + JRESCALE)) {
+        const float m_new = fmaxf(m_run, tmax);
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+        l_run *= alpha;
+        m_run = m_new;
+        float au[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) au[u] = __shfl(alpha, 4 * g + u, 64);
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+          for (int u = 0; u < 4; ++u) acc[i][u] *= au[u];
+      }
+      float pu[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        pu[u] = __builtin_amdgcn_exp2f(z[u] - m_run);
+        l_run += pu[u];
+      }
+      // P.X^V in coefficient space (A: P of head slot n, tokens 4g..4g+3; B: the transposed V reads)
+      dkv_u32x2 pa_hi, pa_lo;
+      if constexpr (DT == DKV_F16) {
+        pa_hi = dkv_u32x2{dkv_pack_f16x2(pu[0], pu[1]), dkv_pack_f16x2(pu[2], pu[3])};
+        pa_lo = pa_hi;
+      } else {
+        uint32_t h01, l01, h23, l23;
+        dkv_split_bf16x2(pu[0], pu[1], h01, l01);
+        dkv_split_bf16x2(pu[2], pu[3], h23, l23);
+        pa_hi = dkv_u32x2{h01, h23};
+        pa_lo = dkv_u32x2{l01, l23};
+      }
+      {
+        const int u = n >> 2, q = n & 3;
+        const uint8_t* vbase =
+            (const uint8_t*)slot + 16 * (16 * (q >> 1) + 4 * g + u) + 8 * (q & 1);
+#pragma unroll
+        for (int blk = 0; blk < 8; ++blk) {
+          const uint8_t* src = vbase + (blk >> 1) * 1024 + (blk & 1) * 512;
+          const dkv_u32x2 xv = __builtin_bit_cast(
+              dkv_u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                             (__attribute__((address_space(3))) dkv_i16x4*)(
+                                 (__attribute__((address_space(3))) uint8_t*)src)));
+          if constexpr (DT == DKV_BF16)
+            acc[blk] = dkv_mfma32<DT>(
+                dkv_u32x4{pa_hi.x, pa_hi.y, pa_lo.x, pa_lo.y},
+                __builtin_bit_cast(dkv_u32x4, dkv_u64x2{__builtin_bit_cast(uint64_t, xv),
+                                                        __builtin_bit_cast(uint64_t, xv)}),
+                acc[blk]);
+          else
+            acc[blk] = __builtin_amdgcn_mfma_f32_16x16x16f16(
+                __builtin_bit_cast(dkv_f16x4, pa_hi), __builtin_bit_cast(dkv_f16x4, xv), acc[blk],
+                0, 0, 0);
+        }
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+    // whole pairs in the loop (every path back to its head has issued both tiles' loads)
+    int j = 0;
+    for (; j + 1 < ntiles; j += 2) {
+      step(j, xA, zA, cA, mlA, moA);
+      step(j + 1, xB, zB, cB, mlB, moB);
+    }
+    if (j < ntiles) step(j, xA, zA, cA, mlA, moA);
+  };
+  if (ntiles > 0) {
+    if (b == p.B - 1)
+      tile_loop(std::integral_constant<bool, true>{});
+    else
+      tile_loop(std::integral_constant<bool, false>{});
   }
 
   // the split's record per head: m and l (identical in every wave: wave 0 writes them), the
@@ -435,50 +509,86 @@ struct JMergeParams {
   int Hq, R, n_splits, hpg;
 };
 
+constexpr int JMH = 8;  // query heads merged and projected together (they share a V basis)
+
+// workgroup = (V basis head hv and a chunk of up to 8 of its query heads, batch row b)
 template <int DT, int MODE, int ODT>
 __global__ __launch_bounds__(256) void joint_merge_kernel(JMergeParams p) {
-  __shared__ float sW[JMAX_SPLITS];
-  __shared__ float sA[JRMAX];
-  __shared__ float sOut[2][JDH];
-  __shared__ float sRed[8];
-  const int hq = blockIdx.x, b = blockIdx.y;
+  __shared__ float sA[JMH][JRMAX];
+  __shared__ float sWt[JMH][JMAX_SPLITS];  // split weights 2^(m_s - M) / den per head
+  __shared__ float sOut[2][JMH][JDH];
+  const int chunks = (p.hpg + JMH - 1) / JMH;
+  const int hv = blockIdx.x / chunks, j0 = (blockIdx.x % chunks) * JMH;
+  const int b = blockIdx.y;
+  const int nh = min(JMH, p.hpg - j0);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const float* base = p.rec + ((long long)b * p.Hq + hq) * p.n_splits * JPREC;
-  // maximum over the splits
-  float M = -INFINITY;
-  for (int s = tid; s < p.n_splits; s += 256) M = fmaxf(M, base[(long long)s * JPREC]);
-  M = dkv_wave_max(M);
-  if (lane == 0) sRed[wave] = M;
-  __syncthreads();
-  M = fmaxf(fmaxf(sRed[0], sRed[1]), fmaxf(sRed[2], sRed[3]));
-  __syncthreads();
-  float L = 0.f;
-  for (int s = tid; s < p.n_splits; s += 256) {
-    const float w = __builtin_amdgcn_exp2f(base[(long long)s * JPREC] - M);
-    sW[s] = w;
-    L += w * base[(long long)s * JPREC + 1];
+  // per head: maximum and denominator over the splits (one wave per head, heads in turn)
+  for (int j = wave; j < nh; j += 4) {
+    const int hq = hv * p.hpg + j0 + j;
+    const float* base = p.rec + ((long long)b * p.Hq + hq) * p.n_splits * JPREC;
+    float M = -INFINITY;
+    for (int s = lane; s < p.n_splits; s += 64) M = fmaxf(M, base[(long long)s * JPREC]);
+    M = dkv_wave_max(M);
+    float L = 0.f;
+    for (int s = lane; s < p.n_splits; s += 64)
+      L += __builtin_amdgcn_exp2f(base[(long long)s * JPREC] - M) * base[(long long)s * JPREC + 1];
+    L = dkv_wave_sum(L);
+    const float den = MODE == 0 ? fmaxf(L, 1e-6f) : L;
+    for (int s = lane; s < p.n_splits; s += 64)
+      sWt[j][s] = __builtin_amdgcn_exp2f(base[(long long)s * JPREC] - M) / den;
   }
-  L = dkv_wave_sum(L);
-  if (lane == 0) sRed[4 + wave] = L;
   __syncthreads();
-  L = sRed[4] + sRed[5] + sRed[6] + sRed[7];
-  const float den = MODE == 0 ? fmaxf(L, 1e-6f) : L;
-  for (int r = tid; r < p.R; r += 256) {
+  // merged, normalised coefficients a[j][r]
+  for (int idx = tid; idx < nh * p.R; idx += 256) {
+    const int j = idx / p.R, r = idx % p.R;
+    const int hq = hv * p.hpg + j0 + j;
+    const float* base = p.rec + ((long long)b * p.Hq + hq) * p.n_splits * JPREC + 2 + r;
+    // eight record loads in flight at a time (splits past the last read the last one, weight 0)
     float a = 0.f;
-    for (int s = 0; s < p.n_splits; ++s) a += sW[s] * base[(long long)s * JPREC + 2 + r];
-    sA[r] = a / den;
+    for (int s0 = 0; s0 < p.n_splits; s0 += 8) {
+      float x[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) x[u] = base[(long long)min(s0 + u, p.n_splits - 1) * JPREC];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (s0 + u < p.n_splits) a += sWt[j][s0 + u] * x[u];
+    }
+    sA[j][r] = a;
   }
   __syncthreads();
-  // out[d] = sum_r a[r] VB[r][d]: two halves of the rank range, then added
+  // out[j][d] = sum_r a[j][r] VB[r][d]: each basis value is loaded once for the nh heads; two
+  // halves of the rank range, four independent loads in flight per thread
   const int d = tid & 127, half = tid >> 7;
-  const uint16_t* vb = p.vb + (long long)(hq / p.hpg) * p.vb_sh + d;
-  float o = 0.f;
-  for (int r = half; r < p.R; r += 2) o = fmaf(sA[r], dkv_elt_to_f32<DT>(vb[(long long)r * p.vb_sr]), o);
-  sOut[half][d] = o;
+  const uint16_t* vb = p.vb + (long long)hv * p.vb_sh + d;
+  float o[JMH];
+#pragma unroll
+  for (int j = 0; j < JMH; ++j) o[j] = 0.f;
+  int r = half;
+  for (; r + 30 < p.R; r += 32) {
+    float v[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) v[k] = dkv_elt_to_f32<DT>(vb[(long long)(r + 2 * k) * p.vb_sr]);
+#pragma unroll
+    for (int k = 0; k < 16; ++k)
+#pragma unroll
+      for (int j = 0; j < JMH; ++j)
+        if (j < nh) o[j] = fmaf(sA[j][r + 2 * k], v[k], o[j]);
+  }
+  for (; r < p.R; r += 2) {
+    const float v = dkv_elt_to_f32<DT>(vb[(long long)r * p.vb_sr]);
+#pragma unroll
+    for (int j = 0; j < JMH; ++j)
+      if (j < nh) o[j] = fmaf(sA[j][r], v, o[j]);
+  }
+#pragma unroll
+  for (int j = 0; j < JMH; ++j) sOut[half][j][d] = o[j];
   __syncthreads();
   if (half == 0)
-    dkv_store_f32<ODT>(p.out, (long long)b * p.out_sb + (long long)hq * p.out_sh + d,
-                       sOut[0][d] + sOut[1][d]);
+    for (int j = 0; j < nh; ++j) {
+      const int hq = hv * p.hpg + j0 + j;
+      dkv_store_f32<ODT>(p.out, (long long)b * p.out_sb + (long long)hq * p.out_sh + d,
+                         sOut[0][j][d] + sOut[1][j][d]);
+    }
 }
 
 int joint_av_split_len(int B, int Hq, int S) {
@@ -644,8 +754,9 @@ extern "C" int dkv_joint_av(void* stream, int mode, int scores_dtype, int dtype,
   m.Hq = Hq;
   m.R = R;
   m.n_splits = ns;
-  m.hpg = Hq / n_basis;
-  const dim3 mgrid((unsigned)Hq, (unsigned)B);
+  const int hpg = Hq / n_basis;
+  m.hpg = hpg;
+  const dim3 mgrid((unsigned)(n_basis * ((hpg + JMH - 1) / JMH)), (unsigned)B);
 #define DKV_JM_LAUNCH(DT_, MODE_, ODT_) \
   hipLaunchKernelGGL((joint_merge_kernel<DT_, MODE_, ODT_>), mgrid, dim3(256), 0, st, m)
   if (dtype == DKV_BF16) {

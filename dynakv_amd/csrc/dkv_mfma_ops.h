@@ -64,19 +64,24 @@ __device__ __forceinline__ dkv_u32x4 dkv_gather8_b16(__amdgpu_buffer_rsrc_t r, i
                    v[6] | (v[7] << 16)};
 }
 
-// The first min(cnt, 8) 16-bit elements at element offset e of a buffer resource covering `end`
-// elements, the rest zero; cnt <= 0 loads nothing (out-of-range offset, no memory traffic).
-__device__ __forceinline__ dkv_u32x4 dkv_load8_prefix(__amdgpu_buffer_rsrc_t r, uint32_t end, int e,
-                                                      int cnt) {
+// 16 bytes at element offset e of a buffer resource, or zeros (no memory traffic) when cnt <= 0;
+// the elements past cnt are not cleared here (dkv_mask8 does that where the value is used, so
+// the load need not complete before the next ones are issued).
+__device__ __forceinline__ dkv_u32x4 dkv_load8_raw(__amdgpu_buffer_rsrc_t r, int e, int cnt) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, cnt > 0 ? e * 2 : DKV_OOB, 0, 0);
+}
+// dkv_load8_raw for a resource whose last windows may cross its end (`end` elements): such a
+// window is gathered element by element (a vector access that crosses the end reads as zero).
+__device__ __forceinline__ dkv_u32x4 dkv_load8_safe(__amdgpu_buffer_rsrc_t r, uint32_t end, int e,
+                                                    int cnt) {
   if (cnt > 0 && (uint32_t)(e + 8) > end) return dkv_gather8_b16(r, e, min(cnt, 8));
-  dkv_u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, cnt > 0 ? e * 2 : DKV_OOB, 0, 0);
-  if (cnt < 8) {
-    v.x &= dkv_prefix_mask_word(cnt, 0);
-    v.y &= dkv_prefix_mask_word(cnt, 1);
-    v.z &= dkv_prefix_mask_word(cnt, 2);
-    v.w &= dkv_prefix_mask_word(cnt, 3);
-  }
-  return v;
+  return dkv_load8_raw(r, e, cnt);
+}
+// v with the elements from index cnt on cleared (cnt <= 0: all, cnt >= 8: none).
+__device__ __forceinline__ dkv_u32x4 dkv_mask8(dkv_u32x4 v, int cnt) {
+  const int k = min(max(cnt, 0), 8);
+  return dkv_u32x4{v.x & dkv_prefix_mask_word(k, 0), v.y & dkv_prefix_mask_word(k, 1),
+                   v.z & dkv_prefix_mask_word(k, 2), v.w & dkv_prefix_mask_word(k, 3)};
 }
 
 // Float maxima without the NaN-quieting the compiler adds around fmaxf (-inf is an ordinary

@@ -143,6 +143,7 @@ def joint_av(scores: torch.Tensor, v_up: torch.Tensor, v_flat: torch.Tensor,
     R = v_up.shape[1]
     if v_up.stride(2) != 1:
         v_up = v_up.contiguous()
+    v_up = _distinct(v_up, Hq)  # the merge projects all query heads of a basis together
     ws = _workspace(scores.device, st, int(lib.dkv_joint_av_workspace_floats(B, Hq, S, R)))
     out = torch.empty((B, Hq, 128), dtype=out_dtype, device=scores.device)
     rc = lib.dkv_joint_av(
