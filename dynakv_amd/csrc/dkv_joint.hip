@@ -23,9 +23,11 @@
 //   log2 domain (every wave computes the same values), P as bf16 hi + lo (fp16 for fp16 caches),
 //   the wave's V coefficients of the tile staged in LDS and read transposed (ds_read_b64_tr_b16)
 //   as the B operand of P.X^V. Each split writes (m, l, acc[R]) per head.
-// joint_merge_kernel -- workgroup = (V basis and up to 8 of its query heads, batch row b): LSE
-//   merge of the split records, the route's denominator, the projection through the V basis
-//   (each basis value loaded once for the group's heads), the output rounding.
+// joint_merge_kernel -- workgroup = (rank block of 128, V basis and up to 8 of its query heads,
+//   batch row b): LSE weights of the split records with the route's denominator, the block's
+//   merged coefficients, their projection through the block's basis rows (each basis value
+//   loaded once for the group's heads); joint_project_sum_kernel adds the blocks' partial
+//   projections and rounds the output.
 #include <type_traits>
 
 #include "dkv_common.h"
@@ -40,12 +42,16 @@ constexpr int JCB = 4;                   // 16-token column blocks per wave (sco
 constexpr int JTOK = JWAVES * JCB * 16;  // tokens per scores workgroup
 constexpr int JCH = 32;                  // ranks per basis chunk
 constexpr int JRMAX = 1024;
-constexpr int JPREC = 2 + JRMAX;         // split record: m (log2 units), l, acc[R]
+constexpr int JPREC = 4 + JRMAX;         // split record: m (log2 units), l, 2 unused, acc[R]
+constexpr int JRB = 128;                 // ranks per merge workgroup
 constexpr int JROPE_FIXED = 17;          // rows of the RoPE table before the per-tile rows
 constexpr int JFLAT_CAP = 0x3ffffff0;    // elements one buffer resource covers
 constexpr int JMAX_SPLITS = 1024;  // token splits of the V pass
 constexpr float JLOG2E = 1.4426950408889634f;
 constexpr float JRESCALE = 11.5f;        // log2 units: rescale when the running max grows more
+
+// piece swizzle of the basis chunk buffers (a function of d mod 16)
+__device__ __forceinline__ int jswz(int d) { return (d ^ (d >> 2)) & 3; }
 
 __device__ __forceinline__ dkv_f32x4 mfma_bf16x32(const dkv_u32x4& a, const dkv_u32x4& b,
                                                   dkv_f32x4 c) {
@@ -72,8 +78,9 @@ struct JScoresParams {
 
 template <int DT, int MODE, int ODT>
 __global__ __launch_bounds__(JTHREADS, 1) void joint_scores_kernel(JScoresParams p) {
-  // basis chunk buffers: piece (dim d, ranks 8k..8k+7) at index 4d + (k ^ ((d >> 2) & 3)), so the
-  // 16 rows one k-group reads land in 16 different bank groups
+  // basis chunk buffers: piece (dim d, ranks 8k..8k+7) at index 4d + (k ^ jswz(d)): the 16 rows
+  // one k-group reads land in 16 different 16-byte bank groups of a 256-byte span, and any 8
+  // aligned ones in 8 different groups of a 128-byte span
   __shared__ __attribute__((aligned(16))) dkv_u32x4 sB[2][JDH * JCH / 8];
   // R(n) of every lane's token slot: [2*pp + k][lane] holds (cos, sin) of frequencies
   // 16pp + 4g + 2k and + 1
@@ -129,15 +136,23 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_scores_kernel(JScoresParams
       (uint32_t)min((long long)(p.B - b) * p.flat_ld, (long long)JFLAT_CAP);
   const __amdgpu_buffer_rsrc_t rs = dkv_make_rsrc(p.flat + (long long)b * p.flat_ld, end * 2u);
   // this thread's basis piece of every chunk: dim bd, ranks 8*bk .. +8 of the chunk
-  const int bd = tid >> 2, bk = (tid & 3) ^ ((bd >> 2) & 3);
+  const int bd = tid >> 2, bk = (tid & 3) ^ jswz(bd);
   const uint16_t* bsrc = p.bt + (long long)h * p.bt_sh + (long long)bd * p.bt_sd + 8 * bk;
 
   int tlen[JCB], toff[JCB];
+  // bit c of pmask[cb]: some lane of column block cb has its count ending inside its 8 ranks of
+  // chunk c. Only those chunks need the loaded pieces masked: past a count, loads read zeros.
+  uint32_t pmask[JCB];
 #pragma unroll
   for (int cb = 0; cb < JCB; ++cb) {
     const int tl = 64 * wave + 16 * cb + n;
     tlen[cb] = sLen[tl];
     toff[cb] = sOff[tl];
+    const int e = tlen[cb] - 8 * g;  // 1..7 past a multiple of 32: partial in chunk e / 32
+    uint32_t bit = (e > 0 && (e & 31) != 0 && (e & 31) < 8) ? (1u << (e >> 5)) : 0u;
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) bit |= (uint32_t)__shfl_xor((int)bit, m, 64);
+    pmask[cb] = __builtin_amdgcn_readfirstlane(bit);
   }
   dkv_f32x4 acc[8][JCB];
 #pragma unroll
@@ -145,10 +160,9 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_scores_kernel(JScoresParams
 #pragma unroll
     for (int cb = 0; cb < JCB; ++cb) acc[i][cb] = dkv_f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // The rank loop. The coefficient loads are not waited for where they are issued (their masks
-  // are applied where the values are used), so each wave keeps two chunks of loads in flight.
-  // Only the last batch row can hold a window that crosses the end of the buffer; its
-  // workgroups run the loop with element-wise gathers for such windows.
+  // The rank loop. The coefficient loads are not waited for where they are issued, so each wave
+  // keeps two chunks of loads in flight. Only the last batch row can hold a window that crosses
+  // the end of the buffer; its workgroups run the loop with element-wise gathers for such windows.
   auto rank_loop = [&](auto safe_tag) {
     constexpr bool SAFE = decltype(safe_tag)::value;
     auto load_x = [&](int c, dkv_u32x4(&x)[JCB]) {
@@ -173,26 +187,26 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_scores_kernel(JScoresParams
     }
     __syncthreads();
     // Chunk c: its basis sits in sB[c & 1] (written before the previous barrier); the basis of
-    // chunk c+1 (loaded one chunk ago, before that chunk's coefficients) goes to the other
-    // buffer, whose readers finished before that barrier; the coefficients run two chunks ahead
-    // and are reloaded into the registers they were used from (x: xa for even c, xb for odd c),
-    // so no loaded value is ever copied and the waits cover only the values being used. Loads
-    // past the last chunk clamp the basis index and have coefficient counts <= 0 (no traffic).
+    // chunk c+1 (loaded one chunk ago) goes to the other buffer, whose readers finished before
+    // that barrier. The coefficients of chunk c+2 are loaded, right after chunk c's products are
+    // issued, into the registers chunk c used (x: xa for even c, xb for odd c), so no loaded value
+    // is ever copied and the waits cover only the values being used. Loads past the last chunk
+    // clamp the basis index and have coefficient counts <= 0 (no traffic).
     auto step = [&](int c, dkv_u32x4(&x)[JCB]) {
-      dkv_u32x4 xm[JCB];
 #pragma unroll
-      for (int cb = 0; cb < JCB; ++cb) xm[cb] = dkv_mask8(x[cb], tlen[cb] - (JCH * c + 8 * g));
+      for (int cb = 0; cb < JCB; ++cb)
+        if ((pmask[cb] >> c) & 1u) x[cb] = dkv_mask8(x[cb], tlen[cb] - (JCH * c + 8 * g));
       sB[(c + 1) & 1][tid] = bnext;
       bnext = *(const dkv_u32x4*)(bsrc + JCH * min(c + 2, nch - 1));
-      load_x(c + 2, x);
       const dkv_u32x4* buf = sB[c & 1];
 #pragma unroll
       for (int blk = 0; blk < 8; ++blk) {
         const int d = 16 * blk + n;
-        const dkv_u32x4 a = buf[4 * d + (g ^ ((d >> 2) & 3))];
+        const dkv_u32x4 a = buf[4 * d + (g ^ jswz(d))];
 #pragma unroll
-        for (int cb = 0; cb < JCB; ++cb) acc[blk][cb] = dkv_mfma32<DT>(a, xm[cb], acc[blk][cb]);
+        for (int cb = 0; cb < JCB; ++cb) acc[blk][cb] = dkv_mfma32<DT>(a, x[cb], acc[blk][cb]);
       }
+      load_x(c + 2, x);
       __syncthreads();
     };
     // whole pairs in the loop (every path back to its head has issued both steps' loads)
@@ -490,7 +504,7 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_av_kernel(JAvParams p) {
   for (int u = 0; u < 4; ++u) {
     const int hs = 16 * hset + 4 * g + u;
     if (hs < p.Hq) {
-      float* rec = p.rec + (((long long)b * p.Hq + hs) * p.n_splits + split) * JPREC + 2;
+      float* rec = p.rec + (((long long)b * p.Hq + hs) * p.n_splits + split) * JPREC + 4;
 #pragma unroll
       for (int blk = 0; blk < 8; ++blk) {
         const int r = r0 + 16 * blk + n;
@@ -502,93 +516,153 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_av_kernel(JAvParams p) {
 
 struct JMergeParams {
   const float* rec;
+  float* part;  // [B][Hq][R/128 rank blocks][Dh] partial projections
   const uint16_t* vb;  // V basis [n_basis][R][Dh] with strides (vb_sh, vb_sr)
   long long vb_sh, vb_sr;
   void* out;
   long long out_sb, out_sh;
-  int Hq, R, n_splits, hpg;
+  int Hq, R, n_splits, hpg, n_rb;
 };
 
 constexpr int JMH = 8;  // query heads merged and projected together (they share a V basis)
 
-// workgroup = (V basis head hv and a chunk of up to 8 of its query heads, batch row b)
-template <int DT, int MODE, int ODT>
+// workgroup = (rank block of 128, V basis hv and up to 8 of its query heads, batch row b): the
+// split weights, the block's merged coefficients, their projection through the block's basis rows.
+// Every load that does not depend on another is issued up front, in the order the values are
+// needed (split maxima and sums, the first 16 splits' coefficients, the basis rows), so the
+// workgroup waits about one memory latency.
+template <int DT, int MODE>
 __global__ __launch_bounds__(256) void joint_merge_kernel(JMergeParams p) {
-  __shared__ float sA[JMH][JRMAX];
-  __shared__ float sWt[JMH][JMAX_SPLITS];  // split weights 2^(m_s - M) / den per head
-  __shared__ float sOut[2][JMH][JDH];
+  extern __shared__ float sWt[];  // [JMH][n_splits]: split weights 2^(m_s - M) / den per head
+  __shared__ __attribute__((aligned(16))) float sA[JMH][JRB];
+  __shared__ float sOut[4][JMH][JDH];
+  const int rb = blockIdx.x;
   const int chunks = (p.hpg + JMH - 1) / JMH;
-  const int hv = blockIdx.x / chunks, j0 = (blockIdx.x % chunks) * JMH;
-  const int b = blockIdx.y;
+  const int hv = blockIdx.y / chunks, j0 = (blockIdx.y % chunks) * JMH;
+  const int b = blockIdx.z;
   const int nh = min(JMH, p.hpg - j0);
+  const int nr = min(JRB, p.R - JRB * rb);  // ranks of this block
+  const int ns = p.n_splits;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  // per head: maximum and denominator over the splits (one wave per head, heads in turn)
-  for (int j = wave; j < nh; j += 4) {
-    const int hq = hv * p.hpg + j0 + j;
-    const float* base = p.rec + ((long long)b * p.Hq + hq) * p.n_splits * JPREC;
-    float M = -INFINITY;
-    for (int s = lane; s < p.n_splits; s += 64) M = fmaxf(M, base[(long long)s * JPREC]);
-    M = dkv_wave_max(M);
-    float L = 0.f;
-    for (int s = lane; s < p.n_splits; s += 64)
-      L += __builtin_amdgcn_exp2f(base[(long long)s * JPREC] - M) * base[(long long)s * JPREC + 1];
-    L = dkv_wave_sum(L);
-    const float den = MODE == 0 ? fmaxf(L, 1e-6f) : L;
-    for (int s = lane; s < p.n_splits; s += 64)
-      sWt[j][s] = __builtin_amdgcn_exp2f(base[(long long)s * JPREC] - M) / den;
+  const long long head0 = (long long)b * p.Hq + hv * p.hpg + j0;
+
+  // (1) m, l of split `lane` for heads wave and wave + 4 (up to 64 splits in registers)
+  float mv[2], lv[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int j = wave + 4 * i;
+    const float* base =
+        p.rec + (head0 + min(j, nh - 1)) * ns * JPREC + (long long)min(lane, ns - 1) * JPREC;
+    mv[i] = base[0];
+    lv[i] = base[1];
   }
-  __syncthreads();
-  // merged, normalised coefficients a[j][r]
-  for (int idx = tid; idx < nh * p.R; idx += 256) {
-    const int j = idx / p.R, r = idx % p.R;
-    const int hq = hv * p.hpg + j0 + j;
-    const float* base = p.rec + ((long long)b * p.Hq + hq) * p.n_splits * JPREC + 2 + r;
-    // eight record loads in flight at a time (splits past the last read the last one, weight 0)
-    float a = 0.f;
-    for (int s0 = 0; s0 < p.n_splits; s0 += 8) {
-      float x[8];
+  // (2) coefficients of the first 16 splits: thread = (head jc, ranks 4q .. 4q+3 of the block)
+  const int jc = tid >> 5, q = tid & 31;
+  const float* cbase =
+      p.rec + (head0 + min(jc, nh - 1)) * ns * JPREC + 4 + JRB * rb + 4 * min(q, (nr - 1) / 4);
+  dkv_f32x4 x[16];
+  auto load_coef = [&](int s0) {
 #pragma unroll
-      for (int u = 0; u < 8; ++u) x[u] = base[(long long)min(s0 + u, p.n_splits - 1) * JPREC];
+    for (int u = 0; u < 16; ++u)
+      x[u] = *(const dkv_f32x4*)(cbase + (long long)min(s0 + u, ns - 1) * JPREC);
+  };
+  load_coef(0);
+  // (3) basis rows: thread = (dims 2dp, 2dp+1, ranks 32rq .. 32rq+31 of the block)
+  const int dp = tid & 63, rq = tid >> 6;
+  uint32_t vbv[32];
+  {
+    const uint16_t* vb = p.vb + (long long)hv * p.vb_sh + (long long)JRB * rb * p.vb_sr + 2 * dp;
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
-        if (s0 + u < p.n_splits) a += sWt[j][s0 + u] * x[u];
+    for (int k = 0; k < 32; ++k)
+      vbv[k] = *(const uint32_t*)(vb + (long long)min(32 * rq + k, nr - 1) * p.vb_sr);
+  }
+
+  // weights: one wave per head
+  auto weights = [&](int j, float m_in, float l_in) {
+    const float* base = p.rec + (head0 + j) * ns * JPREC;
+    float M, L;
+    if (ns <= 64) {
+      const float m = lane < ns ? m_in : -INFINITY;
+      M = dkv_wave_max(m);
+      L = dkv_wave_sum(lane < ns ? __builtin_amdgcn_exp2f(m - M) * l_in : 0.f);
+    } else {
+      M = -INFINITY;
+      for (int s = lane; s < ns; s += 64) M = fmaxf(M, base[(long long)s * JPREC]);
+      M = dkv_wave_max(M);
+      L = 0.f;
+      for (int s = lane; s < ns; s += 64)
+        L += __builtin_amdgcn_exp2f(base[(long long)s * JPREC] - M) * base[(long long)s * JPREC + 1];
+      L = dkv_wave_sum(L);
     }
-    sA[j][r] = a;
+    const float den = MODE == 0 ? fmaxf(L, 1e-6f) : L;
+    if (ns <= 64) {
+      if (lane < ns) sWt[j * ns + lane] = __builtin_amdgcn_exp2f(m_in - M) / den;
+    } else {
+      for (int s = lane; s < ns; s += 64)
+        sWt[j * ns + s] = __builtin_amdgcn_exp2f(base[(long long)s * JPREC] - M) / den;
+    }
+  };
+  if (wave < nh) weights(wave, mv[0], lv[0]);
+  if (wave + 4 < nh) weights(wave + 4, mv[1], lv[1]);
+  __syncthreads();
+
+  // merged, normalised coefficients of the block
+  if (jc < nh) {
+    dkv_f32x4 a = {0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0;;) {
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const float w = s0 + u < ns ? sWt[jc * ns + s0 + u] : 0.f;
+        a += w * x[u];
+      }
+      s0 += 16;
+      if (s0 >= ns) break;
+      load_coef(s0);
+    }
+    // ranks past the block's end (never written by the V pass) hold zeros
+#pragma unroll
+    for (int e = 0; e < 4; ++e) a[e] = 4 * q + e < nr ? a[e] : 0.f;
+    *(dkv_f32x4*)&sA[jc][4 * q] = a;
   }
   __syncthreads();
-  // out[j][d] = sum_r a[j][r] VB[r][d]: each basis value is loaded once for the nh heads; two
-  // halves of the rank range, four independent loads in flight per thread
-  const int d = tid & 127, half = tid >> 7;
-  const uint16_t* vb = p.vb + (long long)hv * p.vb_sh + d;
-  float o[JMH];
+
+  // partial[j][d] = sum over the block's ranks of a[j][r] VB[r][d], per quarter of the block
+  float o0[JMH], o1[JMH];
 #pragma unroll
-  for (int j = 0; j < JMH; ++j) o[j] = 0.f;
-  int r = half;
-  for (; r + 30 < p.R; r += 32) {
-    float v[16];
+  for (int j = 0; j < JMH; ++j) o0[j] = o1[j] = 0.f;
 #pragma unroll
-    for (int k = 0; k < 16; ++k) v[k] = dkv_elt_to_f32<DT>(vb[(long long)(r + 2 * k) * p.vb_sr]);
-#pragma unroll
-    for (int k = 0; k < 16; ++k)
-#pragma unroll
-      for (int j = 0; j < JMH; ++j)
-        if (j < nh) o[j] = fmaf(sA[j][r + 2 * k], v[k], o[j]);
-  }
-  for (; r < p.R; r += 2) {
-    const float v = dkv_elt_to_f32<DT>(vb[(long long)r * p.vb_sr]);
+  for (int k = 0; k < 32; ++k) {
+    const float v0 = dkv_elt_to_f32<DT>(vbv[k] & 0xffffu), v1 = dkv_elt_to_f32<DT>(vbv[k] >> 16);
 #pragma unroll
     for (int j = 0; j < JMH; ++j)
-      if (j < nh) o[j] = fmaf(sA[j][r], v, o[j]);
+      if (j < nh) {
+        const float a = sA[j][32 * rq + k];  // 0 past the block's end
+        o0[j] = fmaf(a, v0, o0[j]);
+        o1[j] = fmaf(a, v1, o1[j]);
+      }
   }
 #pragma unroll
-  for (int j = 0; j < JMH; ++j) sOut[half][j][d] = o[j];
+  for (int j = 0; j < JMH; ++j) {
+    sOut[rq][j][2 * dp] = o0[j];
+    sOut[rq][j][2 * dp + 1] = o1[j];
+  }
   __syncthreads();
-  if (half == 0)
-    for (int j = 0; j < nh; ++j) {
-      const int hq = hv * p.hpg + j0 + j;
-      dkv_store_f32<ODT>(p.out, (long long)b * p.out_sb + (long long)hq * p.out_sh + d,
-                         sOut[0][j][d] + sOut[1][j][d]);
-    }
+  for (int i = tid; i < nh * JDH; i += 256) {
+    const int j = i / JDH, d = i % JDH;
+    p.part[((head0 + j) * p.n_rb + rb) * JDH + d] =
+        (sOut[0][j][d] + sOut[1][j][d]) + (sOut[2][j][d] + sOut[3][j][d]);
+  }
+}
+
+// workgroup = (query head, batch row b), thread = output dim: the sum of the rank blocks' partial
+// projections, the output rounding
+template <int ODT>
+__global__ __launch_bounds__(JDH) void joint_project_sum_kernel(JMergeParams p) {
+  const int hq = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+  const float* part = p.part + (((long long)b * p.Hq + hq) * p.n_rb) * JDH + d;
+  float o = 0.f;
+  for (int k = 0; k < p.n_rb; ++k) o += part[(long long)k * JDH];
+  dkv_store_f32<ODT>(p.out, (long long)b * p.out_sb + (long long)hq * p.out_sh + d, o);
 }
 
 int joint_av_split_len(int B, int Hq, int S) {
@@ -675,11 +749,11 @@ extern "C" int dkv_joint_scores(void* stream, int mode, int dtype, int out_dtype
 }
 
 extern "C" long long dkv_joint_av_workspace_floats(int B, int Hq, int S, int R) {
-  (void)R;
-  if (B <= 0 || Hq <= 0 || S <= 0) return 0;
+  if (B <= 0 || Hq <= 0 || S <= 0 || R <= 0 || R > JRMAX) return 0;
   const int sl = joint_av_split_len(B, Hq, S);
   const long long ns = (S + sl - 1) / sl;
-  return (long long)B * Hq * ns * JPREC;
+  const long long n_rb = (R + JRB - 1) / JRB;
+  return (long long)B * Hq * (ns * JPREC + n_rb * JDH);
 }
 
 extern "C" int dkv_joint_av(void* stream, int mode, int scores_dtype, int dtype, int out_dtype,
@@ -705,7 +779,12 @@ extern "C" int dkv_joint_av(void* stream, int mode, int scores_dtype, int dtype,
   if (B > 65535 || Hq > 65535) return DKV_E_UNSUPPORTED;
   const int sl = joint_av_split_len(B, Hq, S);
   const int ns = (S + sl - 1) / sl;
-  if (workspace_floats < (long long)B * Hq * ns * JPREC) return DKV_E_WORKSPACE;
+  const int n_rb = (R + JRB - 1) / JRB;
+  const long long rec_floats = (long long)B * Hq * ns * JPREC;
+  if (workspace_floats < rec_floats + (long long)B * Hq * n_rb * JDH) return DKV_E_WORKSPACE;
+  if (!aligned16(workspace)) return DKV_E_ARG;
+  // the merge reads the V basis two dims (4 bytes) at a time
+  if (((uintptr_t)basis & 3u) || (basis_sr & 1) || (basis_sh & 1)) return DKV_E_UNSUPPORTED;
   hipStream_t st = (hipStream_t)stream;
 
   JAvParams a;
@@ -745,6 +824,7 @@ extern "C" int dkv_joint_av(void* stream, int mode, int scores_dtype, int dtype,
 
   JMergeParams m;
   m.rec = workspace;
+  m.part = workspace + rec_floats;
   m.vb = (const uint16_t*)basis;
   m.vb_sh = basis_sh;
   m.vb_sr = basis_sr;
@@ -756,31 +836,28 @@ extern "C" int dkv_joint_av(void* stream, int mode, int scores_dtype, int dtype,
   m.n_splits = ns;
   const int hpg = Hq / n_basis;
   m.hpg = hpg;
-  const dim3 mgrid((unsigned)(n_basis * ((hpg + JMH - 1) / JMH)), (unsigned)B);
-#define DKV_JM_LAUNCH(DT_, MODE_, ODT_) \
-  hipLaunchKernelGGL((joint_merge_kernel<DT_, MODE_, ODT_>), mgrid, dim3(256), 0, st, m)
+  m.n_rb = n_rb;
+  const dim3 mgrid((unsigned)n_rb, (unsigned)(n_basis * ((hpg + JMH - 1) / JMH)), (unsigned)B);
+  const size_t wt_bytes = sizeof(float) * JMH * (size_t)ns;
   if (dtype == DKV_BF16) {
-    if (mode == 0) {
-      if (out_dtype == DKV_BF16) DKV_JM_LAUNCH(DKV_BF16, 0, DKV_BF16);
-      else if (out_dtype == DKV_F16) DKV_JM_LAUNCH(DKV_BF16, 0, DKV_F16);
-      else DKV_JM_LAUNCH(DKV_BF16, 0, DKV_F32);
-    } else {
-      if (out_dtype == DKV_BF16) DKV_JM_LAUNCH(DKV_BF16, 1, DKV_BF16);
-      else if (out_dtype == DKV_F16) DKV_JM_LAUNCH(DKV_BF16, 1, DKV_F16);
-      else DKV_JM_LAUNCH(DKV_BF16, 1, DKV_F32);
-    }
+    if (mode == 0)
+      hipLaunchKernelGGL((joint_merge_kernel<DKV_BF16, 0>), mgrid, dim3(256), wt_bytes, st, m);
+    else
+      hipLaunchKernelGGL((joint_merge_kernel<DKV_BF16, 1>), mgrid, dim3(256), wt_bytes, st, m);
   } else {
-    if (mode == 0) {
-      if (out_dtype == DKV_BF16) DKV_JM_LAUNCH(DKV_F16, 0, DKV_BF16);
-      else if (out_dtype == DKV_F16) DKV_JM_LAUNCH(DKV_F16, 0, DKV_F16);
-      else DKV_JM_LAUNCH(DKV_F16, 0, DKV_F32);
-    } else {
-      if (out_dtype == DKV_BF16) DKV_JM_LAUNCH(DKV_F16, 1, DKV_BF16);
-      else if (out_dtype == DKV_F16) DKV_JM_LAUNCH(DKV_F16, 1, DKV_F16);
-      else DKV_JM_LAUNCH(DKV_F16, 1, DKV_F32);
-    }
+    if (mode == 0)
+      hipLaunchKernelGGL((joint_merge_kernel<DKV_F16, 0>), mgrid, dim3(256), wt_bytes, st, m);
+    else
+      hipLaunchKernelGGL((joint_merge_kernel<DKV_F16, 1>), mgrid, dim3(256), wt_bytes, st, m);
   }
-#undef DKV_JM_LAUNCH
+  DKV_HIP_CHECK_LAUNCH();
+  const dim3 pgrid((unsigned)Hq, (unsigned)B);
+  if (out_dtype == DKV_BF16)
+    hipLaunchKernelGGL((joint_project_sum_kernel<DKV_BF16>), pgrid, dim3(JDH), 0, st, m);
+  else if (out_dtype == DKV_F16)
+    hipLaunchKernelGGL((joint_project_sum_kernel<DKV_F16>), pgrid, dim3(JDH), 0, st, m);
+  else
+    hipLaunchKernelGGL((joint_project_sum_kernel<DKV_F32>), pgrid, dim3(JDH), 0, st, m);
   DKV_HIP_CHECK_LAUNCH();
   return DKV_OK;
 }

@@ -103,7 +103,8 @@ def av_eligible(v_up: torch.Tensor, v_flat: torch.Tensor, n_heads: int, S: int) 
     dt = v_up.dtype
     return (dt in (torch.bfloat16, torch.float16) and v_flat.dtype == dt and v_up.dim() == 3
             and v_up.shape[2] == 128 and v_up.shape[1] <= 1024 and v_up.shape[0] > 0
-            and n_heads % v_up.shape[0] == 0 and _flat_ok(v_flat) and S > 0)
+            and n_heads % v_up.shape[0] == 0 and _flat_ok(v_flat) and S > 0
+            and v_up.data_ptr() % 4 == 0 and v_up.stride(0) % 2 == 0 and v_up.stride(1) % 2 == 0)
 
 
 def joint_scores(q3: torch.Tensor, k_up: torch.Tensor, k_flat: torch.Tensor,

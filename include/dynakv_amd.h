@@ -176,15 +176,18 @@ int dkv_joint_scores(void* stream, int mode, int dtype, int out_dtype,
                      void* out, long long out_sb, long long out_sh, long long out_ss,
                      int B, int Hq, int S, int R, int Dh);
 
-/* fp32 workspace dkv_joint_av needs for these sizes (split records). */
+/* fp32 workspace dkv_joint_av needs for these sizes (split records and per rank block partial
+ * projections); 0 for sizes dkv_joint_av does not take. */
 long long dkv_joint_av_workspace_floats(int B, int Hq, int S, int R);
 
 /*
  * dkv_av on MFMA (avx / _avx_proj_fwd, reference two_stage.py:207-324; mode 1: the fused route's V
  * pass): the same inputs and outputs as dkv_av plus a caller workspace of
- * dkv_joint_av_workspace_floats(B, Hq, S, R) floats. Token splits write (m, l, acc[R]) records,
- * merged by LSE and projected through the V basis by a second launch. dtype (cache) DKV_BF16 or
- * DKV_F16, Dh == 128, R <= 1024; S == 0 returns DKV_E_UNSUPPORTED (dkv_av covers it).
+ * dkv_joint_av_workspace_floats(B, Hq, S, R) floats, 16-byte aligned. Token splits write (m, l,
+ * acc[R]) records; a second launch merges them by LSE per block of 128 ranks and projects each
+ * block through its rows of the V basis, a third adds the blocks. dtype (cache) DKV_BF16 or
+ * DKV_F16, Dh == 128, R <= 1024, the basis 4-byte aligned with even strides; S == 0 returns
+ * DKV_E_UNSUPPORTED (dkv_av covers it).
  */
 int dkv_joint_av(void* stream, int mode, int scores_dtype, int dtype, int out_dtype,
                  const void* scores, long long sc_sb, long long sc_sh, long long sc_ss,

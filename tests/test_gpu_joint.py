@@ -121,8 +121,11 @@ def test_scores_match_vector_kernel(dev, dtype, B, S, R, n_basis, repeat):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("B,S,R,n_basis", [(2, 1000, 1024, 8), (1, 17, 1024, 32), (3, 1, 256, 4),
-                                           (2, 300, 1024, 8)])
+@pytest.mark.parametrize("B,S,R,n_basis", [
+    (2, 1000, 1024, 8), (1, 17, 1024, 32), (3, 1, 256, 4), (2, 300, 1024, 8),
+    (2, 50, 97, 2),      # one partial rank block (97 ranks), two chunks of 8 heads per basis
+    (1, 2048, 512, 8),   # 128 token splits: the merge's many-splits path
+])
 def test_av_matches_vector_kernel(dev, dtype, B, S, R, n_basis):
     print(f"[gpu] joint av {dtype} B={B} S={S} R={R} nb={n_basis}", flush=True)
     h = _case(B, S, R, n_basis, dtype=dtype, seed=7 * S + R, exact_end=True)
