@@ -115,17 +115,6 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_scores_kernel(JScoresParams
     const float* delt = p.rope + n * 128 + 2 * i0;
     sRn[k][lane] = dkv_f32x4{delt[0], delt[1], delt[2], delt[3]};
   }
-  // (q_i, q_{i+64}) of the group's heads for frequency i = lane, as 16-bit values
-  uint32_t qh[8];
-  {
-    const long long qo = (long long)b * p.q_sb + (long long)h * p.hpg * p.q_sh + lane;
-#pragma unroll
-    for (int hh = 0; hh < 8; ++hh) {
-      const long long o = qo + (hh < p.hpg ? hh : 0) * p.q_sh;
-      const uint32_t v = (uint32_t)p.q[o] | ((uint32_t)p.q[o + 64] << 16);
-      qh[hh] = hh < p.hpg ? v : 0u;
-    }
-  }
   __syncthreads();
   int maxlen = 0;
 #pragma unroll
@@ -176,46 +165,53 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_scores_kernel(JScoresParams
       }
     };
     dkv_u32x4 xa[JCB], xb[JCB];
-    dkv_u32x4 bnext = dkv_u32x4{0u, 0u, 0u, 0u};
+    dkv_u32x4 ba = dkv_u32x4{0u, 0u, 0u, 0u}, bb = ba;
 #pragma unroll
     for (int cb = 0; cb < JCB; ++cb) xa[cb] = xb[cb] = dkv_u32x4{0u, 0u, 0u, 0u};
+    auto load_b = [&](int c) { return *(const dkv_u32x4*)(bsrc + JCH * min(c, nch - 1)); };
     if (nch > 0) {
-      sB[0][tid] = *(const dkv_u32x4*)bsrc;
-      bnext = *(const dkv_u32x4*)(bsrc + JCH * min(1, nch - 1));
+      sB[0][tid] = load_b(0);
+      ba = load_b(1);
+      bb = load_b(2);
       load_x(0, xa);
       load_x(1, xb);
     }
     __syncthreads();
     // Chunk c: its basis sits in sB[c & 1] (written before the previous barrier); the basis of
-    // chunk c+1 (loaded one chunk ago) goes to the other buffer, whose readers finished before
-    // that barrier. The coefficients of chunk c+2 are loaded, right after chunk c's products are
-    // issued, into the registers chunk c used (x: xa for even c, xb for odd c), so no loaded value
-    // is ever copied and the waits cover only the values being used. Loads past the last chunk
+    // chunk c+1 (loaded two chunks ago) goes to the other buffer, whose readers finished before
+    // that barrier, and the basis of chunk c+3 is loaded into the registers it came from (b: ba
+    // for even c, bb for odd c). The coefficients of chunk c+2 are loaded, right after chunk c's
+    // products are issued, into the registers chunk c used (x: xa, xb in turn). No loaded value
+    // is ever copied, so the waits cover only the values being used. Loads past the last chunk
     // clamp the basis index and have coefficient counts <= 0 (no traffic).
-    auto step = [&](int c, dkv_u32x4(&x)[JCB]) {
+    auto step = [&](int c, dkv_u32x4(&x)[JCB], dkv_u32x4& bn) {
 #pragma unroll
       for (int cb = 0; cb < JCB; ++cb)
         if ((pmask[cb] >> c) & 1u) x[cb] = dkv_mask8(x[cb], tlen[cb] - (JCH * c + 8 * g));
-      sB[(c + 1) & 1][tid] = bnext;
-      bnext = *(const dkv_u32x4*)(bsrc + JCH * min(c + 2, nch - 1));
+      sB[(c + 1) & 1][tid] = bn;
+      bn = load_b(c + 3);
       const dkv_u32x4* buf = sB[c & 1];
+      dkv_u32x4 a[8];
 #pragma unroll
-      for (int blk = 0; blk < 8; ++blk) {
-        const int d = 16 * blk + n;
-        const dkv_u32x4 a = buf[4 * d + (g ^ jswz(d))];
+      for (int blk = 0; blk < 8; ++blk) a[blk] = buf[4 * (16 * blk + n) + (g ^ jswz(n))];
 #pragma unroll
-        for (int cb = 0; cb < JCB; ++cb) acc[blk][cb] = dkv_mfma32<DT>(a, x[cb], acc[blk][cb]);
-      }
+      for (int blk = 0; blk < 8; ++blk)
+#pragma unroll
+        for (int cb = 0; cb < JCB; ++cb) acc[blk][cb] = dkv_mfma32<DT>(a[blk], x[cb], acc[blk][cb]);
+      // the eight basis reads first, then the products (the compiler would otherwise read each
+      // operand just before its products and expose the LDS latency four times per chunk)
+      __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 8 * JCB, 0);
       load_x(c + 2, x);
       __syncthreads();
     };
     // whole pairs in the loop (every path back to its head has issued both steps' loads)
     int c = 0;
     for (; c + 1 < nch; c += 2) {
-      step(c, xa);
-      step(c + 1, xb);
+      step(c, xa, ba);
+      step(c + 1, xb, bb);
     }
-    if (c < nch) step(c, xa);
+    if (c < nch) step(c, xa, ba);
   };
   if (b == p.B - 1)
     rank_loop(std::integral_constant<bool, true>{});
@@ -223,6 +219,17 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_scores_kernel(JScoresParams
     rank_loop(std::integral_constant<bool, false>{});
 
   // ---- per 16-token tile: rotation, K' hi + lo, scores, masking, store ---------------------
+  // (q_i, q_{i+64}) of the group's heads for frequency i = lane, as 16-bit values
+  uint32_t qh[8];
+  {
+    const long long qo = (long long)b * p.q_sb + (long long)h * p.hpg * p.q_sh + lane;
+#pragma unroll
+    for (int hh = 0; hh < 8; ++hh) {
+      const long long o = qo + (hh < p.hpg ? hh : 0) * p.q_sh;
+      const uint32_t v = (uint32_t)p.q[o] | ((uint32_t)p.q[o + 64] << 16);
+      qh[hh] = hh < p.hpg ? v : 0u;
+    }
+  }
   const int hn = n & 7;
   const int qrow = (n & 8) + (hn < p.hpg ? hn : hn % p.hpg);
   uint32_t* qw = sQ[wave];
