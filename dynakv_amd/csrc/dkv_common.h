@@ -101,6 +101,79 @@ __device__ __forceinline__ int dkv_wave_max_i(int v) {
   return v;
 }
 
+// Wave64 all-reductions and an inclusive scan on DPP and permlane swaps (no LDS round trips):
+// quad_perm [1,0,3,2] and [2,3,0,1], row_half_mirror and row_mirror reduce within rows of 16,
+// the permlane16 / permlane32 swaps across them.
+template <int CTRL>
+__device__ __forceinline__ float dkv_dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int dkv_dpp_i32(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
+}
+__device__ __forceinline__ float dkv_wave_sum_fast(float v) {
+  v += dkv_dpp_f32<0xb1>(v);   // quad_perm [1,0,3,2]
+  v += dkv_dpp_f32<0x4e>(v);   // quad_perm [2,3,0,1]
+  v += dkv_dpp_f32<0x141>(v);  // row_half_mirror
+  v += dkv_dpp_f32<0x140>(v);  // row_mirror
+  {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v),
+                                                    false, false);
+    v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
+                                                    false, false);
+    v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  return v;
+}
+__device__ __forceinline__ float dkv_wave_max_fast(float v) {
+  v = fmaxf(v, dkv_dpp_f32<0xb1>(v));
+  v = fmaxf(v, dkv_dpp_f32<0x4e>(v));
+  v = fmaxf(v, dkv_dpp_f32<0x141>(v));
+  v = fmaxf(v, dkv_dpp_f32<0x140>(v));
+  {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v),
+                                                    false, false);
+    v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  }
+  {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
+                                                    false, false);
+    v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  }
+  return v;
+}
+__device__ __forceinline__ int dkv_wave_sum_fast_i(int v) {
+  v += dkv_dpp_i32<0xb1>(v);
+  v += dkv_dpp_i32<0x4e>(v);
+  v += dkv_dpp_i32<0x141>(v);
+  v += dkv_dpp_i32<0x140>(v);
+  {
+    const auto r = __builtin_amdgcn_permlane16_swap((uint32_t)v, (uint32_t)v, false, false);
+    v = (int)r[0] + (int)r[1];
+  }
+  {
+    const auto r = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
+    v = (int)r[0] + (int)r[1];
+  }
+  return v;
+}
+// Inclusive prefix sum over the wave's lanes: row_shr 1, 2, 4, 8 within rows of 16 (lanes
+// without a source add 0), then each row adds the totals of the rows before it (row_bcast15
+// into rows 1 and 3, row_bcast31 into rows 2 and 3).
+__device__ __forceinline__ float dkv_wave_scan_fast(float v) {
+  v += dkv_dpp_f32<0x111>(v);
+  v += dkv_dpp_f32<0x112>(v);
+  v += dkv_dpp_f32<0x114>(v);
+  v += dkv_dpp_f32<0x118>(v);
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x142, 0xa, 0xf, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x143, 0xc, 0xf, false));
+  return v;
+}
+
 // inv_freq_i = exp(-(2i/Dh) * ln(theta)) evaluated in fp32 as the reference kernels do
 // (reference fused.py:65-66, two_stage.py:36-41).
 __device__ __forceinline__ float dkv_inv_freq(int i, int Dh, float log_theta) {

@@ -116,15 +116,13 @@ __global__ __launch_bounds__(256) void cutoff_logits_kernel(CutoffParams p) {
                   blockIdx.x * CT_COLS + wave * 16, lane);
 }
 
-// The retained count of one (row m, group g) of matrix mat, computed by one wave from the
-// rounded logits. Lane l owns the E = D / 64 consecutive positions l*E .. l*E + E - 1 of the
-// row.
+// The retained count of one (row m, group g) of a matrix, computed by one wave from the
+// row's rounded logits (global workspace or LDS). Lane l owns the E = D / 64 consecutive
+// positions l*E .. l*E + E - 1 of the row.
 template <int DT, int E>
-__device__ __forceinline__ int cutoff_row_len(const CutoffParams& p, int mat, long long rg,
+__device__ __forceinline__ int cutoff_row_len(const CutoffParams& p, const uint16_t* row,
                                               int lane) {
-  const CutoffMat& cm = p.mat[mat];
-  const int D = p.D;
-  const uint16_t* lg = cm.logits + rg * D + lane * E;
+  const uint16_t* lg = row + lane * E;
 
   float x[E];
 #pragma unroll
@@ -132,14 +130,14 @@ __device__ __forceinline__ int cutoff_row_len(const CutoffParams& p, int mat, lo
   float mx = x[0];
 #pragma unroll
   for (int e = 1; e < E; ++e) mx = fmaxf(mx, x[e]);
-  mx = dkv_wave_max(mx);
+  mx = dkv_wave_max_fast(mx);
   float s = 0.f;
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     x[e] = expf(x[e] - mx);
     s += x[e];
   }
-  s = dkv_wave_sum(s);
+  s = dkv_wave_sum_fast(s);
   // probabilities in the compute dtype, then their prefix sums accumulated in fp32
   float run = 0.f;
 #pragma unroll
@@ -147,18 +145,12 @@ __device__ __forceinline__ int cutoff_row_len(const CutoffParams& p, int mat, lo
     run += dkv_round_to<DT>(x[e] / s);
     x[e] = run;  // inclusive prefix within the lane
   }
-  float inc = run;  // inclusive scan of the lane totals across the wave
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const float o = __shfl_up(inc, d, 64);
-    if (lane >= d) inc += o;
-  }
+  const float inc = dkv_wave_scan_fast(run);  // inclusive scan of the lane totals
   const float excl = inc - run;
   int cnt = 0;
 #pragma unroll
   for (int e = 0; e < E; ++e) cnt += dkv_round_to<DT>(excl + x[e]) >= p.threshold ? 1 : 0;
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) cnt += __shfl_xor(cnt, d, 64);
+  cnt = dkv_wave_sum_fast_i(cnt);
   return min(cnt, max(p.low_rank, 0));
 }
 
@@ -168,7 +160,7 @@ __device__ __forceinline__ void row_task(const CutoffParams& p, int mat, long lo
   const int m = (int)(rg / p.G), g = (int)(rg % p.G);
   const CutoffMat& cm = p.mat[mat];
   const int D = p.D;
-  const int len = cutoff_row_len<DT, E>(p, mat, rg, lane);
+  const int len = cutoff_row_len<DT, E>(p, cm.logits + rg * D, lane);
 
   const uint16_t* xs = cm.x + (long long)m * p.x_ld + (long long)g * D + lane * E;
   uint16_t* xo = cm.out + (long long)m * p.out_ld + (long long)g * D + lane * E;
@@ -194,17 +186,80 @@ __global__ __launch_bounds__(256) void cutoff_rows_kernel(CutoffParams p) {
   row_task<DT, E>(p, (int)(task / n_rows), task % n_rows, lane);
 }
 
-// Both steps in one launch for a few rows (M <= 16, D <= 128: a decode step): workgroup
-// 2g + mat computes the logits of group g of matrix mat for the rows (wave w: columns
-// 16w + 64c, as cutoff_logits_kernel computes them), then its waves take the rows' counts and
-// masked copies.
+// Few rows (M <= 16, D <= 128: a decode step) in one launch of 8 waves per (group, K|V): the
+// logits of the rows go to LDS (wave w: output columns 16w .. 16w+15; every operand load issued
+// before the first product, the masked copies' inputs loaded ahead as well), then wave w takes
+// rows w and w + 8: count, masked copy, length. One memory round trip before the stores.
+constexpr int CS_WAVES = 8;
+
+template <int DT>
+__device__ __forceinline__ void small_logits(const CutoffParams& p, int mat, int g, int wave,
+                                             int lane, uint16_t (*sLog)[128]) {
+  const int n0 = 16 * wave;
+  if (n0 >= p.D) return;
+  const int i = lane & 15, kg = lane >> 4;
+  const CutoffMat& cm = p.mat[mat];
+  const int D = p.D;
+  const uint16_t* xa = cm.x + (long long)min(i, p.M - 1) * p.x_ld + (long long)g * D + 8 * kg;
+  const uint16_t* wb = cm.wt + ((long long)g * D + n0 + i) * D + 8 * kg;
+  dkv_u32x4 a[4], b[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const int k = min(32 * s, D - 32);  // D = 64: the last two steps are loaded but not used
+    a[s] = *(const dkv_u32x4*)(xa + k);
+    b[s] = *(const dkv_u32x4*)(wb + k);
+  }
+  const float bias = elt_f32<DT>(cm.b[(long long)g * D + n0 + i]);
+  dkv_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+    if (32 * s < D) acc = mfma_16x16x32<DT>(a[s], b[s], acc);
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int m = 4 * kg + u;
+    if (m < p.M) {
+      const uint16_t v = f32_elt<DT>(acc[u] + bias);
+      sLog[m][n0 + i] = v;
+      cm.logits[((long long)m * p.G + g) * D + n0 + i] = v;  // the workspace copy, as the
+                                                               // two-kernel path leaves it
+    }
+  }
+}
+
 template <int DT, int E>
-__global__ __launch_bounds__(256) void cutoff_small_kernel(CutoffParams p) {
+__global__ __launch_bounds__(64 * CS_WAVES) void cutoff_small_kernel(CutoffParams p) {
+  __shared__ uint16_t sLog[CT_ROWS][128];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int mat = blockIdx.x & 1, g = blockIdx.x >> 1;
-  for (int c0 = 0; c0 < p.D; c0 += CT_COLS) logits_tile<DT>(p, mat, g, 0, c0 + 16 * wave, lane);
-  __syncthreads();  // the rows' logits (global workspace) are visible to the workgroup
-  for (int m = wave; m < p.M; m += 4) row_task<DT, E>(p, mat, (long long)m * p.G + g, lane);
+  const CutoffMat& cm = p.mat[mat];
+  const int D = p.D;
+  uint16_t xr[2][E];
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int m = min(wave + CS_WAVES * r, p.M - 1);
+    const uint16_t* xs = cm.x + (long long)m * p.x_ld + (long long)g * D + lane * E;
+#pragma unroll
+    for (int e = 0; e < E; ++e) xr[r][e] = xs[e];
+  }
+  small_logits<DT>(p, mat, g, wave, lane, sLog);
+  __syncthreads();
+  constexpr uint16_t EXP = DT == DKV_BF16 ? 0x7f80 : 0x7c00;
+  constexpr uint16_t QNAN = DT == DKV_BF16 ? 0x7fc0 : 0x7e00;
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int m = wave + CS_WAVES * r;
+    if (m >= p.M) break;
+    const int len = cutoff_row_len<DT, E>(p, &sLog[m][0], lane);
+    uint16_t* xo = cm.out + (long long)m * p.out_ld + (long long)g * D + lane * E;
+    // x * 1 or x * 0 written bitwise, as row_task writes them
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const uint16_t xb = xr[r][e];
+      const uint16_t zb = (xb & EXP) == EXP ? QNAN : (uint16_t)(xb & 0x8000);
+      xo[e] = lane * E + e < len ? xb : zb;
+    }
+    if (lane == 0) cm.lens[(long long)m * p.len_ld + g] = len;
+  }
 }
 
 // Decode step of the per-head layout, after the logits: for each (batch b, group g, K|V) the
@@ -236,7 +291,7 @@ __device__ __forceinline__ void append_row(const TailParams& t, int mat, long lo
                                            const uint16_t* pre_x = nullptr) {
   const CutoffParams& p = t.cp;
   const int m = (int)(rg / p.G), g = (int)(rg % p.G);
-  const int len = cutoff_row_len<DT, E>(p, mat, rg, lane);
+  const int len = cutoff_row_len<DT, E>(p, p.mat[mat].logits + rg * p.D, lane);
   int off = 0;
   if (lane == 0) {
     off = have_pre ? pre_off : t.ptr[mat][rg];
@@ -283,6 +338,54 @@ __global__ __launch_bounds__(256) void cutoff_layer_kernel(TailParams t) {
     return;
   }
   const long long qr = (long long)(blockIdx.x - n_cut) * 4 + wave;
+  if (qr < t.q_rows)
+    dkv_rope_pair<DT>(t.q + (qr / t.Hq) * t.q_sb + (qr % t.Hq) * 128, lane, t.pos, t.log_theta);
+}
+
+// cutoff_layer_kernel for a decode step of the per-head layout (M <= 16 rows, D <= 128), in one
+// memory round trip before the stores: workgroup 2g + mat (8 waves) loads its rows' append
+// pointers and inputs, computes the rows' logits into LDS as cutoff_small_kernel does, then wave
+// w appends rows w and w + 8; the workgroups past 2G rotate the query rows, one per wave.
+template <int DT, int E>
+__global__ __launch_bounds__(64 * CS_WAVES) void cutoff_layer_small_kernel(TailParams t) {
+  __shared__ uint16_t sLog[CT_ROWS][128];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const CutoffParams& p = t.cp;
+  const int n_cut = 2 * p.G;
+  if ((int)blockIdx.x < n_cut) {
+    const int mat = blockIdx.x & 1, g = blockIdx.x >> 1;
+    const int D = p.D;
+    int off[2];
+    uint16_t xr[2][E];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int m = min(wave + CS_WAVES * r, p.M - 1);
+      off[r] = t.ptr[mat][(long long)m * p.G + g];
+      const uint16_t* xs = p.mat[mat].x + (long long)m * p.x_ld + (long long)g * D + lane * E;
+#pragma unroll
+      for (int e = 0; e < E; ++e) xr[r][e] = xs[e];
+    }
+    small_logits<DT>(p, mat, g, wave, lane, sLog);
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int m = wave + CS_WAVES * r;
+      if (m >= p.M) break;
+      const long long rg = (long long)m * p.G + g;
+      const int len = cutoff_row_len<DT, E>(p, &sLog[m][0], lane);
+      if (lane == 0) {
+        t.ptr[mat][rg] = off[r] + len;
+        t.lens[mat][rg * t.tab_sb[mat] + (long long)t.seq * t.tab_ss[mat]] = len;
+        t.offs[mat][rg * t.tab_sb[mat] + (long long)t.seq * t.tab_ss[mat]] = off[r];
+      }
+      uint16_t* dst = (uint16_t*)t.flat[mat] + rg * t.flat_ld[mat] + off[r] + lane * E;
+#pragma unroll
+      for (int e = 0; e < E; ++e)
+        if (lane * E + e < len) dst[e] = xr[r][e];
+    }
+    return;
+  }
+  const long long qr = (long long)(blockIdx.x - n_cut) * CS_WAVES + wave;
   if (qr < t.q_rows)
     dkv_rope_pair<DT>(t.q + (qr / t.Hq) * t.q_sb + (qr % t.Hq) * 128, lane, t.pos, t.log_theta);
 }
@@ -348,14 +451,14 @@ extern "C" int dkv_cutoff_kv(void* stream, int dtype, const void* xk, const void
   if (M <= CT_ROWS && D <= 128) {
     if (dtype == DKV_BF16) {
       if (E == 1)
-        hipLaunchKernelGGL((cutoff_small_kernel<DKV_BF16, 1>), dim3(2 * G), dim3(256), 0, st, p);
+        hipLaunchKernelGGL((cutoff_small_kernel<DKV_BF16, 1>), dim3(2 * G), dim3(64 * CS_WAVES), 0, st, p);
       else
-        hipLaunchKernelGGL((cutoff_small_kernel<DKV_BF16, 2>), dim3(2 * G), dim3(256), 0, st, p);
+        hipLaunchKernelGGL((cutoff_small_kernel<DKV_BF16, 2>), dim3(2 * G), dim3(64 * CS_WAVES), 0, st, p);
     } else {
       if (E == 1)
-        hipLaunchKernelGGL((cutoff_small_kernel<DKV_F16, 1>), dim3(2 * G), dim3(256), 0, st, p);
+        hipLaunchKernelGGL((cutoff_small_kernel<DKV_F16, 1>), dim3(2 * G), dim3(64 * CS_WAVES), 0, st, p);
       else
-        hipLaunchKernelGGL((cutoff_small_kernel<DKV_F16, 2>), dim3(2 * G), dim3(256), 0, st, p);
+        hipLaunchKernelGGL((cutoff_small_kernel<DKV_F16, 2>), dim3(2 * G), dim3(64 * CS_WAVES), 0, st, p);
     }
     DKV_HIP_CHECK_LAUNCH();
     return DKV_OK;
@@ -454,6 +557,26 @@ int dkv_layer_cutoff_append_rope(void* stream, const DkvDecodeLayer* L, const vo
   t.pos = pos;
   t.log_theta = L->log_theta;
   hipStream_t st = (hipStream_t)stream;
+  if (M <= CT_ROWS && D <= 128) {
+    const dim3 sgrid((unsigned)(2 * G + (t.q_rows + CS_WAVES - 1) / CS_WAVES));
+    if (E == 1) {
+      if (dtype == DKV_BF16)
+        hipLaunchKernelGGL((cutoff_layer_small_kernel<DKV_BF16, 1>), sgrid, dim3(64 * CS_WAVES),
+                           0, st, t);
+      else
+        hipLaunchKernelGGL((cutoff_layer_small_kernel<DKV_F16, 1>), sgrid, dim3(64 * CS_WAVES),
+                           0, st, t);
+    } else {
+      if (dtype == DKV_BF16)
+        hipLaunchKernelGGL((cutoff_layer_small_kernel<DKV_BF16, 2>), sgrid, dim3(64 * CS_WAVES),
+                           0, st, t);
+      else
+        hipLaunchKernelGGL((cutoff_layer_small_kernel<DKV_F16, 2>), sgrid, dim3(64 * CS_WAVES),
+                           0, st, t);
+    }
+    DKV_HIP_CHECK_LAUNCH();
+    return DKV_OK;
+  }
   const dim3 grid((unsigned)(2 * G + (t.q_rows + 3) / 4));
 #define DKV_TAIL_CASE(e)                                                                 \
   case e:                                                                                \

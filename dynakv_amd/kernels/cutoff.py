@@ -120,10 +120,9 @@ def cutoff_kv(key_states: torch.Tensor, value_states: torch.Tensor, wt_k: torch.
         xv = xv.clone(memory_format=torch.contiguous_format)
     M = xk.shape[0]
     dev = key_states.device
-    out_k = torch.empty((M, hidden), dtype=dt, device=dev)
-    out_v = torch.empty((M, hidden), dtype=dt, device=dev)
-    len_k = torch.empty((M, G), dtype=torch.int32, device=dev)
-    len_v = torch.empty((M, G), dtype=torch.int32, device=dev)
+    out = torch.empty((2, M, hidden), dtype=dt, device=dev)  # one allocation each for the
+    lens = torch.empty((2, M, G), dtype=torch.int32, device=dev)  # outputs and the lengths
+    out_k, out_v, len_k, len_v = out[0], out[1], lens[0], lens[1]
     if M > 0:
         lib = _lib.load()
         st = _lib.stream_of(key_states)
