@@ -10,18 +10,24 @@
 // Here: dkv_rope_dense rotates dense K in place (rotate-half RoPE, fp32 angles
 // float(pos) * inv_freq as the decode kernels form them, result rounded to the cache dtype);
 // dkv_prefill_attention is a causal GQA flash-attention forward on MFMA:
-//   one workgroup = 64 queries of one query head (4 waves x 16 queries); key tiles of 64
+//   one workgroup = 128 queries of one query head (4 waves x 2 blocks of 16 queries, so every
+//   K and V operand read from LDS serves two products); key tiles of 64
 //   are staged in LDS (double-buffered, direct-to-LDS loads, 16-byte chunks XOR-swizzled by
 //   key so that both the row reads of K and the transposed reads of V avoid bank conflicts);
 //   S^T = K Q^T on 16x16x32 MFMA (each lane then holds one query's scores for 16 keys), online
-//   softmax in fp32 with lane maxima by permlane swaps, P kept as a bf16/fp16 hi + lo pair and
+//   softmax in fp32 with lane maxima by permlane swaps (the running maximum raised only when a
+//   tile's exceeds it by more than 2^8, so most tiles skip the rescale), P kept as a bf16/fp16
+//   hi + lo pair and
 //   P.V on 16x16x32 MFMA with both parts in the k dimension (V read transposed from LDS).
 #include "dkv_common.h"
 
 namespace {
 
 constexpr int FA_DH = 128;
-constexpr int FA_BQ = 64;     // queries per workgroup
+constexpr int FA_QB = 2;      // 16-query blocks per wave
+constexpr int FA_QW = 16 * FA_QB;  // queries per wave
+constexpr int FA_BQ = 4 * FA_QW;   // queries per workgroup (4 waves)
+constexpr float FA_RESCALE = 8.f;  // log2 units a tile's maximum may exceed the running one
 constexpr int FA_BK = 64;     // keys per tile
 constexpr int FA_TILE_BYTES = FA_BK * FA_DH * 2;  // 16 KB
 
@@ -98,9 +104,9 @@ __device__ __forceinline__ void split_hi_lo(const float (&p)[4], dkv_u32x2& hi, 
   }
 }
 
-// grid: (ceil(Sq / 64), Hq, B); 256 threads. ODT: output dtype (DT or fp32).
+// grid: (ceil(Sq / 128), Hq, B); 256 threads. ODT: output dtype (DT or fp32).
 template <int DT, int ODT>
-__global__ __launch_bounds__(256) void fa_prefill_kernel(PrefillParams p) {
+__global__ __launch_bounds__(256, 2) void fa_prefill_kernel(PrefillParams p) {
   __shared__ __attribute__((aligned(16))) uint8_t sK[2][FA_TILE_BYTES];
   __shared__ __attribute__((aligned(16))) uint8_t sV[2][FA_TILE_BYTES];
   const int lane = threadIdx.x & 63;
@@ -109,21 +115,26 @@ __global__ __launch_bounds__(256) void fa_prefill_kernel(PrefillParams p) {
   const int b = blockIdx.z, h = blockIdx.y;
   const int kvh = h / (p.Hq / p.Hkv);
   const int q0 = blockIdx.x * FA_BQ;
-  const int qrow = q0 + wave * 16 + n;  // this lane's query (B operand column, output row)
+  const int wq0 = q0 + FA_QW * wave;  // the wave's first query
+  // this lane's query in block qb (B operand column, output row)
+  auto qrow = [&](int qb) { return wq0 + 16 * qb + n; };
 
-  // Q^T operand: lane (query n, k-group g) holds dims 32s + 8g .. +8 for s = 0..3
-  dkv_u32x4 qop[4];
-  {
-    const uint16_t* qp = p.q + (long long)b * p.q_sb + (long long)h * p.q_sh +
-                         (long long)min(qrow, p.Sq - 1) * p.q_ss + 8 * g;
+  // Q^T operands: lane (query n of block qb, k-group g) holds dims 32s + 8g .. +8
+  dkv_u32x4 qop[FA_QB][4];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) qop[s] = *(const dkv_u32x4*)(qp + 32 * s);
+  for (int qb = 0; qb < FA_QB; ++qb) {
+    const uint16_t* qp = p.q + (long long)b * p.q_sb + (long long)h * p.q_sh +
+                         (long long)min(qrow(qb), p.Sq - 1) * p.q_ss + 8 * g;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) qop[qb][s] = *(const dkv_u32x4*)(qp + 32 * s);
   }
 
-  // keys this workgroup needs: causal limit of its last query
+  // keys this workgroup needs: causal limit of its last query; the wave's own limit
   const int q_last_pos = p.q_offset + min(q0 + FA_BQ, p.Sq) - 1;
   const int k_end = p.causal ? min(p.Sk, q_last_pos + 1) : p.Sk;
   const int n_tiles = (k_end + FA_BK - 1) / FA_BK;
+  const int wave_k_end =
+      p.causal ? min(k_end, p.q_offset + min(wq0 + FA_QW, p.Sq)) : k_end;  // <= k_end
 
   const __amdgpu_buffer_rsrc_t rk = dkv_make_rsrc(p.k, p.k_bytes);
   const __amdgpu_buffer_rsrc_t rv = dkv_make_rsrc(p.v, p.v_bytes);
@@ -146,76 +157,107 @@ __global__ __launch_bounds__(256) void fa_prefill_kernel(PrefillParams p) {
     }
   };
 
-  dkv_f32x4 acc[8];
+  dkv_f32x4 acc[FA_QB][8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) acc[i] = dkv_f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run = -1.0e30f, l_run = 0.f;
-  const int my_pos = p.q_offset + qrow;
+  for (int qb = 0; qb < FA_QB; ++qb)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[qb][i] = dkv_f32x4{0.f, 0.f, 0.f, 0.f};
+  // running maxima (log2 units) and sums per query block; a maximum is only raised when the
+  // tile's exceeds it by more than FA_RESCALE, so P may reach 2^FA_RESCALE
+  float m_run[FA_QB], l_run[FA_QB];
+#pragma unroll
+  for (int qb = 0; qb < FA_QB; ++qb) {
+    m_run[qb] = -1.0e30f;
+    l_run[qb] = 0.f;
+  }
 
   if (n_tiles > 0) issue(0);
   for (int t = 0; t < n_tiles; ++t) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();  // tile t is in LDS for every wave; tile t-1's buffer is free
     if (t + 1 < n_tiles) issue(t + 1);
+    const int key0 = t * FA_BK;
+    if (key0 >= wave_k_end) continue;  // every key of the tile is past the wave's queries
     const uint8_t* kt = sK[t & 1];
     const uint8_t* vt = sV[t & 1];
 
-    // S^T = K Q^T: A = K rows (lane: key 16kb + n, dims 32s + 8g .. +8), B = Q^T
-    float z[4][4];
+    // S^T = K Q^T: A = K rows (lane: key 16kb + n, dims 32s + 8g .. +8), B = Q^T of block qb;
+    // lane (query n, g) then holds keys 16kb + 4g + u
+    float z[FA_QB][4][4];
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
-      dkv_f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
+      dkv_f32x4 sacc[FA_QB];
+#pragma unroll
+      for (int qb = 0; qb < FA_QB; ++qb) sacc[qb] = dkv_f32x4{0.f, 0.f, 0.f, 0.f};
       const uint8_t* row = kt + (16 * kb + n) * 256;
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         const dkv_u32x4 a = *(const dkv_u32x4*)(row + 16 * ((4 * s + g) ^ n));
-        sacc = mfma32<DT>(a, qop[s], sacc);
-      }
-      // lane (query n, g) holds keys 16kb + 4g + u
 #pragma unroll
-      for (int u = 0; u < 4; ++u) z[kb][u] = sacc[u] * p.scale_log2;
+        for (int qb = 0; qb < FA_QB; ++qb) sacc[qb] = mfma32<DT>(a, qop[qb][s], sacc[qb]);
+      }
+#pragma unroll
+      for (int qb = 0; qb < FA_QB; ++qb)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) z[qb][kb][u] = sacc[qb][u] * p.scale_log2;
     }
-    const int key0 = t * FA_BK;
-    if (key0 + FA_BK > k_end || (p.causal && key0 + FA_BK - 1 > p.q_offset + q0 + 16 * wave)) {
+    if (key0 + FA_BK > k_end || (p.causal && key0 + FA_BK - 1 > p.q_offset + wq0)) {
+#pragma unroll
+      for (int qb = 0; qb < FA_QB; ++qb) {
+        const int my_pos = p.q_offset + qrow(qb);
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const int key = key0 + 16 * kb + 4 * g + u;
+            if (key >= k_end || (p.causal && key > my_pos)) z[qb][kb][u] = -INFINITY;
+          }
+      }
+    }
+    float tmax[FA_QB];
+#pragma unroll
+    for (int qb = 0; qb < FA_QB; ++qb) {
+      float m = z[qb][0][0];
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int key = key0 + 16 * kb + 4 * g + u;
-          if (key >= k_end || (p.causal && key > my_pos)) z[kb][u] = -INFINITY;
-        }
+        for (int u = 0; u < 4; ++u) m = fa_max(m, z[qb][kb][u]);
+      tmax[qb] = fa_max4(m);
     }
-    float tmax = z[0][0];
+    if (__ballot(tmax[0] > m_run[0] + FA_RESCALE || tmax[FA_QB - 1] > m_run[FA_QB - 1] + FA_RESCALE)) {
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
+      for (int qb = 0; qb < FA_QB; ++qb) {
+        const float m_new = fa_max(m_run[qb], tmax[qb]);
+        const float alpha = __builtin_amdgcn_exp2f(m_run[qb] - m_new);
+        m_run[qb] = m_new;
+        l_run[qb] *= alpha;
+        // acc rows are dims, columns queries: lane (query n, g) holds dims 16db + 4g + u of
+        // query n, so its rescale factor is its own alpha
 #pragma unroll
-      for (int u = 0; u < 4; ++u) tmax = fa_max(tmax, z[kb][u]);
-    tmax = fa_max4(tmax);
-    const float m_new = fa_max(m_run, tmax);
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-    m_run = m_new;
-    l_run *= alpha;
-    // acc rows are dims, columns queries: lane (query n, g) holds dims 16db + 4g + u of query
-    // n, so its rescale factor is its own alpha
+        for (int i = 0; i < 8; ++i)
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-#pragma unroll
-      for (int u = 0; u < 4; ++u) acc[i][u] *= alpha;
+          for (int u = 0; u < 4; ++u) acc[qb][i][u] *= alpha;
+      }
+    }
 
-    // P.V: for each key block kb, one 16x16x32 product per 16 dims with k = 8g + e pairing
-    // part e/4 of key 16kb + 4g + e%4 (B: this lane's P hi then lo) with that key's V values
-    // (A: the four keys' values of dim 16db + n, twice)
+    // P.V: for each key block kb, one 16x16x32 product per 16 dims and query block with
+    // k = 8g + e pairing part e/4 of key 16kb + 4g + e%4 (B: this lane's P hi then lo) with that
+    // key's V values (A: the four keys' values of dim 16db + n, twice)
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
-      float pu[4];
+      dkv_u32x4 bop[FA_QB];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        pu[u] = __builtin_amdgcn_exp2f(z[kb][u] - m_run);
-        l_run += pu[u];
+      for (int qb = 0; qb < FA_QB; ++qb) {
+        float pu[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          pu[u] = __builtin_amdgcn_exp2f(z[qb][kb][u] - m_run[qb]);
+          l_run[qb] += pu[u];
+        }
+        dkv_u32x2 ph, pl;
+        split_hi_lo<DT>(pu, ph, pl);
+        bop[qb] = dkv_u32x4{ph.x, ph.y, pl.x, pl.y};
       }
-      dkv_u32x2 ph, pl;
-      split_hi_lo<DT>(pu, ph, pl);
-      const dkv_u32x4 bop = dkv_u32x4{ph.x, ph.y, pl.x, pl.y};
       // transposed read: lane L = 4j + q of each 16-lane group reads key 16kb + 4g + j,
       // dims 16db + 4q .. +3 (8 bytes); lane i then holds dim 16db + i of keys 4g .. 4g+3
       const int key = 16 * kb + 4 * g + (n >> 2);
@@ -230,21 +272,28 @@ __global__ __launch_bounds__(256) void fa_prefill_kernel(PrefillParams p) {
                                (__attribute__((address_space(3))) uint8_t*)src)));
         const dkv_u32x4 aop = __builtin_bit_cast(
             dkv_u32x4, dkv_u64x2{__builtin_bit_cast(uint64_t, xv), __builtin_bit_cast(uint64_t, xv)});
-        acc[db] = mfma32<DT>(aop, bop, acc[db]);
+#pragma unroll
+        for (int qb = 0; qb < FA_QB; ++qb) acc[qb][db] = mfma32<DT>(aop, bop[qb], acc[qb][db]);
       }
     }
   }
 
-  // l over the 64 keys of each tile sits in the lane's 16 keys x 4 lanes of the query
-  l_run += __shfl_xor(l_run, 16, 64);
-  l_run += __shfl_xor(l_run, 32, 64);
-  if (qrow < p.Sq) {
-    const float inv = 1.f / l_run;
-    const long long ob = (long long)b * p.o_sb + (long long)h * p.o_sh + (long long)qrow * p.o_ss;
 #pragma unroll
-    for (int db = 0; db < 8; ++db)
+  for (int qb = 0; qb < FA_QB; ++qb) {
+    // l over each tile's 64 keys sits in the lane's 16 keys x 4 lanes of the query
+    float l = l_run[qb];
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    const int qr = qrow(qb);
+    if (qr < p.Sq) {
+      const float inv = 1.f / l;
+      const long long ob = (long long)b * p.o_sb + (long long)h * p.o_sh + (long long)qr * p.o_ss;
 #pragma unroll
-      for (int u = 0; u < 4; ++u) dkv_store_f32<ODT>(p.out, ob + 16 * db + 4 * g + u, acc[db][u] * inv);
+      for (int db = 0; db < 8; ++db)
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          dkv_store_f32<ODT>(p.out, ob + 16 * db + 4 * g + u, acc[qb][db][u] * inv);
+    }
   }
 }
 
