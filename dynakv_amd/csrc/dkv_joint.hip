@@ -6,13 +6,14 @@
 // avx / _avx_proj_fwd (:207-324), the router's long route for this layout; the fused route
 // (fused.py:28-170) is the same scores with -inf masking and the V pass without the 1e-6 clamp.
 // The entry points take what dkv_scores / dkv_av take for these shapes (the K basis transposed
-// to [dim][rank], a RoPE table, a workspace for the V pass) and compute the same results to fp32
-// accuracy:
+// in 32-rank chunks, [chunk][dim][rank], a RoPE table, a workspace for the V pass) and compute
+// the same results to fp32 accuracy:
 //
 // joint_scores_kernel -- workgroup = (512 tokens, basis head h, batch row b); wave w takes 64
 //   tokens (4 column blocks of 16). K^T[128 x 64] = B_h^T . X^T accumulates on 16x16x32 MFMA over
 //   the rank chunks of 32 that the block's longest token needs. Each basis chunk ([128 dims][32
-//   ranks], 8 KB) is loaded once per workgroup into LDS (two buffers) and every A operand read
+//   ranks], 8 KB contiguous in HBM) is loaded once per workgroup into LDS (two buffers) and every
+//   A operand read
 //   from it serves the wave's 4 column blocks; the coefficients go straight into B operand
 //   registers (lane = one token x 8 ranks, elements past the token's count zeroed), two chunks
 //   ahead. Then per 16-token tile T: R(n) applied to the lane's token (n = its slot in the tile,
@@ -62,7 +63,7 @@ struct JScoresParams {
   const uint16_t* q;
   long long q_sb, q_sh;
   const uint16_t* bt;  // K basis [n_basis][Dh][R-stride]
-  long long bt_sh, bt_sd;
+  long long bt_sh, bt_sc;  // basis [h][chunk][dim][32 ranks]: head and chunk strides
   const uint16_t* flat;
   long long flat_ld;
   const int* lens;
@@ -126,7 +127,7 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_scores_kernel(JScoresParams
   const __amdgpu_buffer_rsrc_t rs = dkv_make_rsrc(p.flat + (long long)b * p.flat_ld, end * 2u);
   // this thread's basis piece of every chunk: dim bd, ranks 8*bk .. +8 of the chunk
   const int bd = tid >> 2, bk = (tid & 3) ^ jswz(bd);
-  const uint16_t* bsrc = p.bt + (long long)h * p.bt_sh + (long long)bd * p.bt_sd + 8 * bk;
+  const uint16_t* bsrc = p.bt + (long long)h * p.bt_sh + (long long)bd * JCH + 8 * bk;
 
   int tlen[JCB], toff[JCB];
   // bit c of pmask[cb]: some lane of column block cb has its count ending inside its 8 ranks of
@@ -168,7 +169,7 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_scores_kernel(JScoresParams
     dkv_u32x4 ba = dkv_u32x4{0u, 0u, 0u, 0u}, bb = ba;
 #pragma unroll
     for (int cb = 0; cb < JCB; ++cb) xa[cb] = xb[cb] = dkv_u32x4{0u, 0u, 0u, 0u};
-    auto load_b = [&](int c) { return *(const dkv_u32x4*)(bsrc + JCH * min(c, nch - 1)); };
+    auto load_b = [&](int c) { return *(const dkv_u32x4*)(bsrc + p.bt_sc * min(c, nch - 1)); };
     if (nch > 0) {
       sB[0][tid] = load_b(0);
       ba = load_b(1);
@@ -690,7 +691,7 @@ bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 
 extern "C" int dkv_joint_scores(void* stream, int mode, int dtype, int out_dtype, const void* q,
                                 long long q_sb, long long q_sh, const void* basis_t,
-                                long long bt_sh, long long bt_sd, int n_basis, const void* flat,
+                                long long bt_sh, long long bt_sc, int n_basis, const void* flat,
                                 long long flat_ld, const int* lens, long long lens_sb,
                                 long long lens_ss, const int* offs, long long offs_sb,
                                 long long offs_ss, const float* rope, int rope_tiles, void* out,
@@ -705,7 +706,8 @@ extern "C" int dkv_joint_scores(void* stream, int mode, int dtype, int out_dtype
   if (Hq % n_basis != 0 || Hq / n_basis > 8) return DKV_E_UNSUPPORTED;
   if (B == 0 || Hq == 0 || S == 0) return DKV_OK;
   if (!q || !basis_t || !flat || !lens || !offs || !rope || !out) return DKV_E_ARG;
-  if (!aligned16(basis_t) || bt_sd < R || bt_sd % 8 != 0 || bt_sh % 8 != 0) return DKV_E_UNSUPPORTED;
+  if (!aligned16(basis_t) || bt_sc < JDH * JCH || bt_sc % 8 != 0 || bt_sh % 8 != 0)
+    return DKV_E_UNSUPPORTED;
   if (flat_ld <= 0 || flat_ld > JFLAT_CAP - 8) return DKV_E_UNSUPPORTED;
   if (rope_tiles < (S + 15) / 16) return DKV_E_ARG;
   if (B > 65535 || n_basis > 65535) return DKV_E_UNSUPPORTED;
@@ -715,7 +717,7 @@ extern "C" int dkv_joint_scores(void* stream, int mode, int dtype, int out_dtype
   p.q_sh = q_sh;
   p.bt = (const uint16_t*)basis_t;
   p.bt_sh = bt_sh;
-  p.bt_sd = bt_sd;
+  p.bt_sc = bt_sc;
   p.flat = (const uint16_t*)flat;
   p.flat_ld = flat_ld;
   p.lens = lens;

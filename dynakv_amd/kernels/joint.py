@@ -71,12 +71,14 @@ _BT_CACHE: dict = {}
 
 
 def _transposed(basis: torch.Tensor) -> torch.Tensor:
-    """(nb, Dh, R) contiguous copy of a (nb, R, Dh) basis, cached per tensor object."""
+    """(nb, R/32, Dh, 32) contiguous copy of a (nb, R, Dh) basis (transposed in 32-rank chunks,
+    each chunk contiguous), cached per tensor object."""
     ent = _BT_CACHE.get(id(basis))
     key = (basis.data_ptr(), tuple(basis.shape), tuple(basis.stride()), basis._version)
     if ent is not None and ent[0]() is basis and ent[1] == key:
         return ent[2]
-    bt = basis.transpose(1, 2).contiguous()
+    nb, R, Dh = basis.shape
+    bt = basis.reshape(nb, R // 32, 32, Dh).transpose(2, 3).contiguous()
     _remember(_BT_CACHE, basis, key, bt)
     return bt
 
@@ -123,7 +125,7 @@ def joint_scores(q3: torch.Tensor, k_up: torch.Tensor, k_flat: torch.Tensor,
     rc = _lib.load().dkv_joint_scores(
         st, mode, _lib.dtype_code(q3.dtype), _lib.dtype_code(out_dtype),
         q3.data_ptr(), q3.stride(0), q3.stride(1),
-        bt.data_ptr(), bt.stride(0), bt.stride(1), bt.shape[0],
+        bt.data_ptr(), bt.stride(0), bt.stride(1), bt.shape[0],  # head and chunk strides
         k_flat.data_ptr(), k_flat.stride(0),
         lens.data_ptr(), lens.stride(0), lens.stride(1),
         offs.data_ptr(), offs.stride(0), offs.stride(1),

@@ -159,16 +159,17 @@ int dkv_av(void* stream, int mode, int scores_dtype, int cache_dtype, int out_dt
  * dkv_scores on MFMA for the reference's joint layout and any 16-bit cache with ranks up to 1024
  * (abx_sparse / _abx_sparse_fwd, reference two_stage.py:48-189; with mode 1 the scores of the
  * fused route, fused.py:28-140). Same semantics and outputs as dkv_scores (mode, masking,
- * rounding to out_dtype), with the K basis given transposed: basis_t (n_basis, Dh, R-stride),
- * element [h][d][r] at h*bt_sh + d*bt_sd + r, 16-byte aligned, bt_sd >= R, bt_sh and bt_sd
- * multiples of 8. RoPE: the rope table of dkv_rope_table with rope_tiles >= ceil(S/16).
+ * rounding to out_dtype), with the K basis given transposed in 32-rank chunks: basis_t
+ * (n_basis, R/32, Dh, 32), element B_h[32c + k][d] at h*bt_sh + c*bt_sc + d*32 + k (each
+ * chunk's 8 KB contiguous), 16-byte aligned, bt_sc >= Dh*32, bt_sh and bt_sc multiples of 8.
+ * RoPE: the rope table of dkv_rope_table with rope_tiles >= ceil(S/16).
  * q: (B, Hq, Dh) strides (q_sb, q_sh), unit dim stride; dtype (q and cache) DKV_BF16 or DKV_F16.
  * DKV_E_UNSUPPORTED unless Dh == 128, R % 32 == 0, R <= 1024, Hq / n_basis <= 8,
  * flat_ld <= 0x3fffffe8 (the caller then uses dkv_scores).
  */
 int dkv_joint_scores(void* stream, int mode, int dtype, int out_dtype,
                      const void* q, long long q_sb, long long q_sh,
-                     const void* basis_t, long long bt_sh, long long bt_sd, int n_basis,
+                     const void* basis_t, long long bt_sh, long long bt_sc, int n_basis,
                      const void* flat, long long flat_ld,
                      const int* lens, long long lens_sb, long long lens_ss,
                      const int* offs, long long offs_sb, long long offs_ss,
