@@ -314,10 +314,13 @@ struct JAvParams {
   const int* offs;
   long long offs_sb, offs_ss;
   float* rec;  // [B][Hq][n_splits][JPREC]
+  uint32_t sc_bytes;  // extent of the scores from their base (vector score loads)
   int B, Hq, S, R, n_splits, split_len;
 };
 
-template <int DT, int SDT>
+// VEC: the scores are token-contiguous with rows aligned to 4 elements, and a lane loads its 4
+// tokens' scores of a tile in one 8- or 16-byte access (else one access per score)
+template <int DT, int SDT, bool VEC>
 __global__ __launch_bounds__(JTHREADS, 1) void joint_av_kernel(JAvParams p) {
   // per wave: its rank slice of the current tile's V coefficients, the split kernel's V-window
   // layout: rank r of token t in chunk r/32 at lane slot 16*((r%32)/8) + t, element r%8
@@ -350,14 +353,34 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_av_kernel(JAvParams p) {
     o = p.offs[(long long)b * p.offs_sb + (long long)tc * p.offs_ss];
   };
   auto count = [&](int j, int l) { return s_begin + 16 * j + n < s_end ? min(max(l, 0), p.R) : 0; };
+  const __amdgpu_buffer_rsrc_t rz = dkv_make_rsrc(p.scores, p.sc_bytes);
   auto load_z = [&](int j, uint32_t(&z)[4]) {
+    if constexpr (VEC) {
+      // tokens past the split read their neighbours (or zeros past the extent): replaced at use
+      const uint32_t e = (uint32_t)(sbase + s_begin + 16 * j + 4 * g);
+      if constexpr (SDT == DKV_F32) {
+        const dkv_u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rz, e * 4u, 0, 0);
+        z[0] = v.x;
+        z[1] = v.y;
+        z[2] = v.z;
+        z[3] = v.w;
+      } else {
+        const dkv_u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rz, e * 2u, 0, 0);
+        z[0] = v.x & 0xffffu;
+        z[1] = v.x >> 16;
+        z[2] = v.y & 0xffffu;
+        z[3] = v.y >> 16;
+      }
+    } else {
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const long long i = sbase + (long long)min(s_begin + 16 * j + 4 * g + u, s_end - 1) * p.sc_ss;
-      if constexpr (SDT == DKV_F32)
-        z[u] = ((const uint32_t*)p.scores)[i];
-      else
-        z[u] = ((const uint16_t*)p.scores)[i];
+      for (int u = 0; u < 4; ++u) {
+        const long long i =
+            sbase + (long long)min(s_begin + 16 * j + 4 * g + u, s_end - 1) * p.sc_ss;
+        if constexpr (SDT == DKV_F32)
+          z[u] = ((const uint32_t*)p.scores)[i];
+        else
+          z[u] = ((const uint16_t*)p.scores)[i];
+      }
     }
   };
   auto score = [&](int j, int u, uint32_t raw) {
@@ -817,8 +840,21 @@ extern "C" int dkv_joint_av(void* stream, int mode, int scores_dtype, int dtype,
   a.n_splits = ns;
   a.split_len = sl;
   const dim3 agrid((unsigned)ns, (unsigned)((Hq + 15) / 16), (unsigned)B);
-#define DKV_JA_LAUNCH(DT_, SDT_) \
-  hipLaunchKernelGGL((joint_av_kernel<DT_, SDT_>), agrid, dim3(JTHREADS), 0, st, a)
+  // vector score loads: token-contiguous rows whose starts are 4-element aligned, an extent
+  // that a 32-bit byte offset covers
+  const int sc_elt = scores_dtype == DKV_F32 ? 4 : 2;
+  const long long sc_extent =
+      ((long long)(B - 1) * sc_sb + (long long)(Hq - 1) * sc_sh + S + 4) * sc_elt;
+  const bool vec = sc_ss == 1 && sc_sb % 4 == 0 && sc_sh % 4 == 0 && sc_sb >= 0 && sc_sh >= 0 &&
+                   ((uintptr_t)scores % (4 * sc_elt)) == 0 && sc_extent < (1LL << 31);
+  a.sc_bytes = vec ? (uint32_t)sc_extent : 0u;
+#define DKV_JA_LAUNCH(DT_, SDT_)                                                            \
+  do {                                                                                      \
+    if (vec)                                                                                \
+      hipLaunchKernelGGL((joint_av_kernel<DT_, SDT_, true>), agrid, dim3(JTHREADS), 0, st, a); \
+    else                                                                                    \
+      hipLaunchKernelGGL((joint_av_kernel<DT_, SDT_, false>), agrid, dim3(JTHREADS), 0, st, a); \
+  } while (0)
   if (dtype == DKV_BF16) {
     if (scores_dtype == DKV_F32) DKV_JA_LAUNCH(DKV_BF16, DKV_F32);
     else if (scores_dtype == DKV_BF16) DKV_JA_LAUNCH(DKV_BF16, DKV_BF16);
