@@ -176,3 +176,90 @@ def test_distinct_basis_detection(dev):
     assert J._distinct(rep, 32) is got
     rep[5, 0, 0] += 1  # in place: the copies differ now
     assert J._distinct(rep, 32).shape[0] == 32
+
+
+def _pack_rows_dev(x: torch.Tensor, lens: torch.Tensor):
+    """Packed rows of x (rows, S, R) keeping the first lens[row, t] values of each token:
+    (flat (rows, cap), offs (rows, S)) with exclusive-prefix offsets, on the device."""
+    rows, S, R = x.shape
+    keep = torch.arange(R, device=x.device)[None, None, :] < lens[..., None]
+    tot = lens.sum(dim=1)
+    cap = int(tot.max().item()) + 8
+    offs = torch.zeros_like(lens)
+    offs[:, 1:] = torch.cumsum(lens, dim=1, dtype=torch.int32)[:, :-1]
+    pos = torch.cumsum(keep.reshape(rows, -1), dim=1, dtype=torch.int32) - 1
+    flat = torch.zeros((rows, cap), dtype=x.dtype, device=x.device)
+    ridx = torch.arange(rows, device=x.device)[:, None].expand(rows, S * R)
+    km = keep.reshape(rows, -1)
+    flat[ridx[km], pos[km].long()] = x.reshape(rows, -1)[km]
+    return flat, offs.contiguous()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("route", ["short_fused", "long_two_stage"])
+def test_joint_matches_split_kernel_at_config3_shape(dev, route):
+    """Size-independent cross-check at the config-3 shape (B=16, S=8192, 8 KV heads x rank 128,
+    32 query heads, mean retention 0.29 with 5% full tokens, bf16): a per-head cache and the
+    joint cache holding the same coefficients (token t's joint row is the heads' rows side by
+    side, each padded with zeros to 128 ranks; the joint K/V bases block-diagonal) give the
+    same attention, the per-head one through the split kernel (itself checked against the
+    oracle) and the joint one through dkv_joint_scores / dkv_joint_av."""
+    from dynakv_amd.kernels.decode import grouped_decode_attention
+    from dynakv_amd.synthetic import device_lengths
+
+    print(f"[gpu] joint vs split kernel at config 3, {route}", flush=True)
+    B, S, G, R, Hq, dt = 16, 8192, 8, 128, 32, torch.bfloat16
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(3)
+    lk = device_lengths(B * G, S, R, 0.29, gen, dev, 4, 0.05).view(B, G, S)
+    lv = device_lengths(B * G, S, R, 0.29, gen, dev, 4, 0.05).view(B, G, S)
+    ar = torch.arange(R, device=dev)
+    xk = torch.randn((B, G, S, R), generator=gen, device=dev).to(dt) * (ar < lk[..., None])
+    xv = torch.randn((B, G, S, R), generator=gen, device=dev).to(dt) * (ar < lv[..., None])
+
+    def bases():
+        a = torch.randn((G, R, R), generator=gen, device=dev)
+        qm, rm = torch.linalg.qr(a)
+        return (qm * torch.sign(torch.diagonal(rm, dim1=-2, dim2=-1)).unsqueeze(-2)).to(dt)
+
+    kb, vb = bases(), bases()
+    q = torch.randn((B, Hq, 128), generator=gen, device=dev).to(dt)
+    # per-head layout: row b*G + g
+    fk, ok = _pack_rows_dev(xk.reshape(B * G, S, R), lk.reshape(B * G, S))
+    fv, ov = _pack_rows_dev(xv.reshape(B * G, S, R), lv.reshape(B * G, S))
+    rt = "short_fused" if route == "short_fused" else "long_two_stage"
+    want = grouped_decode_attention(q, fk, fv, lk.reshape(B * G, S).contiguous(), ok,
+                                    lv.reshape(B * G, S).contiguous(), ov, kb, vb, theta=THETA,
+                                    route=rt, out_dtype=torch.float32)
+    del fk, fv, ok, ov
+    # joint layout: one row per batch element, count = the last head's end
+    hk = torch.arange(G, device=dev)[None, :, None] * R
+    jk = (hk + lk).amax(dim=1).to(torch.int32)
+    jv = (hk + lv).amax(dim=1).to(torch.int32)
+    xjk = xk.permute(0, 2, 1, 3).reshape(B, S, G * R)
+    xjv = xv.permute(0, 2, 1, 3).reshape(B, S, G * R)
+    del xk, xv
+    fjk, ojk = _pack_rows_dev(xjk, jk)
+    del xjk
+    fjv, ojv = _pack_rows_dev(xjv, jv)
+    del xjv
+    k_up = torch.zeros((G, G * R, 128), dtype=dt, device=dev)
+    v_up = torch.zeros((G, G * R, 128), dtype=dt, device=dev)
+    for h in range(G):
+        k_up[h, R * h:R * (h + 1)] = kb[h]
+        v_up[h, R * h:R * (h + 1)] = vb[h]
+    mode = 1 if route == "short_fused" else 0
+    sc = J.joint_scores(q, k_up, fjk, jk, ojk, theta=THETA, mode=mode,
+                        out_dtype=torch.float32 if mode == 1 else dt)
+    got = J.joint_av(sc, v_up, fjv, jv, ojv, mode=mode, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    err = (got - want).abs()
+    scale = want.abs().max().item()
+    print(f"[parity] joint vs split {route}: max_abs={err.max().item():.3e} |ref|max={scale:.3e}",
+          flush=True)
+    if mode == 1:
+        # both fp32-faithful: accumulation-order differences only
+        assert err.max().item() <= 1e-4 * max(scale, 1.0)
+    else:
+        # scores rounded to bf16 by both routes; a score on a rounding tie may round apart
+        assert err.max().item() <= 2e-3 and (err.norm() / want.norm()).item() <= 1e-2
