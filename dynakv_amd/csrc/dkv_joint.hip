@@ -555,23 +555,22 @@ struct JMergeParams {
   int Hq, R, n_splits, hpg, n_rb;
 };
 
-constexpr int JMH = 8;  // query heads merged and projected together (they share a V basis)
-
-// workgroup = (rank block of 128, V basis hv and up to 8 of its query heads, batch row b): the
+// workgroup = (rank block of 128, V basis hv and up to NH of its query heads, batch row b): the
 // split weights, the block's merged coefficients, their projection through the block's basis rows.
 // Every load that does not depend on another is issued up front, in the order the values are
 // needed (split maxima and sums, the first 16 splits' coefficients, the basis rows), so the
-// workgroup waits about one memory latency.
-template <int DT, int MODE>
+// workgroup waits about one memory latency. NH (4 or 8, the instance for the heads per basis)
+// fixes the product loops' trip counts; heads past the group's own count carry zeros.
+template <int DT, int MODE, int NH>
 __global__ __launch_bounds__(256) void joint_merge_kernel(JMergeParams p) {
-  extern __shared__ float sWt[];  // [JMH][n_splits]: split weights 2^(m_s - M) / den per head
-  __shared__ __attribute__((aligned(16))) float sA[JMH][JRB];
-  __shared__ float sOut[4][JMH][JDH];
+  extern __shared__ float sWt[];  // [NH][n_splits]: split weights 2^(m_s - M) / den per head
+  __shared__ __attribute__((aligned(16))) float sA[NH][JRB];
+  __shared__ float sOut[4][NH][JDH];
   const int rb = blockIdx.x;
-  const int chunks = (p.hpg + JMH - 1) / JMH;
-  const int hv = blockIdx.y / chunks, j0 = (blockIdx.y % chunks) * JMH;
+  const int chunks = (p.hpg + NH - 1) / NH;
+  const int hv = blockIdx.y / chunks, j0 = (blockIdx.y % chunks) * NH;
   const int b = blockIdx.z;
-  const int nh = min(JMH, p.hpg - j0);
+  const int nh = min(NH, p.hpg - j0);
   const int nr = min(JRB, p.R - JRB * rb);  // ranks of this block
   const int ns = p.n_splits;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -597,15 +596,22 @@ __global__ __launch_bounds__(256) void joint_merge_kernel(JMergeParams p) {
     for (int u = 0; u < 16; ++u)
       x[u] = *(const dkv_f32x4*)(cbase + (long long)min(s0 + u, ns - 1) * JPREC);
   };
-  load_coef(0);
+  if (jc < NH) load_coef(0);
   // (3) basis rows: thread = (dims 2dp, 2dp+1, ranks 32rq .. 32rq+31 of the block)
   const int dp = tid & 63, rq = tid >> 6;
   uint32_t vbv[32];
   {
-    const uint16_t* vb = p.vb + (long long)hv * p.vb_sh + (long long)JRB * rb * p.vb_sr + 2 * dp;
+    const uint16_t* vb = p.vb + (long long)hv * p.vb_sh +
+                         (long long)(JRB * rb + 32 * rq) * p.vb_sr + 2 * dp;
+    const int kmax = nr - 1 - 32 * rq;  // rows past the block's end read its last row
+    if (kmax >= 31) {
 #pragma unroll
-    for (int k = 0; k < 32; ++k)
-      vbv[k] = *(const uint32_t*)(vb + (long long)min(32 * rq + k, nr - 1) * p.vb_sr);
+      for (int k = 0; k < 32; ++k) vbv[k] = *(const uint32_t*)(vb + (long long)k * p.vb_sr);
+    } else {
+#pragma unroll
+      for (int k = 0; k < 32; ++k)
+        vbv[k] = *(const uint32_t*)(vb + (long long)max(min(k, kmax), -32 * rq) * p.vb_sr);
+    }
   }
 
   // weights: one wave per head
@@ -637,43 +643,50 @@ __global__ __launch_bounds__(256) void joint_merge_kernel(JMergeParams p) {
   if (wave + 4 < nh) weights(wave + 4, mv[1], lv[1]);
   __syncthreads();
 
-  // merged, normalised coefficients of the block
-  if (jc < nh) {
+  // merged, normalised coefficients of the block (rows of heads past nh: zeros)
+  if (jc < NH) {
     dkv_f32x4 a = {0.f, 0.f, 0.f, 0.f};
-    for (int s0 = 0;;) {
+    if (jc < nh) {
+      for (int s0 = 0;;) {
 #pragma unroll
-      for (int u = 0; u < 16; ++u) {
-        const float w = s0 + u < ns ? sWt[jc * ns + s0 + u] : 0.f;
-        a += w * x[u];
+        for (int u = 0; u < 16; ++u) {
+          const float w = s0 + u < ns ? sWt[jc * ns + s0 + u] : 0.f;
+          a += w * x[u];
+        }
+        s0 += 16;
+        if (s0 >= ns) break;
+        load_coef(s0);
       }
-      s0 += 16;
-      if (s0 >= ns) break;
-      load_coef(s0);
-    }
-    // ranks past the block's end (never written by the V pass) hold zeros
+      // ranks past the block's end (never written by the V pass) hold zeros
 #pragma unroll
-    for (int e = 0; e < 4; ++e) a[e] = 4 * q + e < nr ? a[e] : 0.f;
+      for (int e = 0; e < 4; ++e) a[e] = 4 * q + e < nr ? a[e] : 0.f;
+    }
     *(dkv_f32x4*)&sA[jc][4 * q] = a;
   }
   __syncthreads();
 
   // partial[j][d] = sum over the block's ranks of a[j][r] VB[r][d], per quarter of the block
-  float o0[JMH], o1[JMH];
+  float o0[NH], o1[NH];
 #pragma unroll
-  for (int j = 0; j < JMH; ++j) o0[j] = o1[j] = 0.f;
+  for (int j = 0; j < NH; ++j) o0[j] = o1[j] = 0.f;
 #pragma unroll
-  for (int k = 0; k < 32; ++k) {
-    const float v0 = dkv_elt_to_f32<DT>(vbv[k] & 0xffffu), v1 = dkv_elt_to_f32<DT>(vbv[k] >> 16);
+  for (int k4 = 0; k4 < 8; ++k4) {
+    dkv_f32x4 av[NH];
 #pragma unroll
-    for (int j = 0; j < JMH; ++j)
-      if (j < nh) {
-        const float a = sA[j][32 * rq + k];  // 0 past the block's end
-        o0[j] = fmaf(a, v0, o0[j]);
-        o1[j] = fmaf(a, v1, o1[j]);
+    for (int j = 0; j < NH; ++j) av[j] = *(const dkv_f32x4*)&sA[j][32 * rq + 4 * k4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t w = vbv[4 * k4 + e];
+      const float v0 = dkv_elt_to_f32<DT>(w & 0xffffu), v1 = dkv_elt_to_f32<DT>(w >> 16);
+#pragma unroll
+      for (int j = 0; j < NH; ++j) {  // a = 0 past the block's end and for absent heads
+        o0[j] = fmaf(av[j][e], v0, o0[j]);
+        o1[j] = fmaf(av[j][e], v1, o1[j]);
       }
+    }
   }
 #pragma unroll
-  for (int j = 0; j < JMH; ++j) {
+  for (int j = 0; j < NH; ++j) {
     sOut[rq][j][2 * dp] = o0[j];
     sOut[rq][j][2 * dp + 1] = o1[j];
   }
@@ -882,18 +895,39 @@ extern "C" int dkv_joint_av(void* stream, int mode, int scores_dtype, int dtype,
   const int hpg = Hq / n_basis;
   m.hpg = hpg;
   m.n_rb = n_rb;
-  const dim3 mgrid((unsigned)n_rb, (unsigned)(n_basis * ((hpg + JMH - 1) / JMH)), (unsigned)B);
-  const size_t wt_bytes = sizeof(float) * JMH * (size_t)ns;
+  const int nhm = hpg <= 4 ? 4 : 8;  // query heads merged and projected together
+  const dim3 mgrid((unsigned)n_rb, (unsigned)(n_basis * ((hpg + nhm - 1) / nhm)), (unsigned)B);
+  const size_t wt_bytes = sizeof(float) * nhm * (size_t)ns;
   if (dtype == DKV_BF16) {
     if (mode == 0)
-      hipLaunchKernelGGL((joint_merge_kernel<DKV_BF16, 0>), mgrid, dim3(256), wt_bytes, st, m);
+      {
+        if (nhm == 4)
+          hipLaunchKernelGGL((joint_merge_kernel<DKV_BF16, 0, 4>), mgrid, dim3(256), wt_bytes, st, m);
+        else
+          hipLaunchKernelGGL((joint_merge_kernel<DKV_BF16, 0, 8>), mgrid, dim3(256), wt_bytes, st, m);
+      }
     else
-      hipLaunchKernelGGL((joint_merge_kernel<DKV_BF16, 1>), mgrid, dim3(256), wt_bytes, st, m);
+      {
+        if (nhm == 4)
+          hipLaunchKernelGGL((joint_merge_kernel<DKV_BF16, 1, 4>), mgrid, dim3(256), wt_bytes, st, m);
+        else
+          hipLaunchKernelGGL((joint_merge_kernel<DKV_BF16, 1, 8>), mgrid, dim3(256), wt_bytes, st, m);
+      }
   } else {
     if (mode == 0)
-      hipLaunchKernelGGL((joint_merge_kernel<DKV_F16, 0>), mgrid, dim3(256), wt_bytes, st, m);
+      {
+        if (nhm == 4)
+          hipLaunchKernelGGL((joint_merge_kernel<DKV_F16, 0, 4>), mgrid, dim3(256), wt_bytes, st, m);
+        else
+          hipLaunchKernelGGL((joint_merge_kernel<DKV_F16, 0, 8>), mgrid, dim3(256), wt_bytes, st, m);
+      }
     else
-      hipLaunchKernelGGL((joint_merge_kernel<DKV_F16, 1>), mgrid, dim3(256), wt_bytes, st, m);
+      {
+        if (nhm == 4)
+          hipLaunchKernelGGL((joint_merge_kernel<DKV_F16, 1, 4>), mgrid, dim3(256), wt_bytes, st, m);
+        else
+          hipLaunchKernelGGL((joint_merge_kernel<DKV_F16, 1, 8>), mgrid, dim3(256), wt_bytes, st, m);
+      }
   }
   DKV_HIP_CHECK_LAUNCH();
   const dim3 pgrid((unsigned)Hq, (unsigned)B);
