@@ -356,7 +356,8 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_av_kernel(JAvParams p) {
   const __amdgpu_buffer_rsrc_t rz = dkv_make_rsrc(p.scores, p.sc_bytes);
   auto load_z = [&](int j, uint32_t(&z)[4]) {
     if constexpr (VEC) {
-      // tokens past the split read their neighbours (or zeros past the extent): replaced at use
+      // tokens past the split read their neighbours (zeros past the scores' last element, where
+      // the buffer range ends): replaced at use
       const uint32_t e = (uint32_t)(sbase + s_begin + 16 * j + 4 * g);
       if constexpr (SDT == DKV_F32) {
         const dkv_u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rz, e * 4u, 0, 0);
@@ -853,13 +854,17 @@ extern "C" int dkv_joint_av(void* stream, int mode, int scores_dtype, int dtype,
   a.n_splits = ns;
   a.split_len = sl;
   const dim3 agrid((unsigned)ns, (unsigned)((Hq + 15) / 16), (unsigned)B);
-  // vector score loads: token-contiguous rows whose starts are 4-element aligned, an extent
-  // that a 32-bit byte offset covers
+  // vector score loads: token-contiguous rows whose starts are 4-element aligned and a token
+  // count that is a multiple of 4, so each lane's group of 4 scores lies wholly inside or
+  // wholly past the scores' last element; the buffer range ends exactly at that element (the
+  // prefetch of tiles past the last row's end returns zeros and touches no memory), within
+  // what a 32-bit byte offset covers
   const int sc_elt = scores_dtype == DKV_F32 ? 4 : 2;
   const long long sc_extent =
-      ((long long)(B - 1) * sc_sb + (long long)(Hq - 1) * sc_sh + S + 4) * sc_elt;
-  const bool vec = sc_ss == 1 && sc_sb % 4 == 0 && sc_sh % 4 == 0 && sc_sb >= 0 && sc_sh >= 0 &&
-                   ((uintptr_t)scores % (4 * sc_elt)) == 0 && sc_extent < (1LL << 31);
+      ((long long)(B - 1) * sc_sb + (long long)(Hq - 1) * sc_sh + (long long)S) * sc_elt;
+  const bool vec = sc_ss == 1 && S % 4 == 0 && sc_sb % 4 == 0 && sc_sh % 4 == 0 && sc_sb >= 0 &&
+                   sc_sh >= 0 && ((uintptr_t)scores % (4 * sc_elt)) == 0 &&
+                   sc_extent < (1LL << 31);
   a.sc_bytes = vec ? (uint32_t)sc_extent : 0u;
 #define DKV_JA_LAUNCH(DT_, SDT_)                                                            \
   do {                                                                                      \
