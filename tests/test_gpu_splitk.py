@@ -73,6 +73,25 @@ def test_split_length_invariance(dev, route):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("route", ROUTES)
+def test_keys_beyond_fp16_range_bf16(dev, route):
+    """bf16 keys whose values lie far past fp16's range (coefficients scaled by 2^17, |K'| up to
+    ~6e5) with the queries scaled by 2^-17: the scores are those of the unscaled case (the power
+    of two commutes with every rounding), so a kernel that narrowed K' or q to fp16 would give
+    inf/NaN scores here while the reference's fp32 dot product stays finite."""
+    print(f"[gpu] splitk keys beyond fp16 range route={route}", flush=True)
+    case = make_case(B=2, G=8, Hq=32, S=700, mean=0.29, force_first=4, force_frac=0.05, seed=33)
+    case.k_coef = case.k_coef * np.float32(2.0 ** 17)
+    case.q = case.q * np.float32(2.0 ** -17)
+    p = packed_from_case(case, torch.bfloat16, dev)
+    assert p["k_flat"].float().abs().max().item() > 4 * 65504
+    got = _run(p, case, route)
+    assert torch.isfinite(got).all()
+    ref = oracle_grouped(case, p["host"], route, "bfloat16")
+    assert_close(got, ref, f"keys beyond fp16 range {route}")
+
+
+@pytest.mark.gpu
 def test_all_keys_empty_in_one_row(dev):
     print("[gpu] splitk empty-key row", flush=True)
     case = make_case(B=2, G=2, Hq=8, S=150, uniform=(1, 128), seed=31)
