@@ -504,6 +504,10 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
   // R(n) of every lane's token slot, in lane order: entry [2*pp + k][lane] holds (cos, sin) of
   // the lane's frequencies 16*pp + 4*g + 2k and + 1 (one conflict-free 16-byte read per lane)
   __shared__ __attribute__((aligned(16))) dkv_f32x4 sRn[8][64];
+  // the unit's query pairs per lane (qh, below) and the rotation step of the per-tile query
+  // rotation, read per tile instead of held in registers (the same for every wave)
+  __shared__ __attribute__((aligned(16))) dkv_u32x4 sQh[(HMAX + 3) / 4][64];
+  __shared__ __attribute__((aligned(8))) float sStep[64][2];
   // 256-byte aligned: the query operand's row swizzle XORs bits 4..7 of ring addresses
   __shared__ __attribute__((aligned(256))) uint8_t sRing[WAVES * NSLOT * GSLOT_BYTES];
   static_assert(DH * BK_LD * 2 <= WAVES * NSLOT * GSLOT_BYTES, "basis staging fits the rings");
@@ -607,6 +611,15 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
       const long long o = qo + (h < p.hpg ? h : 0) * p.q_sh;
       const uint32_t v = (uint32_t)p.q[o] | ((uint32_t)p.q[o + 64] << 16);
       qh[h] = h < p.hpg ? v : 0u;
+    }
+    if (wave == 0) {
+#pragma unroll
+      for (int k = 0; k < (QH + 3) / 4; ++k)
+        sQh[k][lane] = dkv_u32x4{qh[4 * k], 4 * k + 1 < QH ? qh[4 * k + 1] : 0u,
+                                 4 * k + 2 < QH ? qh[4 * k + 2] : 0u,
+                                 4 * k + 3 < QH ? qh[4 * k + 3] : 0u};
+      sStep[lane][0] = p.rope[TILE * 128 + 2 * lane];
+      sStep[lane][1] = p.rope[TILE * 128 + 2 * lane + 1];
     }
   }
   // R(n) table in LDS (see sRn): thread t fills entry t (8 x 64 entries, 512 threads)
@@ -746,23 +759,17 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
   // scale (the fused route's scores come out in log2 units, the two-stage route's in natural
   // units), advanced by angle addition (WAVES*TILE positions per tile); bc/bs start at the
   // table's exact value for the wave's first tile
-  float bc, bs, stc, sts;
+  float bc, bs;
   {
     const int t = min(tile0, n_tb - 1);
     const float* row = p.rope + (long long)(ROPE_FIXED_ROWS + t) * 128 + 2 * lane;
     bc = row[0] * p.score_scale;
     bs = row[1] * p.score_scale;
-    stc = p.rope[TILE * 128 + 2 * lane];
-    sts = p.rope[TILE * 128 + 2 * lane + 1];
   }
   // loop-invariant loaded values: settled here, so the loop carries no wait for their loads
   // (such a wait would also drain the gathers in flight)
   settle(bc);
   settle(bs);
-  settle(stc);
-  settle(sts);
-#pragma unroll
-  for (int h = 0; h < QH; ++h) settle(qh[h]);
 
   // T0 and T1 (a full wait: compiler-generated memory operations of the prologue, such as
   // register spill stores, may lie between them and here and need not complete in order)
@@ -812,11 +819,21 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
       // formed per tile (not hoisted as one register per row)
       uint32_t wr = q_wr + (uint32_t)(par * GSLOT_BYTES);
       settle(wr);
+      uint32_t qv[4 * ((QH + 3) / 4)];
+#pragma unroll
+      for (int k = 0; k < (QH + 3) / 4; ++k) {
+        const dkv_u32x4 v = sQh[k][lane];
+        qv[4 * k] = v.x;
+        qv[4 * k + 1] = v.y;
+        qv[4 * k + 2] = v.z;
+        qv[4 * k + 3] = v.w;
+      }
       auto rotate = [&](int h, uint32_t& hi, uint32_t& lo) {
-        const float x = elt_to_f32<DT>(qh[h] & 0xffffu), y = elt_to_f32<DT>(qh[h] >> 16);
+        const float x = elt_to_f32<DT>(qv[h] & 0xffffu), y = elt_to_f32<DT>(qv[h] >> 16);
         split_bf16x2(cb * x + sb * y, cb * y - sb * x, hi, lo);
       };
       // the next tile's base rotation
+      const float stc = sStep[lane][0], sts = sStep[lane][1];
       bc = cb * stc - sb * sts;
       bs = sb * stc + cb * sts;
       auto put = [&](uint32_t v, int r) {
