@@ -4,7 +4,8 @@
 // Work unit: (batch b, KV head k) with hpg query heads sharing K/V basis k; its packed
 // coefficients are cache row b*G + k/(Hkv/G). A workgroup (8 waves, one per CU) owns one unit
 // and one contiguous token range ("split", a multiple of 64 tokens); waves take 16-token tiles
-// round-robin.
+// round-robin, or, in splits of at least 16 tiles, pairs of consecutive tiles that share the
+// per-tile query operand (the second tile's token slots rotated by R(16 + n)).
 //
 // Prologue: the K basis goes to registers (MFMA A operands; NREG_PP < 4 keeps part of it in
 // LDS instead, [dim][rank], read per tile), the mask table and the table of every lane's fixed
@@ -490,7 +491,7 @@ __device__ __forceinline__ void merge_unit(const SplitParams& p, int unit, uint8
 // heads (WIDE) the query operand carries the heads' hi parts in its 16 columns and a second
 // product takes the lo parts; with up to 8 heads the hi parts sit in columns 0..7 and the lo
 // parts in columns 8..15 of one product.
-template <int DT, int ROUTE, int HMAX>
+template <int DT, int ROUTE, int HMAX, bool PAIR>
 __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
   constexpr bool WIDE = HMAX > 8;
   // LDS: per-wave rings (NSLOT gather slots: K then V, 4 chunks x 64 lanes x 16 bytes each;
@@ -504,10 +505,12 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
   // R(n) of every lane's token slot, in lane order: entry [2*pp + k][lane] holds (cos, sin) of
   // the lane's frequencies 16*pp + 4*g + 2k and + 1 (one conflict-free 16-byte read per lane)
   __shared__ __attribute__((aligned(16))) dkv_f32x4 sRn[8][64];
+  // R(16 + n): the token slots of the second tile of a wave's pair (same layout as sRn)
+  __shared__ __attribute__((aligned(16))) dkv_f32x4 sRn2[8][64];
   // the unit's query pairs per lane (qh, below) and the rotation step of the per-tile query
   // rotation, read per tile instead of held in registers (the same for every wave)
   __shared__ __attribute__((aligned(16))) dkv_u32x4 sQh[(HMAX + 3) / 4][64];
-  __shared__ __attribute__((aligned(8))) float sStep[64][2];
+  __shared__ __attribute__((aligned(16))) float sStep[64][4];
   // 256-byte aligned: the query operand's row swizzle XORs bits 4..7 of ring addresses
   __shared__ __attribute__((aligned(256))) uint8_t sRing[WAVES * NSLOT * GSLOT_BYTES];
   static_assert(DH * BK_LD * 2 <= WAVES * NSLOT * GSLOT_BYTES, "basis staging fits the rings");
@@ -541,9 +544,20 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
   const int ns = s_end - s_begin;
 
   const int tile_first = s_begin / TILE;  // splits are whole tiles (multiples of 64 tokens)
-  const int tile0 = tile_first + wave;
+  // PAIR: a wave takes pairs of consecutive tiles (2*wave, 2*wave + 1, then 16 tiles on), which
+  // share one query operand (the second tile's token slots use R(16 + n)); otherwise waves
+  // take single tiles round-robin. The host pairs splits of at least 2 * WAVES tiles, where
+  // both schemes give every wave the same number of tiles.
+  const int n_tiles = (ns + TILE - 1) / TILE;
+  constexpr bool paired = PAIR;
+  const int tile0 = tile_first + (paired ? 2 * wave : wave);
+  auto tix = [&](int j) {
+    return paired ? tile0 + (j & 1) + 2 * WAVES * (j >> 1) : tile0 + WAVES * j;
+  };
   const int n_tb = (p.S + TILE - 1) / TILE;
-  const int n_iter = max(0, ((ns + TILE - 1) / TILE - wave + WAVES - 1) / WAVES);
+  const int n_iter = paired ? 2 * (n_tiles / (2 * WAVES)) +
+                                   max(0, min(2, n_tiles % (2 * WAVES) - 2 * wave))
+                             : max(0, (n_tiles - wave + WAVES - 1) / WAVES);
   // table loads: lane (table l/16, token l%16) -> one 4-byte load per lane and tile
   const int* tab_base;
   int tab_ss;
@@ -555,7 +569,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
     tab_ss = tsel < 2 ? (int)p.tk_ss : (int)p.tv_ss;
   }
   auto load_tab = [&](int j) {  // one load per lane into table slot j % TSLOT
-    const uint32_t t = (uint32_t)min((tile0 + WAVES * j) * TILE + n, s_end - 1);
+    const uint32_t t = (uint32_t)min(tix(j) * TILE + n, s_end - 1);
     lds_load4(tab_base + __umul24(t, (uint32_t)tab_ss), lds_addr(&sTabRing[wave][j % TSLOT][0][0]));
   };
   // the first two tiles' tables (the table ring does not alias the staging copy) are in
@@ -618,8 +632,13 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
         sQh[k][lane] = dkv_u32x4{qh[4 * k], 4 * k + 1 < QH ? qh[4 * k + 1] : 0u,
                                  4 * k + 2 < QH ? qh[4 * k + 2] : 0u,
                                  4 * k + 3 < QH ? qh[4 * k + 3] : 0u};
-      sStep[lane][0] = p.rope[TILE * 128 + 2 * lane];
-      sStep[lane][1] = p.rope[TILE * 128 + 2 * lane + 1];
+      // the rotation by WAVES * TILE positions (single tiles) and by twice that (pairs),
+      // R(128) doubled
+      const float c = p.rope[TILE * 128 + 2 * lane], sn = p.rope[TILE * 128 + 2 * lane + 1];
+      sStep[lane][0] = c;
+      sStep[lane][1] = sn;
+      sStep[lane][2] = c * c - sn * sn;
+      sStep[lane][3] = 2.f * c * sn;
     }
   }
   // R(n) table in LDS (see sRn): thread t fills entry t (8 x 64 entries, 512 threads)
@@ -628,6 +647,20 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
     const int nn = ln & 15, gg = ln >> 4, i0 = 16 * (k >> 1) + 4 * gg + 2 * (k & 1);
     const float* delt = p.rope + (long long)nn * 128 + 2 * i0;
     sRn[k][ln] = dkv_f32x4{delt[0], delt[1], delt[2], delt[3]};
+    // R(16) = R(15) R(1) by angle addition, then R(16 + n) = R(16) R(n)
+    if constexpr (PAIR) {
+    const float* r15 = p.rope + 15 * 128 + 2 * i0;
+    const float* r1 = p.rope + 1 * 128 + 2 * i0;
+    float o[4];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const float c16 = r15[2 * e] * r1[2 * e] - r15[2 * e + 1] * r1[2 * e + 1];
+      const float s16 = r15[2 * e + 1] * r1[2 * e] + r15[2 * e] * r1[2 * e + 1];
+      o[2 * e] = c16 * delt[2 * e] - s16 * delt[2 * e + 1];
+      o[2 * e + 1] = s16 * delt[2 * e] + c16 * delt[2 * e + 1];
+    }
+    sRn2[k][ln] = dkv_f32x4{o[0], o[1], o[2], o[3]};
+    }
   }
   // The per-tile query operand lives in the K half of the tile's gather slot once the K
   // coefficients are in registers: row r (one per operand column), chunk c (16 bytes: dwords
@@ -776,7 +809,8 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
   wait_vm<0>();
   issue(0);
 
-  // one tile; par = j % NSLOT
+  dkv_u32x4 bq[4], bq_lo[4];  // the query operand of the wave's current pair of tiles
+  // one tile; par = j % NSLOT (par 0: the first tile of a pair, which forms the query operand)
   auto tile = [&](int j, const int par) {
     wait_vm<0>();  // G(j), T(j+1)
     const Tok cur = tok_of(j);
@@ -813,8 +847,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
     // ---- query of this tile: R(-16T) q times the score scale, as bf16 hi + lo, written to the
     //      K half of the slot (its coefficients are in xk; LDS accesses of a wave run in order)
     //      and read back as the B operand of the score MFMAs (lane: column n, k-group g) ----
-    dkv_u32x4 bq[4], bq_lo[4];
-    {
+    if (par == 0 || !paired) {
       const float cb = bc, sb = bs;
       // formed per tile (not hoisted as one register per row)
       uint32_t wr = q_wr + (uint32_t)(par * GSLOT_BYTES);
@@ -833,7 +866,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
         split_bf16x2(cb * x + sb * y, cb * y - sb * x, hi, lo);
       };
       // the next tile's base rotation
-      const float stc = sStep[lane][0], sts = sStep[lane][1];
+      const float stc = sStep[lane][paired ? 2 : 0], sts = sStep[lane][paired ? 3 : 1];
       bc = cb * stc - sb * sts;
       bs = sb * stc + cb * sts;
       auto put = [&](uint32_t v, int r) {
@@ -906,6 +939,8 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
         }
       }
     };
+    // R(n), or R(16 + n) for the second tile of a pair
+    const dkv_f32x4(*rtab)[64] = (par == 1 && paired) ? sRn2 : sRn;
     // software-pipelined by one block pair: the products of pp+1 are issued before the
     // rotation of pp, so the MFMA pipe and the VALU work of one wave overlap
     __builtin_amdgcn_s_setprio(0);
@@ -918,7 +953,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
       // K' rotated in fp32 and split into bf16 hi + lo parts: the score products are
       // (K'hi + K'lo) . (q hi + q lo) to ~16 bits per factor, with fp32's range
       uint32_t kh[4], kl[4];
-      const dkv_f32x4 r01 = sRn[2 * pp][lane], r23 = sRn[2 * pp + 1][lane];
+      const dkv_f32x4 r01 = rtab[2 * pp][lane], r23 = rtab[2 * pp + 1][lane];
       const float rc[4] = {r01.x, r01.z, r23.x, r23.z}, rs[4] = {r01.y, r01.w, r23.y, r23.w};
 #pragma unroll
       for (int w = 0; w < 4; ++w)
@@ -953,7 +988,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
         else
           z[u] = dkv_round_to<DT>(has ? sc[u] : p.masked_score);
       }
-      const int nvalid = s_end - (tile0 + WAVES * j) * TILE;  // tokens of the tile in range
+      const int nvalid = s_end - tix(j) * TILE;  // tokens of the tile in range
       if (__builtin_expect(nvalid < TILE, 0)) {  // wave-uniform: the split's last tile
 #pragma unroll
         for (int u = 0; u < 4; ++u)
@@ -1339,12 +1374,19 @@ static void launch_splitk_t(const SplitParams& p, int out_dtype, dim3 grid, dim3
   const int slot = (g_prof.on && g_prof.n < g_prof.cap) ? g_prof.n++ : -1;
   hipEvent_t* ev = slot >= 0 ? g_prof.ev + 3 * slot : nullptr;
   if (ev) (void)hipEventRecord(ev[0], st);
+  // tile pairs for splits of at least 2 * WAVES tiles (up to 8 heads per unit: with 16 the
+  // pair's query operand of hi and lo rows would add spills)
+  const bool pair = p.split_len >= 2 * WAVES * TILE;
   if (p.hpg > 8)
-    hipLaunchKernelGGL((splitk_kernel<DT, RT, 16>), grid, dim3(NTHREADS), 0, st, p);
+    hipLaunchKernelGGL((splitk_kernel<DT, RT, 16, false>), grid, dim3(NTHREADS), 0, st, p);
+  else if (p.hpg > 4 && pair)
+    hipLaunchKernelGGL((splitk_kernel<DT, RT, 8, true>), grid, dim3(NTHREADS), 0, st, p);
   else if (p.hpg > 4)
-    hipLaunchKernelGGL((splitk_kernel<DT, RT, 8>), grid, dim3(NTHREADS), 0, st, p);
+    hipLaunchKernelGGL((splitk_kernel<DT, RT, 8, false>), grid, dim3(NTHREADS), 0, st, p);
+  else if (pair)
+    hipLaunchKernelGGL((splitk_kernel<DT, RT, 4, true>), grid, dim3(NTHREADS), 0, st, p);
   else
-    hipLaunchKernelGGL((splitk_kernel<DT, RT, 4>), grid, dim3(NTHREADS), 0, st, p);
+    hipLaunchKernelGGL((splitk_kernel<DT, RT, 4, false>), grid, dim3(NTHREADS), 0, st, p);
   if (ev) (void)hipEventRecord(ev[1], st);
   if (!p.fused_merge) {
     if (out_dtype == DKV_F32)
