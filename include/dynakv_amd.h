@@ -233,7 +233,8 @@ int dkv_rope_table(void* stream, float* rope, int from_tile, int to_tile, float 
  * Hkv % G == 0, flat row strides k_ld, v_ld <= 0x3fffffe8 elements (each workgroup addresses
  * the buffer from its own row, so the number of rows is not limited), S and the table token
  * strides < 2^24 with S * table token stride < 2^31. split_len is a multiple of 64
- * (0 = dkv_splitk_choose_split: about one workgroup per CU).
+ * (0 = dkv_splitk_choose_split: about one workgroup per CU, at least 128 tokens per split when
+ * the cache is that long). Splits of 256 tokens or more run their waves on pairs of tiles.
  */
 long long dkv_splitk_workspace_floats(int B, int Hq, int Hkv, int S, int R, int split_len);
 int dkv_splitk_choose_split(int B, int Hkv, int S);
