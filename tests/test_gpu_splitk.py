@@ -74,6 +74,24 @@ def test_split_length_invariance(dev, route):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("route", ROUTES)
+@pytest.mark.parametrize("S,split_len", [(976, 320), (1009, 256), (4097, 256), (250, 128)])
+def test_tile_pair_edges_against_oracle(dev, route, S, split_len):
+    """Splits of 256+ tokens run their waves on pairs of consecutive tiles (the second tile's
+    keys rotated by R(16 + n) under the first tile's query operand). Edge cases of that mapping
+    against the oracle: a last split of a single tile (976 = 3 x 320 + 16), a ragged last tile
+    (1009), a one-token last split (4097 = 16 x 256 + 1), and a cache short enough for single
+    tiles (250 tokens in 128-token splits)."""
+    print(f"[gpu] splitk tile-pair edges S={S} split_len={split_len} route={route}", flush=True)
+    case = make_case(B=2, G=8, Hq=32, S=S, mean=0.29, force_first=4, force_frac=0.05,
+                     seed=40 + S % 97)
+    p = packed_from_case(case, torch.bfloat16, dev)
+    got = _run(p, case, route, split_len)
+    ref = oracle_grouped(case, p["host"], route, "bfloat16")
+    assert_close(got, ref, f"tile pairs S={S} split_len={split_len} {route}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("route", ROUTES)
 def test_keys_beyond_fp16_range_bf16(dev, route):
     """bf16 keys whose values lie far past fp16's range (coefficients scaled by 2^17, |K'| up to
     ~6e5) with the queries scaled by 2^-17: the scores are those of the unscaled case (the power
