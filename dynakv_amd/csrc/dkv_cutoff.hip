@@ -116,6 +116,49 @@ __global__ __launch_bounds__(256) void cutoff_logits_kernel(CutoffParams p) {
                   blockIdx.x * CT_COLS + wave * 16, lane);
 }
 
+// Split-K logits for wide heads (D = 128 * STEPS, the joint 1024-d head: STEPS = 8): grid
+// (D / 16, ceil(M / 16), 2 * G), one workgroup per 16 logits of 16 rows; wave w takes the
+// quarter w of the input dimension, issues every operand load of its STEPS k-steps before the
+// first product, and the four partial sums are added in wave order through LDS (one memory
+// round trip per workgroup instead of one per k-step, four times the workgroups of
+// cutoff_logits_kernel).
+template <int DT, int STEPS>
+__global__ __launch_bounds__(256) void cutoff_logits_ks_kernel(CutoffParams p) {
+  __shared__ dkv_f32x4 sP[4][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int mat = blockIdx.z & 1, g = blockIdx.z >> 1;
+  const int row0 = blockIdx.y * CT_ROWS, n0 = blockIdx.x * 16;
+  const int i = lane & 15, kg = lane >> 4;
+  const CutoffMat& cm = p.mat[mat];
+  const int D = p.D;
+  const int k0 = wave * STEPS * 32;
+  const int xrow = min(row0 + i, p.M - 1);  // rows past M compute a copy of the last row
+  const uint16_t* xa = cm.x + (long long)xrow * p.x_ld + (long long)g * D + k0 + 8 * kg;
+  const uint16_t* wb = cm.wt + ((long long)g * D + n0 + i) * D + k0 + 8 * kg;
+  dkv_u32x4 a[STEPS], b[STEPS];
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s) {
+    a[s] = *(const dkv_u32x4*)(xa + 32 * s);
+    b[s] = *(const dkv_u32x4*)(wb + 32 * s);
+  }
+  dkv_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s) acc = mfma_16x16x32<DT>(a[s], b[s], acc);
+  sP[wave][lane] = acc;
+  __syncthreads();
+  if (wave == 0) {
+    dkv_f32x4 t = sP[0][lane];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) t += sP[w][lane];
+    const float bias = elt_f32<DT>(cm.b[(long long)g * D + n0 + i]);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int m = row0 + 4 * kg + u;
+      if (m < p.M) cm.logits[((long long)m * p.G + g) * D + n0 + i] = f32_elt<DT>(t[u] + bias);
+    }
+  }
+}
+
 // The retained count of one (row m, group g) of a matrix, computed by one wave from the
 // row's rounded logits (global workspace or LDS). Lane l owns the E = D / 64 consecutive
 // positions l*E .. l*E + E - 1 of the row.
@@ -125,8 +168,20 @@ __device__ __forceinline__ int cutoff_row_len(const CutoffParams& p, const uint1
   const uint16_t* lg = row + lane * E;
 
   float x[E];
+  if constexpr (E >= 8) {
+    // 16-byte loads (the row and each lane's E elements are 16-byte aligned)
 #pragma unroll
-  for (int e = 0; e < E; ++e) x[e] = elt_f32<DT>(lg[e]);
+    for (int v = 0; v < E / 8; ++v) {
+      const dkv_u32x4 w = *(const dkv_u32x4*)(lg + 8 * v);
+      const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        x[8 * v + e] = elt_f32<DT>((uint16_t)(ww[e >> 1] >> (16 * (e & 1))));
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < E; ++e) x[e] = elt_f32<DT>(lg[e]);
+  }
   float mx = x[0];
 #pragma unroll
   for (int e = 1; e < E; ++e) mx = fmaxf(mx, x[e]);
@@ -164,6 +219,20 @@ __device__ __forceinline__ void row_task(const CutoffParams& p, int mat, long lo
 
   const uint16_t* xs = cm.x + (long long)m * p.x_ld + (long long)g * D + lane * E;
   uint16_t* xo = cm.out + (long long)m * p.out_ld + (long long)g * D + lane * E;
+  uint16_t xv[E];
+  if constexpr (E >= 8) {
+    // 16-byte loads of the input (x rows are 16-byte aligned: checked by the host)
+#pragma unroll
+    for (int v = 0; v < E / 8; ++v) {
+      const dkv_u32x4 w = *(const dkv_u32x4*)(xs + 8 * v);
+      const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xv[8 * v + e] = (uint16_t)(ww[e >> 1] >> (16 * (e & 1)));
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < E; ++e) xv[e] = xs[e];
+  }
   // x * 1 or x * 0 in the compute dtype, written out bitwise: x * 0 is a zero with x's sign,
   // or NaN for an infinite or NaN x (a multiply would do the same, but the compiler may turn
   // it into an fma with a +0 addend, which loses the sign of -0)
@@ -171,7 +240,7 @@ __device__ __forceinline__ void row_task(const CutoffParams& p, int mat, long lo
   constexpr uint16_t QNAN = DT == DKV_BF16 ? 0x7fc0 : 0x7e00;
 #pragma unroll
   for (int e = 0; e < E; ++e) {
-    const uint16_t xb = xs[e];
+    const uint16_t xb = xv[e];
     const uint16_t zb = (xb & EXP) == EXP ? QNAN : (uint16_t)(xb & 0x8000);
     xo[e] = lane * E + e < len ? xb : zb;
   }
@@ -390,6 +459,32 @@ __global__ __launch_bounds__(64 * CS_WAVES) void cutoff_layer_small_kernel(TailP
     dkv_rope_pair<DT>(t.q + (qr / t.Hq) * t.q_sb + (qr % t.Hq) * 128, lane, t.pos, t.log_theta);
 }
 
+// the logits of every (row, group, K|V) into the workspace: split-K for D of 256 and more
+void launch_logits(const CutoffParams& p, int dtype, hipStream_t st) {
+  const int D = p.D, M = p.M, G = p.G;
+  const unsigned gy = (unsigned)((M + CT_ROWS - 1) / CT_ROWS), gz = (unsigned)(2 * G);
+#define DKV_LKS(STEPS_)                                                                        \
+  do {                                                                                         \
+    if (dtype == DKV_BF16)                                                                     \
+      hipLaunchKernelGGL((cutoff_logits_ks_kernel<DKV_BF16, STEPS_>), dim3(D / 16, gy, gz),    \
+                         dim3(256), 0, st, p);                                                 \
+    else                                                                                       \
+      hipLaunchKernelGGL((cutoff_logits_ks_kernel<DKV_F16, STEPS_>), dim3(D / 16, gy, gz),     \
+                         dim3(256), 0, st, p);                                                 \
+  } while (0)
+  if (D == 1024)
+    DKV_LKS(8);
+  else if (D == 512)
+    DKV_LKS(4);
+  else if (D == 256)
+    DKV_LKS(2);
+  else if (dtype == DKV_BF16)
+    hipLaunchKernelGGL(cutoff_logits_kernel<DKV_BF16>, dim3(D / CT_COLS, gy, gz), dim3(256), 0, st, p);
+  else
+    hipLaunchKernelGGL(cutoff_logits_kernel<DKV_F16>, dim3(D / CT_COLS, gy, gz), dim3(256), 0, st, p);
+#undef DKV_LKS
+}
+
 template <int DT, int E>
 void launch_rows(const CutoffParams& p, hipStream_t st) {
   const long long tasks = 2LL * p.M * p.G;
@@ -463,11 +558,7 @@ extern "C" int dkv_cutoff_kv(void* stream, int dtype, const void* xk, const void
     DKV_HIP_CHECK_LAUNCH();
     return DKV_OK;
   }
-  const dim3 lgrid(D / CT_COLS, (M + CT_ROWS - 1) / CT_ROWS, 2 * G);
-  if (dtype == DKV_BF16)
-    hipLaunchKernelGGL(cutoff_logits_kernel<DKV_BF16>, lgrid, dim3(256), 0, st, p);
-  else
-    hipLaunchKernelGGL(cutoff_logits_kernel<DKV_F16>, lgrid, dim3(256), 0, st, p);
+  launch_logits(p, dtype, st);
   DKV_HIP_CHECK_LAUNCH();
 #define DKV_ROWS_CASE(e)                                        \
   case e:                                                       \
