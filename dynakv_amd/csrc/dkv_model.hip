@@ -177,6 +177,7 @@ namespace {
 
 constexpr int GV_WAVES = 4;
 constexpr int GV_ROWS = 4;
+constexpr int GV_UNROLL = 4;  // k-steps per batch of loads (K-split instances)
 
 template <int DT>
 __device__ __forceinline__ float dot8(const dkv_u32x4& a, const dkv_u32x4& b, float c) {
@@ -298,7 +299,33 @@ __global__ __launch_bounds__(GV_WAVES * 64) void gemv_kernel(
     const uint16_t* wr[GV_ROWS];
 #pragma unroll
     for (int r = 0; r < GV_ROWS; ++r) wr[r] = W + (long long)min(n0 + r, N - 1) * w_ld;
-    for (int k = kb + 8 * lane; k < ke; k += 512) {
+    int k = kb + 8 * lane;
+    if constexpr (KSPLIT) {
+      // batches of GV_UNROLL k-steps: every weight load of a batch is issued before its first
+      // product (the products keep the k order, so results are unchanged). Measured on MI355X
+      // with cold weights: the long K-split rows gain (down, K = 14336, at 4 rows: 28.0 ->
+      // 25.0 us), the 4096-wide ones are unchanged, and the shapes with a block per wave
+      // (gate/up) lose, so only the K-split instances batch.
+      for (; k + (GV_UNROLL - 1) * 512 < ke; k += GV_UNROLL * 512) {
+        dkv_u32x4 wv[GV_UNROLL][GV_ROWS];
+#pragma unroll
+        for (int u = 0; u < GV_UNROLL; ++u)
+#pragma unroll
+          for (int r = 0; r < GV_ROWS; ++r)
+            wv[u][r] = __builtin_nontemporal_load((const dkv_u32x4*)(wr[r] + k + 512 * u));
+#pragma unroll
+        for (int u = 0; u < GV_UNROLL; ++u)
+#pragma unroll
+          for (int m = 0; m < M; ++m) {
+            const int kk = k + 512 * u;
+            const dkv_u32x4 xv = XLDS ? *(const dkv_u32x4*)(sx + m * K + kk)
+                                      : *(const dkv_u32x4*)(x + (long long)m * x_ld + kk);
+#pragma unroll
+            for (int r = 0; r < GV_ROWS; ++r) acc[r][m] = dot8<DT>(wv[u][r], xv, acc[r][m]);
+          }
+      }
+    }
+    for (; k < ke; k += 512) {
       dkv_u32x4 wv[GV_ROWS];
 #pragma unroll
       for (int r = 0; r < GV_ROWS; ++r)
