@@ -9,8 +9,10 @@
 // in 32-rank chunks, [chunk][dim][rank], a RoPE table, a workspace for the V pass) and compute
 // the same results to fp32 accuracy:
 //
-// joint_scores_kernel -- workgroup = (512 tokens, basis head h, batch row b); wave w takes 64
-//   tokens (4 column blocks of 16). K^T[128 x 64] = B_h^T . X^T accumulates on 16x16x32 MFMA over
+// joint_scores_kernel -- workgroup = (512 tokens, basis head h, batch row b), or with the heads
+//   in pairs (256 tokens, heads 2h and 2h+1, b) so that each coefficient load serves both heads'
+//   products; wave w takes 64 tokens (4 column blocks of 16) of its head, or 32 tokens of both.
+//   K^T[128 x 64] = B_h^T . X^T accumulates on 16x16x32 MFMA over
 //   the rank chunks of 32 that the block's longest token needs. Each basis chunk ([128 dims][32
 //   ranks], 8 KB contiguous in HBM) is loaded once per workgroup into LDS (two buffers) and every
 //   A operand read
@@ -77,36 +79,42 @@ struct JScoresParams {
   float scale;
 };
 
-template <int DT, int MODE, int ODT>
+// NHB basis heads per workgroup (1 or 2): with 2, a workgroup takes 256 tokens of two heads
+// (each wave 32 tokens of both), so every coefficient load serves both heads' products
+template <int DT, int MODE, int ODT, int NHB>
 __global__ __launch_bounds__(JTHREADS, 1) void joint_scores_kernel(JScoresParams p) {
+  constexpr int CB = JCB / NHB;            // 16-token column blocks per wave
+  constexpr int TOK = JWAVES * CB * 16;    // tokens per workgroup
   // basis chunk buffers: piece (dim d, ranks 8k..8k+7) at index 4d + (k ^ jswz(d)): the 16 rows
   // one k-group reads land in 16 different 16-byte bank groups of a 256-byte span, and any 8
   // aligned ones in 8 different groups of a 128-byte span
-  __shared__ __attribute__((aligned(16))) dkv_u32x4 sB[2][JDH * JCH / 8];
+  __shared__ __attribute__((aligned(16))) dkv_u32x4 sB[2][NHB][JDH * JCH / 8];
   // R(n) of every lane's token slot: [2*pp + k][lane] holds (cos, sin) of frequencies
   // 16pp + 4g + 2k and + 1
   __shared__ __attribute__((aligned(16))) dkv_f32x4 sRn[8][64];
   // per-wave query operand: row r (column r of the score product: head r's hi part for r < 8,
   // head r-8's lo part), dword i = frequency i, 16-byte chunk c stored at chunk position c ^ r
   __shared__ __attribute__((aligned(16))) uint32_t sQ[JWAVES][16 * 64];
-  __shared__ int sLen[JTOK], sOff[JTOK];
+  __shared__ int sLen[TOK], sOff[TOK];
   __shared__ int sMax[JWAVES];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15, g = lane >> 4;
-  const int t0 = blockIdx.x * JTOK, h = blockIdx.y, b = blockIdx.z;
+  const int t0 = blockIdx.x * TOK, h0 = blockIdx.y * NHB, b = blockIdx.z;
 
   {
     const int t = t0 + tid;
     int len = 0, off = 0;
-    if (t < p.S) {
+    if (tid < TOK && t < p.S) {
       len = p.lens[(long long)b * p.lens_sb + (long long)t * p.lens_ss];
       off = p.offs[(long long)b * p.offs_sb + (long long)t * p.offs_ss];
     }
     len = min(max(len, 0), p.R);
-    sLen[tid] = len;
-    sOff[tid] = off;
+    if (tid < TOK) {
+      sLen[tid] = len;
+      sOff[tid] = off;
+    }
     const int m = dkv_wave_max_i(len);
     if (lane == 0) sMax[wave] = m;
   }
@@ -127,15 +135,15 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_scores_kernel(JScoresParams
   const __amdgpu_buffer_rsrc_t rs = dkv_make_rsrc(p.flat + (long long)b * p.flat_ld, end * 2u);
   // this thread's basis piece of every chunk: dim bd, ranks 8*bk .. +8 of the chunk
   const int bd = tid >> 2, bk = (tid & 3) ^ jswz(bd);
-  const uint16_t* bsrc = p.bt + (long long)h * p.bt_sh + (long long)bd * JCH + 8 * bk;
+  const uint16_t* bsrc = p.bt + (long long)h0 * p.bt_sh + (long long)bd * JCH + 8 * bk;
 
-  int tlen[JCB], toff[JCB];
+  int tlen[CB], toff[CB];
   // bit c of pmask[cb]: some lane of column block cb has its count ending inside its 8 ranks of
   // chunk c. Only those chunks need the loaded pieces masked: past a count, loads read zeros.
-  uint32_t pmask[JCB];
+  uint32_t pmask[CB];
 #pragma unroll
-  for (int cb = 0; cb < JCB; ++cb) {
-    const int tl = 64 * wave + 16 * cb + n;
+  for (int cb = 0; cb < CB; ++cb) {
+    const int tl = 16 * CB * wave + 16 * cb + n;
     tlen[cb] = sLen[tl];
     toff[cb] = sOff[tl];
     const int e = tlen[cb] - 8 * g;  // 1..7 past a multiple of 32: partial in chunk e / 32
@@ -144,20 +152,22 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_scores_kernel(JScoresParams
     for (int m = 32; m >= 1; m >>= 1) bit |= (uint32_t)__shfl_xor((int)bit, m, 64);
     pmask[cb] = __builtin_amdgcn_readfirstlane(bit);
   }
-  dkv_f32x4 acc[8][JCB];
+  dkv_f32x4 acc[NHB][8][CB];
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int hh = 0; hh < NHB; ++hh)
 #pragma unroll
-    for (int cb = 0; cb < JCB; ++cb) acc[i][cb] = dkv_f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb) acc[hh][i][cb] = dkv_f32x4{0.f, 0.f, 0.f, 0.f};
 
   // The rank loop. The coefficient loads are not waited for where they are issued, so each wave
   // keeps two chunks of loads in flight. Only the last batch row can hold a window that crosses
   // the end of the buffer; its workgroups run the loop with element-wise gathers for such windows.
   auto rank_loop = [&](auto safe_tag) {
     constexpr bool SAFE = decltype(safe_tag)::value;
-    auto load_x = [&](int c, dkv_u32x4(&x)[JCB]) {
+    auto load_x = [&](int c, dkv_u32x4(&x)[CB]) {
 #pragma unroll
-      for (int cb = 0; cb < JCB; ++cb) {
+      for (int cb = 0; cb < CB; ++cb) {
         const int j0 = JCH * c + 8 * g;
         if constexpr (SAFE)
           x[cb] = dkv_load8_safe(rs, end, toff[cb] + j0, tlen[cb] - j0);
@@ -165,15 +175,22 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_scores_kernel(JScoresParams
           x[cb] = dkv_load8_raw(rs, toff[cb] + j0, tlen[cb] - j0);
       }
     };
-    dkv_u32x4 xa[JCB], xb[JCB];
-    dkv_u32x4 ba = dkv_u32x4{0u, 0u, 0u, 0u}, bb = ba;
+    dkv_u32x4 xa[CB], xb[CB];
+    dkv_u32x4 ba[NHB], bb[NHB];
 #pragma unroll
-    for (int cb = 0; cb < JCB; ++cb) xa[cb] = xb[cb] = dkv_u32x4{0u, 0u, 0u, 0u};
-    auto load_b = [&](int c) { return *(const dkv_u32x4*)(bsrc + p.bt_sc * min(c, nch - 1)); };
+    for (int hh = 0; hh < NHB; ++hh) ba[hh] = bb[hh] = dkv_u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) xa[cb] = xb[cb] = dkv_u32x4{0u, 0u, 0u, 0u};
+    auto load_b = [&](int c, int hh) {
+      return *(const dkv_u32x4*)(bsrc + hh * p.bt_sh + p.bt_sc * min(c, nch - 1));
+    };
     if (nch > 0) {
-      sB[0][tid] = load_b(0);
-      ba = load_b(1);
-      bb = load_b(2);
+#pragma unroll
+      for (int hh = 0; hh < NHB; ++hh) {
+        sB[0][hh][tid] = load_b(0, hh);
+        ba[hh] = load_b(1, hh);
+        bb[hh] = load_b(2, hh);
+      }
       load_x(0, xa);
       load_x(1, xb);
     }
@@ -185,24 +202,32 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_scores_kernel(JScoresParams
     // products are issued, into the registers chunk c used (x: xa, xb in turn). No loaded value
     // is ever copied, so the waits cover only the values being used. Loads past the last chunk
     // clamp the basis index and have coefficient counts <= 0 (no traffic).
-    auto step = [&](int c, dkv_u32x4(&x)[JCB], dkv_u32x4& bn) {
+    auto step = [&](int c, dkv_u32x4(&x)[CB], dkv_u32x4(&bn)[NHB]) {
 #pragma unroll
-      for (int cb = 0; cb < JCB; ++cb)
+      for (int cb = 0; cb < CB; ++cb)
         if ((pmask[cb] >> c) & 1u) x[cb] = dkv_mask8(x[cb], tlen[cb] - (JCH * c + 8 * g));
-      sB[(c + 1) & 1][tid] = bn;
-      bn = load_b(c + 3);
-      const dkv_u32x4* buf = sB[c & 1];
-      dkv_u32x4 a[8];
 #pragma unroll
-      for (int blk = 0; blk < 8; ++blk) a[blk] = buf[4 * (16 * blk + n) + (g ^ jswz(n))];
+      for (int hh = 0; hh < NHB; ++hh) {
+        sB[(c + 1) & 1][hh][tid] = bn[hh];
+        bn[hh] = load_b(c + 3, hh);
+      }
+      dkv_u32x4 a[NHB][8];
 #pragma unroll
-      for (int blk = 0; blk < 8; ++blk)
+      for (int hh = 0; hh < NHB; ++hh)
 #pragma unroll
-        for (int cb = 0; cb < JCB; ++cb) acc[blk][cb] = dkv_mfma32<DT>(a[blk], x[cb], acc[blk][cb]);
-      // the eight basis reads first, then the products (the compiler would otherwise read each
-      // operand just before its products and expose the LDS latency four times per chunk)
-      __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 8 * JCB, 0);
+        for (int blk = 0; blk < 8; ++blk)
+          a[hh][blk] = sB[c & 1][hh][4 * (16 * blk + n) + (g ^ jswz(n))];
+#pragma unroll
+      for (int hh = 0; hh < NHB; ++hh)
+#pragma unroll
+        for (int blk = 0; blk < 8; ++blk)
+#pragma unroll
+          for (int cb = 0; cb < CB; ++cb)
+            acc[hh][blk][cb] = dkv_mfma32<DT>(a[hh][blk], x[cb], acc[hh][blk][cb]);
+      // the basis reads first, then the products (the compiler would otherwise read each
+      // operand just before its products and expose the LDS latency once per operand)
+      __builtin_amdgcn_sched_group_barrier(0x100, 8 * NHB, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 8 * NHB * CB, 0);
       load_x(c + 2, x);
       __syncthreads();
     };
@@ -221,6 +246,9 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_scores_kernel(JScoresParams
 
   // ---- per 16-token tile: rotation, K' hi + lo, scores, masking, store ---------------------
   // (q_i, q_{i+64}) of the group's heads for frequency i = lane, as 16-bit values
+#pragma unroll
+  for (int hb = 0; hb < NHB; ++hb) {
+  const int h = h0 + hb;
   uint32_t qh[8];
   {
     const long long qo = (long long)b * p.q_sb + (long long)h * p.hpg * p.q_sh + lane;
@@ -235,8 +263,8 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_scores_kernel(JScoresParams
   const int qrow = (n & 8) + (hn < p.hpg ? hn : hn % p.hpg);
   uint32_t* qw = sQ[wave];
 #pragma unroll
-  for (int cb = 0; cb < JCB; ++cb) {
-    const int tbase = t0 + 64 * wave + 16 * cb;
+  for (int cb = 0; cb < CB; ++cb) {
+    const int tbase = t0 + 16 * CB * wave + 16 * cb;
     if (tbase >= p.S) break;  // wave-uniform
     const int tile = tbase / 16;
     {
@@ -265,7 +293,7 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_scores_kernel(JScoresParams
     dkv_f32x4 sc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int pp = 0; pp < 4; ++pp) {
-      const dkv_f32x4 c0 = acc[pp][cb], c1 = acc[pp + 4][cb];
+      const dkv_f32x4 c0 = acc[hb][pp][cb], c1 = acc[hb][pp + 4][cb];
       const dkv_f32x4 r01 = sRn[2 * pp][lane], r23 = sRn[2 * pp + 1][lane];
       const float rc[4] = {r01.x, r01.z, r23.x, r23.z}, rsn[4] = {r01.y, r01.w, r23.y, r23.w};
       uint32_t kh[4], kl[4];
@@ -288,7 +316,7 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_scores_kernel(JScoresParams
       const long long ob = (long long)b * p.out_sb + (long long)(h * p.hpg + n) * p.out_sh;
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const int tl = 64 * wave + 16 * cb + 4 * g + u;
+        const int tl = 16 * CB * wave + 16 * cb + 4 * g + u;
         const int t = t0 + tl;
         if (t < p.S) {
           const int len = sLen[tl];
@@ -301,6 +329,11 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_scores_kernel(JScoresParams
         }
       }
     }
+  }
+  // the next head reuses the wave's query operand rows
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
 }
 
@@ -773,10 +806,21 @@ extern "C" int dkv_joint_scores(void* stream, int mode, int dtype, int out_dtype
   p.R = R;
   p.hpg = Hq / n_basis;
   p.scale = 1.0f / sqrtf((float)Dh);
-  const dim3 grid((unsigned)((S + JTOK - 1) / JTOK), (unsigned)n_basis, (unsigned)B);
+  // two basis heads per workgroup when the heads pair up (each coefficient load then serves
+  // both heads' products)
+  const int nhb = n_basis % 2 == 0 ? 2 : 1;
+  const int tok = JTOK / nhb;
+  const dim3 grid((unsigned)((S + tok - 1) / tok), (unsigned)(n_basis / nhb), (unsigned)B);
   hipStream_t st = (hipStream_t)stream;
-#define DKV_JS_LAUNCH(DT_, MODE_, ODT_) \
-  hipLaunchKernelGGL((joint_scores_kernel<DT_, MODE_, ODT_>), grid, dim3(JTHREADS), 0, st, p)
+#define DKV_JS_LAUNCH(DT_, MODE_, ODT_)                                                        \
+  do {                                                                                         \
+    if (nhb == 2)                                                                              \
+      hipLaunchKernelGGL((joint_scores_kernel<DT_, MODE_, ODT_, 2>), grid, dim3(JTHREADS), 0,  \
+                         st, p);                                                               \
+    else                                                                                       \
+      hipLaunchKernelGGL((joint_scores_kernel<DT_, MODE_, ODT_, 1>), grid, dim3(JTHREADS), 0,  \
+                         st, p);                                                               \
+  } while (0)
   if (mode == 1) {
     if (dtype == DKV_BF16) DKV_JS_LAUNCH(DKV_BF16, 1, DKV_F32);
     else DKV_JS_LAUNCH(DKV_F16, 1, DKV_F32);
