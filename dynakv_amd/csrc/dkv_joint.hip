@@ -12,13 +12,12 @@
 // joint_scores_kernel -- workgroup = (512 tokens, basis head h, batch row b), or with the heads
 //   in pairs (256 tokens, heads 2h and 2h+1, b) so that each coefficient load serves both heads'
 //   products; wave w takes 64 tokens (4 column blocks of 16) of its head, or 32 tokens of both.
-//   K^T[128 x 64] = B_h^T . X^T accumulates on 16x16x32 MFMA over
-//   the rank chunks of 32 that the block's longest token needs. Each basis chunk ([128 dims][32
-//   ranks], 8 KB contiguous in HBM) is loaded once per workgroup into LDS (two buffers) and every
-//   A operand read
-//   from it serves the wave's 4 column blocks; the coefficients go straight into B operand
-//   registers (lane = one token x 8 ranks, elements past the token's count zeroed), two chunks
-//   ahead. Then per 16-token tile T: R(n) applied to the lane's token (n = its slot in the tile,
+//   K^T = B_h^T . X^T accumulates on 16x16x32 MFMA over the rank chunks of 32 that the block's
+//   longest token needs. Each basis chunk ([128 dims][32 ranks], 8 KB contiguous in HBM) is
+//   loaded once per workgroup into LDS (two buffers per head) and every A operand read from it
+//   serves the wave's column blocks; the coefficients go straight into B operand registers
+//   (lane = one token x 8 ranks, elements past the token's count zeroed), two chunks ahead,
+//   each serving every head of the workgroup. Then per 16-token tile T: R(n) applied to the lane's token (n = its slot in the tile,
 //   LDS table) in fp32, K' split into bf16 hi + lo, scores on MFMA against R(-16T) q (hi and lo
 //   parts in separate operand columns), the route's masking and rounding.
 // joint_av_kernel -- workgroup = (token split, 16 query heads, batch row b); wave w takes ranks
