@@ -20,11 +20,12 @@
 //   each serving every head of the workgroup. Then per 16-token tile T: R(n) applied to the lane's token (n = its slot in the tile,
 //   LDS table) in fp32, K' split into bf16 hi + lo, scores on MFMA against R(-16T) q (hi and lo
 //   parts in separate operand columns), the route's masking and rounding.
-// joint_av_kernel -- workgroup = (token split, 16 query heads, batch row b); wave w takes ranks
-//   [128w, 128w + 128). Per 16-token tile: the 16 heads' scores through an online softmax in the
-//   log2 domain (every wave computes the same values), P as bf16 hi + lo (fp16 for fp16 caches),
-//   the wave's V coefficients of the tile staged in LDS and read transposed (ds_read_b64_tr_b16)
-//   as the B operand of P.X^V. Each split writes (m, l, acc[R]) per head.
+// joint_av_kernel -- workgroup = (token split, 16 or 32 query heads, batch row b); wave w takes
+//   ranks [128w, 128w + 128). Per 16-token tile: each set of 16 heads' scores through an online
+//   softmax in the log2 domain (every wave computes the same values), P as bf16 hi + lo (fp16
+//   for fp16 caches), the wave's V coefficients of the tile staged in LDS and read transposed
+//   (ds_read_b64_tr_b16) once as the B operand of every set's P.X^V. Each split writes (m, l,
+//   acc[R]) per head.
 // joint_merge_kernel -- workgroup = (rank block of 128, V basis and up to 8 of its query heads,
 //   batch row b): LSE weights of the split records with the route's denominator, the block's
 //   merged coefficients, their projection through the block's basis rows (each basis value
@@ -352,7 +353,9 @@ struct JAvParams {
 
 // VEC: the scores are token-contiguous with rows aligned to 4 elements, and a lane loads its 4
 // tokens' scores of a tile in one 8- or 16-byte access (else one access per score)
-template <int DT, int SDT, bool VEC>
+// NHS sets of 16 query heads per workgroup (1 or 2): with 2, each V window is staged and read
+// once for both sets' products
+template <int DT, int SDT, bool VEC, int NHS>
 __global__ __launch_bounds__(JTHREADS, 1) void joint_av_kernel(JAvParams p) {
   // per wave: its rank slice of the current tile's V coefficients, the split kernel's V-window
   // layout: rank r of token t in chunk r/32 at lane slot 16*((r%32)/8) + t, element r%8
@@ -366,13 +369,19 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_av_kernel(JAvParams p) {
   const int s_end = min(p.S, s_begin + p.split_len);
   const int ntiles = s_end > s_begin ? (s_end - s_begin + 15) / 16 : 0;
   const int r0 = 128 * wave;
-  const int hq = 16 * hset + n;  // head slot n of this lane's softmax values
-  const bool hq_ok = hq < p.Hq;
+  int hq[NHS];     // head slot n of each set: this lane's softmax values
+  bool hq_ok[NHS];
+  long long sbase[NHS];
+#pragma unroll
+  for (int s = 0; s < NHS; ++s) {
+    hq[s] = 16 * (NHS * hset + s) + n;
+    hq_ok[s] = hq[s] < p.Hq;
+    sbase[s] = (long long)b * p.sc_sb + (long long)(hq_ok[s] ? hq[s] : 0) * p.sc_sh;
+  }
 
   const uint32_t end =
       (uint32_t)min((long long)(p.B - b) * p.flat_ld, (long long)JFLAT_CAP);
   const __amdgpu_buffer_rsrc_t rs = dkv_make_rsrc(p.flat + (long long)b * p.flat_ld, end * 2u);
-  const long long sbase = (long long)b * p.sc_sb + (long long)(hq_ok ? hq : 0) * p.sc_sh;
 
   // Tile j's inputs for this lane: the metadata (count, offset) of token n, its V pieces (ranks
   // r0 + 32c + 8g .. +8) and the scores of head slot n for tokens 4g .. 4g+3. Every lane issues
@@ -386,11 +395,11 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_av_kernel(JAvParams p) {
   };
   auto count = [&](int j, int l) { return s_begin + 16 * j + n < s_end ? min(max(l, 0), p.R) : 0; };
   const __amdgpu_buffer_rsrc_t rz = dkv_make_rsrc(p.scores, p.sc_bytes);
-  auto load_z = [&](int j, uint32_t(&z)[4]) {
+  auto load_z1 = [&](int j, int hs, uint32_t(&z)[4]) {
     if constexpr (VEC) {
       // tokens past the split read their neighbours (zeros past the scores' last element, where
       // the buffer range ends): replaced at use
-      const uint32_t e = (uint32_t)(sbase + s_begin + 16 * j + 4 * g);
+      const uint32_t e = (uint32_t)(sbase[hs] + s_begin + 16 * j + 4 * g);
       if constexpr (SDT == DKV_F32) {
         const dkv_u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rz, e * 4u, 0, 0);
         z[0] = v.x;
@@ -398,17 +407,16 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_av_kernel(JAvParams p) {
         z[2] = v.z;
         z[3] = v.w;
       } else {
+        // kept packed (two scores per register) until used
         const dkv_u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rz, e * 2u, 0, 0);
-        z[0] = v.x & 0xffffu;
-        z[1] = v.x >> 16;
-        z[2] = v.y & 0xffffu;
-        z[3] = v.y >> 16;
+        z[0] = v.x;
+        z[1] = v.y;
       }
     } else {
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const long long i =
-            sbase + (long long)min(s_begin + 16 * j + 4 * g + u, s_end - 1) * p.sc_ss;
+            sbase[hs] + (long long)min(s_begin + 16 * j + 4 * g + u, s_end - 1) * p.sc_ss;
         if constexpr (SDT == DKV_F32)
           z[u] = ((const uint32_t*)p.scores)[i];
         else
@@ -416,20 +424,33 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_av_kernel(JAvParams p) {
       }
     }
   };
-  auto score = [&](int j, int u, uint32_t raw) {
+  auto load_z = [&](int j, uint32_t(&z)[NHS][4]) {
+#pragma unroll
+    for (int hs = 0; hs < NHS; ++hs) load_z1(j, hs, z[hs]);
+  };
+  auto score = [&](int j, int hs, int u, const uint32_t(&zr)[4]) {
+    uint32_t raw;
+    if constexpr (VEC && SDT != DKV_F32)
+      raw = (zr[u >> 1] >> (16 * (u & 1))) & 0xffffu;
+    else
+      raw = zr[u];
     float v;
     if constexpr (SDT == DKV_F32)
       v = __uint_as_float(raw);
     else
       v = dkv_elt_to_f32<SDT>(raw);
-    return (hq_ok && s_begin + 16 * j + 4 * g + u < s_end) ? v * JLOG2E : -INFINITY;
+    return (hq_ok[hs] && s_begin + 16 * j + 4 * g + u < s_end) ? v * JLOG2E : -INFINITY;
   };
 
-  dkv_f32x4 acc[8];
+  dkv_f32x4 acc[NHS][8];
+  float m_run[NHS], l_run[NHS];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) acc[i] = dkv_f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run = -1.0e30f;  // finite floor: excluded tokens give exp2(-inf) = 0
-  float l_run = 0.f;
+  for (int hs = 0; hs < NHS; ++hs) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[hs][i] = dkv_f32x4{0.f, 0.f, 0.f, 0.f};
+    m_run[hs] = -1.0e30f;  // finite floor: excluded tokens give exp2(-inf) = 0
+    l_run[hs] = 0.f;
+  }
   dkv_u32x4* slot = sV[wave];
 
   auto tile_loop = [&](auto safe_tag) {
@@ -448,7 +469,7 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_av_kernel(JAvParams p) {
     // tile, that tile's count, and the raw metadata (ml, mo) of the tile two ahead. A tile's
     // loads go into the registers its set just used, so no loaded value is ever copied.
     dkv_u32x4 xA[4], xB[4];
-    uint32_t zA[4], zB[4];
+    uint32_t zA[NHS][4], zB[NHS][4];
     int cA, cB, mlA, moA, mlB, moB;
     {
       int l0, o0, l1, o1;
@@ -463,12 +484,14 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_av_kernel(JAvParams p) {
       load_v(cB, o1, xB);
       load_z(1, zB);
     }
-    auto step = [&](int j, dkv_u32x4(&x)[4], uint32_t(&zr)[4], int& cnt, int& ml, int& mo) {
+    auto step = [&](int j, dkv_u32x4(&x)[4], uint32_t(&zr)[NHS][4], int& cnt, int& ml, int& mo) {
 #pragma unroll
       for (int c = 0; c < 4; ++c) slot[c * 64 + lane] = dkv_mask8(x[c], cnt - (r0 + 32 * c + 8 * g));
-      float z[4];
+      float z[NHS][4];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) z[u] = score(j, u, zr[u]);
+      for (int hs = 0; hs < NHS; ++hs)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) z[hs][u] = score(j, hs, u, zr[hs]);
       cnt = count(j + 2, ml);
       load_v(cnt, mo, x);
       load_z(j + 2, zr);
@@ -477,41 +500,8 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_av_kernel(JAvParams p) {
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-      // online softmax of head slot n (its 16 tokens sit in lanes n, n+16, n+32, n+48)
-      float tmax = dkv_max3(dkv_max3(z[0], z[1], z[2]), z[3], z[3]);
-      tmax = dkv_lane_max32(tmax);
-      tmax = dkv_lane_max16(tmax);
-      if (__ballot(tmax > m_run + JRESCALE)) {
-        const float m_new = fmaxf(m_run, tmax);
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-        l_run *= alpha;
-        m_run = m_new;
-        float au[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) au[u] = __shfl(alpha, 4 * g + u, 64);
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-#pragma unroll
-          for (int u = 0; u < 4; ++u) acc[i][u] *= au[u];
-      }
-      float pu[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        pu[u] = __builtin_amdgcn_exp2f(z[u] - m_run);
-        l_run += pu[u];
-      }
-      // P.X^V in coefficient space (A: P of head slot n, tokens 4g..4g+3; B: the transposed V reads)
-      dkv_u32x2 pa_hi, pa_lo;
-      if constexpr (DT == DKV_F16) {
-        pa_hi = dkv_u32x2{dkv_pack_f16x2(pu[0], pu[1]), dkv_pack_f16x2(pu[2], pu[3])};
-        pa_lo = pa_hi;
-      } else {
-        uint32_t h01, l01, h23, l23;
-        dkv_split_bf16x2(pu[0], pu[1], h01, l01);
-        dkv_split_bf16x2(pu[2], pu[3], h23, l23);
-        pa_hi = dkv_u32x2{h01, h23};
-        pa_lo = dkv_u32x2{l01, l23};
-      }
+      // the wave's V operands of the tile: B of P.X^V by transposed reads
+      dkv_u32x2 xv[8];
       {
         const int u = n >> 2, q = n & 3;
         const uint8_t* vbase =
@@ -519,21 +509,62 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_av_kernel(JAvParams p) {
 #pragma unroll
         for (int blk = 0; blk < 8; ++blk) {
           const uint8_t* src = vbase + (blk >> 1) * 1024 + (blk & 1) * 512;
-          const dkv_u32x2 xv = __builtin_bit_cast(
+          xv[blk] = __builtin_bit_cast(
               dkv_u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                              (__attribute__((address_space(3))) dkv_i16x4*)(
                                  (__attribute__((address_space(3))) uint8_t*)src)));
-          if constexpr (DT == DKV_BF16)
-            acc[blk] = dkv_mfma32<DT>(
-                dkv_u32x4{pa_hi.x, pa_hi.y, pa_lo.x, pa_lo.y},
-                __builtin_bit_cast(dkv_u32x4, dkv_u64x2{__builtin_bit_cast(uint64_t, xv),
-                                                        __builtin_bit_cast(uint64_t, xv)}),
-                acc[blk]);
-          else
-            acc[blk] = __builtin_amdgcn_mfma_f32_16x16x16f16(
-                __builtin_bit_cast(dkv_f16x4, pa_hi), __builtin_bit_cast(dkv_f16x4, xv), acc[blk],
-                0, 0, 0);
         }
+      }
+      // per set: online softmax of head slot n (its 16 tokens sit in lanes n, n+16, n+32,
+      // n+48), P as the A operand, the set's products; one set at a time
+#pragma unroll
+      for (int hs = 0; hs < NHS; ++hs) {
+        float tmax = dkv_max3(dkv_max3(z[hs][0], z[hs][1], z[hs][2]), z[hs][3], z[hs][3]);
+        tmax = dkv_lane_max32(tmax);
+        tmax = dkv_lane_max16(tmax);
+        if (__ballot(tmax > m_run[hs] + JRESCALE)) {
+          const float m_new = fmaxf(m_run[hs], tmax);
+          const float alpha = __builtin_amdgcn_exp2f(m_run[hs] - m_new);
+          l_run[hs] *= alpha;
+          m_run[hs] = m_new;
+          float au[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) au[u] = __shfl(alpha, 4 * g + u, 64);
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) acc[hs][i][u] *= au[u];
+        }
+        float pu[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          pu[u] = __builtin_amdgcn_exp2f(z[hs][u] - m_run[hs]);
+          l_run[hs] += pu[u];
+        }
+        // P.X^V in coefficient space (A: P of head slot n, tokens 4g..4g+3; B: the V reads)
+        dkv_u32x4 pa;
+        if constexpr (DT == DKV_F16) {
+          pa = dkv_u32x4{dkv_pack_f16x2(pu[0], pu[1]), dkv_pack_f16x2(pu[2], pu[3]), 0u, 0u};
+        } else {
+          uint32_t h01, l01, h23, l23;
+          dkv_split_bf16x2(pu[0], pu[1], h01, l01);
+          dkv_split_bf16x2(pu[2], pu[3], h23, l23);
+          pa = dkv_u32x4{h01, h23, l01, l23};
+        }
+#pragma unroll
+        for (int blk = 0; blk < 8; ++blk) {
+          if constexpr (DT == DKV_BF16)
+            acc[hs][blk] = dkv_mfma32<DT>(
+                pa,
+                __builtin_bit_cast(dkv_u32x4, dkv_u64x2{__builtin_bit_cast(uint64_t, xv[blk]),
+                                                        __builtin_bit_cast(uint64_t, xv[blk])}),
+                acc[hs][blk]);
+          else
+            acc[hs][blk] = __builtin_amdgcn_mfma_f32_16x16x16f16(
+                __builtin_bit_cast(dkv_f16x4, dkv_u32x2{pa.x, pa.y}),
+                __builtin_bit_cast(dkv_f16x4, xv[blk]), acc[hs][blk], 0, 0, 0);
+        }
+        if (NHS > 1) __builtin_amdgcn_sched_barrier(0);
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
@@ -543,7 +574,9 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_av_kernel(JAvParams p) {
     int j = 0;
     for (; j + 1 < ntiles; j += 2) {
       step(j, xA, zA, cA, mlA, moA);
+      if (NHS > 1) __builtin_amdgcn_sched_barrier(0);
       step(j + 1, xB, zB, cB, mlB, moB);
+      if (NHS > 1) __builtin_amdgcn_sched_barrier(0);
     }
     if (j < ntiles) step(j, xA, zA, cA, mlA, moA);
   };
@@ -556,23 +589,26 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_av_kernel(JAvParams p) {
 
   // the split's record per head: m and l (identical in every wave: wave 0 writes them), the
   // wave's rank slice of acc (head slot 4g+u, rank r0 + 16*blk + n)
-  float l_tot = l_run;
-  l_tot += __shfl_xor(l_tot, 16, 64);
-  l_tot += __shfl_xor(l_tot, 32, 64);
-  if (wave == 0 && g == 0 && hq_ok) {
-    float* rec = p.rec + (((long long)b * p.Hq + hq) * p.n_splits + split) * JPREC;
-    rec[0] = m_run;
-    rec[1] = l_tot;
-  }
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int hs = 16 * hset + 4 * g + u;
-    if (hs < p.Hq) {
-      float* rec = p.rec + (((long long)b * p.Hq + hs) * p.n_splits + split) * JPREC + 4;
+  for (int hs = 0; hs < NHS; ++hs) {
+    float l_tot = l_run[hs];
+    l_tot += __shfl_xor(l_tot, 16, 64);
+    l_tot += __shfl_xor(l_tot, 32, 64);
+    if (wave == 0 && g == 0 && hq_ok[hs]) {
+      float* rec = p.rec + (((long long)b * p.Hq + hq[hs]) * p.n_splits + split) * JPREC;
+      rec[0] = m_run[hs];
+      rec[1] = l_tot;
+    }
 #pragma unroll
-      for (int blk = 0; blk < 8; ++blk) {
-        const int r = r0 + 16 * blk + n;
-        if (r < p.R) rec[r] = acc[blk][u];
+    for (int u = 0; u < 4; ++u) {
+      const int head = 16 * (NHS * hset + hs) + 4 * g + u;
+      if (head < p.Hq) {
+        float* rec = p.rec + (((long long)b * p.Hq + head) * p.n_splits + split) * JPREC + 4;
+#pragma unroll
+        for (int blk = 0; blk < 8; ++blk) {
+          const int r = r0 + 16 * blk + n;
+          if (r < p.R) rec[r] = acc[hs][blk][u];
+        }
       }
     }
   }
@@ -742,8 +778,12 @@ __global__ __launch_bounds__(JDH) void joint_project_sum_kernel(JMergeParams p) 
   dkv_store_f32<ODT>(p.out, (long long)b * p.out_sb + (long long)hq * p.out_sh + d, o);
 }
 
+// sets of 16 query heads per V-pass workgroup: two when the sets pair up
+int joint_av_hsets(int Hq) { return ((Hq + 15) / 16) % 2 == 0 ? 2 : 1; }
+
 int joint_av_split_len(int B, int Hq, int S) {
-  const long long groups = (long long)B * ((Hq + 15) / 16);
+  // about 512 workgroups: token splits x workgroups of head sets x batch rows
+  const long long groups = (long long)B * ((Hq + 15) / 16) / joint_av_hsets(Hq);
   long long ns = (512 + groups - 1) / groups;
   const long long max_ns = (S + 15) / 16;
   if (ns > max_ns) ns = max_ns;
@@ -896,7 +936,8 @@ extern "C" int dkv_joint_av(void* stream, int mode, int scores_dtype, int dtype,
   a.R = R;
   a.n_splits = ns;
   a.split_len = sl;
-  const dim3 agrid((unsigned)ns, (unsigned)((Hq + 15) / 16), (unsigned)B);
+  const int nhs = joint_av_hsets(Hq);
+  const dim3 agrid((unsigned)ns, (unsigned)((Hq + 15) / 16 / nhs), (unsigned)B);
   // vector score loads: token-contiguous rows whose starts are 4-element aligned and a token
   // count that is a multiple of 4, so each lane's group of 4 scores lies wholly inside or
   // wholly past the scores' last element; the buffer range ends exactly at that element (the
@@ -909,12 +950,16 @@ extern "C" int dkv_joint_av(void* stream, int mode, int scores_dtype, int dtype,
                    sc_sh >= 0 && ((uintptr_t)scores % (4 * sc_elt)) == 0 &&
                    sc_extent < (1LL << 31);
   a.sc_bytes = vec ? (uint32_t)sc_extent : 0u;
-#define DKV_JA_LAUNCH(DT_, SDT_)                                                            \
-  do {                                                                                      \
-    if (vec)                                                                                \
-      hipLaunchKernelGGL((joint_av_kernel<DT_, SDT_, true>), agrid, dim3(JTHREADS), 0, st, a); \
-    else                                                                                    \
-      hipLaunchKernelGGL((joint_av_kernel<DT_, SDT_, false>), agrid, dim3(JTHREADS), 0, st, a); \
+#define DKV_JA_LAUNCH(DT_, SDT_)                                                              \
+  do {                                                                                        \
+    if (vec && nhs == 2)                                                                      \
+      hipLaunchKernelGGL((joint_av_kernel<DT_, SDT_, true, 2>), agrid, dim3(JTHREADS), 0, st, a); \
+    else if (vec)                                                                             \
+      hipLaunchKernelGGL((joint_av_kernel<DT_, SDT_, true, 1>), agrid, dim3(JTHREADS), 0, st, a); \
+    else if (nhs == 2)                                                                        \
+      hipLaunchKernelGGL((joint_av_kernel<DT_, SDT_, false, 2>), agrid, dim3(JTHREADS), 0, st, a); \
+    else                                                                                      \
+      hipLaunchKernelGGL((joint_av_kernel<DT_, SDT_, false, 1>), agrid, dim3(JTHREADS), 0, st, a); \
   } while (0)
   if (dtype == DKV_BF16) {
     if (scores_dtype == DKV_F32) DKV_JA_LAUNCH(DKV_BF16, DKV_F32);
