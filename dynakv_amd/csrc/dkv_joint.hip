@@ -53,8 +53,11 @@ constexpr int JMAX_SPLITS = 1024;  // token splits of the V pass
 constexpr float JLOG2E = 1.4426950408889634f;
 constexpr float JRESCALE = 11.5f;        // log2 units: rescale when the running max grows more
 
-// piece swizzle of the basis chunk buffers (a function of d mod 16)
-__device__ __forceinline__ int jswz(int d) { return (d ^ (d >> 2)) & 3; }
+// piece swizzle of the basis chunk buffers (a function of d mod 16): the 16-byte slot of ranks
+// 8k..8k+7 of row d is k ^ ((d >> 1) & 3). Measured on MI355X for ds_read_b128 with lane
+// (n, g) reading slot g of row 16*blk + n: 270-290 bytes per clock and CU, as fast as
+// consecutive addresses (168-177 for (d ^ (d >> 2)) & 3 or no swizzle)
+__device__ __forceinline__ int jswz(int d) { return (d >> 1) & 3; }
 
 __device__ __forceinline__ dkv_f32x4 mfma_bf16x32(const dkv_u32x4& a, const dkv_u32x4& b,
                                                   dkv_f32x4 c) {
@@ -85,9 +88,8 @@ template <int DT, int MODE, int ODT, int NHB>
 __global__ __launch_bounds__(JTHREADS, 1) void joint_scores_kernel(JScoresParams p) {
   constexpr int CB = JCB / NHB;            // 16-token column blocks per wave
   constexpr int TOK = JWAVES * CB * 16;    // tokens per workgroup
-  // basis chunk buffers: piece (dim d, ranks 8k..8k+7) at index 4d + (k ^ jswz(d)): the 16 rows
-  // one k-group reads land in 16 different 16-byte bank groups of a 256-byte span, and any 8
-  // aligned ones in 8 different groups of a 128-byte span
+  // basis chunk buffers: piece (dim d, ranks 8k..8k+7) at index 4d + (k ^ jswz(d)), so that the
+  // A operand reads (lane (n, g): slot g of row 16*blk + n) are free of bank conflicts
   __shared__ __attribute__((aligned(16))) dkv_u32x4 sB[2][NHB][JDH * JCH / 8];
   // R(n) of every lane's token slot: [2*pp + k][lane] holds (cos, sin) of frequencies
   // 16pp + 4g + 2k and + 1
