@@ -90,15 +90,18 @@ ULP = {torch.float16: 2.0 ** -10, torch.bfloat16: 2.0 ** -7}
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("B,S,R,n_basis,repeat", [
-    (2, 777, 1024, 8, 4),   # the reference's repeated k_up (32 bases -> 8 distinct)
-    (3, 513, 512, 4, 1),    # 8 query heads per basis
-    (1, 40, 32, 32, 1),     # one rank chunk, one query head per basis
-    (2, 1100, 1024, 8, 1),  # 4 query heads per basis, three 512-token blocks
+@pytest.mark.parametrize("B,S,R,n_basis,repeat,Hq", [
+    (2, 777, 1024, 8, 4, 32),   # the reference's repeated k_up (32 bases -> 8 distinct)
+    (3, 513, 512, 4, 1, 32),    # 8 query heads per basis
+    (1, 40, 32, 32, 1, 32),     # one rank chunk, one query head per basis
+    (2, 1100, 1024, 8, 1, 32),  # 4 query heads per basis, blocks of 256 tokens x 2 bases
+    (2, 700, 256, 3, 1, 12),    # an odd number of bases: one basis per workgroup
+    (1, 300, 512, 1, 1, 8),     # a single basis for 8 query heads
 ])
-def test_scores_match_vector_kernel(dev, dtype, B, S, R, n_basis, repeat):
-    print(f"[gpu] joint scores {dtype} B={B} S={S} R={R} nb={n_basis} rep={repeat}", flush=True)
-    h = _case(B, S, R, n_basis, dtype=dtype, seed=S + R, exact_end=True)
+def test_scores_match_vector_kernel(dev, dtype, B, S, R, n_basis, repeat, Hq):
+    print(f"[gpu] joint scores {dtype} B={B} S={S} R={R} nb={n_basis} rep={repeat} Hq={Hq}",
+          flush=True)
+    h = _case(B, S, R, n_basis, Hq=Hq, dtype=dtype, seed=S + R, exact_end=True)
     d = _dev(h, dev, dtype)
     k_up = d["kb"].repeat_interleave(repeat, dim=0).contiguous() if repeat > 1 else d["kb"]
     for mode, odt in ((0, dtype), (1, torch.float32)):
@@ -121,19 +124,21 @@ def test_scores_match_vector_kernel(dev, dtype, B, S, R, n_basis, repeat):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("B,S,R,n_basis", [
-    (2, 1000, 1024, 8), (1, 17, 1024, 32), (3, 1, 256, 4), (2, 300, 1024, 8),
-    (2, 50, 97, 2),      # one partial rank block (97 ranks), two chunks of 8 heads per basis
-    (1, 2048, 512, 8),   # 128 token splits: the merge's many-splits path
+@pytest.mark.parametrize("B,S,R,n_basis,Hq", [
+    (2, 1000, 1024, 8, 32), (1, 17, 1024, 32, 32), (3, 1, 256, 4, 32), (2, 300, 1024, 8, 32),
+    (2, 50, 97, 2, 32),      # one partial rank block (97 ranks), two chunks of 8 heads per basis
+    (1, 2048, 512, 8, 32),   # many token splits: the merge's many-splits path
+    (2, 400, 256, 3, 12),    # one set of 16 query heads (12 used) per workgroup
+    (2, 300, 1024, 8, 48),   # three sets of 16 query heads: one set per workgroup
 ])
-def test_av_matches_vector_kernel(dev, dtype, B, S, R, n_basis):
-    print(f"[gpu] joint av {dtype} B={B} S={S} R={R} nb={n_basis}", flush=True)
-    h = _case(B, S, R, n_basis, dtype=dtype, seed=7 * S + R, exact_end=True)
+def test_av_matches_vector_kernel(dev, dtype, B, S, R, n_basis, Hq):
+    print(f"[gpu] joint av {dtype} B={B} S={S} R={R} nb={n_basis} Hq={Hq}", flush=True)
+    h = _case(B, S, R, n_basis, Hq=Hq, dtype=dtype, seed=7 * S + R, exact_end=True)
     d = _dev(h, dev, dtype)
     rng = np.random.default_rng(S)
     for mode in (0, 1):
         sdt = dtype if mode == 0 else torch.float32
-        z = rng.standard_normal((B, 32, S)) * 2
+        z = rng.standard_normal((B, Hq, S)) * 2
         if mode == 1:
             z[:, :, rng.random(S) < 0.3] = -np.inf  # the fused route's masked tokens
             z[:, :, 0] = 0.5
