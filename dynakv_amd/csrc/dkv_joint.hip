@@ -14,7 +14,8 @@
 //   products; wave w takes 64 tokens (4 column blocks of 16) of its head, or 32 tokens of both.
 //   K^T = B_h^T . X^T accumulates on 16x16x32 MFMA over the rank chunks of 32 that the block's
 //   longest token needs. Each basis chunk ([128 dims][32 ranks], 8 KB contiguous in HBM) is
-//   loaded once per workgroup into LDS (two buffers per head) and every A operand read from it
+//   loaded once per workgroup into LDS (four buffers per head, one barrier per two chunks, so
+//   the waves drift by up to a chunk between barriers) and every A operand read from it
 //   serves the wave's column blocks; the coefficients go straight into B operand registers
 //   (lane = one token x 8 ranks, elements past the token's count zeroed), two chunks ahead,
 //   each serving every head of the workgroup. Then per 16-token tile T: R(n) applied to the lane's token (n = its slot in the tile,
@@ -90,7 +91,7 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_scores_kernel(JScoresParams
   constexpr int TOK = JWAVES * CB * 16;    // tokens per workgroup
   // basis chunk buffers: piece (dim d, ranks 8k..8k+7) at index 4d + (k ^ jswz(d)), so that the
   // A operand reads (lane (n, g): slot g of row 16*blk + n) are free of bank conflicts
-  __shared__ __attribute__((aligned(16))) dkv_u32x4 sB[2][NHB][JDH * JCH / 8];
+  __shared__ __attribute__((aligned(16))) dkv_u32x4 sB[4][NHB][JDH * JCH / 8];
   // R(n) of every lane's token slot: [2*pp + k][lane] holds (cos, sin) of frequencies
   // 16pp + 4g + 2k and + 1
   __shared__ __attribute__((aligned(16))) dkv_f32x4 sRn[8][64];
@@ -190,35 +191,39 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_scores_kernel(JScoresParams
 #pragma unroll
       for (int hh = 0; hh < NHB; ++hh) {
         sB[0][hh][tid] = load_b(0, hh);
-        ba[hh] = load_b(1, hh);
-        bb[hh] = load_b(2, hh);
+        sB[1][hh][tid] = load_b(1, hh);
+        ba[hh] = load_b(2, hh);
+        bb[hh] = load_b(3, hh);
       }
       load_x(0, xa);
       load_x(1, xb);
     }
     __syncthreads();
-    // Chunk c: its basis sits in sB[c & 1] (written before the previous barrier); the basis of
-    // chunk c+1 (loaded two chunks ago) goes to the other buffer, whose readers finished before
-    // that barrier, and the basis of chunk c+3 is loaded into the registers it came from (b: ba
+    // Chunk c: its basis sits in sB[c & 3], written at step c-2 (or before the loop), and a
+    // barrier follows every odd step. The basis of chunk c+2 (loaded two steps ago) goes to
+    // buffer (c+2) & 3, whose previous chunk c-2 was read at step c-2, before the barrier that
+    // ends the pair of steps preceding c; chunk c's own buffer was written before that barrier
+    // too. The basis of chunk c+4 is then loaded into the registers chunk c+2 came from (b: ba
     // for even c, bb for odd c). The coefficients of chunk c+2 are loaded, right after chunk c's
     // products are issued, into the registers chunk c used (x: xa, xb in turn). No loaded value
     // is ever copied, so the waits cover only the values being used. Loads past the last chunk
-    // clamp the basis index and have coefficient counts <= 0 (no traffic).
-    auto step = [&](int c, dkv_u32x4(&x)[CB], dkv_u32x4(&bn)[NHB]) {
+    // clamp the basis index and have coefficient counts <= 0 (no traffic). One barrier per pair
+    // of chunks instead of one per chunk: 3-4% less time at the config-3 shape.
+    auto step = [&](int c, dkv_u32x4(&x)[CB], dkv_u32x4(&bn)[NHB], bool sync) {
 #pragma unroll
       for (int cb = 0; cb < CB; ++cb)
         if ((pmask[cb] >> c) & 1u) x[cb] = dkv_mask8(x[cb], tlen[cb] - (JCH * c + 8 * g));
 #pragma unroll
       for (int hh = 0; hh < NHB; ++hh) {
-        sB[(c + 1) & 1][hh][tid] = bn[hh];
-        bn[hh] = load_b(c + 3, hh);
+        sB[(c + 2) & 3][hh][tid] = bn[hh];
+        bn[hh] = load_b(c + 4, hh);
       }
       dkv_u32x4 a[NHB][8];
 #pragma unroll
       for (int hh = 0; hh < NHB; ++hh)
 #pragma unroll
         for (int blk = 0; blk < 8; ++blk)
-          a[hh][blk] = sB[c & 1][hh][4 * (16 * blk + n) + (g ^ jswz(n))];
+          a[hh][blk] = sB[c & 3][hh][4 * (16 * blk + n) + (g ^ jswz(n))];
 #pragma unroll
       for (int hh = 0; hh < NHB; ++hh)
 #pragma unroll
@@ -231,15 +236,15 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_scores_kernel(JScoresParams
       __builtin_amdgcn_sched_group_barrier(0x100, 8 * NHB, 0);
       __builtin_amdgcn_sched_group_barrier(0x008, 8 * NHB * CB, 0);
       load_x(c + 2, x);
-      __syncthreads();
+      if (sync) __syncthreads();
     };
     // whole pairs in the loop (every path back to its head has issued both steps' loads)
     int c = 0;
     for (; c + 1 < nch; c += 2) {
-      step(c, xa, ba);
-      step(c + 1, xb, bb);
+      step(c, xa, ba, false);
+      step(c + 1, xb, bb, true);
     }
-    if (c < nch) step(c, xa, ba);
+    if (c < nch) step(c, xa, ba, false);
   };
   if (b == p.B - 1)
     rank_loop(std::integral_constant<bool, true>{});
