@@ -71,6 +71,84 @@ def test_decode_steps_across_switch(dev):
 
 
 @pytest.mark.gpu
+def test_config2_32_layers_100_steps(dev):
+    """Config 2 at its stated size: 32 layer caches (fp16, B=4, 8 groups, mean retention 0.47)
+    from 480 tokens for 100 decode steps each. Every step of every layer is routed by its own
+    length (fused up to 499 tokens, two-stage from 500); sampled layers and steps are checked
+    against the oracle, and every layer's packed tables and buffers bit-exactly at the end."""
+    print("[gpu] config2 32 layers x 100 steps", flush=True)
+    dtype = torch.float16
+    B, G, Hq, R, S0, steps, layers = 4, 8, 32, 128, 480, 100, 32
+    rows = B * G
+    cache = CustomDynamicCache()
+    slots, bases = [], []
+    for layer in range(layers):
+        case = make_case(B=B, G=G, Hq=Hq, S=S0, mean=0.47, seed=1000 + layer)
+        kc, vc = cast_np(case.k_coef, dtype), cast_np(case.v_coef, dtype)
+        cache.update_sp(torch.from_numpy(kc).to(dev, dtype), torch.from_numpy(case.k_len).to(dev),
+                        torch.from_numpy(vc).to(dev, dtype), torch.from_numpy(case.v_len).to(dev),
+                        R, layer, R)
+        sk, sv = PackedSlot(), PackedSlot()
+        sk.append_prefill(kc, case.k_len, R)
+        sv.append_prefill(vc, case.v_len, R)
+        slots.append((sk, sv))
+        bases.append((cast_np(case.k_basis, dtype), cast_np(case.v_basis, dtype), case.theta))
+    dbases = [(torch.from_numpy(kb).to(dev, dtype), torch.from_numpy(vb).to(dev, dtype))
+              for kb, vb, _ in bases]
+    rng = np.random.default_rng(1041)
+    policy = KernelPolicy()
+    check_layers, check_steps = (0, 17, 31), (0, 18, 19, 20, 99)
+    n_checked = 0
+    last = [None] * layers
+    for step in range(steps):
+        for layer in range(layers):
+            kx = cast_np(rng.standard_normal((rows, 1, R)), dtype)
+            vx = cast_np(rng.standard_normal((rows, 1, R)), dtype)
+            kl = beta_lengths((rows, 1), 0.47, R, rng)
+            vl = beta_lengths((rows, 1), 0.47, R, rng)
+            fk, fv, lk, lv, okk, ovv = cache.update_sp(
+                torch.from_numpy(kx).to(dev, dtype), torch.from_numpy(kl).to(dev),
+                torch.from_numpy(vx).to(dev, dtype), torch.from_numpy(vl).to(dev), R, layer, R)
+            last[layer] = (fk, fv, lk, lv, okk, ovv)
+            sk, sv = slots[layer]
+            sk.append_decode(kx, kl, R)
+            sv.append_decode(vx, vl, R)
+            L = cache.get_seq_length_sp(layer)
+            assert L == S0 + step + 1
+            route = policy.select(L)
+            assert route == oracle_router.select(L)
+            assert route == ("short_fused" if L < 500 else "long_two_stage")
+            q = cast_np(rng.standard_normal((B, Hq, 128)), dtype)
+            kb, vb = dbases[layer]
+            got = grouped_decode_attention(torch.from_numpy(q).to(dev, dtype), fk, fv, lk, okk,
+                                           lv, ovv, kb, vb, theta=bases[layer][2], route=route)
+            if layer in check_layers and step in check_steps:
+                hk, ho = sk.tables()
+                hv, hov = sv.tables()
+                ref = A.decode_attention(q, sk.flat, bases[layer][0], sv.flat, bases[layer][1],
+                                         hk, ho, hv, hov, bases[layer][2], route=route,
+                                         q_dtype="float16", row_of=lambda b, h: b * G + h // 4,
+                                         basis_of=lambda h: h // 4)
+                assert_close(got, ref, f"layer {layer} step {step} ({route})")
+                n_checked += 1
+    assert n_checked == len(check_layers) * len(check_steps)
+    for layer in range(layers):
+        sk, sv = slots[layer]
+        fk, fv, lk, lv, okk, ovv = last[layer]
+        hk, ho = sk.tables()
+        hv, hov = sv.tables()
+        for got_t, want_t, what in ((lk, hk, "K lens"), (okk, ho, "K offsets"),
+                                    (lv, hv, "V lens"), (ovv, hov, "V offsets")):
+            np.testing.assert_array_equal(got_t.cpu().numpy(), want_t,
+                                          err_msg=f"layer {layer} {what}")
+        for got_f, slot, what in ((fk, sk, "K flat"), (fv, sv, "V flat")):
+            n = int(slot.ptr.max())
+            np.testing.assert_array_equal(got_f[:, :n].float().cpu().numpy(),
+                                          slot.flat[:, :n].astype(np.float32),
+                                          err_msg=f"layer {layer} {what}")
+
+
+@pytest.mark.gpu
 def test_config4_ragged_batch(dev):
     """Config 4: 32 sequences with lengths log-uniform in [64, 16384], one B=1 reference cache per
     sequence (the reference cache shares seq_ptr across a batch), fp16, mean retention 0.20;
