@@ -151,11 +151,11 @@ def test_av_matches_vector_kernel(dev, dtype, B, S, R, n_basis, Hq):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("route", ["short_fused", "long_two_stage"])
-def test_joint_attention_against_oracle(dev, route):
+def test_joint_attention_against_oracle(dev, route, dtype):
     """The router's joint path end to end against the oracle (two rows, 700 tokens)."""
-    print(f"[gpu] joint attention {route}", flush=True)
-    dtype = torch.bfloat16
+    print(f"[gpu] joint attention {route} {dtype}", flush=True)
     h = _case(2, 700, 1024, 8, dtype=dtype, seed=11, len_lo=0)
     d = _dev(h, dev, dtype)
     k_up = d["kb"].repeat_interleave(4, dim=0).contiguous()
@@ -166,8 +166,9 @@ def test_joint_attention_against_oracle(dev, route):
     assert got is not None and got.dtype == dtype
     ref = A.decode_attention(h["q"], h["fk"], np.repeat(h["kb"], 4, axis=0), h["fv"],
                              np.repeat(h["vb"], 4, axis=0), h["lk"], h["ok"], h["lv"], h["ov"],
-                             THETA, route=route, q_dtype="bfloat16")
-    assert_close(got, ref, f"joint {route}")
+                             THETA, route=route,
+                             q_dtype="bfloat16" if dtype == torch.bfloat16 else "float16")
+    assert_close(got, ref, f"joint {route} {dtype}")
 
 
 @pytest.mark.gpu
