@@ -11,7 +11,10 @@
 // float(pos) * inv_freq as the decode kernels form them, result rounded to the cache dtype);
 // dkv_prefill_attention is a causal GQA flash-attention forward on MFMA:
 //   one workgroup = 128 queries of one query head (4 waves x 2 blocks of 16 queries, so every
-//   K and V operand read from LDS serves two products); key tiles of 64
+//   K and V operand read from LDS serves two products), the work items handed out longest
+//   first and evenly over the 8 XCDs, a KV head's query heads on one XCD (the grid's own
+//   order gave XCD k only the query blocks k, k+8, ...: 0.40 ms against 0.25 at B=4,
+//   S=2048); key tiles of 64
 //   are staged in LDS (double-buffered, direct-to-LDS loads, 16-byte chunks XOR-swizzled by
 //   key so that both the row reads of K and the transposed reads of V avoid bank conflicts);
 //   S^T = K Q^T on 16x16x32 MFMA (each lane then holds one query's scores for 16 keys), online
@@ -104,7 +107,8 @@ __device__ __forceinline__ void split_hi_lo(const float (&p)[4], dkv_u32x2& hi, 
   }
 }
 
-// grid: (ceil(Sq / 128), Hq, B); 256 threads. ODT: output dtype (DT or fp32).
+// grid: (ceil(Sq / 128), Hq, B); 256 threads (the workgroup's item is remapped from its
+// linear id, see below). ODT: output dtype (DT or fp32).
 template <int DT, int ODT>
 __global__ __launch_bounds__(256, 2) void fa_prefill_kernel(PrefillParams p) {
   __shared__ __attribute__((aligned(16))) uint8_t sK[2][FA_TILE_BYTES];
@@ -112,9 +116,36 @@ __global__ __launch_bounds__(256, 2) void fa_prefill_kernel(PrefillParams p) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 15, g = lane >> 4;
-  const int b = blockIdx.z, h = blockIdx.y;
+  // Work item of this workgroup. Workgroups go to the 8 XCDs round-robin by linear id L (XCD
+  // L % 8, in order of L on each), so items are handed out by L in longest-first order of
+  // causal work: units (query block, b, KV head) from the last query block down, unit
+  // c + 8j to XCD c, each unit's query heads consecutive on it (they read the same K and V
+  // tiles, from that XCD's L2). Every XCD then gets the same mix of query blocks, each
+  // longest first. (The grid's own order gave XCD k the query blocks k, k+8, ... only: 2.4x
+  // the work on XCD 7 as on XCD 0 at 16 blocks.) When the units do not divide among the
+  // XCDs the items go out by L in the same longest-first order, query heads spread.
+  int b, h, qblk;
+  {
+    const int nx = gridDim.x, ny = gridDim.y, nz = gridDim.z;
+    const int L = blockIdx.x + nx * (blockIdx.y + ny * blockIdx.z);
+    const int grp = p.Hq / p.Hkv;       // query heads per KV head
+    const int units = nx * nz * p.Hkv;  // (query block, b, KV head)
+    if (units % 8 == 0) {
+      const int xcd = L & 7, rank = L >> 3;
+      const int u = xcd + 8 * (rank / grp);
+      const int per = nz * p.Hkv;  // units per query block
+      qblk = nx - 1 - u / per;
+      b = (u % per) / p.Hkv;
+      h = ((u % per) % p.Hkv) * grp + rank % grp;
+    } else {
+      const int per = ny * nz;  // items per query block
+      qblk = nx - 1 - L / per;
+      h = (L % per) % ny;
+      b = (L % per) / ny;
+    }
+  }
   const int kvh = h / (p.Hq / p.Hkv);
-  const int q0 = blockIdx.x * FA_BQ;
+  const int q0 = qblk * FA_BQ;
   const int wq0 = q0 + FA_QW * wave;  // the wave's first query
   // this lane's query in block qb (B operand column, output row)
   auto qrow = [&](int qb) { return wq0 + 16 * qb + n; };
