@@ -230,7 +230,7 @@ __global__ __launch_bounds__(256, 2) void fa_prefill_kernel(PrefillParams p) {
 #pragma unroll
       for (int qb = 0; qb < FA_QB; ++qb)
 #pragma unroll
-        for (int u = 0; u < 4; ++u) z[qb][kb][u] = sacc[qb][u] * p.scale_log2;
+        for (int u = 0; u < 4; ++u) z[qb][kb][u] = sacc[qb][u];  // unscaled (see below)
     }
     if (key0 + FA_BK > k_end || (p.causal && key0 + FA_BK - 1 > p.q_offset + wq0)) {
 #pragma unroll
@@ -253,7 +253,10 @@ __global__ __launch_bounds__(256, 2) void fa_prefill_kernel(PrefillParams p) {
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
         for (int u = 0; u < 4; ++u) m = fa_max(m, z[qb][kb][u]);
-      tmax[qb] = fa_max4(m);
+      // the scale is applied to the tile's maximum and inside the exponent's fma (one VALU
+      // per score less than scaling every score: 2-3% of the launch); it is positive (the
+      // entry point checks), so the maximum commutes with it
+      tmax[qb] = fa_max4(m) * p.scale_log2;
     }
     if (__ballot(tmax[0] > m_run[0] + FA_RESCALE || tmax[FA_QB - 1] > m_run[FA_QB - 1] + FA_RESCALE)) {
 #pragma unroll
@@ -282,7 +285,7 @@ __global__ __launch_bounds__(256, 2) void fa_prefill_kernel(PrefillParams p) {
         float pu[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-          pu[u] = __builtin_amdgcn_exp2f(z[qb][kb][u] - m_run[qb]);
+          pu[u] = __builtin_amdgcn_exp2f(__builtin_fmaf(z[qb][kb][u], p.scale_log2, -m_run[qb]));
           l_run[qb] += pu[u];
         }
         dkv_u32x2 ph, pl;
@@ -372,6 +375,8 @@ extern "C" int dkv_prefill_attention(void* stream, int dtype, const void* q, lon
                                      long long v_elems, void* out, int out_dtype, long long o_sb,
                                      long long o_sh, long long o_ss, int B, int Hq, int Hkv,
                                      int Sq, int Sk, int Dh, int causal, float scale) {
+  // the kernel takes each tile's maximum before scaling: a positive, finite scale only
+  if (!(scale > 0.f) || !(scale < INFINITY)) return DKV_E_UNSUPPORTED;
   if (dtype != DKV_F16 && dtype != DKV_BF16) return DKV_E_UNSUPPORTED;
   if (out_dtype != dtype && out_dtype != DKV_F32) return DKV_E_ARG;
   if (B < 0 || Hq <= 0 || Hkv <= 0 || Sq < 0 || Sk < 0) return DKV_E_ARG;

@@ -331,7 +331,8 @@ int dkv_cutoff_kv(void* stream, int dtype, const void* xk, const void* xv, long 
  * and token, unit dim stride, 16-byte aligned rows; k_elems / v_elems: elements addressable
  * from k / v (bounds of the buffer loads). fp32 softmax, probabilities as a hi + lo pair in
  * the compute dtype for the P.V product. dtype: DKV_F16 or DKV_BF16; out_dtype: dtype or
- * DKV_F32 (the normalised result before rounding). Replaces the eager /
+ * DKV_F32 (the normalised result before rounding). scale: positive and finite (else
+ * DKV_E_UNSUPPORTED; the reference passes 1/sqrt(128)). Replaces the eager /
  * SDPA attention call of the prefill branch (:373-383).
  */
 int dkv_rope_dense(void* stream, int dtype, void* x, long long row_ld, long long tok_ld,

@@ -67,6 +67,11 @@ def test_argument_validation_without_device():
     assert rc == -2
     with pytest.raises(NotImplementedError):
         _lib.check(rc, "dkv_decode_splitk")
+    # prefill attention: the scale must be positive and finite (checked before anything else)
+    for scale in (0.0, -0.088, float("nan"), float("inf")):
+        rc = lib.dkv_prefill_attention(None, 2, None, 0, 0, 0, None, 0, 0, 0, 0, None, 0, 0, 0, 0,
+                                       None, 2, 0, 0, 0, 1, 32, 8, 16, 16, 128, 1, scale)
+        assert rc == -2, scale
 
 
 def test_no_cpu_fallback():
