@@ -47,6 +47,27 @@ def test_prefill_attention_matches_oracle(dev, name):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("scale", [0.3, 0.01])
+def test_prefill_attention_custom_scale(dev, scale):
+    """A positive scale other than 1/sqrt(128): the kernel takes each tile's maximum of the
+    unscaled scores and applies the scale there and inside the exponent, so a sharp (0.3) and a
+    flat (0.01) softmax check that fold against the oracle; scales <= 0 are rejected."""
+    print(f"[gpu] prefill attention scale {scale}", flush=True)
+    B, Hq, Hkv, S = 2, 8, 2, 200
+    dtype = torch.bfloat16
+    rng = np.random.default_rng(31)
+    q = cast_np(rng.standard_normal((B, Hq, S, 128)).astype(np.float32), dtype)
+    k = cast_np(rng.standard_normal((B, Hkv, S, 128)).astype(np.float32), dtype)
+    v = cast_np(rng.standard_normal((B, Hkv, S, 128)).astype(np.float32), dtype)
+    t = lambda a: torch.from_numpy(a).to(device=dev, dtype=dtype)  # noqa: E731
+    got = prefill_attention(t(q), t(k), t(v), causal=True, scale=scale, out_dtype=torch.float32)
+    ref = P.attention(q, k, v, causal=True, scale=scale)
+    assert_close(got, ref, f"scale {scale}")
+    with pytest.raises(NotImplementedError):
+        prefill_attention(t(q), t(k), t(v), causal=True, scale=-scale)
+
+
+@pytest.mark.gpu
 def test_prefill_attention_strided_views(dev):
     """(B, S, H, D) activations viewed as (B, H, S, D) without a copy."""
     print("[gpu] prefill attention strided", flush=True)
