@@ -23,6 +23,8 @@ CASES = {
     "chunk_Sq50_Sk300": (2, 8, 2, 50, 300, True, torch.bfloat16),
     "noncausal": (1, 8, 2, 33, 129, False, torch.bfloat16),
     "S1024": (1, 32, 8, 1024, 1024, True, torch.bfloat16),
+    # 9 (query block, batch, KV head) units: the work items go out in the ungrouped order
+    "S300_units9": (1, 6, 3, 300, 300, True, torch.float16),
 }
 
 
