@@ -29,6 +29,8 @@ _vp, _ll, _i, _f = C.c_void_p, C.c_longlong, C.c_int, C.c_float
 _SIGNATURES = {
     "dkv_version": (_i, []),
     "dkv_status_string": (C.c_char_p, [_i]),
+    "dkv_flat_range_elems": (_ll, [_ll, _ll, _ll]),
+    "dkv_view_extent_elems": (_ll, [_i, _vp, _vp]),
     "dkv_append_decode": (_i, [_vp, _i, _vp, _ll, _vp, _ll, _vp, _ll, _vp, _vp, _ll, _ll, _vp, _i, _i, _i]),
     "dkv_append_decode_kv": (_i, [_vp, _i, _i, _i, _i,
                                   _vp, _ll, _vp, _ll, _vp, _ll, _vp, _vp, _ll, _ll, _vp,
@@ -149,6 +151,38 @@ def dtype_code(dt: torch.dtype) -> int:
         return _DTYPE_CODE[dt]
     except KeyError:
         raise ValueError(f"unsupported dtype {dt}") from None
+
+
+def flat_covers_rows(t: torch.Tensor) -> bool:
+    """The C ABI's contract for packed flat buffers (rows, ld): rows * ld elements addressable
+    from the base pointer inside the tensor's storage (each kernel's buffer resource for row r
+    covers the elements from row r to the buffer's end, ``dkv_flat_range_elems``)."""
+    if t.dim() != 2 or t.stride(0) < 0:
+        return False
+    avail = t.untyped_storage().nbytes() // t.element_size() - t.storage_offset()
+    return t.shape[0] * t.stride(0) <= avail
+
+
+def view_extent(t: torch.Tensor) -> int:
+    """Elements addressable from ``t.data_ptr()`` by its shape and strides (one past its last
+    element), from the library's own definition (``dkv_view_extent_elems``)."""
+    nd = t.dim()
+    shape = (C.c_longlong * max(nd, 1))(*t.shape)
+    stride = (C.c_longlong * max(nd, 1))(*t.stride())
+    n = int(load().dkv_view_extent_elems(nd, shape, stride))
+    if n < 0:
+        raise ValueError("dkv_view_extent_elems rejected the view")
+    return n
+
+
+def flat_operand(t: torch.Tensor) -> torch.Tensor:
+    """``t`` when it meets the flat-buffer contract (``flat_covers_rows``), else a contiguous
+    copy (a column slice whose storage ends inside its last row's stride: the last row's
+    resource would otherwise reach past the allocation)."""
+    if flat_covers_rows(t):
+        return t
+    # clone rather than contiguous(): a one-row view counts as contiguous whatever its stride
+    return t.clone(memory_format=torch.contiguous_format)
 
 
 def stream_of(t: torch.Tensor) -> int:

@@ -206,6 +206,16 @@ __global__ __launch_bounds__(256) void decompress_kernel(const T* __restrict__ f
 
 extern "C" int dkv_version(void) { return DKV_VERSION; }
 
+extern "C" long long dkv_flat_range_elems(long long rows, long long row, long long ld) {
+  return dkv_flat_tail_elems(rows, row, ld, DKV_FLAT_RSRC_CAP);
+}
+
+extern "C" long long dkv_view_extent_elems(int nd, const long long* shape,
+                                           const long long* stride) {
+  if (nd < 0 || (nd > 0 && (!shape || !stride))) return -1;
+  return dkv_view_extent(nd, shape, stride);
+}
+
 extern "C" const char* dkv_status_string(int status) {
   switch (status) {
     case DKV_OK: return "ok";

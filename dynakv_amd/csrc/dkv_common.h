@@ -84,6 +84,34 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t dkv_make_rsrc(const void* base
   return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)bytes, 0x00020000);
 }
 
+// Buffer-resource ranges. A raw buffer resource returns zero for a load past its range without
+// touching memory, so the range decides which loads may reach memory: it must never extend past
+// memory the caller owns. Every range a kernel uses comes from one of these two functions
+// (exported for host-side tests as dkv_flat_range_elems / dkv_view_extent_elems).
+//
+// Elements one flat-buffer resource covers at most (its byte size stays below 2^31).
+constexpr int DKV_FLAT_RSRC_CAP = 0x3ffffff0;
+// Elements from row `row` of a packed (rows, ld) flat buffer to the buffer's end, at most `cap`.
+// The C ABI's contract for flat buffers: rows * ld elements are addressable from the base
+// pointer (a whole (rows, capacity) buffer, or a column slice of one whose storage runs to the
+// end of its last row; the Python wrappers pass a contiguous copy of any other view).
+__host__ __device__ inline long long dkv_flat_tail_elems(long long rows, long long row,
+                                                         long long ld, long long cap) {
+  const long long n = (rows - row) * ld;
+  return n < 0 ? 0 : (n < cap ? n : cap);
+}
+// One past the last element of a view with non-negative strides: the elements addressable from
+// its base pointer (0 for an empty view).
+__host__ __device__ inline long long dkv_view_extent(int nd, const long long* shape,
+                                                     const long long* stride) {
+  long long last = 0;
+  for (int i = 0; i < nd; ++i) {
+    if (shape[i] <= 0) return 0;
+    last += (shape[i] - 1) * stride[i];
+  }
+  return last + 1;
+}
+
 // Wave64 reductions via cross-lane xor shuffles.
 __device__ __forceinline__ float dkv_wave_sum(float v) {
 #pragma unroll

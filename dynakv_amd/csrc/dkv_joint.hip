@@ -49,7 +49,7 @@ constexpr int JRMAX = 1024;
 constexpr int JPREC = 4 + JRMAX;         // split record: m (log2 units), l, 2 unused, acc[R]
 constexpr int JRB = 128;                 // ranks per merge workgroup
 constexpr int JROPE_FIXED = 17;          // rows of the RoPE table before the per-tile rows
-constexpr int JFLAT_CAP = 0x3ffffff0;    // elements one buffer resource covers
+constexpr int JFLAT_CAP = DKV_FLAT_RSRC_CAP;  // elements one buffer resource covers
 constexpr int JMAX_SPLITS = 1024;  // token splits of the V pass
 constexpr float JLOG2E = 1.4426950408889634f;
 constexpr float JRESCALE = 11.5f;        // log2 units: rescale when the running max grows more
@@ -133,8 +133,7 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_scores_kernel(JScoresParams
   for (int w = 0; w < JWAVES; ++w) maxlen = max(maxlen, sMax[w]);
   const int nch = (maxlen + JCH - 1) / JCH;
 
-  const uint32_t end =
-      (uint32_t)min((long long)(p.B - b) * p.flat_ld, (long long)JFLAT_CAP);
+  const uint32_t end = (uint32_t)dkv_flat_tail_elems(p.B, b, p.flat_ld, JFLAT_CAP);
   const __amdgpu_buffer_rsrc_t rs = dkv_make_rsrc(p.flat + (long long)b * p.flat_ld, end * 2u);
   // this thread's basis piece of every chunk: dim bd, ranks 8*bk .. +8 of the chunk
   const int bd = tid >> 2, bk = (tid & 3) ^ jswz(bd);
@@ -386,8 +385,7 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_av_kernel(JAvParams p) {
     sbase[s] = (long long)b * p.sc_sb + (long long)(hq_ok[s] ? hq[s] : 0) * p.sc_sh;
   }
 
-  const uint32_t end =
-      (uint32_t)min((long long)(p.B - b) * p.flat_ld, (long long)JFLAT_CAP);
+  const uint32_t end = (uint32_t)dkv_flat_tail_elems(p.B, b, p.flat_ld, JFLAT_CAP);
   const __amdgpu_buffer_rsrc_t rs = dkv_make_rsrc(p.flat + (long long)b * p.flat_ld, end * 2u);
 
   // Tile j's inputs for this lane: the metadata (count, offset) of token n, its V pieces (ranks
@@ -953,8 +951,8 @@ extern "C" int dkv_joint_av(void* stream, int mode, int scores_dtype, int dtype,
   // prefetch of tiles past the last row's end returns zeros and touches no memory), within
   // what a 32-bit byte offset covers
   const int sc_elt = scores_dtype == DKV_F32 ? 4 : 2;
-  const long long sc_extent =
-      ((long long)(B - 1) * sc_sb + (long long)(Hq - 1) * sc_sh + (long long)S) * sc_elt;
+  const long long sc_shape[3] = {B, Hq, S}, sc_stride[3] = {sc_sb, sc_sh, sc_ss};
+  const long long sc_extent = dkv_view_extent(3, sc_shape, sc_stride) * sc_elt;
   const bool vec = sc_ss == 1 && S % 4 == 0 && sc_sb % 4 == 0 && sc_sh % 4 == 0 && sc_sb >= 0 &&
                    sc_sh >= 0 && ((uintptr_t)scores % (4 * sc_elt)) == 0 &&
                    sc_extent < (1LL << 31);

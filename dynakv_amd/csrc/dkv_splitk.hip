@@ -59,7 +59,7 @@ constexpr float RESCALE_THRESH = 11.5f;  // log2 units
 constexpr int OOB = 0x7ffffff0;          // buffer offset that reads as zero
 // elements a flat-buffer resource covers at most (its byte size stays below OOB), and the
 // largest row stride the kernel accepts (a row's last 16-byte window stays inside that range)
-constexpr int FLAT_ELEM_CAP = 0x3ffffff0;
+constexpr int FLAT_ELEM_CAP = DKV_FLAT_RSRC_CAP;
 constexpr int FLAT_LD_MAX = FLAT_ELEM_CAP - 8;
 constexpr int DPP_ROW_SHL8 = 0x108;      // DPP row_shl:8: lane i of a 16-lane row reads lane i+8
 
@@ -716,8 +716,8 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
   // covering the rest of the buffer up to FLAT_ELEM_CAP elements; token offsets go in the
   // voffset. Row strides are at most FLAT_LD_MAX, so a row's last window stays in range unless
   // the row is the buffer's last.
-  const uint32_t k_end = (uint32_t)min((long long)(p.rows - row) * p.k_ld, (long long)FLAT_ELEM_CAP);
-  const uint32_t v_end = (uint32_t)min((long long)(p.rows - row) * p.v_ld, (long long)FLAT_ELEM_CAP);
+  const uint32_t k_end = (uint32_t)dkv_flat_tail_elems(p.rows, row, p.k_ld, FLAT_ELEM_CAP);
+  const uint32_t v_end = (uint32_t)dkv_flat_tail_elems(p.rows, row, p.v_ld, FLAT_ELEM_CAP);
   const __amdgpu_buffer_rsrc_t rk_src = dkv_make_rsrc(p.k_flat + (long long)row * p.k_ld, k_end * 2u);
   const __amdgpu_buffer_rsrc_t rv_src = dkv_make_rsrc(p.v_flat + (long long)row * p.v_ld, v_end * 2u);
   constexpr int k_row0 = 0, v_row0 = 0;

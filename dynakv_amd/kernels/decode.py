@@ -154,6 +154,7 @@ def splitk_attention(q3: torch.Tensor, k_flat: torch.Tensor, v_flat: torch.Tenso
         out = torch.empty((B, hq, dh), dtype=odt, device=q3.device)
     elif out.dtype != odt or out.stride(2) != 1:
         raise ValueError("out must have unit last stride and the requested dtype")
+    k_flat, v_flat = _lib.flat_operand(k_flat), _lib.flat_operand(v_flat)
     st = _lib.stream_of(q3)
     nfl = lib.dkv_splitk_workspace_floats(B, hq, layout.n_kv, S, R, split_len)
     ws = workspace(q3.device, st, int(nfl))

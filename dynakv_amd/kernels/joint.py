@@ -25,7 +25,8 @@ import torch
 from .. import _lib
 from .decode import FLAT_LD_MAX, rope_table
 
-_BASIS_CACHE: dict = {}  # id(basis) -> (weakref to it, (ptr, shape, strides, version), distinct)
+_BASIS_CACHE: dict = {}  # id(basis) -> (weakref to it, (ptr, shape, strides, version), factor)
+_BT_CACHE: dict = {}  # id(k_up) -> (weakref to it, (ptr, shape, strides, version, heads), copy)
 _WS_CACHE: dict = {}
 
 
@@ -41,45 +42,60 @@ def _workspace(device: torch.device, stream: int, floats: int) -> torch.Tensor:
 
 
 def _remember(cache: dict, t: torch.Tensor, key, value) -> None:
-    """Cache ``value`` for tensor object ``t``; the entry goes when ``t`` is collected."""
+    """Cache ``value`` for tensor object ``t``; the entry goes when ``t`` is collected. ``value``
+    must not refer to ``t`` (no view of it: a view keeps its base alive through ``_base``), or
+    the entry would keep ``t`` alive for good."""
     if id(t) not in cache:
         weakref.finalize(t, cache.pop, id(t), None)
     cache[id(t)] = (weakref.ref(t), key, value)
 
 
-def _distinct(basis: torch.Tensor, n_heads: int) -> torch.Tensor:
-    """The distinct bases of ``basis`` (Hb, R, Dh) when every group of k consecutive entries
-    repeats its first (k the largest of 8, 4, 2 that does so), else ``basis`` itself. Cached per
-    tensor object and in-place version, so the comparison runs once per basis."""
+def _key(t: torch.Tensor, *extra):
+    return (t.data_ptr(), tuple(t.shape), tuple(t.stride()), t._version, *extra)
+
+
+def _repeat_factor(basis: torch.Tensor, n_heads: int) -> int:
+    """k > 1 when every group of k consecutive entries of ``basis`` (Hb, R, Dh) repeats its first
+    (k the largest of 8, 4, 2 that does so), else 1. Cached per tensor object and in-place
+    version, so the comparison runs once per basis; the cache holds only the integer."""
     ent = _BASIS_CACHE.get(id(basis))
-    key = (basis.data_ptr(), tuple(basis.shape), tuple(basis.stride()), basis._version)
+    key = _key(basis, n_heads)
     if ent is not None and ent[0]() is basis and ent[1] == key:
         return ent[2]
     Hb = basis.shape[0]
-    out = basis
+    factor = 1
     for k in (8, 4, 2):
         if Hb % k == 0 and Hb // k >= 1 and n_heads % (Hb // k) == 0 and n_heads // (Hb // k) <= 8:
             v = basis.reshape(Hb // k, k, *basis.shape[1:])
             if torch.equal(v, v[:, :1].expand_as(v)):
-                out = v[:, 0]
+                factor = k
                 break
-    _remember(_BASIS_CACHE, basis, key, out)
-    return out
+    _remember(_BASIS_CACHE, basis, key, factor)
+    return factor
 
 
-_BT_CACHE: dict = {}
+def _distinct(basis: torch.Tensor, n_heads: int) -> torch.Tensor:
+    """The distinct bases of ``basis`` (Hb, R, Dh) -- a view of its first entry of every repeated
+    group -- when its entries repeat in groups (``_repeat_factor``), else ``basis`` itself."""
+    k = _repeat_factor(basis, n_heads)
+    if k == 1:
+        return basis
+    return basis.reshape(basis.shape[0] // k, k, *basis.shape[1:])[:, 0]
 
 
-def _transposed(basis: torch.Tensor) -> torch.Tensor:
-    """(nb, R/32, Dh, 32) contiguous copy of a (nb, R, Dh) basis (transposed in 32-rank chunks,
-    each chunk contiguous), cached per tensor object."""
-    ent = _BT_CACHE.get(id(basis))
-    key = (basis.data_ptr(), tuple(basis.shape), tuple(basis.stride()), basis._version)
-    if ent is not None and ent[0]() is basis and ent[1] == key:
+def _transposed(k_up: torch.Tensor, n_heads: int) -> torch.Tensor:
+    """(nb, R/32, Dh, 32) contiguous copy of the distinct bases (nb, R, Dh) of ``k_up``
+    (transposed in 32-rank chunks, each chunk contiguous), cached per ``k_up`` object and
+    in-place version. The copy is its own storage, so the cache does not keep ``k_up`` alive."""
+    ent = _BT_CACHE.get(id(k_up))
+    key = _key(k_up, n_heads)
+    if ent is not None and ent[0]() is k_up and ent[1] == key:
         return ent[2]
+    basis = _distinct(k_up, n_heads)
     nb, R, Dh = basis.shape
-    bt = basis.reshape(nb, R // 32, 32, Dh).transpose(2, 3).contiguous()
-    _remember(_BT_CACHE, basis, key, bt)
+    bt = basis.reshape(nb, R // 32, 32, Dh).transpose(2, 3).clone(
+        memory_format=torch.contiguous_format)
+    _remember(_BT_CACHE, k_up, key, bt)
     return bt
 
 
@@ -117,8 +133,8 @@ def joint_scores(q3: torch.Tensor, k_up: torch.Tensor, k_flat: torch.Tensor,
     S = lens.shape[1]
     if q3.stride(2) != 1:
         q3 = q3.contiguous()
-    basis = _distinct(k_up, Hq)
-    bt = _transposed(basis)
+    bt = _transposed(k_up, Hq)
+    k_flat = _lib.flat_operand(k_flat)
     st = _lib.stream_of(q3)
     rope, tiles = rope_table(q3.device, st, theta, S)
     out = torch.empty((B, Hq, S), dtype=out_dtype, device=q3.device)
@@ -147,6 +163,7 @@ def joint_av(scores: torch.Tensor, v_up: torch.Tensor, v_flat: torch.Tensor,
     if v_up.stride(2) != 1:
         v_up = v_up.contiguous()
     v_up = _distinct(v_up, Hq)  # the merge projects all query heads of a basis together
+    v_flat = _lib.flat_operand(v_flat)
     ws = _workspace(scores.device, st, int(lib.dkv_joint_av_workspace_floats(B, Hq, S, R)))
     out = torch.empty((B, Hq, 128), dtype=out_dtype, device=scores.device)
     rc = lib.dkv_joint_av(

@@ -48,6 +48,8 @@ class DecodeLayerPlan:
         fk, lk, ok, pk = ck[0], ck[1], ck[2], ck[3]
         fv, lv, ov, pv = cv[0], cv[1], cv[2], cv[3]
         dev = fk.device
+        if not (_lib.flat_covers_rows(fk) and _lib.flat_covers_rows(fv)):
+            raise ValueError("the cache's flat buffers must hold rows * ld elements")
         st = _lib.stream_of(fk)
         lib = _lib.load()
         B, G, R, Dh, Hq = self.B, self.G, self.R, self.Dh, self.Hq

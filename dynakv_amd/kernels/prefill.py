@@ -22,8 +22,9 @@ from .. import _lib
 
 
 def _extent(t: torch.Tensor) -> int:
-    """Elements addressable from ``t.data_ptr()`` by its strides."""
-    return 1 + sum((s - 1) * st for s, st in zip(t.shape, t.stride()) if s > 0)
+    """Elements addressable from ``t.data_ptr()`` by its strides: the byte range of the kernel's
+    buffer resource over ``t`` is this count times the element size."""
+    return _lib.view_extent(t)
 
 
 def rope_dense_(x: torch.Tensor, *, theta: float, pos0: int = 0) -> torch.Tensor:

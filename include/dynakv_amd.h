@@ -51,6 +51,22 @@ int dkv_version(void);
 const char* dkv_status_string(int status);
 
 /*
+ * Buffer-resource ranges (no reference counterpart: they state the memory contract of the
+ * kernels that read through raw buffer resources, and let host-side tests check it).
+ *
+ * Packed flat buffers (rows, ld) passed to dkv_decode_splitk, dkv_decode_layer,
+ * dkv_joint_scores and dkv_joint_av: rows * ld elements must be addressable from the base
+ * pointer (a whole (rows, capacity) buffer, or a column slice of one whose storage runs to the
+ * end of its last row). A workgroup reading row `row` covers the elements from that row to the
+ * buffer's end, at most 0x3ffffff0: dkv_flat_range_elems returns that count.
+ * dkv_view_extent_elems: one past the last element of a view of nd dimensions with non-negative
+ * strides (0 when empty; -1 for a bad argument), the range of a strided operand such as
+ * dkv_joint_av's scores.
+ */
+long long dkv_flat_range_elems(long long rows, long long row, long long ld);
+long long dkv_view_extent_elems(int nd, const long long* shape, const long long* stride);
+
+/*
  * Decode append: one new token per row.
  * Replaces update_cache_decode_kernel and its launch
  * (reference src/dynakv/kernels/compressed_cache.py:7-34, launch :170-181).

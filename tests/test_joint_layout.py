@@ -18,7 +18,8 @@ def test_distinct_bases_of_a_repeated_basis():
     rep = kb.repeat_interleave(4, dim=0).contiguous()  # the reference's k_up for 32 heads
     got = J._distinct(rep, 32)
     assert got.shape == (8, 64, 128) and torch.equal(got, kb)
-    assert J._distinct(rep, 32) is got  # cached per object and version
+    assert got.data_ptr() == rep.data_ptr()  # a view of the first copy of every group
+    assert J._BASIS_CACHE[id(rep)][2] == 4  # cached per object and version: the factor only
     # a repeat by 2 of 16 bases (2 query heads per basis)
     kb16 = _basis(16, 32, seed=1)
     assert J._distinct(kb16.repeat_interleave(2, dim=0).contiguous(), 32).shape[0] == 16
@@ -32,12 +33,33 @@ def test_chunk_major_transpose():
     """Element B[h][32c + k][d] sits at [h][c][d][k]: each 32-rank chunk of the transposed basis
     is one contiguous (Dh, 32) block."""
     b = _basis(3, 96, dt=torch.float32)
-    bt = J._transposed(b)
+    bt = J._transposed(b, 3)
     assert bt.shape == (3, 3, 128, 32) and bt.is_contiguous()
     h, c, d, k = 2, 1, 77, 5
     assert bt[h, c, d, k] == b[h, 32 * c + k, d]
     assert torch.equal(bt.permute(0, 1, 3, 2).reshape(3, 96, 128), b)
-    assert J._transposed(b) is bt
+    assert J._transposed(b, 3) is bt
+    # a repeated basis: the copy holds its distinct bases only
+    rep = b.repeat_interleave(4, dim=0).contiguous()
+    assert torch.equal(J._transposed(rep, 12), bt)
+
+
+def test_basis_caches_release_their_tensors():
+    """Neither cache keeps its key tensor alive: once the caller drops a basis (repeated or not)
+    and it is collected, both entries are gone."""
+    import gc
+
+    for nrep in (1, 4):
+        b = _basis(8, 64).repeat_interleave(nrep, dim=0).contiguous()
+        ident = id(b)
+        J._distinct(b, 8 * nrep)
+        J._transposed(b, 8 * nrep)
+        assert ident in J._BASIS_CACHE and ident in J._BT_CACHE
+        ref = __import__("weakref").ref(b)
+        del b
+        gc.collect()
+        assert ref() is None, "a cache entry keeps the basis alive"
+        assert ident not in J._BASIS_CACHE and ident not in J._BT_CACHE
 
 
 def test_eligibility():
