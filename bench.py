@@ -391,8 +391,14 @@ def bench_prefill(dev, iters=10, B=4, S=2048, Hq=32, Hkv=8, dtype=torch.bfloat16
         torch.cuda.synchronize(dev)
         times[name] = e0.elapsed_time(e1) / iters
     flops = 2.0 * 2 * B * Hq * (S * (S + 1) / 2) * 128  # QK and PV over the causal triangle
+    # agreement with torch on the same inputs (both in the compute dtype; torch's output is
+    # itself rounded, so this is a cross-check, the oracle tests are the parity bar)
+    ours = prefill_attention(q, k, v, causal=True, out_dtype=torch.float32)
+    theirs = sdpa().float()
+    diff = (ours - theirs).abs().max().item()
     return {
         "shape": f"B={B}, S={S}, {Hq}/{Hkv} heads, Dh 128, causal, {str(dtype).split('.')[-1]}",
+        "max_abs_vs_torch_sdpa": float(f"{diff:.3e}"),
         "ms_per_call": round(times["dynakv"], 4),
         "tflops": round(flops / (times["dynakv"] * 1e-3) / 1e12, 1),
         "torch_sdpa_ms_per_call": round(times["torch_sdpa"], 4),

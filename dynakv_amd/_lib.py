@@ -76,7 +76,8 @@ _SIGNATURES = {
     "dkv_decode_layer": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i]),
     "dkv_prefill_attention": (_i, [_vp, _i, _vp, _ll, _ll, _ll, _vp, _ll, _ll, _ll, _ll,
                                    _vp, _ll, _ll, _ll, _ll, _vp, _i, _ll, _ll, _ll,
-                                   _i, _i, _i, _i, _i, _i, _i, _f]),
+                                   _i, _i, _i, _i, _i, _i, _i, _f, _vp]),
+    "dkv_rope_apply": (_i, [_vp, _i, _vp, _ll, _ll, _ll, _vp, _vp, _ll, _ll, _i, _i, _i]),
     "dkv_cutoff_kv": (_i, [_vp, _i, _vp, _vp, _ll, _vp, _vp, _vp, _vp, _f, _i, _vp, _vp, _ll,
                            _vp, _vp, _ll, _vp, _ll, _i, _i, _i]),
 }

@@ -643,7 +643,7 @@ int dkv_layer_cutoff_append_rope(void* stream, const DkvDecodeLayer* L, const vo
   t.seq = seq;
   t.q = (uint16_t*)q;
   t.q_sb = q_sb;
-  t.q_rows = M * L->Hq;
+  t.q_rows = pos < 0 ? 0 : M * L->Hq;  // pos < 0: the caller rotated q already
   t.Hq = L->Hq;
   t.pos = pos;
   t.log_theta = L->log_theta;

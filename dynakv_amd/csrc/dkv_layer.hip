@@ -15,7 +15,8 @@
 extern "C" int dkv_decode_layer(void* stream, const DkvDecodeLayer* L, void* q,
                                 const void* k_coef, const void* v_coef, void* out, int seq,
                                 int pos) {
-  if (!L || !q || !k_coef || !v_coef || !out || seq < 0 || pos < 0) return DKV_E_ARG;
+  // pos == -1: q arrives rotated by the caller (the HF decoder's position embeddings)
+  if (!L || !q || !k_coef || !v_coef || !out || seq < 0 || pos < -1) return DKV_E_ARG;
   // cutoff logits, counts, the K+V appends and the q rotation in one launch
   int rc = dkv_layer_cutoff_append_rope(stream, L, k_coef, v_coef, q, seq, pos);
   if (rc != DKV_OK) return rc;

@@ -46,6 +46,7 @@ struct PrefillParams {
   int B, Hq, Hkv, Sq, Sk, q_offset, causal;
   float scale_log2;  // softmax scale * log2(e)
   uint32_t k_bytes, v_bytes;
+  const int* kstart;  // per batch row: keys before it are masked (left padding); may be null
 };
 
 template <int DT>
@@ -164,6 +165,9 @@ __global__ __launch_bounds__(256, 2) void fa_prefill_kernel(PrefillParams p) {
   const int q_last_pos = p.q_offset + min(q0 + FA_BQ, p.Sq) - 1;
   const int k_end = p.causal ? min(p.Sk, q_last_pos + 1) : p.Sk;
   const int n_tiles = (k_end + FA_BK - 1) / FA_BK;
+  // keys before ks are masked (a left-padded row's padding); tiles wholly before it are skipped
+  const int ks = p.kstart ? min(max(p.kstart[b], 0), p.Sk) : 0;
+  const int t0 = ks / FA_BK;
   const int wave_k_end =
       p.causal ? min(k_end, p.q_offset + min(wq0 + FA_QW, p.Sq)) : k_end;  // <= k_end
 
@@ -202,8 +206,8 @@ __global__ __launch_bounds__(256, 2) void fa_prefill_kernel(PrefillParams p) {
     l_run[qb] = 0.f;
   }
 
-  if (n_tiles > 0) issue(0);
-  for (int t = 0; t < n_tiles; ++t) {
+  if (t0 < n_tiles) issue(t0);
+  for (int t = t0; t < n_tiles; ++t) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();  // tile t is in LDS for every wave; tile t-1's buffer is free
     if (t + 1 < n_tiles) issue(t + 1);
@@ -232,7 +236,7 @@ __global__ __launch_bounds__(256, 2) void fa_prefill_kernel(PrefillParams p) {
 #pragma unroll
         for (int u = 0; u < 4; ++u) z[qb][kb][u] = sacc[qb][u];  // unscaled (see below)
     }
-    if (key0 + FA_BK > k_end || (p.causal && key0 + FA_BK - 1 > p.q_offset + wq0)) {
+    if (key0 + FA_BK > k_end || key0 < ks || (p.causal && key0 + FA_BK - 1 > p.q_offset + wq0)) {
 #pragma unroll
       for (int qb = 0; qb < FA_QB; ++qb) {
         const int my_pos = p.q_offset + qrow(qb);
@@ -241,7 +245,7 @@ __global__ __launch_bounds__(256, 2) void fa_prefill_kernel(PrefillParams p) {
 #pragma unroll
           for (int u = 0; u < 4; ++u) {
             const int key = key0 + 16 * kb + 4 * g + u;
-            if (key >= k_end || (p.causal && key > my_pos)) z[qb][kb][u] = -INFINITY;
+            if (key >= k_end || key < ks || (p.causal && key > my_pos)) z[qb][kb][u] = -INFINITY;
           }
       }
     }
@@ -320,7 +324,8 @@ __global__ __launch_bounds__(256, 2) void fa_prefill_kernel(PrefillParams p) {
     l += __shfl_xor(l, 32, 64);
     const int qr = qrow(qb);
     if (qr < p.Sq) {
-      const float inv = 1.f / l;
+      // a query with no key to attend (a padding position before the row's first key) gets 0
+      const float inv = l > 0.f ? 1.f / l : 0.f;
       const long long ob = (long long)b * p.o_sb + (long long)h * p.o_sh + (long long)qr * p.o_ss;
 #pragma unroll
       for (int db = 0; db < 8; ++db)
@@ -347,6 +352,39 @@ __global__ __launch_bounds__(256) void rope_dense_kernel(uint16_t* __restrict__ 
   dkv_rope_pair<DT>(x + r * r_ld + (long long)s * s_ld, i, pos0 + s, log_theta);
 }
 
+// In-place rotate-half RoPE of x (B, H, S, 128) with given cos / sin tables (B, S, 128) in the
+// dtype, rounded as the reference's apply_rotary_pos_emb_ computes (x * cos) + (rotate_half(x)
+// * sin) in the dtype (compressed_attention.py:18-22): each product rounded, then their sum.
+template <int DT>
+__global__ __launch_bounds__(256) void rope_apply_kernel(uint16_t* __restrict__ x, long long x_sb,
+                                                         long long x_sh, long long x_ss,
+                                                         const uint16_t* __restrict__ cs,
+                                                         const uint16_t* __restrict__ sn,
+                                                         long long c_sb, long long c_ss, int B,
+                                                         int H, int S) {
+  // no contraction: for fp16 the compiler narrows the products and the sum to half arithmetic
+  // and would fuse them into one fma, skipping the product's rounding
+#pragma clang fp contract(off)
+  const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+  const long long total = (long long)B * H * S * 64;
+  if (idx >= total) return;
+  const int i = (int)(idx % 64);
+  long long r = idx / 64;
+  const int s = (int)(r % S);
+  r /= S;
+  const int h = (int)(r % H);
+  const int b = (int)(r / H);
+  uint16_t* xr = x + (long long)b * x_sb + (long long)h * x_sh + (long long)s * x_ss;
+  const long long co = (long long)b * c_sb + (long long)s * c_ss;
+  const float x1 = dkv_load_f32<DT>(xr, i), x2 = dkv_load_f32<DT>(xr, i + 64);
+  const float c1 = dkv_load_f32<DT>(cs, co + i), c2 = dkv_load_f32<DT>(cs, co + i + 64);
+  const float s1 = dkv_load_f32<DT>(sn, co + i), s2 = dkv_load_f32<DT>(sn, co + i + 64);
+  const float o1 = dkv_round_to<DT>(x1 * c1) + dkv_round_to<DT>(-x2 * s1);
+  const float o2 = dkv_round_to<DT>(x2 * c2) + dkv_round_to<DT>(x1 * s2);
+  dkv_store_f32<DT>(xr, i, o1);
+  dkv_store_f32<DT>(xr, i + 64, o2);
+}
+
 }  // namespace
 
 extern "C" int dkv_rope_dense(void* stream, int dtype, void* x, long long row_ld, long long tok_ld,
@@ -368,13 +406,36 @@ extern "C" int dkv_rope_dense(void* stream, int dtype, void* x, long long row_ld
   return DKV_OK;
 }
 
+extern "C" int dkv_rope_apply(void* stream, int dtype, void* x, long long x_sb, long long x_sh,
+                              long long x_ss, const void* cos, const void* sin, long long cs_sb,
+                              long long cs_ss, int B, int H, int S) {
+  if (dtype != DKV_F16 && dtype != DKV_BF16) return DKV_E_UNSUPPORTED;
+  if (B < 0 || H < 0 || S < 0 || cs_sb < 0 || cs_ss < 0) return DKV_E_ARG;
+  const long long total = (long long)B * H * S * 64;
+  if (total == 0) return DKV_OK;
+  if (!x || !cos || !sin) return DKV_E_ARG;
+  const dim3 grid((unsigned)((total + 255) / 256));
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == DKV_BF16)
+    hipLaunchKernelGGL(rope_apply_kernel<DKV_BF16>, grid, dim3(256), 0, st, (uint16_t*)x, x_sb,
+                       x_sh, x_ss, (const uint16_t*)cos, (const uint16_t*)sin, cs_sb, cs_ss, B, H,
+                       S);
+  else
+    hipLaunchKernelGGL(rope_apply_kernel<DKV_F16>, grid, dim3(256), 0, st, (uint16_t*)x, x_sb,
+                       x_sh, x_ss, (const uint16_t*)cos, (const uint16_t*)sin, cs_sb, cs_ss, B, H,
+                       S);
+  DKV_HIP_CHECK_LAUNCH();
+  return DKV_OK;
+}
+
 extern "C" int dkv_prefill_attention(void* stream, int dtype, const void* q, long long q_sb,
                                      long long q_sh, long long q_ss, const void* k, long long k_sb,
                                      long long k_sh, long long k_ss, long long k_elems,
                                      const void* v, long long v_sb, long long v_sh, long long v_ss,
                                      long long v_elems, void* out, int out_dtype, long long o_sb,
                                      long long o_sh, long long o_ss, int B, int Hq, int Hkv,
-                                     int Sq, int Sk, int Dh, int causal, float scale) {
+                                     int Sq, int Sk, int Dh, int causal, float scale,
+                                     const int* kstart) {
   // the kernel takes each tile's maximum before scaling: a positive, finite scale only
   if (!(scale > 0.f) || !(scale < INFINITY)) return DKV_E_UNSUPPORTED;
   if (dtype != DKV_F16 && dtype != DKV_BF16) return DKV_E_UNSUPPORTED;
@@ -404,6 +465,7 @@ extern "C" int dkv_prefill_attention(void* stream, int dtype, const void* q, lon
   p.scale_log2 = scale * 1.4426950408889634f;
   p.k_bytes = (uint32_t)(k_elems * 2);
   p.v_bytes = (uint32_t)(v_elems * 2);
+  p.kstart = kstart;
   const dim3 grid((unsigned)((Sq + FA_BQ - 1) / FA_BQ), (unsigned)Hq, (unsigned)B);
   hipStream_t st = (hipStream_t)stream;
   if (dtype == DKV_BF16) {

@@ -25,9 +25,17 @@ call: cutoff, appends, q RoPE, split-K attention), prefill attends from the mask
 reference's joint layout is used (one ``D x D`` basis and cutoff head, rank up to ``D``, one row
 per batch element) through ``compressed_decode_attention`` and a reconstruct-and-attend prefill.
 
-Position handling: q is rotated by the kernels' RoPE (angles ``float32(pos) * inv_freq`` in
-fp32, rounded once), the same rotation the kernels apply to the reconstructed keys; the
-``position_embeddings`` the HF decoder passes are not used.
+Positions and masks, as the reference's model passes them (``custom_llama.py:146-172``,
+``compressed_attention.py:305-386``): q is rotated by the decoder's position embeddings
+(``LlamaRotaryEmbedding`` at ``position_ids``, ``rope_scaling`` included) with the reference's
+``apply_rotary_pos_emb_`` rounding (``dkv_rope_apply``); in prefill the reconstructed K is
+rotated by the layer's own rotary embedding at positions 0..L-1 (``calc_cos_sin``); in decode the
+kernels rotate K with plain theta by row index, as the reference's Triton kernels do. A prompt's
+``attention_mask`` masks its left padding in the prefill attention (keys before each row's first
+real token); decode attends the whole cache, padding included, as the reference's decode
+kernels do. Masks with zeros after a one (right or inner padding) raise: the reference's
+decode would attend those positions as real tokens. Called without position embeddings (outside
+the decoder) the attention rotates q with the kernels' plain-theta RoPE at the cache position.
 """
 
 from __future__ import annotations
@@ -38,7 +46,8 @@ import sys
 import torch
 from torch import nn
 from transformers.models.llama.modeling_llama import (LlamaAttention, LlamaForCausalLM,
-                                                      LlamaModel, LlamaPreTrainedModel)
+                                                      LlamaModel, LlamaPreTrainedModel,
+                                                      LlamaRotaryEmbedding)
 from transformers.modeling_outputs import BaseModelOutputWithPast
 
 from . import formats as F
@@ -47,7 +56,7 @@ from .kernels.cutoff import CutoffHead
 from .kernels.decode import grouped_decode_attention
 from .kernels.layer import DecodeLayerPlan
 from .kernels.prefill import (coef_prefill_attention, compressed_prefill_attention,
-                              prefill_attention, rope_dense_)
+                              prefill_attention, rope_apply_, rope_dense_)
 from .kernels.router import KernelPolicy, compressed_decode_attention
 
 PHYSICAL_ENV = "DYNAKV_PHYSICAL_KERNELS"
@@ -69,6 +78,32 @@ def get_model_class(model_type: str):
                          f"{PHYSICAL_ENV}=1 (the research masked-dimension classes are not part "
                          f"of it)")
     return CustomLlamaForCausalLM
+
+
+class PaddingStart:
+    """Left padding of a prompt batch, from its 2-D ``attention_mask``: ``start[b]`` (int32 on
+    the device) is row b's first real token; keys before it are masked in the prefill attention
+    (the reference's ``create_causal_mask(attention_mask, ...)``, ``custom_llama.py:161-168``)."""
+
+    def __init__(self, start: torch.Tensor):
+        self.start = start
+
+    @staticmethod
+    def from_mask(attention_mask) -> "PaddingStart | None":
+        """``None`` for no mask or an all-ones mask; raises for masks other than left padding
+        (zeros, then ones, per row) and for 4-D masks."""
+        if attention_mask is None or isinstance(attention_mask, PaddingStart):
+            return attention_mask
+        if not torch.is_tensor(attention_mask) or attention_mask.dim() != 2:
+            raise NotImplementedError("CustomLlamaModel takes a 2-D attention_mask (B, L)")
+        m = attention_mask != 0
+        if bool(m.all()):
+            return None
+        if m.shape[1] > 1 and not bool((m[:, 1:].int() >= m[:, :-1].int()).all()):
+            raise NotImplementedError(
+                "only left padding is supported: a mask with zeros after a one (right or inner "
+                "padding) would be attended as real tokens by the decode kernels")
+        return PaddingStart((~m).sum(dim=1).to(torch.int32).contiguous())
 
 
 def _block_diagonal(W: torch.Tensor, G: int, n: int) -> bool:
@@ -114,6 +149,9 @@ class CustomAttention(LlamaAttention):
         self.v_down = nn.Parameter(self._initial_basis("v_Ut", dt))
         self.v_up = nn.Parameter(self._initial_basis("v_U", dt))
         self.low_rank = D
+        # the layer's own rotary embedding: the prefill K's positions 0..L-1 (the reference's
+        # calc_cos_sin, compressed_attention.py:193-200,214)
+        self.rotary_emb = LlamaRotaryEmbedding(config)
         self.policy = KernelPolicy()
         self.merged = False
         self.per_head = None
@@ -180,25 +218,51 @@ class CustomAttention(LlamaAttention):
         if past_key_values is not None and cache is None:
             raise TypeError("CustomAttention needs a CustomDynamicCache as past_key_values")
         pos0 = cache.get_seq_length_sp(self.layer_idx) if cache is not None else 0
-        if self.per_head:
-            a = self._per_head(q, kc, vc, cache, pos0)
+        decoding = cache is not None and S == 1 and pos0 > 0
+        # decode attends the whole cache (the reference's decode kernels take no mask)
+        pad = None if decoding else PaddingStart.from_mask(attention_mask)
+        kstart = None if pad is None else pad.start
+        # q rotated by the decoder's position embeddings (compressed_attention.py:314,360)
+        qh = q.transpose(1, 2).contiguous()
+        if position_embeddings is not None:
+            rope_apply_(qh, *position_embeddings)
         else:
-            a = self._joint(q, kc, vc, cache, pos0)
+            rope_dense_(qh, theta=self.theta, pos0=pos0)
+        k_rope = None if decoding else self._k_rope(hidden_states, cache, pos0 + S,
+                                                    position_embeddings)
+        if self.per_head:
+            a = self._per_head(qh, kc, vc, cache, pos0, k_rope, kstart)
+        else:
+            a = self._joint(qh, kc, vc, cache, pos0, k_rope, kstart)
         return self.o_proj(a.reshape(B, S, self.n_q * self.head_dim)), None
+
+    def _k_rope(self, x, cache, L, position_embeddings):
+        """cos / sin of the prefill K: the layer's rotary embedding at positions 0..L-1 when a
+        cache holds the tokens (calc_cos_sin, compressed_attention.py:193-200,375-376), else the
+        decoder's position embeddings; ``None`` (the kernels' plain-theta RoPE) outside the
+        decoder."""
+        if position_embeddings is None:
+            return None
+        if cache is None:
+            return position_embeddings
+        pos = torch.arange(L, dtype=torch.long, device=x.device).unsqueeze(0)
+        return self.rotary_emb(x, pos)
 
     def _rows(self, x, B, S):
         G, Dh = self.n_kv, self.head_dim
         return x.view(B, S, G, Dh).transpose(1, 2).reshape(B * G, S, Dh).contiguous()
 
-    def _per_head(self, q, kc, vc, cache, pos0):
-        B, S = q.shape[:2]
+    def _per_head(self, qh, kc, vc, cache, pos0, k_rope, kstart):
+        """``qh`` (B, Hq, S, Dh) rotated; returns (B, S, Hq, Dh)."""
+        B, S = qh.shape[0], qh.shape[2]
         G, Dh = self.n_kv, self.head_dim
         if cache is not None and S == 1 and pos0 > 0:
             plan = self._plan
             if (plan is not None and plan.cache is cache and plan.B == B and plan.can_step()):
-                # one call: cutoff head, K+V appends, q RoPE, routed split-K attention
-                a = plan.step(q.view(B, self.n_q, Dh), kc.view(B, G * Dh), vc.view(B, G * Dh),
-                              pos0)
+                # one call: cutoff head, K+V appends, routed split-K attention (q arrives
+                # rotated: pos -1)
+                a = plan.step(qh.view(B, self.n_q, Dh), kc.view(B, G * Dh), vc.view(B, G * Dh),
+                              -1)
                 return a.view(B, 1, self.n_q, Dh)
             k_out, v_out, len_k, len_v, _, _ = self.cutoff.kv_process_fused(kc, vc)
             lk = len_k.view(B, 1, G).transpose(1, 2).reshape(B * G, 1).contiguous()
@@ -207,9 +271,9 @@ class CustomAttention(LlamaAttention):
                                                      self._rows(v_out, B, 1), lv, Dh,
                                                      self.layer_idx, Dh)
             L = cache.get_seq_length_sp(self.layer_idx)
-            qh = rope_dense_(q.transpose(1, 2).contiguous(), theta=self.theta, pos0=pos0)[:, :, 0]
-            a = grouped_decode_attention(qh, fk, fv, tk, ok, tv, ov, self.k_basis, self.v_basis,
-                                         theta=self.theta, route=self.policy.select(L))
+            a = grouped_decode_attention(qh[:, :, 0], fk, fv, tk, ok, tv, ov, self.k_basis,
+                                         self.v_basis, theta=self.theta,
+                                         route=self.policy.select(L))
             self._plan = DecodeLayerPlan(cache, self.layer_idx, self.cutoff, self.k_basis,
                                          self.v_basis, batch=B, heads=self.n_q, theta=self.theta,
                                          policy=self.policy)
@@ -217,7 +281,6 @@ class CustomAttention(LlamaAttention):
         # prefill (or a cache-less forward): masked coefficients, appended, then attended
         k_out, v_out, len_k, len_v, _, _ = self.cutoff.kv_process_fused(kc, vc)
         rk, rv = self._rows(k_out, B, S), self._rows(v_out, B, S)
-        qh = rope_dense_(q.transpose(1, 2).contiguous(), theta=self.theta, pos0=pos0)
         if cache is not None:
             lk = len_k.view(B, S, G).transpose(1, 2).reshape(B * G, S).contiguous()
             lv = len_v.view(B, S, G).transpose(1, 2).reshape(B * G, S).contiguous()
@@ -225,17 +288,19 @@ class CustomAttention(LlamaAttention):
             self._plan = None
             if pos0 > 0:  # attend over the cached tokens too
                 a = compressed_prefill_attention(qh, cache, self.layer_idx, self.k_basis,
-                                                 self.v_basis, theta=self.theta)
+                                                 self.v_basis, theta=self.theta, k_rope=k_rope,
+                                                 kstart=kstart)
                 return a.transpose(1, 2)
-        a = coef_prefill_attention(qh, rk, rv, self.k_basis, self.v_basis, theta=self.theta)
+        a = coef_prefill_attention(qh, rk, rv, self.k_basis, self.v_basis, theta=self.theta,
+                                   k_rope=k_rope, kstart=kstart)
         return a.transpose(1, 2)
 
-    def _joint(self, q, kc, vc, cache, pos0):
-        B, S = q.shape[:2]
+    def _joint(self, qh, kc, vc, cache, pos0, k_rope, kstart):
+        """``qh`` (B, Hq, S, Dh) rotated; returns (B, S, Hq, Dh)."""
+        B, S = qh.shape[0], qh.shape[2]
         D, Dh, G = self.d, self.head_dim, self.n_kv
         R = int(self.low_rank)
         k_out, v_out, len_k, len_v, _, _ = self.cutoff.kv_process_fused(kc, vc)
-        qh = rope_dense_(q.transpose(1, 2).contiguous(), theta=self.theta, pos0=pos0)
         if cache is not None and S == 1 and pos0 > 0:
             fk, fv, lk, lv, ok, ov = cache.update_sp(k_out, len_k, v_out, len_v, D,
                                                      self.layer_idx, R)
@@ -254,15 +319,19 @@ class CustomAttention(LlamaAttention):
         # positions 0..L-1
         k = torch.matmul(ck.unsqueeze(1), self.k_basis).contiguous()
         v = torch.matmul(cv.unsqueeze(1), self.v_basis).contiguous()
-        rope_dense_(k, theta=self.theta, pos0=0)
-        a = prefill_attention(qh, k, v, causal=True)
+        if k_rope is None:
+            rope_dense_(k, theta=self.theta, pos0=0)
+        else:
+            rope_apply_(k, *k_rope)
+        a = prefill_attention(qh, k, v, causal=True, kstart=kstart)
         return a.transpose(1, 2)
 
 
 class CustomLlamaModel(LlamaModel):
-    """``LlamaModel`` with ``CustomAttention`` in every layer (reference ``custom_llama.py:93-248``).
-    The attention is causal by construction (prefill) or over the whole cache (decode), so no
-    attention mask is built."""
+    """``LlamaModel`` with ``CustomAttention`` in every layer (reference ``custom_llama.py:93-248``):
+    cache positions, position ids and the rotary position embeddings as the reference forms them
+    (``:146-172``); the prompt's ``attention_mask`` becomes the left-padding bound of the prefill
+    attention (``PaddingStart``; the attention is causal by construction)."""
 
     def __init__(self, config):
         super().__init__(config)
@@ -283,11 +352,21 @@ class CustomLlamaModel(LlamaModel):
             inputs_embeds = self.embed_tokens(input_ids)
         if use_cache and past_key_values is None:
             past_key_values = CustomDynamicCache()
+        S = inputs_embeds.shape[1]
+        if cache_position is None:
+            past = past_key_values.get_seq_length() if past_key_values is not None else 0
+            cache_position = torch.arange(past, past + S, device=inputs_embeds.device)
+        if position_ids is None:
+            position_ids = cache_position.unsqueeze(0)
         h = inputs_embeds
+        position_embeddings = self.rotary_emb(h, position_ids)
+        # decode steps attend the whole cache: the mask matters for a prompt only
+        pad = PaddingStart.from_mask(attention_mask) if S > 1 else None
         for layer in self.layers[: self.config.num_hidden_layers]:
-            h = layer(h, attention_mask=None, position_ids=position_ids,
+            h = layer(h, attention_mask=pad, position_ids=position_ids,
                       past_key_values=past_key_values, use_cache=use_cache,
-                      position_embeddings=None, **kwargs)
+                      cache_position=cache_position, position_embeddings=position_embeddings,
+                      **kwargs)
         h = self.norm(h)
         return BaseModelOutputWithPast(last_hidden_state=h,
                                        past_key_values=past_key_values if use_cache else None)

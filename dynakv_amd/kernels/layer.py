@@ -107,7 +107,8 @@ class DecodeLayerPlan:
 
     def step(self, q: torch.Tensor, k_coef: torch.Tensor, v_coef: torch.Tensor,
              pos: int) -> torch.Tensor:
-        """q (B, Hq, Dh) with contiguous heads (any batch stride), rotated in place; k/v_coef
+        """q (B, Hq, Dh) with contiguous heads (any batch stride), rotated in place at ``pos``
+        (``pos == -1``: q arrives rotated, e.g. by the HF decoder's position embeddings); k/v_coef
         (B, G*R) with unit element stride and one shared row stride (views into one projection
         output are fine). Returns the attention output (B, Hq, Dh) contiguous in the cache
         dtype."""

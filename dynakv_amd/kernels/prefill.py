@@ -47,12 +47,39 @@ def rope_dense_(x: torch.Tensor, *, theta: float, pos0: int = 0) -> torch.Tensor
     return x
 
 
+def rope_apply_(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """In place: ``x = x * cos + rotate_half(x) * sin`` in x's dtype, each product and the sum
+    rounded as the reference's ``apply_rotary_pos_emb_`` computes it
+    (``compressed_attention.py:18-22``). ``x`` (B, H, S, 128); ``cos`` / ``sin`` (B or 1, S, 128)
+    as ``LlamaRotaryEmbedding`` returns them (the decoder's position embeddings)."""
+    if x.dim() != 4 or x.shape[-1] != 128 or x.stride(-1) != 1:
+        raise ValueError("rope_apply_ needs x (B, H, S, 128) with unit last stride")
+    B, H, S, _ = x.shape
+    cos, sin = cos.to(x.dtype), sin.to(x.dtype)
+    if cos.dim() == 2:
+        cos, sin = cos.unsqueeze(0), sin.unsqueeze(0)
+    if cos.shape != sin.shape or cos.shape[0] not in (1, B) or cos.shape[1:] != (S, 128):
+        raise ValueError(f"cos/sin {tuple(cos.shape)} do not match x {tuple(x.shape)}")
+    if cos.stride() != sin.stride() or cos.stride(-1) != 1:
+        cos, sin = cos.contiguous(), sin.contiguous()
+    cs_sb = 0 if cos.shape[0] == 1 else cos.stride(0)
+    lib = _lib.load()
+    _lib.check(lib.dkv_rope_apply(_lib.stream_of(x), _lib.dtype_code(x.dtype), x.data_ptr(),
+                                  x.stride(0), x.stride(1), x.stride(2), cos.data_ptr(),
+                                  sin.data_ptr(), cs_sb, cos.stride(1), B, H, S),
+               "dkv_rope_apply")
+    return x
+
+
 def prefill_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, causal: bool = True,
                       scale: float | None = None, out: torch.Tensor | None = None,
-                      out_dtype: torch.dtype | None = None) -> torch.Tensor:
+                      out_dtype: torch.dtype | None = None,
+                      kstart: torch.Tensor | None = None) -> torch.Tensor:
     """Causal GQA attention: ``q`` (B, Hq, Sq, 128), ``k``/``v`` (B, Hkv, Sk, 128) ->
     (B, Hq, Sq, 128) in q's dtype (or ``out_dtype=torch.float32``: the result before that
-    rounding). With ``causal`` the queries are the last ``Sq`` positions."""
+    rounding). With ``causal`` the queries are the last ``Sq`` positions. ``kstart`` (B,) int32
+    on the device: keys before ``kstart[b]`` are masked (left padding); a query with no key left
+    gets 0."""
     B, Hq, Sq, Dh = q.shape
     _, Hkv, Sk, _ = k.shape
     if v.shape != k.shape or k.shape[0] != B or k.shape[3] != Dh:
@@ -70,6 +97,10 @@ def prefill_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, caus
     elif out.dtype != odt or out.stride(-1) != 1:
         raise ValueError("out must have unit last stride and the requested dtype")
     scale = 1.0 / math.sqrt(Dh) if scale is None else float(scale)
+    if kstart is not None:
+        if kstart.shape != (B,) or kstart.device != q.device:
+            raise ValueError("kstart must be (B,) on q's device")
+        kstart = kstart.to(torch.int32).contiguous()
     lib = _lib.load()
     rc = lib.dkv_prefill_attention(
         _lib.stream_of(q), _lib.dtype_code(q.dtype),
@@ -77,13 +108,25 @@ def prefill_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, caus
         k.data_ptr(), k.stride(0), k.stride(1), k.stride(2), _extent(k),
         v.data_ptr(), v.stride(0), v.stride(1), v.stride(2), _extent(v),
         out.data_ptr(), _lib.dtype_code(out.dtype), out.stride(0), out.stride(1), out.stride(2),
-        B, Hq, Hkv, Sq, Sk, Dh, 1 if causal else 0, scale)
+        B, Hq, Hkv, Sq, Sk, Dh, 1 if causal else 0, scale,
+        None if kstart is None else kstart.data_ptr())
     _lib.check(rc, "dkv_prefill_attention")
     return out
 
 
+def _rotate_k(k: torch.Tensor, theta: float, k_rope) -> None:
+    """RoPE of dense K (B, G, S, 128) at positions 0..S-1: the kernels' own rotation (fp32
+    angles), or ``k_rope = (cos, sin)`` tables (S or B x S rows) applied as the reference's
+    ``apply_rotary_pos_emb_`` does (its prefill rotates K by ``calc_cos_sin``,
+    ``compressed_attention.py:193-200,375-378``)."""
+    if k_rope is None:
+        rope_dense_(k, theta=theta, pos0=0)
+    else:
+        rope_apply_(k, *k_rope)
+
+
 def reconstruct_kv(cache, layer_idx: int, k_basis: torch.Tensor, v_basis: torch.Tensor, *,
-                   batch: int, theta: float):
+                   batch: int, theta: float, k_rope=None):
     """Dense head-space K (RoPE'd at positions 0..S-1) and V ``(B, G, S, Dh)`` of a per-head
     cache (rows ``b*G + g``, bases ``(G, R, Dh)``)."""
     G, R, Dh = k_basis.shape
@@ -93,22 +136,25 @@ def reconstruct_kv(cache, layer_idx: int, k_basis: torch.Tensor, v_basis: torch.
         raise ValueError(f"cache has {rows} rows, expected batch * G = {batch * G}")
     k = torch.matmul(dk.view(batch, G, S, R), k_basis.contiguous())
     v = torch.matmul(dv.view(batch, G, S, R), v_basis.contiguous())
-    rope_dense_(k, theta=theta, pos0=0)
+    _rotate_k(k, theta, k_rope)
     return k, v
 
 
 def compressed_prefill_attention(q: torch.Tensor, cache, layer_idx: int, k_basis: torch.Tensor,
                                  v_basis: torch.Tensor, *, theta: float,
-                                 out_dtype: torch.dtype | None = None) -> torch.Tensor:
+                                 out_dtype: torch.dtype | None = None, k_rope=None,
+                                 kstart: torch.Tensor | None = None) -> torch.Tensor:
     """The reference's prefill attention for the per-head layout: ``q`` (B, Hq, Sq, 128)
     already RoPE'd at its positions (the last ``Sq`` of the cache)."""
-    k, v = reconstruct_kv(cache, layer_idx, k_basis, v_basis, batch=q.shape[0], theta=theta)
-    return prefill_attention(q, k, v, causal=True, out_dtype=out_dtype)
+    k, v = reconstruct_kv(cache, layer_idx, k_basis, v_basis, batch=q.shape[0], theta=theta,
+                          k_rope=k_rope)
+    return prefill_attention(q, k, v, causal=True, out_dtype=out_dtype, kstart=kstart)
 
 
 def coef_prefill_attention(q: torch.Tensor, ck: torch.Tensor, cv: torch.Tensor,
                            k_basis: torch.Tensor, v_basis: torch.Tensor, *, theta: float,
-                           out_dtype: torch.dtype | None = None) -> torch.Tensor:
+                           out_dtype: torch.dtype | None = None, k_rope=None,
+                           kstart: torch.Tensor | None = None) -> torch.Tensor:
     """``compressed_prefill_attention`` from the masked coefficient rows themselves, ``ck`` /
     ``cv`` (B*G, S, R) zero past each token's count -- exactly what decompressing the packed
     cache returns -- so a prefill can attend before (or without) its appends."""
@@ -119,5 +165,5 @@ def coef_prefill_attention(q: torch.Tensor, ck: torch.Tensor, cv: torch.Tensor,
         raise ValueError(f"coefficient rows {tuple(ck.shape)}, expected ({batch * G}, S, {R})")
     k = torch.matmul(ck.view(batch, G, S, R), k_basis.contiguous())
     v = torch.matmul(cv.view(batch, G, S, R), v_basis.contiguous())
-    rope_dense_(k, theta=theta, pos0=0)
-    return prefill_attention(q, k, v, causal=True, out_dtype=out_dtype)
+    _rotate_k(k, theta, k_rope)
+    return prefill_attention(q, k, v, causal=True, out_dtype=out_dtype, kstart=kstart)

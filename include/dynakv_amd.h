@@ -348,8 +348,19 @@ int dkv_cutoff_kv(void* stream, int dtype, const void* xk, const void* xv, long 
  * from k / v (bounds of the buffer loads). fp32 softmax, probabilities as a hi + lo pair in
  * the compute dtype for the P.V product. dtype: DKV_F16 or DKV_BF16; out_dtype: dtype or
  * DKV_F32 (the normalised result before rounding). scale: positive and finite (else
- * DKV_E_UNSUPPORTED; the reference passes 1/sqrt(128)). Replaces the eager /
- * SDPA attention call of the prefill branch (:373-383).
+ * DKV_E_UNSUPPORTED; the reference passes 1/sqrt(128)). kstart: NULL, or B int32 on the
+ * device; keys j < kstart[b] are masked for every query of row b (a left-padded prompt: the
+ * reference passes create_causal_mask(attention_mask, ...) to this call, custom_llama.py:161-168);
+ * a query left with no key (a padding position) gets 0. Replaces the eager / SDPA attention
+ * call of the prefill branch (:373-383).
+ *
+ * dkv_rope_apply: in-place rotate-half RoPE of x (B, H, S, 128) (strides x_sb / x_sh / x_ss,
+ * unit dim stride) with given cos / sin tables (B, S, 128) in the dtype (batch stride cs_sb,
+ * 0 to share one table, token stride cs_ss, unit dim stride): x <- (x * cos) +
+ * (rotate_half(x) * sin), each product and the sum rounded to the dtype as the reference's
+ * apply_rotary_pos_emb_ computes it (compressed_attention.py:18-22). Rotates q by the
+ * position embeddings of the HF decoder (LlamaRotaryEmbedding, rope_scaling included,
+ * :314,:360) and the prefill K by calc_cos_sin's (:193-200, :375-378).
  */
 int dkv_rope_dense(void* stream, int dtype, void* x, long long row_ld, long long tok_ld,
                    int rows, int S, int pos0, float log_theta);
@@ -358,7 +369,11 @@ int dkv_prefill_attention(void* stream, int dtype, const void* q, long long q_sb
                           long long k_ss, long long k_elems, const void* v, long long v_sb,
                           long long v_sh, long long v_ss, long long v_elems, void* out,
                           int out_dtype, long long o_sb, long long o_sh, long long o_ss, int B,
-                          int Hq, int Hkv, int Sq, int Sk, int Dh, int causal, float scale);
+                          int Hq, int Hkv, int Sq, int Sk, int Dh, int causal, float scale,
+                          const int* kstart);
+int dkv_rope_apply(void* stream, int dtype, void* x, long long x_sb, long long x_sh,
+                   long long x_ss, const void* cos, const void* sin, long long cs_sb,
+                   long long cs_ss, int B, int H, int S);
 
 /*
  * One decode step of one attention layer (per-head layout, rows b*G + g) in one call: the
@@ -368,7 +383,9 @@ int dkv_prefill_attention(void* stream, int dtype, const void* q, long long q_sb
  * switch_tokens (:335-348 and router.py:20-59, dkv_decode_splitk). The caller fills a
  * DkvDecodeLayer once per layer (and again after the cache grows or the RoPE table is
  * extended) and calls dkv_decode_layer per step with the step's q (B, Hq, Dh) (batch stride
- * q_sb, rotated in place), the layer's K/V coefficients (B, G*R) (row stride coef_ld) and the
+ * q_sb, rotated in place at position pos; pos == -1: q arrives rotated by the caller, as the
+ * reference rotates it with the decoder's position embeddings), the layer's K/V coefficients
+ * (B, G*R) (row stride coef_ld) and the
  * output (B, Hq, Dh) contiguous in the cache dtype. The caller guarantees room for one more token:
  * seq + 1 <= the tables' capacity, every row's used length + R <= the flat capacity, and
  * rope_tiles * 16 >= seq + 1. Three launches: the cutoff logits; the counts, the appends of

@@ -35,8 +35,11 @@ def rope_dense(x: np.ndarray, theta: float, dtype: str, pos0: int = 0) -> np.nda
 
 
 def attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, causal: bool = True,
-              scale: float | None = None) -> np.ndarray:
-    """q (B, Hq, Sq, D), k/v (B, Hkv, Sk, D) -> (B, Hq, Sq, D) float64."""
+              scale: float | None = None, kstart=None) -> np.ndarray:
+    """q (B, Hq, Sq, D), k/v (B, Hkv, Sk, D) -> (B, Hq, Sq, D) float64. ``kstart`` (B,): keys
+    before ``kstart[b]`` are masked (a left-padded prompt: the reference's
+    ``create_causal_mask(attention_mask, ...)``, custom_llama.py:161-168); a query with no key
+    left gets 0."""
     q = np.asarray(q, np.float64)
     k = np.asarray(k, np.float64)
     v = np.asarray(v, np.float64)
@@ -49,10 +52,15 @@ def attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, causal: bool = True,
     for b in range(B):
         for h in range(Hq):
             s = q[b, h] @ k[b, h // hpg].T * scale  # (Sq, Sk)
+            mask = np.zeros((Sq, Sk), dtype=bool)
             if causal:
-                mask = np.arange(Sk)[None, :] > (off + np.arange(Sq))[:, None]
-                s = np.where(mask, -np.inf, s)
-            s = s - s.max(axis=-1, keepdims=True)
-            p = np.exp(s)
-            out[b, h] = (p / p.sum(axis=-1, keepdims=True)) @ v[b, h // hpg]
+                mask |= np.arange(Sk)[None, :] > (off + np.arange(Sq))[:, None]
+            if kstart is not None:
+                mask |= np.arange(Sk)[None, :] < int(kstart[b])
+            s = np.where(mask, -np.inf, s)
+            live = ~mask.all(axis=-1)
+            m = np.where(live, np.where(mask, -np.inf, s).max(axis=-1), 0.0)
+            p = np.where(mask, 0.0, np.exp(s - m[:, None]))
+            den = np.where(live, p.sum(axis=-1), 1.0)
+            out[b, h] = (p / den[:, None]) @ v[b, h // hpg]
     return out

@@ -70,7 +70,7 @@ def test_argument_validation_without_device():
     # prefill attention: the scale must be positive and finite (checked before anything else)
     for scale in (0.0, -0.088, float("nan"), float("inf")):
         rc = lib.dkv_prefill_attention(None, 2, None, 0, 0, 0, None, 0, 0, 0, 0, None, 0, 0, 0, 0,
-                                       None, 2, 0, 0, 0, 1, 32, 8, 16, 16, 128, 1, scale)
+                                       None, 2, 0, 0, 0, 1, 32, 8, 16, 16, 128, 1, scale, None)
         assert rc == -2, scale
 
 

@@ -153,3 +153,85 @@ def test_full_shape_keep_all_dims_matches_dense(dev):
     # the compressed cache adds no error beyond the dense bf16 model's own rounding
     assert errs["compressed"] <= 1.25 * errs["dense"] + 0.01 * scale, errs
     assert errs["compressed"] <= 0.1 * scale, errs
+
+
+@pytest.mark.gpu
+def test_config5_workload_against_float32_forward(dev):
+    """Config 5 at its stated workload: the full Llama-3-8B shape with the cutoff heads as
+    RandomLlama builds them (mean retention ~0.47), a 2048-token prompt and 24 greedy decode
+    steps; the first decode step grows every layer's packed caches (flat and tables), the later
+    ones run one dkv_decode_layer call per layer. The logits at the prompt's last position and at
+    every decoded one are checked against the float32 forward of the same weights with the
+    retained lengths read back from the cache; every layer's K and V tables, pointers, upper
+    bounds and buffer capacities bit-exact against the oracle's packing and growth model
+    (compressed_cache.py:96-214) fed the same lengths; the flat buffers zero past each row's
+    pointer, and layer 0's packed prompt kept bit for bit across its growth."""
+    import numpy as np
+
+    from oracle.packing import PackedSlot
+
+    print("[gpu] config 5 workload: full shape, retention 0.47, prompt 2048, 24 steps",
+          flush=True)
+    shape = LlamaShape()
+    model = RandomLlama(shape, device=dev, seed=7)
+    gen = CompressedLlama(model)
+    B, S, steps = 1, 2048, 24
+    G, Dh = shape.kv_heads, shape.head_dim
+    g = torch.Generator(device="cpu").manual_seed(9)
+    prompt = torch.randint(0, shape.vocab, (B, S), generator=g)
+    with torch.no_grad():
+        x = gen.prefill(prompt.to(dev))
+        lg = [gen.logits(x[:, -1:]).float()]
+        fk0 = gen.cache.key_cache_sp[0][0].clone()
+        ptr0 = gen.cache.key_cache_sp[0][3].clone()
+        cap0 = gen.cache.key_cache_sp[0][0].shape[1]
+        toks = [lg[-1].argmax(-1)]
+        for j in range(steps):
+            x = gen.decode(toks[-1], S + j)
+            lg.append(gen.logits(x).float())
+            toks.append(lg[-1].argmax(-1))
+    got = torch.cat(lg, dim=1).cpu()  # (B, steps + 1, vocab)
+    L = S + steps
+    assert gen.cache.get_seq_length_sp(0) == L
+    assert gen.cache.key_cache_sp[0][0].shape[1] > cap0, "the decode steps grew the flat buffer"
+    lk = [c[1][:, :L].cpu() for c in gen.cache.key_cache_sp]
+    lv = [c[1][:, :L].cpu() for c in gen.cache.value_cache_sp]
+    frac = torch.stack(lk).float().mean().item() / Dh
+    print(f"[gpu] config 5: mean retained fraction {frac:.3f}", flush=True)
+    assert 0.35 < frac < 0.6
+    # packing: the oracle's slot model fed the read-back lengths (prefill, then one token a step)
+    for slots, lens in ((gen.cache.key_cache_sp, lk), (gen.cache.value_cache_sp, lv)):
+        for i, c in enumerate(slots):
+            ln = lens[i].numpy()
+            slot = PackedSlot()
+            slot.append_prefill(np.zeros((B * G, S, Dh), np.float32), ln[:, :S], Dh)
+            for j in range(steps):
+                slot.append_decode(np.zeros((B * G, Dh), np.float32), ln[:, S + j:S + j + 1], Dh)
+            ol, oo = slot.tables()
+            assert np.array_equal(c[1][:, :L].cpu().numpy(), ol), f"layer {i} lens"
+            assert np.array_equal(c[2][:, :L].cpu().numpy(), oo), f"layer {i} offsets"
+            assert np.array_equal(c[3].cpu().numpy(), slot.ptr), f"layer {i} pointers"
+            assert list(c[5]) == list(slot.ub), f"layer {i} upper bounds"
+            assert c[0].shape == slot.flat.shape, f"layer {i} flat capacity"
+            assert c[1].shape == slot.lens.shape and c[2].shape == slot.offs.shape
+            assert c[4] == slot.seq
+            tail = torch.arange(c[0].shape[1], device=dev)[None, :] >= c[3][:, None].long()
+            assert not (c[0] * tail).any(), f"layer {i}: elements past the row pointers"
+    # the packed prompt of layer 0 survives the growth bit for bit
+    fk = gen.cache.key_cache_sp[0][0]
+    for r in range(B * G):
+        n = int(ptr0[r])
+        assert torch.equal(fk[r, :n], fk0[r, :n])
+    tokens = torch.cat([prompt, torch.cat(toks[:-1], dim=1).cpu()], dim=1)  # (B, L)
+    del gen
+    torch.cuda.empty_cache()
+    with torch.no_grad():
+        ref = _reference_logits(model, tokens, [t.to(dev) for t in lk], [t.to(dev) for t in lv],
+                                device=dev)[:, S - 1:].float().cpu()
+    err = (got - ref).abs().amax().item()
+    scale = ref.abs().amax().item()
+    corr = torch.corrcoef(torch.stack([got.flatten(), ref.flatten()]))[0, 1].item()
+    print(f"[parity] config 5 workload vs float32: max_abs={err:.3e} |ref|max={scale:.3e} "
+          f"corr={corr:.5f}", flush=True)
+    assert err <= 0.1 * scale
+    assert corr > 0.99

@@ -140,3 +140,46 @@ def test_compressed_prefill_matches_oracle(dev, dtype):
     K = P.rope_dense(K, theta, nd)
     ref = P.attention(q, K, V, causal=True)
     assert_close(got.float(), ref, f"compressed prefill {dtype}")
+
+
+def _oracle_heads(q, k, v, picks, scale=None):
+    """The oracle for sampled (b, h) pairs only: (len(picks), Sq, D)."""
+    Hq, Hkv = q.shape[1], k.shape[1]
+    out = []
+    for b, h in picks:
+        kv = h // (Hq // Hkv)
+        out.append(P.attention(q[b:b + 1, h:h + 1], k[b:b + 1, kv:kv + 1],
+                               v[b:b + 1, kv:kv + 1], causal=True, scale=scale)[0, 0])
+    return np.stack(out)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("scores", ["normal", "wide_rising"])
+def test_prefill_attention_bench_shape(dev, dtype, scores):
+    """The shape bench times (B=4, S=2048, 32 query / 8 KV heads, causal) against the oracle on
+    sampled (b, h) pairs spread over the batch rows, KV heads and query slots of a group (one
+    per XCD-balanced work unit class). "wide_rising": keys whose norm grows with the position
+    and queries scaled by 3, so later tiles' maxima exceed the running one by more than the
+    2^8 the kernel defers its rescale by -- the rescale path runs for most query blocks, and
+    peaked rows check P's hi + lo split at large values."""
+    print(f"[gpu] prefill attention bench shape {dtype} {scores}", flush=True)
+    B, Hq, Hkv, S = 4, 32, 8, 2048
+    rng = np.random.default_rng(2048 + (scores == "wide_rising"))
+    q = rng.standard_normal((B, Hq, S, 128)).astype(np.float32)
+    k = rng.standard_normal((B, Hkv, S, 128)).astype(np.float32)
+    v = rng.standard_normal((B, Hkv, S, 128)).astype(np.float32)
+    if scores == "wide_rising":
+        q *= 3.0
+        k *= (1.0 + 3.0 * np.arange(S, dtype=np.float32) / S)[None, None, :, None]
+    q, k, v = cast_np(q, dtype), cast_np(k, dtype), cast_np(v, dtype)
+    t = lambda a: torch.from_numpy(a).to(device=dev, dtype=dtype)  # noqa: E731
+    got = prefill_attention(t(q), t(k), t(v), causal=True, out_dtype=torch.float32)
+    low = prefill_attention(t(q), t(k), t(v), causal=True)
+    torch.cuda.synchronize()
+    picks = [(0, 0), (1, 13), (2, 22), (3, 31), (3, 4), (0, 27)]
+    ref = _oracle_heads(q, k, v, picks)
+    g = torch.stack([got[b, h] for b, h in picks])
+    assert_close(g, ref, f"bench shape {dtype} {scores}")
+    assert torch.equal(low, got.to(dtype))
+    assert torch.isfinite(got).all()

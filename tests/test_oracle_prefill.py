@@ -65,3 +65,47 @@ def test_reconstruct_is_the_projection():
     c = rng.standard_normal((3, 5, 16))
     U = rng.standard_normal((16, 128))
     assert np.allclose(P.reconstruct(c, U, "float32"), (c @ U).astype(np.float32), rtol=1e-6)
+
+
+def test_left_padding_closed_forms():
+    """kstart[b]: keys before it are masked. kstart 0 is the plain causal attention; a query at
+    the first real position attends only that key (its value comes back); queries before it have
+    no key left and give 0."""
+    rng = np.random.default_rng(5)
+    B, Hq, Hkv, S, D = 2, 4, 2, 10, 128
+    q = rng.standard_normal((B, Hq, S, D))
+    k = rng.standard_normal((B, Hkv, S, D))
+    v = rng.standard_normal((B, Hkv, S, D))
+    assert np.array_equal(P.attention(q, k, v, kstart=[0, 0]), P.attention(q, k, v))
+    out = P.attention(q, k, v, kstart=[3, 0])
+    assert np.array_equal(out[0, :, :3], np.zeros((Hq, 3, D)))
+    for h in range(Hq):
+        assert np.allclose(out[0, h, 3], v[0, h // 2, 3])
+    assert np.allclose(out[1], P.attention(q, k, v)[1])
+    # every key masked: all zeros
+    assert not np.any(P.attention(q, k, v, kstart=[S, S]))
+
+
+@pytest.mark.parametrize("Sq", [10, 4])
+def test_left_padding_matches_torch_sdpa(Sq):
+    """Real queries (at or past each row's first real key) against torch SDPA in float64 with
+    the padding and causal masks built as one boolean mask."""
+    rng = np.random.default_rng(6)
+    B, Hq, Hkv, Sk, D = 3, 4, 2, 10, 128
+    kstart = [2, 0, 5]
+    q = rng.standard_normal((B, Hq, Sq, D))
+    k = rng.standard_normal((B, Hkv, Sk, D))
+    v = rng.standard_normal((B, Hkv, Sk, D))
+    out = P.attention(q, k, v, kstart=kstart)
+    kt = torch.from_numpy(k).repeat_interleave(Hq // Hkv, dim=1)
+    vt = torch.from_numpy(v).repeat_interleave(Hq // Hkv, dim=1)
+    qpos = torch.arange(Sk - Sq, Sk)
+    for b in range(B):
+        keys = torch.arange(Sk)
+        mask = (keys[None, :] <= qpos[:, None]) & (keys[None, :] >= kstart[b])
+        live = mask.any(dim=1)
+        ref = torch.nn.functional.scaled_dot_product_attention(
+            torch.from_numpy(q[b:b + 1, :, live]), kt[b:b + 1], vt[b:b + 1],
+            attn_mask=mask[live])
+        assert np.allclose(out[b][:, live.numpy()], ref[0].numpy(), atol=1e-10)
+        assert not np.any(out[b][:, ~live.numpy()])
