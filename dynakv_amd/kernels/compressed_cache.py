@@ -59,15 +59,34 @@ class CustomDynamicCache(_CacheBase):
                  device=None, layer_device_map=None, **kwargs):
         if _CacheBase is not object:
             super().__init__()
-        # stored for API compatibility (the reference keeps them but never reads them)
-        self.dkv_max_batch_size = max_batch_size
-        self.dkv_max_cache_len = max_cache_len
+        # kept under the reference's names (it stores them and never reads them)
+        self.max_batch_size = max_batch_size
+        self.max_cache_len = max_cache_len
         self.dtype = dtype
         self.device = device
         self.layer_device_map = layer_device_map
         self.key_cache_sp: list = []
         self.value_cache_sp: list = []
         self.device_syncs = 0  # host reads of device state (growth checks, prefill bounds)
+
+    # transformers 5 makes these read-only (deprecated) properties of its Cache class; the
+    # reference's cache assigns them in its constructor (compressed_cache.py:61-62), so they are
+    # plain stored values here
+    @property
+    def max_batch_size(self):
+        return self._max_batch_size
+
+    @max_batch_size.setter
+    def max_batch_size(self, value):
+        self._max_batch_size = value
+
+    @property
+    def max_cache_len(self):
+        return self._max_cache_len
+
+    @max_cache_len.setter
+    def max_cache_len(self, value):
+        self._max_cache_len = value
 
     # ------------------------------------------------------------------ queries
     def get_origin_states(self, max_dim, layer_idx):

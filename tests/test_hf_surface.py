@@ -128,3 +128,16 @@ def test_merge_and_layout(joint):
         assert attn.cutoff.groups == G and attn.cutoff.D == Dh
         # cutoff weights per group: the diagonal blocks, transposed for the kernel
         assert torch.equal(attn.cutoff.wt_k[1], Wk[Dh:, Dh:].T)
+
+
+def test_cache_constructor_attributes():
+    """CustomDynamicCache keeps the reference constructor's values under its names
+    (compressed_cache.py:59-68), although transformers 5 makes max_batch_size / max_cache_len
+    read-only properties of its Cache class."""
+    from dynakv_amd.kernels.compressed_cache import CustomDynamicCache
+
+    c = CustomDynamicCache(max_batch_size=4, max_cache_len=1024, dtype=torch.bfloat16)
+    assert (c.max_batch_size, c.max_cache_len, c.dtype) == (4, 1024, torch.bfloat16)
+    d = CustomDynamicCache()
+    assert d.max_batch_size is None and d.max_cache_len is None
+    assert d.key_cache_sp == [] and d.value_cache_sp == [] and d.get_seq_length_sp(0) == 0
