@@ -9,18 +9,20 @@
 // in 32-rank chunks, [chunk][dim][rank], a RoPE table, a workspace for the V pass) and compute
 // the same results to fp32 accuracy:
 //
-// joint_scores_kernel -- workgroup = (512 tokens, basis head h, batch row b), or with the heads
-//   in pairs (256 tokens, heads 2h and 2h+1, b) so that each coefficient load serves both heads'
-//   products; wave w takes 64 tokens (4 column blocks of 16) of its head, or 32 tokens of both.
-//   K^T = B_h^T . X^T accumulates on 16x16x32 MFMA over the rank chunks of 32 that the block's
-//   longest token needs. Each basis chunk ([128 dims][32 ranks], 8 KB contiguous in HBM) is
-//   loaded once per workgroup into LDS (four buffers per head, one barrier per two chunks, so
-//   the waves drift by up to a chunk between barriers) and every A operand read from it
-//   serves the wave's column blocks; the coefficients go straight into B operand registers
-//   (lane = one token x 8 ranks, elements past the token's count zeroed), two chunks ahead,
-//   each serving every head of the workgroup. Then per 16-token tile T: R(n) applied to the lane's token (n = its slot in the tile,
-//   LDS table) in fp32, K' split into bf16 hi + lo, scores on MFMA against R(-16T) q (hi and lo
-//   parts in separate operand columns), the route's masking and rounding.
+// joint_scores_sorted_kernel -- workgroup = (512 tokens, basis head h, batch row b), or with the
+//   heads in pairs (256 tokens, heads 2h and 2h+1, b) so that each coefficient load serves both
+//   heads' products. The workgroup's tokens are sorted by their count of 32-rank chunks
+//   (counting sort in LDS) into blocks of 16; wave w takes sorted blocks w and NBLK-1-w (one
+//   short, one long). K^T = B_h^T . X^T accumulates on 16x16x32 MFMA over the rank chunks of
+//   32, each block only up to its own longest token's chunk. Each basis chunk ([128 dims][32
+//   ranks], 8 KB contiguous in HBM) is loaded once per workgroup into LDS (four buffers per
+//   head, one barrier per two chunks) and every A operand read from it serves the wave's active
+//   blocks; the coefficients go straight into B operand registers (lane = one token x 8 ranks,
+//   elements past the token's count zeroed), two chunks ahead, each serving every head of the
+//   workgroup. Then per block: the lane's token rotated by R(p) = R(16T) R(n) (p = 16T + n, its
+//   position; composed from LDS tables) in fp32, K' split into bf16 hi + lo, scores on MFMA
+//   against the unrotated query (hi and lo parts in separate operand columns, formed once per
+//   head), the route's masking and rounding, stored at the token's position.
 // joint_av_kernel -- workgroup = (token split, 16 or 32 query heads, batch row b); wave w takes
 //   ranks [128w, 128w + 128). Per 16-token tile: each set of 16 heads' scores through an online
 //   softmax in the log2 domain (every wave computes the same values), P as bf16 hi + lo (fp16
@@ -77,49 +79,67 @@ struct JScoresParams {
   const int* offs;
   long long offs_sb, offs_ss;
   const float* rope;
+  int rope_tiles;
   void* out;
   long long out_sb, out_sh, out_ss;
   int B, S, R, hpg;
   float scale;
 };
 
-// NHB basis heads per workgroup (1 or 2): with 2, a workgroup takes 256 tokens of two heads
-// (each wave 32 tokens of both), so every coefficient load serves both heads' products
+// joint_scores_sorted_kernel: the scores with the rank chunks bounded per 16-token block instead of
+// per workgroup. The workgroup's TOK tokens are sorted by their count of
+// 32-rank chunks (counting sort in LDS), so each block of 16 consecutive sorted tokens needs the
+// chunks up to its own last token's count; a block's products and coefficient loads stop there
+// (in the reference's joint layout a few full-rank tokens sit in almost every 256-token range and
+// made every token take all 32 chunks, ~2.9x the products the tokens' counts need). Wave w takes
+// sorted blocks w and NBLK-1-w (with one basis head: also 16+w and 31-w), one short and one long,
+// so the waves' products per chunk stay balanced. A token's position is arbitrary within its
+// block, so the key takes the whole rotation R(p) = R(16T) R(n) (p = 16T + n), composed per lane
+// from the R(n) table and the workgroup's R(16T) rows in LDS; the query operand is then the
+// same for every token and formed once per head. Scores are stored at the tokens' positions.
 template <int DT, int MODE, int ODT, int NHB>
-__global__ __launch_bounds__(JTHREADS, 1) void joint_scores_kernel(JScoresParams p) {
-  constexpr int CB = JCB / NHB;            // 16-token column blocks per wave
+__global__ __launch_bounds__(JTHREADS, 1) void joint_scores_sorted_kernel(JScoresParams p) {
+  constexpr int CB = JCB / NHB;            // 16-token blocks per wave
   constexpr int TOK = JWAVES * CB * 16;    // tokens per workgroup
-  // basis chunk buffers: piece (dim d, ranks 8k..8k+7) at index 4d + (k ^ jswz(d)), so that the
-  // A operand reads (lane (n, g): slot g of row 16*blk + n) are free of bank conflicts
+  constexpr int NBLK = TOK / 16;           // sorted blocks (and 16-token tiles) per workgroup
+  constexpr int NK = JRMAX / JCH + 1;      // chunk-count buckets 0..32
   __shared__ __attribute__((aligned(16))) dkv_u32x4 sB[4][NHB][JDH * JCH / 8];
-  // R(n) of every lane's token slot: [2*pp + k][lane] holds (cos, sin) of frequencies
-  // 16pp + 4g + 2k and + 1
+  // R(n): [2*pp + k][16*g + n] holds (cos, sin) of frequencies 16pp + 4g + 2k and + 1 at delta n
   __shared__ __attribute__((aligned(16))) dkv_f32x4 sRn[8][64];
-  // per-wave query operand: row r (column r of the score product: head r's hi part for r < 8,
-  // head r-8's lo part), dword i = frequency i, 16-byte chunk c stored at chunk position c ^ r
-  __shared__ __attribute__((aligned(16))) uint32_t sQ[JWAVES][16 * 64];
-  __shared__ int sLen[TOK], sOff[TOK];
-  __shared__ int sMax[JWAVES];
+  // R(16T) of the workgroup's tiles: [T - T0][2*pp + k][g], the same frequencies
+  __shared__ __attribute__((aligned(16))) dkv_f32x4 sRT[NBLK][8][4];
+  // the query operand of each head: row r = head r's hi part (r < 8) or head r-8's lo part,
+  // dword i = frequency i, 16-byte chunk c stored at chunk position c ^ r
+  __shared__ __attribute__((aligned(16))) uint32_t sQ[NHB][16 * 64];
+  __shared__ int sLen[TOK], sOff[TOK], sPos[TOK];  // in sorted order; sPos -1: past S
+  __shared__ int sCnt[NK], sStart[NK];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15, g = lane >> 4;
   const int t0 = blockIdx.x * TOK, h0 = blockIdx.y * NHB, b = blockIdx.z;
+  const int T0 = t0 / 16;
 
-  {
-    const int t = t0 + tid;
-    int len = 0, off = 0;
-    if (tid < TOK && t < p.S) {
-      len = p.lens[(long long)b * p.lens_sb + (long long)t * p.lens_ss];
-      off = p.offs[(long long)b * p.offs_sb + (long long)t * p.offs_ss];
+  // ---- this thread's token (tid < TOK), the query and table loads, all issued first ----------
+  int tlen0 = 0, toff0 = 0;
+  const int tme = t0 + tid;
+  const bool tvalid = tid < TOK && tme < p.S;
+  if (tvalid) {
+    tlen0 = p.lens[(long long)b * p.lens_sb + (long long)tme * p.lens_ss];
+    toff0 = p.offs[(long long)b * p.offs_sb + (long long)tme * p.offs_ss];
+  }
+  tlen0 = min(max(tlen0, 0), p.R);
+  const int kme = (tlen0 + JCH - 1) / JCH;
+  // query: (q_i, q_{i+64}) of head slot hh for frequency i = lane; wave hb of the first NHB
+  // forms head h0 + hb's operand
+  uint32_t qh[8];
+  if (wave < NHB) {
+    const long long qo = (long long)b * p.q_sb + (long long)(h0 + wave) * p.hpg * p.q_sh + lane;
+#pragma unroll
+    for (int hh = 0; hh < 8; ++hh) {
+      const long long o = qo + (hh < p.hpg ? hh : 0) * p.q_sh;
+      qh[hh] = (uint32_t)p.q[o] | ((uint32_t)p.q[o + 64] << 16);
     }
-    len = min(max(len, 0), p.R);
-    if (tid < TOK) {
-      sLen[tid] = len;
-      sOff[tid] = off;
-    }
-    const int m = dkv_wave_max_i(len);
-    if (lane == 0) sMax[wave] = m;
   }
   {
     const int k = tid >> 6;
@@ -127,33 +147,75 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_scores_kernel(JScoresParams
     const float* delt = p.rope + n * 128 + 2 * i0;
     sRn[k][lane] = dkv_f32x4{delt[0], delt[1], delt[2], delt[3]};
   }
+  for (int e = tid; e < NBLK * 32; e += JTHREADS) {
+    const int tl = e >> 5, k = (e >> 2) & 7, gg = e & 3;
+    const int i0 = 16 * (k >> 1) + 4 * gg + 2 * (k & 1);
+    const int T = min(T0 + tl, p.rope_tiles - 1);
+    const float* row = p.rope + (long long)(JROPE_FIXED + T) * 128 + 2 * i0;
+    sRT[tl][k][gg] = dkv_f32x4{row[0], row[1], row[2], row[3]};
+  }
+  if (tid < NK) sCnt[tid] = 0;
   __syncthreads();
-  int maxlen = 0;
+  // ---- counting sort by chunk count: order within a bucket is arbitrary (a token's products
+  //      and rotation do not depend on its place in the block; chunks past its count add zeros)
+  int myrank = 0;
+  if (tid < TOK) myrank = atomicAdd(&sCnt[kme], 1);
+  if (wave < NHB) {
+    // the query operand of head h0 + wave: R(0) (no rotation) times the score scale, bf16 hi + lo
+    uint32_t* qw = sQ[wave];
 #pragma unroll
-  for (int w = 0; w < JWAVES; ++w) maxlen = max(maxlen, sMax[w]);
-  const int nch = (maxlen + JCH - 1) / JCH;
+    for (int hh = 0; hh < 8; ++hh)
+      if (hh < p.hpg) {
+        const float x = dkv_elt_to_f32<DT>(qh[hh] & 0xffffu) * p.scale;
+        const float y = dkv_elt_to_f32<DT>(qh[hh] >> 16) * p.scale;
+        uint32_t hi, lo;
+        dkv_split_bf16x2(x, y, hi, lo);
+        qw[hh * 64 + 4 * ((lane >> 2) ^ hh) + (lane & 3)] = hi;
+        qw[(8 + hh) * 64 + 4 * ((lane >> 2) ^ (8 + hh)) + (lane & 3)] = lo;
+      }
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int acc = 0;
+    for (int k = 0; k < NK; ++k) {
+      sStart[k] = acc;
+      acc += sCnt[k];
+    }
+  }
+  __syncthreads();
+  if (tid < TOK) {
+    const int r = sStart[kme] + myrank;
+    sLen[r] = tlen0;
+    sOff[r] = toff0;
+    sPos[r] = tvalid ? tme : -1;
+  }
+  __syncthreads();
 
-  const uint32_t end = (uint32_t)dkv_flat_tail_elems(p.B, b, p.flat_ld, JFLAT_CAP);
-  const __amdgpu_buffer_rsrc_t rs = dkv_make_rsrc(p.flat + (long long)b * p.flat_ld, end * 2u);
-  // this thread's basis piece of every chunk: dim bd, ranks 8*bk .. +8 of the chunk
-  const int bd = tid >> 2, bk = (tid & 3) ^ jswz(bd);
-  const uint16_t* bsrc = p.bt + (long long)h0 * p.bt_sh + (long long)bd * JCH + 8 * bk;
-
-  int tlen[CB], toff[CB];
-  // bit c of pmask[cb]: some lane of column block cb has its count ending inside its 8 ranks of
-  // chunk c. Only those chunks need the loaded pieces masked: past a count, loads read zeros.
+  // this wave's blocks: 8*cb + (w or 7-w), short and long alternately
+  int tlen[CB], toff[CB], nchk[CB];
   uint32_t pmask[CB];
 #pragma unroll
   for (int cb = 0; cb < CB; ++cb) {
-    const int tl = 16 * CB * wave + 16 * cb + n;
-    tlen[cb] = sLen[tl];
-    toff[cb] = sOff[tl];
+    const int blk = 8 * cb + ((cb & 1) ? 7 - wave : wave);
+    tlen[cb] = sLen[16 * blk + n];
+    toff[cb] = sOff[16 * blk + n];
+    nchk[cb] = __builtin_amdgcn_readfirstlane((sLen[16 * blk + 15] + JCH - 1) / JCH);
     const int e = tlen[cb] - 8 * g;  // 1..7 past a multiple of 32: partial in chunk e / 32
     uint32_t bit = (e > 0 && (e & 31) != 0 && (e & 31) < 8) ? (1u << (e >> 5)) : 0u;
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) bit |= (uint32_t)__shfl_xor((int)bit, m, 64);
     pmask[cb] = __builtin_amdgcn_readfirstlane(bit);
   }
+  int wmax = 0;
+#pragma unroll
+  for (int cb = 0; cb < CB; ++cb) wmax = max(wmax, nchk[cb]);
+  const int nch = (sLen[TOK - 1] + JCH - 1) / JCH;  // the workgroup's longest token
+
+  const uint32_t end = (uint32_t)dkv_flat_tail_elems(p.B, b, p.flat_ld, JFLAT_CAP);
+  const __amdgpu_buffer_rsrc_t rs = dkv_make_rsrc(p.flat + (long long)b * p.flat_ld, end * 2u);
+  const int bd = tid >> 2, bk = (tid & 3) ^ jswz(bd);
+  const uint16_t* bsrc = p.bt + (long long)h0 * p.bt_sh + (long long)bd * JCH + 8 * bk;
+
   dkv_f32x4 acc[NHB][8][CB];
 #pragma unroll
   for (int hh = 0; hh < NHB; ++hh)
@@ -162,19 +224,24 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_scores_kernel(JScoresParams
 #pragma unroll
       for (int cb = 0; cb < CB; ++cb) acc[hh][i][cb] = dkv_f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // The rank loop. The coefficient loads are not waited for where they are issued, so each wave
-  // keeps two chunks of loads in flight. Only the last batch row can hold a window that crosses
-  // the end of the buffer; its workgroups run the loop with element-wise gathers for such windows.
+  // The rank loop: chunk c's basis sits in sB[c & 3], written at step c-2 (or before the loop),
+  // and a barrier follows every odd step, so buffer (c+2) & 3 (last read at step c-2) may take
+  // chunk c+2's basis, loaded two steps ago, and the registers it came from the basis of c+4.
+  // The coefficients of chunk c+2 are loaded, after chunk c's products are issued, into the
+  // registers chunk c used. Each block's products and coefficient loads stop at its own chunk
+  // count (wave-uniform branches); loads past the last chunk clamp the basis index.
   auto rank_loop = [&](auto safe_tag) {
     constexpr bool SAFE = decltype(safe_tag)::value;
     auto load_x = [&](int c, dkv_u32x4(&x)[CB]) {
 #pragma unroll
       for (int cb = 0; cb < CB; ++cb) {
-        const int j0 = JCH * c + 8 * g;
-        if constexpr (SAFE)
-          x[cb] = dkv_load8_safe(rs, end, toff[cb] + j0, tlen[cb] - j0);
-        else
-          x[cb] = dkv_load8_raw(rs, toff[cb] + j0, tlen[cb] - j0);
+        if (c < nchk[cb]) {
+          const int j0 = JCH * c + 8 * g;
+          if constexpr (SAFE)
+            x[cb] = dkv_load8_safe(rs, end, toff[cb] + j0, tlen[cb] - j0);
+          else
+            x[cb] = dkv_load8_raw(rs, toff[cb] + j0, tlen[cb] - j0);
+        }
       }
     };
     dkv_u32x4 xa[CB], xb[CB];
@@ -198,46 +265,36 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_scores_kernel(JScoresParams
       load_x(1, xb);
     }
     __syncthreads();
-    // Chunk c: its basis sits in sB[c & 3], written at step c-2 (or before the loop), and a
-    // barrier follows every odd step. The basis of chunk c+2 (loaded two steps ago) goes to
-    // buffer (c+2) & 3, whose previous chunk c-2 was read at step c-2, before the barrier that
-    // ends the pair of steps preceding c; chunk c's own buffer was written before that barrier
-    // too. The basis of chunk c+4 is then loaded into the registers chunk c+2 came from (b: ba
-    // for even c, bb for odd c). The coefficients of chunk c+2 are loaded, right after chunk c's
-    // products are issued, into the registers chunk c used (x: xa, xb in turn). No loaded value
-    // is ever copied, so the waits cover only the values being used. Loads past the last chunk
-    // clamp the basis index and have coefficient counts <= 0 (no traffic). One barrier per pair
-    // of chunks instead of one per chunk: 3-4% less time at the config-3 shape.
     auto step = [&](int c, dkv_u32x4(&x)[CB], dkv_u32x4(&bn)[NHB], bool sync) {
-#pragma unroll
-      for (int cb = 0; cb < CB; ++cb)
-        if ((pmask[cb] >> c) & 1u) x[cb] = dkv_mask8(x[cb], tlen[cb] - (JCH * c + 8 * g));
 #pragma unroll
       for (int hh = 0; hh < NHB; ++hh) {
         sB[(c + 2) & 3][hh][tid] = bn[hh];
         bn[hh] = load_b(c + 4, hh);
       }
-      dkv_u32x4 a[NHB][8];
+      if (c < wmax) {
 #pragma unroll
-      for (int hh = 0; hh < NHB; ++hh)
+        for (int cb = 0; cb < CB; ++cb)
+          if (c < nchk[cb] && ((pmask[cb] >> c) & 1u))
+            x[cb] = dkv_mask8(x[cb], tlen[cb] - (JCH * c + 8 * g));
+        dkv_u32x4 a[NHB][8];
 #pragma unroll
-        for (int blk = 0; blk < 8; ++blk)
-          a[hh][blk] = sB[c & 3][hh][4 * (16 * blk + n) + (g ^ jswz(n))];
+        for (int hh = 0; hh < NHB; ++hh)
 #pragma unroll
-      for (int hh = 0; hh < NHB; ++hh)
+          for (int blk = 0; blk < 8; ++blk)
+            a[hh][blk] = sB[c & 3][hh][4 * (16 * blk + n) + (g ^ jswz(n))];
 #pragma unroll
-        for (int blk = 0; blk < 8; ++blk)
+        for (int cb = 0; cb < CB; ++cb)
+          if (c < nchk[cb]) {
 #pragma unroll
-          for (int cb = 0; cb < CB; ++cb)
-            acc[hh][blk][cb] = dkv_mfma32<DT>(a[hh][blk], x[cb], acc[hh][blk][cb]);
-      // the basis reads first, then the products (the compiler would otherwise read each
-      // operand just before its products and expose the LDS latency once per operand)
-      __builtin_amdgcn_sched_group_barrier(0x100, 8 * NHB, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 8 * NHB * CB, 0);
-      load_x(c + 2, x);
+            for (int hh = 0; hh < NHB; ++hh)
+#pragma unroll
+              for (int blk = 0; blk < 8; ++blk)
+                acc[hh][blk][cb] = dkv_mfma32<DT>(a[hh][blk], x[cb], acc[hh][blk][cb]);
+          }
+        load_x(c + 2, x);
+      }
       if (sync) __syncthreads();
     };
-    // whole pairs in the loop (every path back to its head has issued both steps' loads)
     int c = 0;
     for (; c + 1 < nch; c += 2) {
       step(c, xa, ba, false);
@@ -250,96 +307,71 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_scores_kernel(JScoresParams
   else
     rank_loop(std::integral_constant<bool, false>{});
 
-  // ---- per 16-token tile: rotation, K' hi + lo, scores, masking, store ---------------------
-  // (q_i, q_{i+64}) of the group's heads for frequency i = lane, as 16-bit values
-#pragma unroll
-  for (int hb = 0; hb < NHB; ++hb) {
-  const int h = h0 + hb;
-  uint32_t qh[8];
-  {
-    const long long qo = (long long)b * p.q_sb + (long long)h * p.hpg * p.q_sh + lane;
-#pragma unroll
-    for (int hh = 0; hh < 8; ++hh) {
-      const long long o = qo + (hh < p.hpg ? hh : 0) * p.q_sh;
-      const uint32_t v = (uint32_t)p.q[o] | ((uint32_t)p.q[o + 64] << 16);
-      qh[hh] = hh < p.hpg ? v : 0u;
-    }
-  }
+  // ---- per block: R(p) of the lane's token, K' hi + lo, scores, masking, stores --------------
   const int hn = n & 7;
   const int qrow = (n & 8) + (hn < p.hpg ? hn : hn % p.hpg);
-  uint32_t* qw = sQ[wave];
 #pragma unroll
   for (int cb = 0; cb < CB; ++cb) {
-    const int tbase = t0 + 16 * CB * wave + 16 * cb;
-    if (tbase >= p.S) break;  // wave-uniform
-    const int tile = tbase / 16;
+    const int blk = 8 * cb + ((cb & 1) ? 7 - wave : wave);
+    const int pos_n = sPos[16 * blk + n];
+    // R(p) = R(16T) R(n) for the lane's token: (cos, sin) of its 16 frequencies
+    float rc[16], rsn[16];
     {
-      // R(-16T) q times the score scale for frequency i = lane, as bf16 hi + lo
-      const float* row = p.rope + (long long)(JROPE_FIXED + tile) * 128 + 2 * lane;
-      const float cs = row[0] * p.scale, sn = row[1] * p.scale;
+      const int pl = pos_n < 0 ? 0 : pos_n - t0;
+      const int tl = pl >> 4, nn = pl & 15;
 #pragma unroll
-      for (int hh = 0; hh < 8; ++hh)
-        if (hh < p.hpg) {
-          const float x = dkv_elt_to_f32<DT>(qh[hh] & 0xffffu);
-          const float y = dkv_elt_to_f32<DT>(qh[hh] >> 16);
-          uint32_t hi, lo;
-          dkv_split_bf16x2(cs * x + sn * y, cs * y - sn * x, hi, lo);
-          qw[hh * 64 + 4 * ((lane >> 2) ^ hh) + (lane & 3)] = hi;
-          qw[(8 + hh) * 64 + 4 * ((lane >> 2) ^ (8 + hh)) + (lane & 3)] = lo;
-        }
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    dkv_u32x4 bq[4];
+      for (int k = 0; k < 8; ++k) {
+        const dkv_f32x4 d = sRn[k][16 * g + nn];
+        const dkv_f32x4 t = sRT[tl][k][g];
 #pragma unroll
-    for (int pp = 0; pp < 4; ++pp)
-      bq[pp] = *(const dkv_u32x4*)&qw[qrow * 64 + 4 * ((4 * pp + g) ^ qrow)];
-
-    dkv_f32x4 sc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int pp = 0; pp < 4; ++pp) {
-      const dkv_f32x4 c0 = acc[hb][pp][cb], c1 = acc[hb][pp + 4][cb];
-      const dkv_f32x4 r01 = sRn[2 * pp][lane], r23 = sRn[2 * pp + 1][lane];
-      const float rc[4] = {r01.x, r01.z, r23.x, r23.z}, rsn[4] = {r01.y, r01.w, r23.y, r23.w};
-      uint32_t kh[4], kl[4];
-#pragma unroll
-      for (int w = 0; w < 4; ++w)
-        dkv_split_bf16x2(c0[w] * rc[w] - c1[w] * rsn[w], c1[w] * rc[w] + c0[w] * rsn[w], kh[w],
-                         kl[w]);
-      sc = mfma_bf16x32(dkv_u32x4{kh[0], kh[1], kh[2], kh[3]}, bq[pp], sc);
-      sc = mfma_bf16x32(dkv_u32x4{kl[0], kl[1], kl[2], kl[3]}, bq[pp], sc);
-    }
-    // column n += column n + 8 (the lo part of head n) within each row of 16 lanes
-#pragma unroll
-    for (int u = 0; u < 4; ++u)
-      sc[u] += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sc[u]),
-                                                          DKV_DPP_ROW_SHL8, 0xf, 0xf, false));
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    if (n < p.hpg) {
-      const long long ob = (long long)b * p.out_sb + (long long)(h * p.hpg + n) * p.out_sh;
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int tl = 16 * CB * wave + 16 * cb + 4 * g + u;
-        const int t = t0 + tl;
-        if (t < p.S) {
-          const int len = sLen[tl];
-          float z;
-          if constexpr (MODE == 0)
-            z = len > 0 ? sc[u] : -1.0e4f * p.scale;
-          else
-            z = len > 0 ? sc[u] : -INFINITY;
-          dkv_store_f32<ODT>(p.out, ob + (long long)t * p.out_ss, z);
+        for (int e = 0; e < 2; ++e) {
+          const float ct = t[2 * e], st = t[2 * e + 1], cn = d[2 * e], sn = d[2 * e + 1];
+          // frequency 16pp + 4g + 2k' + e with k = 2pp + k': element w = 2k' + e of pair pp
+          rc[4 * (k >> 1) + 2 * (k & 1) + e] = ct * cn - st * sn;
+          rsn[4 * (k >> 1) + 2 * (k & 1) + e] = st * cn + ct * sn;
         }
       }
     }
-  }
-  // the next head reuses the wave's query operand rows
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int hb = 0; hb < NHB; ++hb) {
+      const int h = h0 + hb;
+      const uint32_t* qw = sQ[hb];
+      dkv_f32x4 sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int pp = 0; pp < 4; ++pp) {
+        const dkv_u32x4 bq = *(const dkv_u32x4*)&qw[qrow * 64 + 4 * ((4 * pp + g) ^ qrow)];
+        const dkv_f32x4 c0 = acc[hb][pp][cb], c1 = acc[hb][pp + 4][cb];
+        uint32_t kh[4], kl[4];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const float cw = rc[4 * pp + w], sw = rsn[4 * pp + w];
+          dkv_split_bf16x2(c0[w] * cw - c1[w] * sw, c1[w] * cw + c0[w] * sw, kh[w], kl[w]);
+        }
+        sc = mfma_bf16x32(dkv_u32x4{kh[0], kh[1], kh[2], kh[3]}, bq, sc);
+        sc = mfma_bf16x32(dkv_u32x4{kl[0], kl[1], kl[2], kl[3]}, bq, sc);
+      }
+      // column n += column n + 8 (the lo part of head n) within each row of 16 lanes
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        sc[u] += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sc[u]),
+                                                            DKV_DPP_ROW_SHL8, 0xf, 0xf, false));
+      if (n < p.hpg) {
+        const long long ob = (long long)b * p.out_sb + (long long)(h * p.hpg + n) * p.out_sh;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int r = 16 * blk + 4 * g + u;
+          const int t = sPos[r];
+          if (t >= 0) {
+            float z;
+            if constexpr (MODE == 0)
+              z = sLen[r] > 0 ? sc[u] : -1.0e4f * p.scale;
+            else
+              z = sLen[r] > 0 ? sc[u] : -INFINITY;
+            dkv_store_f32<ODT>(p.out, ob + (long long)t * p.out_ss, z);
+          }
+        }
+      }
+    }
   }
 }
 
@@ -843,6 +875,7 @@ extern "C" int dkv_joint_scores(void* stream, int mode, int dtype, int out_dtype
   p.offs_sb = offs_sb;
   p.offs_ss = offs_ss;
   p.rope = rope;
+  p.rope_tiles = rope_tiles;
   p.out = out;
   p.out_sb = out_sb;
   p.out_sh = out_sh;
@@ -861,11 +894,11 @@ extern "C" int dkv_joint_scores(void* stream, int mode, int dtype, int out_dtype
 #define DKV_JS_LAUNCH(DT_, MODE_, ODT_)                                                        \
   do {                                                                                         \
     if (nhb == 2)                                                                              \
-      hipLaunchKernelGGL((joint_scores_kernel<DT_, MODE_, ODT_, 2>), grid, dim3(JTHREADS), 0,  \
-                         st, p);                                                               \
+      hipLaunchKernelGGL((joint_scores_sorted_kernel<DT_, MODE_, ODT_, 2>), grid,              \
+                         dim3(JTHREADS), 0, st, p);                                            \
     else                                                                                       \
-      hipLaunchKernelGGL((joint_scores_kernel<DT_, MODE_, ODT_, 1>), grid, dim3(JTHREADS), 0,  \
-                         st, p);                                                               \
+      hipLaunchKernelGGL((joint_scores_sorted_kernel<DT_, MODE_, ODT_, 1>), grid,              \
+                         dim3(JTHREADS), 0, st, p);                                            \
   } while (0)
   if (mode == 1) {
     if (dtype == DKV_BF16) DKV_JS_LAUNCH(DKV_BF16, 1, DKV_F32);
