@@ -227,23 +227,74 @@ class CustomDynamicCache(_CacheBase):
             raise ValueError("update_sp_prefill_many takes prefill appends (S > 1)")
         # per slot and row: the summed counts (buffer sizing) and the clipped sums (the row's
         # pointer after the append, for a slot that starts empty), in one transfer
-        host = torch.cat([l.sum(dim=1) for l in lens] +
-                         [l.clamp(0, max_dim).sum(dim=1) for l in lens]).tolist()
+        if len({tuple(l.shape) for l in lens}) == 1:
+            L = torch.stack(lens)  # one reduction over every slot instead of one per slot
+            host = torch.cat([L.sum(dim=2).flatten(),
+                              L.clamp(0, max_dim).sum(dim=2).flatten()]).tolist()
+        else:
+            host = torch.cat([l.sum(dim=1) for l in lens] +
+                             [l.clamp(0, max_dim).sum(dim=1) for l in lens]).tolist()
         self.device_syncs += 1
         rows = [l.shape[0] for l in lens]
         starts = [sum(rows[:k]) for k in range(len(lens))]
         half = sum(rows)
+        created = self._create_fresh_slots(items, lens, host, starts)
         for n, (layer_idx, ks, kl, vs, vl) in enumerate(items):
             for j, (cache_list, st, ln) in enumerate(((self.key_cache_sp, ks, kl),
                                                       (self.value_cache_sp, vs, vl))):
                 k = 2 * n + j
                 su = host[starts[k]:starts[k] + rows[k]]
                 sc = host[half + starts[k]:half + starts[k] + rows[k]]
-                fresh = len(cache_list) <= layer_idx or cache_list[layer_idx] is None
+                fresh = (j, layer_idx) in created or (len(cache_list) <= layer_idx
+                                                      or cache_list[layer_idx] is None)
                 cache, added = self._prepare_slot(cache_list, layer_idx, st, ln, max_dim, False,
                                                   row_max=max(su))
                 self._launch_prefill(cache, st, ln, max_dim, ub=sc if fresh else None)
                 self._finish_slot(cache, ln.shape[1], added, False)
+
+    def _create_fresh_slots(self, items, lens, host, starts):
+        """The slots of ``items`` that do not exist yet, created as ``_prepare_slot`` creates
+        them (flat sized to the largest row total, tables to the prompt, pointers zero) but
+        from one zeroed buffer for every flat and pointer array and one unfilled buffer for the
+        tables (the prefill append writes every table entry of a fresh slot): two fills in all
+        instead of four per slot. Returns the created slots as ``(0 (K) | 1 (V), layer)``;
+        a slot whose rows hold no coefficient at all is left to ``_prepare_slot``."""
+        fresh = []
+        for n, it in enumerate(items):
+            layer_idx = it[0]
+            for j, (cache_list, st) in enumerate(((self.key_cache_sp, it[1]),
+                                                  (self.value_cache_sp, it[3]))):
+                while len(cache_list) <= layer_idx:
+                    cache_list.append(None)
+                if cache_list[layer_idx] is None:
+                    k = 2 * n + j
+                    cap = max(host[starts[k]:starts[k] + lens[k].shape[0]])
+                    if cap > 0:
+                        fresh.append((cache_list, layer_idx, st, lens[k], cap, j))
+        if not fresh:
+            return set()
+        dev = fresh[0][2].device
+        by_dtype = {}
+        for f in fresh:
+            by_dtype.setdefault(f[2].dtype, []).append(f)
+        tab_elems = sum(f[3].numel() for f in fresh)
+        tabs = torch.empty(2 * tab_elems, dtype=torch.int32, device=dev)
+        ptrs = torch.zeros(sum(f[3].shape[0] for f in fresh), dtype=torch.int32, device=dev)
+        t_at = p_at = 0
+        for dt, group in by_dtype.items():
+            flats = torch.zeros(sum(f[3].shape[0] * f[4] for f in group), dtype=dt, device=dev)
+            f_at = 0
+            for cache_list, layer_idx, st, ln, cap, _ in group:
+                B, S = ln.shape
+                flat = flats[f_at:f_at + B * cap].view(B, cap)
+                f_at += B * cap
+                lt = tabs[t_at:t_at + B * S].view(B, S)
+                ot = tabs[tab_elems + t_at:tab_elems + t_at + B * S].view(B, S)
+                t_at += B * S
+                ptr = ptrs[p_at:p_at + B]
+                p_at += B
+                cache_list[layer_idx] = [flat, lt, ot, ptr, 0, [0] * B]
+        return {(f[5], f[1]) for f in fresh}
 
     def update_sp(self, key_states, key_len, value_states, value_len, max_dim, layer_idx,
                   tensor_d, k_scalar=None, v_scalar=None):

@@ -233,6 +233,14 @@ class CompressedLlama(_Generator):
         kc, vc = kc.contiguous(), vc.contiguous()  # (B, S, G*Dh) coefficients
         k_out, v_out, len_k, len_v, _, _ = lw.cutoff.kv_process_fused(kc, vc)
         G, Dh = s.kv_heads, s.head_dim
+        if B == 1:
+            # rows b*G + g are strided views (row stride Dh, token stride G*Dh): the appends and
+            # the prefill products take the strides, so no transposed copy is made
+            rows_k = k_out.view(S, G, Dh).transpose(0, 1)
+            rows_v = v_out.view(S, G, Dh).transpose(0, 1)
+            lk = len_k.view(S, G).transpose(0, 1)
+            lv = len_v.view(S, G).transpose(0, 1)
+            return q, rows_k, lk, rows_v, lv
         rows_k = k_out.view(B, S, G, Dh).transpose(1, 2).reshape(B * G, S, Dh)
         rows_v = v_out.view(B, S, G, Dh).transpose(1, 2).reshape(B * G, S, Dh)
         lk = len_k.view(B, S, G).transpose(1, 2).reshape(B * G, S).contiguous()
@@ -250,7 +258,6 @@ class CompressedLlama(_Generator):
 
         def attn(i, lw, y):
             q, rk, lk, rv, lv = self._qkv(lw, y)
-            rk, rv = rk.contiguous(), rv.contiguous()
             pending.append((i, rk, lk, rv, lv))
             qh = _rope_q(q, 0, s.theta)
             # the masked coefficients are what the packed cache returns once appended

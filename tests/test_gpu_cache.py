@@ -129,13 +129,18 @@ def test_bulk_prefill_append_equals_per_layer(dev, dtype):
         a.update_sp(ks, lk, vs, lv, R, i, R)
     b.update_sp_prefill_many(items, R)
     assert b.device_syncs == 1
-    for i in range(layers):
-        for sa, sb in ((a.key_cache_sp[i], b.key_cache_sp[i]),
-                       (a.value_cache_sp[i], b.value_cache_sp[i])):
-            assert tuple(sa[0].shape) == tuple(sb[0].shape)
-            for t in range(4):
-                assert torch.equal(sa[t], sb[t]), (i, t)
-            assert sa[4] == sb[4] and list(sa[5]) == list(sb[5])
+
+    def same(tag):
+        for i in range(layers):
+            for sa, sb in ((a.key_cache_sp[i], b.key_cache_sp[i]),
+                           (a.value_cache_sp[i], b.value_cache_sp[i])):
+                assert tuple(sa[0].shape) == tuple(sb[0].shape), tag
+                assert tuple(sa[1].shape) == tuple(sb[1].shape), tag
+                for t in range(4):
+                    assert torch.equal(sa[t], sb[t]), (tag, i, t)
+                assert sa[4] == sb[4] and list(sa[5]) == list(sb[5]), tag
+
+    same("prefill")
     kb = torch.linalg.qr(torch.randn(G, R, R, generator=g))[0].to(dtype).to(dev)
     vb = torch.linalg.qr(torch.randn(G, R, R, generator=g))[0].to(dtype).to(dev)
     q = torch.randn(B, 2 * G, S, 128, generator=g).to(dtype).to(dev)
@@ -143,3 +148,14 @@ def test_bulk_prefill_append_equals_per_layer(dev, dtype):
     o1 = compressed_prefill_attention(q, a, 1, kb, vb, theta=500000.0)
     o2 = coef_prefill_attention(q, ks, vs, kb, vb, theta=500000.0)
     assert torch.equal(o1, o2)
+    # decode appends on both: the first grows every slot (flat and tables) out of the bulk
+    # prefill's shared buffers
+    for step in range(3):
+        for i in range(layers):
+            lk = torch.randint(0, R + 1, (B * G, 1), generator=g, dtype=torch.int32).to(dev)
+            lv = torch.randint(0, R + 1, (B * G, 1), generator=g, dtype=torch.int32).to(dev)
+            ks = torch.randn(B * G, 1, R, generator=g).to(dtype).to(dev)
+            vs = torch.randn(B * G, 1, R, generator=g).to(dtype).to(dev)
+            for c in (a, b):
+                c.update_sp(ks, lk, vs, lv, R, i, R)
+        same(f"decode {step}")
