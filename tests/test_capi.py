@@ -1,5 +1,6 @@
 """The C-ABI library loads and exports every function declared in include/dynakv_amd.h, the ctypes
 signatures match the header's parameter counts, and host-only calls behave (no device needed)."""
+import ctypes
 import os
 import re
 
@@ -11,14 +12,32 @@ from dynakv_amd import _lib
 HEADER = os.path.join(os.path.dirname(os.path.dirname(__file__)), "include", "dynakv_amd.h")
 
 
-def _header_functions():
+def _header_declarations():
+    """name -> (return type, [parameter types]) of every dkv_ function in the header."""
     text = open(HEADER).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     out = {}
-    for m in re.finditer(r"\b(?:int|long long|const char\*)\s+(dkv_\w+)\s*\(([^)]*)\)\s*;", text):
-        params = [p.strip() for p in m.group(2).split(",") if p.strip() and p.strip() != "void"]
-        out[m.group(1)] = len(params)
+    for m in re.finditer(r"\b(int|long long|const char\*)\s+(dkv_\w+)\s*\(([^)]*)\)\s*;", text):
+        params = [p.strip() for p in m.group(3).split(",") if p.strip() and p.strip() != "void"]
+        # a parameter's type: its declaration without the trailing name
+        types = [" ".join(re.sub(r"\w+$", "", p).split()) for p in params]
+        out[m.group(2)] = (m.group(1), types)
     return out
+
+
+def _header_functions():
+    return {k: len(v[1]) for k, v in _header_declarations().items()}
+
+
+# ctypes type each C type of the header must be bound with
+_CTYPE = {"int": ctypes.c_int, "long long": ctypes.c_longlong, "float": ctypes.c_float,
+          "const char*": ctypes.c_char_p}
+
+
+def _ctype_of(c: str):
+    if c.endswith("*"):  # every pointer parameter crosses as a void*
+        return ctypes.c_void_p
+    return _CTYPE[c]
 
 
 def test_header_parses():
@@ -34,10 +53,27 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_ctypes_signatures_match_header():
-    fns = _header_functions()
-    assert set(fns) == set(_lib.exported_symbols())
-    for name, n in fns.items():
-        assert len(_lib._SIGNATURES[name][1]) == n, name
+    """Every binding's return and parameter types are the header's, position by position (a
+    long long bound as int, or a float as a pointer, would pass a count check and corrupt the
+    call)."""
+    decls = _header_declarations()
+    assert set(decls) == set(_lib.exported_symbols())
+    for name, (ret, types) in decls.items():
+        res, args = _lib._SIGNATURES[name]
+        assert res is _CTYPE[ret], (name, "return", ret)
+        assert len(args) == len(types), name
+        for i, (c, bound) in enumerate(zip(types, args)):
+            assert bound is _ctype_of(c), (name, i, c, bound)
+
+
+def test_header_type_parser():
+    """The parser reads pointer, const and multi-word types."""
+    decls = _header_declarations()
+    ret, types = decls["dkv_view_extent_elems"]
+    assert ret == "long long" and types == ["int", "const long long*", "const long long*"]
+    ret, types = decls["dkv_status_string"]
+    assert ret == "const char*" and types == ["int"]
+    assert decls["dkv_prefill_attention"][1][-2:] == ["float", "const int*"]
 
 
 def test_host_only_entry_points():

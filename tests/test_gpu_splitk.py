@@ -129,15 +129,15 @@ def test_all_keys_empty_in_one_row(dev):
 @pytest.mark.gpu
 @pytest.mark.parametrize("route", ROUTES)
 def test_full_config3_size_rows_against_oracle(dev, route):
-    """Config 3 at full size (B=16, S=8192, bf16): batch rows 0 and 15 against the oracle, and
+    """Config 3 at full size (B=16, S=8192, bf16): every batch row against the oracle, and
     properties of the whole output (finite, linear in V)."""
     print(f"[gpu] splitk full config3 route={route}", flush=True)
     case = make_case(B=16, G=8, Hq=32, S=8192, mean=0.29, force_first=4, force_frac=0.05, seed=32)
     p = packed_from_case(case, torch.bfloat16, dev)
     got = _run(p, case, route)
     assert torch.isfinite(got.float()).all()
-    ref = oracle_grouped(case, p["host"], route, "bfloat16", batches=[0, 15])
-    assert_close(got[[0, 15]], ref, "config3 rows 0,15")
+    ref = oracle_grouped(case, p["host"], route, "bfloat16")
+    assert_close(got, ref, "config3 all 16 rows")
     # linearity in the V coefficients: doubling every V coefficient doubles the output (exact
     # in binary floating point up to the final rounding)
     p2 = dict(p)
