@@ -413,9 +413,10 @@ def bench_joint(dev, iters=5, B=16, S=8192, R=1024, Hq=32, Hkv=8, mean=0.29,
     reference ships them (compressed_attention.py:278-286), the router's long route
     (abx_sparse + avx semantics) through the MFMA kernels of ``kernels/joint.py``. GPU time from
     events around ``iters`` back-to-back calls; the scores kernel's MFMA work counted as
-    launched (2 * 128 * 32 flop per rank chunk, token slot and KV head, chunks up to each
-    512-token block's longest token). The vector kernels (dkv_scores / dkv_av, what a joint
-    layout ran on before) are timed on a 2 x 512-token slice of the same data."""
+    launched (2 * 128 * 32 flop per rank chunk, token slot and KV head, each workgroup's tokens
+    sorted by chunk count and every 16 sorted tokens run up to their longest token's chunks).
+    The vector kernels (dkv_scores / dkv_av, what a joint layout ran on before) are timed on a
+    2 x 512-token slice of the same data."""
     import math as _m
 
     from dynakv_amd import _lib
@@ -464,6 +465,7 @@ def bench_joint(dev, iters=5, B=16, S=8192, R=1024, Hq=32, Hkv=8, mean=0.29,
     t_av = timed(lambda: J.joint_av(sc, v_up, fv, lv, ov, mode=0, out_dtype=dtype), iters)
     flops = J.joint_flops(lk, R, Hkv, B)
     dense_flops = 2.0 * B * S * Hkv * 128 * R
+    useful_flops = 2.0 * 128 * Hkv * float(lk.clamp(0, R).sum().item())
     coef_bytes = 2 * int(lk.clamp(0, R).sum().item() + lv.clamp(0, R).sum().item())
 
     # the vector kernels on a slice: 2 rows x 512 tokens
@@ -503,6 +505,9 @@ def bench_joint(dev, iters=5, B=16, S=8192, R=1024, Hq=32, Hkv=8, mean=0.29,
         "scores_mfma_peak_frac": round(flops / (t_sc * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
         "scores_flop_as_launched": flops,
         "reconstruction_flop_dense": dense_flops,
+        "reconstruction_flop_useful": useful_flops,
+        "scores_useful_peak_frac": round(useful_flops / (t_sc * 1e-6) / 1e12
+                                         / MFMA_BF16_PEAK_TFLOPS, 4),
         "coefficient_bytes": coef_bytes,
         "vector_kernels_slice": {"slice": f"B={b2}, S={s2}", "us_per_call": round(t_vec, 1),
                                  "mfma_us_per_call": round(t_mfma_slice, 1)},

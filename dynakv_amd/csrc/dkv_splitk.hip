@@ -576,6 +576,18 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
   // flight during the prologue
   load_tab(0);
   load_tab(1);
+  // rotation R(16*T) of the wave's current tile T for frequency i = lane, times the score
+  // scale (the fused route's scores come out in log2 units, the two-stage route's in natural
+  // units), advanced by angle addition (WAVES*TILE positions per tile); bc/bs start at the
+  // table's exact value for the wave's first tile. Loaded here, with the tables, so that their
+  // round trip overlaps the prologue's instead of following its barriers.
+  float bc, bs;
+  {
+    const int t = min(tile0, n_tb - 1);
+    const float* rrow = p.rope + (long long)(ROPE_FIXED_ROWS + t) * 128 + 2 * lane;
+    bc = rrow[0] * p.score_scale;
+    bs = rrow[1] * p.score_scale;
+  }
 
   // ---- prologue: K basis, mask table, rotation step ---------------------------------------
   {
@@ -788,17 +800,6 @@ __global__ __launch_bounds__(NTHREADS, 1) void splitk_kernel(SplitParams p) {
   //      Loads are issued for every iteration, also past the wave's last tile (indices clamp
   //      to the split's last token), so at the top of iteration j nothing but G(j) and T(j+1)
   //      can be in flight and a full wait costs nothing extra. -------------------------------
-  // rotation R(16*T) of the wave's current tile T for frequency i = lane, times the score
-  // scale (the fused route's scores come out in log2 units, the two-stage route's in natural
-  // units), advanced by angle addition (WAVES*TILE positions per tile); bc/bs start at the
-  // table's exact value for the wave's first tile
-  float bc, bs;
-  {
-    const int t = min(tile0, n_tb - 1);
-    const float* row = p.rope + (long long)(ROPE_FIXED_ROWS + t) * 128 + 2 * lane;
-    bc = row[0] * p.score_scale;
-    bs = row[1] * p.score_scale;
-  }
   // loop-invariant loaded values: settled here, so the loop carries no wait for their loads
   // (such a wait would also drain the gathers in flight)
   settle(bc);

@@ -200,13 +200,16 @@ def joint_attention(q3, k_flat, k_up, v_flat, v_up, l_k, o_k, l_v, o_v, *, theta
 
 def joint_flops(lens_k: torch.Tensor, R: int, n_basis: int, B: int) -> float:
     """MFMA flops of the scores kernel as launched: 2 * 128 dims * 32 ranks per processed chunk,
-    per token slot and basis head (chunks up to each 512-token block's longest token)."""
+    per token slot and basis head. A workgroup takes 512 tokens (256 when the basis heads pair
+    up), sorts them by chunk count and runs each block of 16 sorted tokens up to its own
+    longest token's chunk count."""
     S = lens_k.shape[1]
-    blocks = (S + 511) // 512
-    pad = blocks * 512 - S
-    L = torch.nn.functional.pad(lens_k.clamp(0, R), (0, pad)).view(B, blocks, 512)
-    chunks = (L.amax(dim=2) + 31) // 32
-    return float(chunks.sum().item()) * 512 * 2 * 128 * 32 * n_basis
+    tok = 256 if n_basis % 2 == 0 else 512
+    groups = (S + tok - 1) // tok
+    pad = groups * tok - S
+    L = torch.nn.functional.pad(lens_k.clamp(0, R), (0, pad)).view(B, groups, tok)
+    chunks = ((L + 31) // 32).sort(dim=2).values.view(B, groups, tok // 16, 16)[..., -1]
+    return float(chunks.sum().item()) * 16 * 2 * 128 * 32 * n_basis
 
 
 __all__ = ["joint_attention", "joint_scores", "joint_av", "scores_eligible", "av_eligible",
