@@ -220,8 +220,11 @@ def run_gpu(cfg, steps, warmup, dev, layers):
     calls = steps * layers
     # fused merge (one launch per call) unless the call has more units than arrival counters
     units = cfg.B * cfg.G
+    step_ms = [e0.elapsed_time(e1) for e0, e1 in evs]
+    step_len = [lens[j * layers][1] for j in range(steps)]  # layer 0's length at each step
     return dict(
         wall_s=wall, attn_ms=attn_ms, split_ms=attn_ms, merge_ms=0.0, calls=calls,
+        step_ms=step_ms, step_len=step_len,
         merged_in_split=units <= 16384,
         bytes_total=tot_bytes, bytes_per_call=tot_bytes / calls,
         split_bytes_per_call=float(sum(attention_bytes(cfg, Ws[l]["lk_h"], Ws[l]["lv_h"], L,
@@ -230,6 +233,37 @@ def run_gpu(cfg, steps, warmup, dev, layers):
         syncs=sum(W["cache"].device_syncs for W in Ws),
         cache=Ws[0]["cache"], workload=Ws[0],
     )
+
+
+def bench_config2(dev, steps=100, warmup=10, layers=4):
+    """Config 2 as one layer of its 32-layer stack (fp16, B=4, 8 KV groups x rank 128, mean
+    retention 0.47): ``steps`` decode steps from 480 tokens on, so the router's switch at 500
+    tokens is crossed (fused route below it, two-stage from it on), each step appending to
+    ``layers`` independent layer caches and timing their back-to-back attention launches as the
+    main workload does. Reports us per layer-step overall and per route, and the algorithmic
+    bytes per launch against HBM peak (a latency-bound launch: 4.4-5.4 MB per call)."""
+    cfg = Config2
+    r = run_gpu(cfg, steps, warmup, dev, layers)
+    calls = r["calls"]
+    us = r["attn_ms"] * 1e3 / calls
+    fused = [ms for ms, L in zip(r["step_ms"], r["step_len"]) if L < 500]
+    two = [ms for ms, L in zip(r["step_ms"], r["step_len"]) if L >= 500]
+    per = lambda v: round(sum(v) * 1e3 / (len(v) * layers), 3) if v else None  # noqa: E731
+    bpc = r["bytes_per_call"]
+    return {
+        "workload": cfg.name, "batch": cfg.B, "q_heads": cfg.Hq, "kv_heads": cfg.G,
+        "rank": cfg.R, "dtype": "fp16", "mean_retention": cfg.mean,
+        "cache_len_start": cfg.S0, "cache_len_end": r["final_len"], "steps": steps,
+        "layers_per_step": layers,
+        "us_per_layer_step": round(us, 3),
+        "us_per_layer_step_fused_route": per(fused),
+        "us_per_layer_step_two_stage_route": per(two),
+        "bytes_per_launch": round(bpc),
+        "achieved_gbs": round(bpc / (us * 1e-6) / 1e9, 2),
+        "frac_hbm_peak": round(bpc / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        "timing": "HIP events around each step's back-to-back attention launches (as the "
+                  "main workload)",
+    }
 
 
 def cpu_baseline(cfg, W, cache, budget_s: float):
@@ -593,6 +627,8 @@ def main():
     ap.add_argument("--cpu-baseline-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-cutoff", action="store_true", help="skip the cutoff-head timing")
+    ap.add_argument("--no-config2", action="store_true",
+                    help="skip the config-2 timing (fp16, B=4, 480 -> 580 tokens, one layer)")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill-attention timing")
     ap.add_argument("--no-joint", action="store_true",
                     help="skip the joint-layout (rank 1024) attention timing")
@@ -697,6 +733,9 @@ def main():
             "traffic_source": traffic["source"] if traffic else None,
         },
     }
+    if not args.no_config2 and cfg.name == "config3":
+        _log("config 2 (one layer, 480 -> 580 tokens)")
+        line["config2"] = bench_config2(dev)
     if not args.no_cutoff:
         _log("cutoff head")
         line["cutoff_head"] = bench_cutoff(cfg, dev)

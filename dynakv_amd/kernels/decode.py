@@ -200,3 +200,64 @@ def grouped_decode_attention(q: torch.Tensor, k_flat: torch.Tensor, v_flat: torc
     return splitk_attention(q3, k_flat, v_flat, layout, lens_k, offs_k, lens_v, offs_v,
                             theta=theta, route=rt, groups=G, split_len=split_len, out=out,
                             out_dtype=out_dtype)
+
+
+def dense_decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                           S: int, *, split_len: int = 0, out: torch.Tensor | None = None,
+                           out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """Dense GQA decode attention over an uncompressed cache (``dkv_decode_dense``): the
+    end-to-end comparison's baseline, the attention of the reference's uncompressed model.
+
+    ``q``: (B, Hq, 128) or (B, Hq, 1, 128), rotated. ``k_cache`` / ``v_cache``: (B * Hkv, ld)
+    with unit last stride; row b * Hkv + g holds token t's rotated key (value) at elements
+    t * 128 .. t * 128 + 127; tokens 0 .. S-1 are attended."""
+    lib = _lib.load()
+    q3 = q.squeeze(2) if q.dim() == 4 else q
+    if q3.stride(2) != 1 or q3.data_ptr() % 16 or q3.stride(0) % 8 or q3.stride(1) % 8:
+        q3 = q3.contiguous()
+    B, hq, dh = q3.shape
+    if k_cache.shape != v_cache.shape or k_cache.dim() != 2 or k_cache.shape[0] % max(B, 1):
+        raise ValueError("k_cache / v_cache must be (B * Hkv, ld) of the same shape")
+    if k_cache.dtype != q3.dtype or v_cache.dtype != q3.dtype:
+        raise ValueError("cache and query dtypes differ")
+    if k_cache.stride(1) != 1 or v_cache.stride(1) != 1 or k_cache.stride(0) != v_cache.stride(0):
+        raise ValueError("cache rows must be contiguous with one row stride for K and V")
+    hkv = k_cache.shape[0] // B
+    odt = out_dtype if out_dtype is not None else (out.dtype if out is not None else q3.dtype)
+    if odt not in (q3.dtype, torch.float32):
+        raise ValueError("out_dtype must be the query dtype or float32")
+    if out is None:
+        out = torch.empty((B, hq, dh), dtype=odt, device=q3.device)
+    elif out.dtype != odt or out.stride(2) != 1:
+        raise ValueError("out must have unit last stride and the requested dtype")
+    st = _lib.stream_of(q3)
+    nfl = lib.dkv_dense_workspace_floats(B, hq, hkv, S, split_len)
+    ws = workspace(q3.device, st, int(nfl))
+    rc = lib.dkv_decode_dense(
+        st, _lib.dtype_code(q3.dtype), q3.data_ptr(), q3.stride(0), q3.stride(1),
+        k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0), S, ws.data_ptr(), ws.numel(),
+        out.data_ptr(), out.stride(0), out.stride(1), _lib.dtype_code(out.dtype),
+        B, hq, hkv, dh, split_len)
+    _lib.check(rc, "dkv_decode_dense")
+    return out
+
+
+def dense_append_(y: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, *,
+                  q_pos: int, k_pos: int, heads: int, kv_heads: int, theta: float) -> None:
+    """One decode step's cache write of the dense baseline (``dkv_dense_append``): ``y`` (B, W)
+    rows of the fused q/k/v projection (``heads`` query heads, then ``kv_heads`` key heads, then
+    ``kv_heads`` value heads of 128); the query heads are rotated in place at ``q_pos``, the key
+    heads rotated at ``k_pos`` into ``k_cache`` (B * kv_heads, ld) at token ``k_pos``, the value
+    heads copied into ``v_cache``."""
+    lib = _lib.load()
+    if y.dim() != 2 or y.stride(1) != 1:
+        raise ValueError("y must be (B, W) with unit last stride")
+    if k_cache.stride(1) != 1 or v_cache.stride(1) != 1 or k_cache.stride(0) != v_cache.stride(0):
+        raise ValueError("cache rows must be contiguous with one row stride for K and V")
+    if not (y.dtype == k_cache.dtype == v_cache.dtype):
+        raise ValueError("y and cache dtypes differ")
+    _lib.check(lib.dkv_dense_append(_lib.stream_of(y), _lib.dtype_code(y.dtype), y.data_ptr(),
+                                    y.stride(0), k_cache.data_ptr(), v_cache.data_ptr(),
+                                    k_cache.stride(0), int(q_pos), int(k_pos), y.shape[0],
+                                    int(heads), int(kv_heads), math.log(theta)),
+               "dkv_dense_append")

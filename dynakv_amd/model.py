@@ -39,7 +39,7 @@ from torch.nn.attention import SDPBackend, sdpa_kernel
 from .formats import merge_projection
 from .kernels.compressed_cache import CustomDynamicCache
 from .kernels.cutoff import CutoffHead
-from .kernels.decode import grouped_decode_attention
+from .kernels.decode import dense_append_, dense_decode_attention, grouped_decode_attention
 from .kernels.layer import DecodeLayerPlan
 from .kernels.model_ops import linear, rmsnorm_glu, rmsnorm_linear
 from .kernels.prefill import coef_prefill_attention, rope_dense_
@@ -316,12 +316,12 @@ _FAST_SDPA = [SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]
 
 
 class DenseLlama(_Generator):
-    """The same weights with an uncompressed cache: every token's K and V kept in full (head dim
-    128 per KV head, K before RoPE). Decode attention runs the compressed path's split kernel on
-    that cache read as a packed cache with every token retaining all 128 dims and an identity
-    basis -- dense GQA decode attention in the packed format (fused-route semantics: fp32
-    scores, no rounding) -- so the two models differ in the bytes their caches hold, not in the
-    attention implementation. Prefill attention is torch's fused attention on the rotated keys."""
+    """The same weights with an uncompressed cache, the reference's baseline (the original model
+    with transformers' KV cache, ``scripts/benchmark_throughput.py:17-77``): every token's
+    rotated key and its value kept in full (head dim 128 per KV head). A decode step writes the
+    new token's rotated key and value and rotates q in one launch (``dkv_dense_append``), then
+    runs dense GQA decode attention (``dkv_decode_dense``: no reconstruction, no RoPE in the
+    attention, fp32 scores). Prefill attention is torch's fused attention on the rotated keys."""
 
     def __init__(self, model: RandomLlama, max_len: int = 4096):
         super().__init__(model)
@@ -352,18 +352,14 @@ class DenseLlama(_Generator):
                   for _ in range(s.layers)]
         self.v = [torch.empty((rows, self.max_len * Dh), device=dev, dtype=dt)
                   for _ in range(s.layers)]
-        self.lens = torch.full((rows, self.max_len), Dh, device=dev, dtype=torch.int32)
-        self.offs = (torch.arange(self.max_len, device=dev, dtype=torch.int32) * Dh).expand(
-            rows, -1).contiguous()
-        self.eye = torch.eye(Dh, device=dev, dtype=dt).expand(G, Dh, Dh).contiguous()
         hpg = s.heads // s.kv_heads
         x = F.embedding(prompt, self.m.embed)
 
         def attn(i, lw, y):
             qh, k, v = self._kv(lw, y, 0)
-            self.k[i][:, :S * Dh] = k.reshape(rows, S * Dh)
-            self.v[i][:, :S * Dh] = v.reshape(rows, S * Dh)
             kr = rope_dense_(k.contiguous(), theta=s.theta, pos0=0)
+            self.k[i][:, :S * Dh] = kr.reshape(rows, S * Dh)
+            self.v[i][:, :S * Dh] = v.reshape(rows, S * Dh)
             with sdpa_kernel(_FAST_SDPA):
                 a = F.scaled_dot_product_attention(qh, kr.repeat_interleave(hpg, dim=1),
                                                    v.repeat_interleave(hpg, dim=1),
@@ -375,22 +371,20 @@ class DenseLlama(_Generator):
         return x
 
     def decode(self, tok: torch.Tensor, pos: int) -> torch.Tensor:
-        """One token: K/V written at position len, then decode attention over len + 1 tokens."""
+        """One token: the rotated K and V written at position len (q rotated at ``pos`` in the
+        same launch), then dense decode attention over len + 1 tokens."""
         s = self.s
         x = F.embedding(tok, self.m.embed)
         B = tok.shape[0]
         L = self.len
         Dh = s.head_dim
-        rows = B * s.kv_heads
-        lens, offs = self.lens[:, :L + 1], self.offs[:, :L + 1]
 
         def attn(i, lw, y):
-            qh, k, v = self._kv(lw, y, pos)
-            self.k[i][:, L * Dh:(L + 1) * Dh] = k.reshape(rows, Dh)
-            self.v[i][:, L * Dh:(L + 1) * Dh] = v.reshape(rows, Dh)
-            a = grouped_decode_attention(qh[:, :, 0], self.k[i], self.v[i], lens, offs, lens,
-                                         offs, self.eye, self.eye, theta=s.theta,
-                                         route="short_fused")
+            y2 = y[:, 0, :]
+            dense_append_(y2, self.k[i], self.v[i], q_pos=pos, k_pos=L, heads=s.heads,
+                          kv_heads=s.kv_heads, theta=s.theta)
+            qh = y2[:, :s.heads * Dh].view(B, s.heads, Dh)
+            a = dense_decode_attention(qh, self.k[i], self.v[i], L + 1)
             return a.reshape(B, 1, s.hidden)
 
         x = self._run(x, attn, "w_qkv")

@@ -267,6 +267,40 @@ int dkv_decode_splitk(void* stream, int route, int dtype,
                       int B, int Hq, int Hkv, int G, int S, int R, int Dh, int split_len);
 
 /*
+ * Dense GQA decode attention over an uncompressed cache: the baseline of the end-to-end
+ * comparison (the reference's uncompressed model, scripts/benchmark_throughput.py:17-77, reads
+ * every cached token's rotated key and value at full width; it has no kernel of its own for it).
+ *   q: (B, Hq, Dh) strides (q_sb, q_sh), rotated by the caller.
+ *   k / v: rows b * Hkv + g of kv_ld elements; token t of a row at elements t * Dh .. + Dh - 1,
+ *          keys already rotated.
+ *   workspace: dkv_dense_workspace_floats(...) floats, the same contract as dkv_decode_splitk's
+ *              (16384 leading arrival counters, zero before the first call and after each).
+ *   out: (B, Hq, Dh) strides (out_sb, out_sh), out_dtype = the cache dtype or DKV_F32.
+ * Semantics: softmax(q . k / sqrt(Dh)) v over tokens 0..S-1 with fp32 scores and accumulation.
+ * Requirements: dtype f16 or bf16, Dh == 128, hpg <= 16, 16-byte aligned q rows and cache
+ * rows (kv_ld % 8 == 0, kv_ld >= S * Dh), S * Dh * 2 < 2^31, split_len a multiple of 64
+ * (0 = dkv_dense_choose_split).
+ */
+long long dkv_dense_workspace_floats(int B, int Hq, int Hkv, int S, int split_len);
+/*
+ * A decode step's cache write for the dense baseline (the uncompressed model's KV-cache update
+ * and its q/k rotation, transformers' Llama attention, run as one launch): y holds B rows (stride
+ * y_ld) of the fused q/k/v projection, Hq query heads then Hkv key heads then Hkv value heads of
+ * 128; the query heads are rotated in place at q_pos, the key heads rotated at k_pos into
+ * k_cache[(b * Hkv + g) * kv_ld + k_pos * 128 ..], the value heads copied into v_cache likewise.
+ * RoPE as dkv_rope_dense (angle float(pos) * inv_freq in fp32, rotation in fp32).
+ */
+int dkv_dense_append(void* stream, int dtype, void* y, long long y_ld, void* k_cache,
+                     void* v_cache, long long kv_ld, int q_pos, int k_pos, int B, int Hq,
+                     int Hkv, float log_theta);
+int dkv_dense_choose_split(int B, int Hkv, int S);
+int dkv_decode_dense(void* stream, int dtype, const void* q, long long q_sb, long long q_sh,
+                     const void* k, const void* v, long long kv_ld, int S,
+                     float* workspace, long long workspace_floats,
+                     void* out, long long out_sb, long long out_sh, int out_dtype,
+                     int B, int Hq, int Hkv, int Dh, int split_len);
+
+/*
  * dkv_decode_splitk without a workspace argument, for callers that cannot allocate device memory
  * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). It has no
  * counterpart in the reference. Same arguments, semantics and results as dkv_decode_splitk; the
