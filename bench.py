@@ -235,6 +235,45 @@ def run_gpu(cfg, steps, warmup, dev, layers):
     )
 
 
+def bench_dense_same_shape(dev, S=8192, B=16, Hkv=8, hpg=4, layers=4, steps=20):
+    """The uncompressed baseline's decode attention (``dkv_decode_dense``) at the main workload's
+    shape: every token's rotated key and value at 128 dims (the reference's original model,
+    ``scripts/benchmark_throughput.py``), ``layers`` caches cycled so that none stays in the
+    last-level cache, their launches timed back to back with one event pair per step as the
+    compressed workload is. Bytes: K and V of every token, q and the output."""
+    from dynakv_amd.kernels.decode import dense_decode_attention
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(99)
+    rows = B * Hkv
+    caches = [(torch.randn((rows, S * 128), generator=g, device=dev).to(torch.bfloat16),
+               torch.randn((rows, S * 128), generator=g, device=dev).to(torch.bfloat16))
+              for _ in range(layers)]
+    q = torch.randn((B, Hkv * hpg, 128), generator=g, device=dev).to(torch.bfloat16)
+    out = torch.empty_like(q)
+    for _ in range(2):
+        for k, v in caches:
+            dense_decode_attention(q, k, v, S, out=out)
+    torch.cuda.synchronize(dev)
+    evs = []
+    for _ in range(steps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for k, v in caches:
+            dense_decode_attention(q, k, v, S, out=out)
+        e1.record()
+        evs.append((e0, e1))
+    torch.cuda.synchronize(dev)
+    us = sum(a.elapsed_time(b) for a, b in evs) * 1e3 / (steps * layers)
+    nbytes = 2 * rows * S * 128 * 2 + 2 * q.numel() * 2
+    del caches
+    torch.cuda.empty_cache()
+    return {"kernel": "dense_decode_kernel<bf16>", "batch": B, "kv_heads": Hkv,
+            "q_heads": Hkv * hpg, "cache_len": S, "bytes_per_call": nbytes,
+            "us_per_call": round(us, 3), "achieved_gbs": round(nbytes / (us * 1e-6) / 1e9, 2),
+            "frac_hbm_peak": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
 def bench_config2(dev, steps=100, warmup=10, layers=4):
     """Config 2 as one layer of its 32-layer stack (fp16, B=4, 8 KV groups x rank 128, mean
     retention 0.47): ``steps`` decode steps from 480 tokens on, so the router's switch at 500
@@ -548,29 +587,34 @@ def bench_joint(dev, iters=5, B=16, S=8192, R=1024, Hq=32, Hkv=8, mean=0.29,
     }
 
 
-def bench_e2e(dev, batches=(1, 2, 4), prompt_len=2048, new_tokens=100, models="both"):
+def bench_e2e(dev, batches=(1, 2, 4), prompt_len=2048, new_tokens=100, models="all"):
     """Config 5: greedy generation with a random-init Llama-3-8B (bf16 N(0, 0.02) weights,
     per-head random orthogonal bases, cutoff heads set for mean retention 0.47) over the
-    compressed cache, against the same weights with an uncompressed cache (decode attention by
-    the same split kernel over the full cache, every token at 128 dims with an identity basis;
-    prefill attention by torch's fused attention). tokens/s = batch * new tokens / wall time
+    compressed cache, against the same weights with an uncompressed cache (the reference's
+    original model: rotated keys and values at 128 dims, decode attention by the dense GQA
+    kernel ``dkv_decode_dense``, the cache write and q rotation in one launch; prefill attention
+    by torch's fused attention). tokens/s = batch * new tokens / wall time
     with prefill, as the reference's benchmark_throughput.py:73 counts it; decode-only tokens/s
-    beside it. Both models run eagerly (one launch per op, no graph capture). ``models``:
-    "both", "compressed" or "dense" (one model alone, for a kernel trace of it)."""
+    beside it. A third run keeps the dense cache but decodes through torch's fused
+    ``scaled_dot_product_attention``, the attention of the reference's transformers baseline.
+    All run eagerly (one launch per op, no graph capture). ``models``: "all", "compressed",
+    "dense" or "sdpa" (one model alone, for a kernel trace of it)."""
     from dynakv_amd.model import CompressedLlama, DenseLlama, LlamaShape, RandomLlama
 
     shape = LlamaShape()
     model = RandomLlama(shape, device=dev, seed=5)
-    comp = CompressedLlama(model) if models in ("both", "compressed") else None
+    comp = CompressedLlama(model) if models in ("all", "compressed") else None
     dense = (DenseLlama(model, max_len=prompt_len + new_tokens + 8)
-             if models in ("both", "dense") else None)
+             if models in ("all", "dense") else None)
+    sdpa = (DenseLlama(model, max_len=prompt_len + new_tokens + 8, attention="sdpa")
+            if models in ("all", "sdpa") else None)
     g = torch.Generator(device="cpu").manual_seed(11)
     res = {"model": "random-init Llama-3-8B shape (32 layers, 4096 hidden, 32/8 heads, FFN "
                     "14336, vocab 128256), bf16", "prompt_len": prompt_len,
            "new_tokens": new_tokens, "runs": []}
     # one short warm-up of each path (kernel loading, library handles)
     warm = torch.randint(0, shape.vocab, (1, 64), generator=g).to(dev)
-    for m in (comp, dense):
+    for m in (comp, dense, sdpa):
         if m is not None:
             m.generate(warm, 4)
     empty = {"tokens_per_s": 0.0, "decode_tokens_per_s": 0.0, "prefill_s": 0.0, "kv_bytes": 0,
@@ -579,6 +623,7 @@ def bench_e2e(dev, batches=(1, 2, 4), prompt_len=2048, new_tokens=100, models="b
         prompt = torch.randint(0, shape.vocab, (B, prompt_len), generator=g).to(dev)
         rc = comp.generate(prompt, new_tokens) if comp is not None else empty
         rd = dense.generate(prompt, new_tokens) if dense is not None else empty
+        rs = sdpa.generate(prompt, new_tokens) if sdpa is not None else empty
         lens = ([int(c[1][:, :c[4]].float().mean().item()) for c in comp.cache.key_cache_sp[:1]]
                 if comp is not None else [])
         res["runs"].append({
@@ -587,6 +632,8 @@ def bench_e2e(dev, batches=(1, 2, 4), prompt_len=2048, new_tokens=100, models="b
             "dense_tokens_per_s": round(rd["tokens_per_s"], 1),
             "compressed_decode_tokens_per_s": round(rc["decode_tokens_per_s"], 1),
             "dense_decode_tokens_per_s": round(rd["decode_tokens_per_s"], 1),
+            "dense_sdpa_tokens_per_s": round(rs["tokens_per_s"], 1),
+            "dense_sdpa_decode_tokens_per_s": round(rs["decode_tokens_per_s"], 1),
             "compressed_prefill_s": round(rc["prefill_s"], 4),
             "dense_prefill_s": round(rd["prefill_s"], 4),
             "compressed_kv_bytes": rc["kv_bytes"],
@@ -595,7 +642,7 @@ def bench_e2e(dev, batches=(1, 2, 4), prompt_len=2048, new_tokens=100, models="b
             "same_tokens_frac": (round(float((rc["tokens"] == rd["tokens"]).float().mean()), 3)
                                  if comp is not None and dense is not None else None),
         })
-    del comp, dense, model
+    del comp, dense, sdpa, model
     torch.cuda.empty_cache()
     return res
 
@@ -627,6 +674,8 @@ def main():
     ap.add_argument("--cpu-baseline-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-cutoff", action="store_true", help="skip the cutoff-head timing")
+    ap.add_argument("--no-dense", action="store_true",
+                    help="skip the dense (uncompressed) attention timing at the main shape")
     ap.add_argument("--no-config2", action="store_true",
                     help="skip the config-2 timing (fp16, B=4, 480 -> 580 tokens, one layer)")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill-attention timing")
@@ -639,9 +688,10 @@ def main():
                     help="run config 5 alone (for a kernel trace of the decoder) and print its "
                          "JSON object")
     ap.add_argument("--e2e-batches", default="1,2,4", help="config 5 batch sizes")
-    ap.add_argument("--e2e-model", default="both", choices=["both", "compressed", "dense"],
+    ap.add_argument("--e2e-model", default="all", choices=["all", "compressed", "dense", "sdpa"],
                     help="config 5 models to run (one alone for a kernel trace of it)")
     ap.add_argument("--e2e-tokens", type=int, default=100, help="config 5 new tokens")
+    ap.add_argument("--e2e-prompt", type=int, default=2048, help="config 5 prompt length")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="run one device copy of this many MiB first (counter calibration)")
     args = ap.parse_args()
@@ -658,7 +708,8 @@ def main():
     e2e_batches = tuple(int(b) for b in args.e2e_batches.split(","))
     if args.e2e_only:
         print(json.dumps({"e2e": bench_e2e(dev, batches=e2e_batches, new_tokens=args.e2e_tokens,
-                                           models=args.e2e_model)}),
+                                           models=args.e2e_model,
+                                           prompt_len=args.e2e_prompt)}),
               flush=True)
         return
     cfg = Config3 if args.workload == "config3" else Config2
@@ -733,6 +784,10 @@ def main():
             "traffic_source": traffic["source"] if traffic else None,
         },
     }
+    if not args.no_dense and cfg.name == "config3":
+        _log("dense baseline attention at the same shape")
+        line["dense_same_shape"] = bench_dense_same_shape(dev, S=r["final_len"])
+        line["dense_same_shape"]["compressed_split_kernel_us"] = line["roofline"]["split_kernel_us"]
     if not args.no_config2 and cfg.name == "config3":
         _log("config 2 (one layer, 480 -> 580 tokens)")
         line["config2"] = bench_config2(dev)

@@ -323,9 +323,15 @@ class DenseLlama(_Generator):
     runs dense GQA decode attention (``dkv_decode_dense``: no reconstruction, no RoPE in the
     attention, fp32 scores). Prefill attention is torch's fused attention on the rotated keys."""
 
-    def __init__(self, model: RandomLlama, max_len: int = 4096):
+    def __init__(self, model: RandomLlama, max_len: int = 4096, attention: str = "kernel"):
+        """``attention``: "kernel" (``dkv_decode_dense``) or "sdpa" (torch's
+        ``scaled_dot_product_attention`` over the cached keys and values, the attention path the
+        reference's uncompressed transformers model takes)."""
         super().__init__(model)
+        if attention not in ("kernel", "sdpa"):
+            raise ValueError("attention must be 'kernel' or 'sdpa'")
         self.max_len = max_len
+        self.attention = attention
         self.k = self.v = None
         self.len = 0
 
@@ -384,6 +390,15 @@ class DenseLlama(_Generator):
             dense_append_(y2, self.k[i], self.v[i], q_pos=pos, k_pos=L, heads=s.heads,
                           kv_heads=s.kv_heads, theta=s.theta)
             qh = y2[:, :s.heads * Dh].view(B, s.heads, Dh)
+            if self.attention == "sdpa":
+                G, hpg = s.kv_heads, s.heads // s.kv_heads
+                kk = self.k[i][:, :(L + 1) * Dh].view(B, G, L + 1, Dh)
+                vv = self.v[i][:, :(L + 1) * Dh].view(B, G, L + 1, Dh)
+                with sdpa_kernel(_FAST_SDPA):
+                    a = F.scaled_dot_product_attention(
+                        qh.unsqueeze(2), kk.repeat_interleave(hpg, dim=1),
+                        vv.repeat_interleave(hpg, dim=1))
+                return a.reshape(B, 1, s.hidden)
             a = dense_decode_attention(qh, self.k[i], self.v[i], L + 1)
             return a.reshape(B, 1, s.hidden)
 

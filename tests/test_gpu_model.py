@@ -70,14 +70,15 @@ def _close(got, ref, what, rel=0.05):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("kind", ["compressed", "compressed_per_op", "dense"])
+@pytest.mark.parametrize("kind", ["compressed", "compressed_per_op", "dense", "dense_sdpa"])
 def test_model_matches_float32_forward(dev, kind):
     """compressed: the first decode step per layer takes the regular path, the later ones one
-    dkv_decode_layer call; compressed_per_op: every step the regular path."""
+    dkv_decode_layer call; compressed_per_op: every step the regular path; dense: the
+    uncompressed cache with dkv_decode_dense; dense_sdpa: the same cache through torch's SDPA."""
     print(f"[gpu] model {kind}", flush=True)
     model = RandomLlama(SHAPE, device=dev, seed=3, std=0.05)
-    if kind == "dense":
-        gen = DenseLlama(model, max_len=64)
+    if kind.startswith("dense"):
+        gen = DenseLlama(model, max_len=64, attention="sdpa" if kind == "dense_sdpa" else "kernel")
     else:
         gen = CompressedLlama(model, one_call_layers=(kind == "compressed"))
     g = torch.Generator(device="cpu").manual_seed(1)
@@ -91,7 +92,7 @@ def test_model_matches_float32_forward(dev, kind):
         got.append(gen.logits(x).float().cpu())
     got = torch.cat(got, dim=1)  # prompt positions, then the three decoded positions
     lk = lv = None
-    if kind != "dense":
+    if not kind.startswith("dense"):
         lk = [c[1][:, :S].cpu() for c in gen.cache.key_cache_sp]
         lv = [c[1][:, :S].cpu() for c in gen.cache.value_cache_sp]
         frac = torch.stack(lk).float().mean().item() / SHAPE.head_dim
