@@ -21,7 +21,8 @@ LIB_DIR = PKG_DIR / "lib"
 LIB_PATH = LIB_DIR / "libdynakv_amd.so"
 OBJ_DIR = PKG_DIR / "_build"
 SOURCES = ("dkv_append.hip", "dkv_generic.hip", "dkv_splitk.hip", "dkv_cutoff.hip",
-           "dkv_prefill.hip", "dkv_layer.hip", "dkv_model.hip", "dkv_joint.hip", "dkv_dense.hip")
+           "dkv_prefill.hip", "dkv_layer.hip", "dkv_model.hip", "dkv_joint.hip", "dkv_dense.hip",
+           "dkv_recon.hip")
 ARCH = os.environ.get("DYNAKV_AMD_ARCH", "gfx950")
 
 COMMON_FLAGS = [

@@ -125,6 +125,34 @@ def _rotate_k(k: torch.Tensor, theta: float, k_rope) -> None:
         rope_apply_(k, *k_rope)
 
 
+def recon_kv(ck: torch.Tensor, cv: torch.Tensor, k_basis: torch.Tensor, v_basis: torch.Tensor,
+             *, batch: int, theta: float, pos0: int = 0):
+    """Dense K (rotated at positions ``pos0 + t``) and V ``(B, G, S, 128)`` from masked
+    coefficient rows ``ck`` / ``cv`` ``(B*G, S, R)`` in one launch (``dkv_recon_kv``), or ``None``
+    when the operands do not fit it (the caller then takes the library-GEMM path)."""
+    G, R, Dh = k_basis.shape
+    rows, S, Rc = ck.shape
+    dt = ck.dtype
+    if (dt not in (torch.float16, torch.bfloat16) or Dh != 128 or Rc != R or R % 8 or R > 128
+            or cv.shape != ck.shape or cv.stride() != ck.stride() or ck.stride(2) != 1
+            or not (cv.dtype == k_basis.dtype == v_basis.dtype == dt)
+            or v_basis.shape != k_basis.shape or rows != batch * G):
+        return None
+    kb, vb = k_basis.contiguous(), v_basis.contiguous()
+    if (ck.stride(0) % 8 or ck.stride(1) % 8 or ck.data_ptr() % 16 or cv.data_ptr() % 16
+            or kb.data_ptr() % 16 or vb.data_ptr() % 16):
+        return None
+    k = torch.empty((batch, G, S, Dh), dtype=dt, device=ck.device)
+    v = torch.empty_like(k)
+    lib = _lib.load()
+    _lib.check(lib.dkv_recon_kv(_lib.stream_of(ck), _lib.dtype_code(dt), ck.data_ptr(),
+                                cv.data_ptr(), ck.stride(0), ck.stride(1), kb.data_ptr(),
+                                vb.data_ptr(), kb.stride(0), kb.stride(1), k.data_ptr(),
+                                v.data_ptr(), S * Dh, Dh, rows, G, S, R, int(pos0),
+                                math.log(theta)), "dkv_recon_kv")
+    return k, v
+
+
 def reconstruct_kv(cache, layer_idx: int, k_basis: torch.Tensor, v_basis: torch.Tensor, *,
                    batch: int, theta: float, k_rope=None):
     """Dense head-space K (RoPE'd at positions 0..S-1) and V ``(B, G, S, Dh)`` of a per-head
@@ -134,6 +162,10 @@ def reconstruct_kv(cache, layer_idx: int, k_basis: torch.Tensor, v_basis: torch.
     rows, S, _ = dk.shape
     if rows != batch * G:
         raise ValueError(f"cache has {rows} rows, expected batch * G = {batch * G}")
+    if k_rope is None:
+        kv = recon_kv(dk, dv, k_basis, v_basis, batch=batch, theta=theta)
+        if kv is not None:
+            return kv
     k = torch.matmul(dk.view(batch, G, S, R), k_basis.contiguous())
     v = torch.matmul(dv.view(batch, G, S, R), v_basis.contiguous())
     _rotate_k(k, theta, k_rope)
@@ -163,7 +195,11 @@ def coef_prefill_attention(q: torch.Tensor, ck: torch.Tensor, cv: torch.Tensor,
     batch = q.shape[0]
     if rows != batch * G or cv.shape != ck.shape:
         raise ValueError(f"coefficient rows {tuple(ck.shape)}, expected ({batch * G}, S, {R})")
-    k = torch.matmul(ck.view(batch, G, S, R), k_basis.contiguous())
-    v = torch.matmul(cv.view(batch, G, S, R), v_basis.contiguous())
-    _rotate_k(k, theta, k_rope)
+    kv = recon_kv(ck, cv, k_basis, v_basis, batch=batch, theta=theta) if k_rope is None else None
+    if kv is not None:
+        k, v = kv
+    else:
+        k = torch.matmul(ck.view(batch, G, S, R), k_basis.contiguous())
+        v = torch.matmul(cv.view(batch, G, S, R), v_basis.contiguous())
+        _rotate_k(k, theta, k_rope)
     return prefill_attention(q, k, v, causal=True, out_dtype=out_dtype, kstart=kstart)
