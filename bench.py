@@ -27,6 +27,7 @@ against uncompressed cache).
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -160,7 +161,7 @@ class SplitKRunner:
         return self.out
 
 
-def run_gpu(cfg, steps, warmup, dev, layers):
+def run_gpu(cfg, steps, warmup, dev, layers, lib_profile=False):
     """Time ``steps`` decode steps; each step appends K and V to every one of ``layers``
     independent layer caches (a model's decode step runs all its layers) and then runs their
     decode attention back to back (router + attention launch per layer). Several layers keep a
@@ -169,7 +170,11 @@ def run_gpu(cfg, steps, warmup, dev, layers):
 
     Attention GPU time: one pair of HIP events (torch events on the stream the kernels are
     launched on) around each step's ``layers`` attention launches, so the figure is kernel time
-    plus the gaps between back-to-back launches, without an event pair's own cost per launch."""
+    plus the gaps between back-to-back launches, without an event pair's own cost per launch.
+    When a launch takes less GPU time than the host needs to submit the next one (short
+    caches), those gaps are host time. ``lib_profile`` also records the library's own event
+    pair around every launch (``dkv_profile_begin`` / ``dkv_profile_end``, one session per
+    route): ``lib_ms`` maps each route to (GPU ms summed over its launches, launches)."""
     from dynakv_amd import _lib
     from dynakv_amd.kernels.router import KernelPolicy
 
@@ -202,6 +207,23 @@ def run_gpu(cfg, steps, warmup, dev, layers):
             events[1].record()
         return [L for _, L in apps]
 
+    lib = _lib.load()
+    lib_ms = {}
+    cur = [None]  # route of the open library-profiling session
+
+    def lib_session(route):
+        if cur[0] == route:
+            return
+        if cur[0] is not None:
+            split_ms, merge_ms, n = ctypes.c_double(), ctypes.c_double(), ctypes.c_int()
+            _lib.check(lib.dkv_profile_end(ctypes.byref(split_ms), ctypes.byref(merge_ms),
+                                           ctypes.byref(n)), "dkv_profile_end")
+            t, c = lib_ms.get(cur[0], (0.0, 0))
+            lib_ms[cur[0]] = (t + split_ms.value + merge_ms.value, c + n.value)
+        cur[0] = route
+        if route is not None:
+            _lib.check(lib.dkv_profile_begin(steps * layers), "dkv_profile_begin")
+
     for i in range(warmup):
         step(i)
     torch.cuda.synchronize(dev)
@@ -210,10 +232,14 @@ def run_gpu(cfg, steps, warmup, dev, layers):
     t0 = time.perf_counter()
     for j in range(steps):
         ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+        if lib_profile:  # the route of this step's launches, from the length after its append
+            lib_session(policy.select(Ws[0]["cache"].get_seq_length_sp(0) + 1))
         lens.extend(enumerate(step(warmup + j, ev)))
         evs.append(ev)
     torch.cuda.synchronize(dev)
     wall = time.perf_counter() - t0
+    if lib_profile:
+        lib_session(None)
     attn_ms = sum(e0.elapsed_time(e1) for e0, e1 in evs)
     step_bytes = [attention_bytes(cfg, Ws[l]["lk_h"], Ws[l]["lv_h"], L) for l, L in lens]
     tot_bytes = float(sum(step_bytes))
@@ -224,7 +250,7 @@ def run_gpu(cfg, steps, warmup, dev, layers):
     step_len = [lens[j * layers][1] for j in range(steps)]  # layer 0's length at each step
     return dict(
         wall_s=wall, attn_ms=attn_ms, split_ms=attn_ms, merge_ms=0.0, calls=calls,
-        step_ms=step_ms, step_len=step_len,
+        step_ms=step_ms, step_len=step_len, lib_ms=lib_ms,
         merged_in_split=units <= 16384,
         bytes_total=tot_bytes, bytes_per_call=tot_bytes / calls,
         split_bytes_per_call=float(sum(attention_bytes(cfg, Ws[l]["lk_h"], Ws[l]["lv_h"], L,
@@ -280,11 +306,19 @@ def bench_config2(dev, steps=100, warmup=10, layers=4):
     tokens is crossed (fused route below it, two-stage from it on), each step appending to
     ``layers`` independent layer caches and timing their back-to-back attention launches as the
     main workload does. Reports us per layer-step overall and per route, and the algorithmic
-    bytes per launch against HBM peak (a latency-bound launch: 4.4-5.4 MB per call)."""
+    bytes per launch against HBM peak (a latency-bound launch: 4.4-5.4 MB per call).
+
+    A launch here takes less GPU time than the host needs to submit it from Python, so the
+    step's event pair measures the host's pace; the figures are the library's event pairs
+    around each launch (GPU time per launch), with the host-paced figures beside them."""
     cfg = Config2
-    r = run_gpu(cfg, steps, warmup, dev, layers)
+    r = run_gpu(cfg, steps, warmup, dev, layers, lib_profile=True)
     calls = r["calls"]
-    us = r["attn_ms"] * 1e3 / calls
+    lib_ms = r["lib_ms"]
+    lib_total = sum(t for t, _ in lib_ms.values())
+    lib_calls = sum(c for _, c in lib_ms.values())
+    us = lib_total * 1e3 / lib_calls
+    per_route = {k: round(t * 1e3 / c, 3) for k, (t, c) in lib_ms.items() if c}
     fused = [ms for ms, L in zip(r["step_ms"], r["step_len"]) if L < 500]
     two = [ms for ms, L in zip(r["step_ms"], r["step_len"]) if L >= 500]
     per = lambda v: round(sum(v) * 1e3 / (len(v) * layers), 3) if v else None  # noqa: E731
@@ -295,13 +329,18 @@ def bench_config2(dev, steps=100, warmup=10, layers=4):
         "cache_len_start": cfg.S0, "cache_len_end": r["final_len"], "steps": steps,
         "layers_per_step": layers,
         "us_per_layer_step": round(us, 3),
-        "us_per_layer_step_fused_route": per(fused),
-        "us_per_layer_step_two_stage_route": per(two),
+        "us_per_layer_step_fused_route": per_route.get("short_fused"),
+        "us_per_layer_step_two_stage_route": per_route.get("long_two_stage"),
         "bytes_per_launch": round(bpc),
         "achieved_gbs": round(bpc / (us * 1e-6) / 1e9, 2),
         "frac_hbm_peak": round(bpc / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-        "timing": "HIP events around each step's back-to-back attention launches (as the "
-                  "main workload)",
+        "timing": "the library's HIP event pair around each attention launch (dkv_profile_begin"
+                  " / dkv_profile_end): GPU time per launch",
+        "host_paced_us_per_layer_step": round(r["attn_ms"] * 1e3 / calls, 3),
+        "host_paced_us_per_layer_step_fused_route": per(fused),
+        "host_paced_us_per_layer_step_two_stage_route": per(two),
+        "host_paced_timing": "HIP events around each step's back-to-back attention launches "
+                             "(as the main workload); here the host's submission rate",
     }
 
 
