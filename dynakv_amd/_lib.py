@@ -43,8 +43,9 @@ _SIGNATURES = {
     "dkv_av": (_i, [_vp, _i, _i, _i, _i, _vp, _ll, _ll, _ll, _vp, _ll, _ll, _i, _vp, _ll,
                     _vp, _ll, _ll, _vp, _ll, _ll, _vp, _ll, _ll, _i, _i, _i, _i, _i]),
     "dkv_joint_scores": (_i, [_vp, _i, _i, _i, _vp, _ll, _ll, _vp, _ll, _ll, _i, _vp, _ll,
-                              _vp, _ll, _ll, _vp, _ll, _ll, _vp, _i, _vp, _ll, _ll, _ll,
-                              _i, _i, _i, _i, _i]),
+                              _vp, _ll, _ll, _vp, _ll, _ll, _vp, _i, _vp, _ll, _vp, _ll, _ll,
+                              _ll, _i, _i, _i, _i, _i]),
+    "dkv_joint_scores_workspace_ints": (_ll, [_i, _i]),
     "dkv_joint_av_workspace_floats": (_ll, [_i, _i, _i, _i]),
     "dkv_joint_av": (_i, [_vp, _i, _i, _i, _i, _vp, _ll, _ll, _ll, _vp, _ll, _ll, _i, _vp, _ll,
                           _vp, _ll, _ll, _vp, _ll, _ll, _vp, _ll, _vp, _ll, _ll,

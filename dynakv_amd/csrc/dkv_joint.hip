@@ -9,11 +9,13 @@
 // in 32-rank chunks, [chunk][dim][rank], a RoPE table, a workspace for the V pass) and compute
 // the same results to fp32 accuracy:
 //
-// joint_scores_sorted_kernel -- workgroup = (512 tokens, basis head h, batch row b), or with the
-//   heads in pairs (256 tokens, heads 2h and 2h+1, b) so that each coefficient load serves both
-//   heads' products. The workgroup's tokens are sorted by their count of 32-rank chunks
-//   (counting sort in LDS) into blocks of 16; wave w takes sorted blocks w and NBLK-1-w (one
-//   short, one long). K^T = B_h^T . X^T accumulates on 16x16x32 MFMA over the rank chunks of
+// joint_sort_kernel -- workgroup = (window of up to 2048 positions, batch row b): the window's
+//   tokens ordered by their count of 32-rank chunks (a counting sort) into a workspace.
+// joint_scores_sorted_kernel -- workgroup = (512 sorted tokens of a window, basis head h, batch
+//   row b), or with the heads in pairs (256 tokens, heads 2h and 2h+1, b) so that each
+//   coefficient load serves both heads' products; the longest ranges are dispatched first. The
+//   workgroup's tokens form blocks of 16; wave w takes blocks w and NBLK-1-w (one short, one
+//   long). K^T = B_h^T . X^T accumulates on 16x16x32 MFMA over the rank chunks of
 //   32, each block only up to its own longest token's chunk. Each basis chunk ([128 dims][32
 //   ranks], 8 KB contiguous in HBM) is loaded once per workgroup into LDS (four buffers per
 //   head, one barrier per two chunks) and every A operand read from it serves the wave's active
@@ -55,6 +57,11 @@ constexpr int JFLAT_CAP = DKV_FLAT_RSRC_CAP;  // elements one buffer resource co
 constexpr int JMAX_SPLITS = 1024;  // token splits of the V pass
 constexpr float JLOG2E = 1.4426950408889634f;
 constexpr float JRESCALE = 11.5f;        // log2 units: rescale when the running max grows more
+// the scores kernel's tokens are ordered by chunk count within windows of at most JSWIN
+// positions (a multiple of every scores workgroup's token count); the R(16T) rows of a window's
+// tiles fit in LDS
+constexpr int JSWIN = 2048;
+constexpr int JSORT_THREADS = 1024;
 
 // piece swizzle of the basis chunk buffers (a function of d mod 16): the 16-byte slot of ranks
 // 8k..8k+7 of row d is k ^ ((d >> 1) & 3). Measured on MI355X for ds_read_b128 with lane
@@ -84,52 +91,188 @@ struct JScoresParams {
   long long out_sb, out_sh, out_ss;
   int B, S, R, hpg;
   float scale;
+  // per (batch row, window): 3 x win ints, the window's (length, offset, position) triplets in
+  // ascending chunk-count order, pad entries (0, 0, -1) first up to a multiple of the
+  // workgroup's tokens (joint_sort_kernel)
+  const int* sorted;
+  int win, nwin, n_basis;
 };
 
+// Window length for S positions: JSWIN, or S rounded up to 512 when shorter.
+__host__ __device__ inline int joint_window(int S) {
+  return S >= JSWIN ? JSWIN : ((S + 511) / 512) * 512;
+}
+
+// joint_sort_kernel -- workgroup = (window of win positions, batch row): the window's tokens in
+// ascending order of their count of 32-rank chunks (a counting sort: per-wave bucket counts by
+// ballots, bucket starts, scatter; within a bucket by (pass, wave, lane), an order no score
+// depends on), preceded by pad entries up to a multiple of tok, as (length, offset, position)
+// triplets.
+struct JSortParams {
+  const int* lens;
+  long long lens_sb, lens_ss;
+  const int* offs;
+  long long offs_sb, offs_ss;
+  int* sorted;
+  int S, R, win, nwin, tok;
+};
+
+__global__ __launch_bounds__(JSORT_THREADS) void joint_sort_kernel(JSortParams p) {
+  constexpr int NK = JRMAX / JCH + 1;             // chunk-count buckets 0..32
+  constexpr int NW = JSORT_THREADS / 64;          // waves
+  constexpr int IT = JSWIN / JSORT_THREADS;       // tokens per thread
+  static_assert(NK <= 64, "one lane per bucket");
+  // per (pass it, wave w) the wave's token count in each bucket, then its first slot there
+  __shared__ int sW[IT * NW][NK];
+  const int w = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
+  const int wave = tid >> 6;
+  const int base = w * p.win;
+  const int nt = min(p.win, p.S - base);
+  const int npad = (nt + p.tok - 1) / p.tok * p.tok - nt;
+  const int* lr = p.lens + (long long)b * p.lens_sb;
+  const int* orow = p.offs + (long long)b * p.offs_sb;
+  int* out = p.sorted + ((long long)b * p.nwin + w) * 3 * p.win;
+  for (int e = tid; e < IT * NW * NK; e += JSORT_THREADS) (&sW[0][0])[e] = 0;
+  // token i = it * JSORT_THREADS + tid of the window: its length, offset, bucket and its rank
+  // among the wave's lanes of the same bucket (lanes in order)
+  int len[IT], off[IT], bk[IT], rk[IT];
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    const int i = it * JSORT_THREADS + tid;
+    len[it] = 0;
+    off[it] = 0;
+    bk[it] = -1;
+    if (i < nt) {
+      len[it] = min(max(lr[(long long)(base + i) * p.lens_ss], 0), p.R);
+      off[it] = orow[(long long)(base + i) * p.offs_ss];
+      bk[it] = (len[it] + JCH - 1) / JCH;
+    }
+  }
+  __syncthreads();  // sW cleared
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    const int k = bk[it];
+    uint64_t pending = __ballot(k >= 0);
+    rk[it] = 0;
+    while (pending) {  // one step per distinct bucket of the wave
+      const int kk = __shfl(k, __ffsll((unsigned long long)pending) - 1, 64);
+      const uint64_t same = __ballot(k == kk);
+      if (k == kk)
+        rk[it] = __builtin_amdgcn_mbcnt_hi((uint32_t)(same >> 32),
+                                           __builtin_amdgcn_mbcnt_lo((uint32_t)same, 0u));
+      if (lane == 0) sW[it * NW + wave][kk] = __popcll(same);
+      pending &= ~same;
+    }
+  }
+  __syncthreads();
+  // bucket k (thread k): its total, the buckets' starts by a scan over the first wave's lanes
+  // (pad entries first), then the first slot of every (pass, wave) in the bucket
+  if (wave == 0) {
+    int tot = 0;
+    if (lane < NK)
+      for (int j = 0; j < IT * NW; ++j) tot += sW[j][lane];
+    int incl = tot;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int v = __shfl_up(incl, d, 64);
+      if (lane >= d) incl += v;
+    }
+    if (lane < NK) {
+      int run = npad + incl - tot;
+      for (int j = 0; j < IT * NW; ++j) {
+        const int c = sW[j][lane];
+        sW[j][lane] = run;
+        run += c;
+      }
+    }
+  }
+  for (int i = tid; i < npad; i += JSORT_THREADS) {
+    out[i] = 0;
+    out[p.win + i] = 0;
+    out[2 * p.win + i] = -1;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    if (bk[it] >= 0) {
+      const int slot = sW[it * NW + wave][bk[it]] + rk[it];
+      out[slot] = len[it];
+      out[p.win + slot] = off[it];
+      out[2 * p.win + slot] = base + it * JSORT_THREADS + tid;
+    }
+  }
+}
+
 // joint_scores_sorted_kernel: the scores with the rank chunks bounded per 16-token block instead of
-// per workgroup. The workgroup's TOK tokens are sorted by their count of
-// 32-rank chunks (counting sort in LDS), so each block of 16 consecutive sorted tokens needs the
-// chunks up to its own last token's count; a block's products and coefficient loads stop there
-// (in the reference's joint layout a few full-rank tokens sit in almost every 256-token range and
-// made every token take all 32 chunks, ~2.9x the products the tokens' counts need). Wave w takes
-// sorted blocks w and NBLK-1-w (with one basis head: also 16+w and 31-w), one short and one long,
-// so the waves' products per chunk stay balanced. A token's position is arbitrary within its
-// block, so the key takes the whole rotation R(p) = R(16T) R(n) (p = 16T + n), composed per lane
-// from the R(n) table and the workgroup's R(16T) rows in LDS; the query operand is then the
-// same for every token and formed once per head. Scores are stored at the tokens' positions.
+// per workgroup. joint_sort_kernel orders each window of JSWIN positions by the tokens' count of
+// 32-rank chunks, and a workgroup takes TOK consecutive sorted tokens of one window, so each
+// block of 16 of them needs the chunks up to its own last token's count (a block's products and
+// coefficient loads stop there) and the workgroup's basis chunks only up to its last token's:
+// in the reference's joint layout a few full-rank tokens sit in almost every 256-token range of
+// positions, which made a workgroup of consecutive positions stage all 32 basis chunks (~12.9 on
+// average with sorted windows of 2048 at the config-3 shape, 11.8 -> 11.0 products per block).
+// Wave w takes sorted blocks w and NBLK-1-w (with one basis head: also 16+w and 31-w), one short
+// and one long, so the waves' products per chunk stay balanced. A token's position is arbitrary
+// within the window, so the key takes the whole rotation R(p) = R(16T) R(n) (p = 16T + n),
+// composed per lane from the R(n) table and the window's R(16T) rows in LDS; the query operand
+// is then the same for every token and formed once per head. Scores are stored at the tokens'
+// positions.
 template <int DT, int MODE, int ODT, int NHB>
 __global__ __launch_bounds__(JTHREADS, 1) void joint_scores_sorted_kernel(JScoresParams p) {
   constexpr int CB = JCB / NHB;            // 16-token blocks per wave
   constexpr int TOK = JWAVES * CB * 16;    // tokens per workgroup
-  constexpr int NBLK = TOK / 16;           // sorted blocks (and 16-token tiles) per workgroup
-  constexpr int NK = JRMAX / JCH + 1;      // chunk-count buckets 0..32
+  static_assert(JSWIN % TOK == 0 && 512 % TOK == 0, "windows hold whole workgroups");
   __shared__ __attribute__((aligned(16))) dkv_u32x4 sB[4][NHB][JDH * JCH / 8];
   // R(n): [2*pp + k][16*g + n] holds (cos, sin) of frequencies 16pp + 4g + 2k and + 1 at delta n
   __shared__ __attribute__((aligned(16))) dkv_f32x4 sRn[8][64];
-  // R(16T) of the workgroup's tiles: [T - T0][2*pp + k][g], the same frequencies
-  __shared__ __attribute__((aligned(16))) dkv_f32x4 sRT[NBLK][8][4];
+  // R(16T) of the window's tiles: [T - T0][2*pp + k][g], the same frequencies
+  __shared__ __attribute__((aligned(16))) dkv_f32x4 sRT[JSWIN / 16][8][4];
   // the query operand of each head: row r = head r's hi part (r < 8) or head r-8's lo part,
   // dword i = frequency i, 16-byte chunk c stored at chunk position c ^ r
   __shared__ __attribute__((aligned(16))) uint32_t sQ[NHB][16 * 64];
-  __shared__ int sLen[TOK], sOff[TOK], sPos[TOK];  // in sorted order; sPos -1: past S
-  __shared__ int sCnt[NK], sStart[NK];
+  __shared__ int sLen[TOK], sOff[TOK], sPos[TOK];  // in sorted order; sPos -1: a pad entry
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15, g = lane >> 4;
-  const int t0 = blockIdx.x * TOK, h0 = blockIdx.y * NHB, b = blockIdx.z;
-  const int T0 = t0 / 16;
+  // workgroup id -> (range of TOK sorted slots, unit = (batch row, window), head group): the
+  // ranges from the windows' longest tokens down are the slowest index, so the heaviest
+  // workgroups of the whole launch are dispatched first; the head groups of one (range, unit)
+  // are consecutive on one XCD (ids are dispatched to the 8 XCDs round-robin), so their shared
+  // coefficient loads meet in that XCD's L2
+  const int nhg = p.n_basis / NHB, nunits = p.B * p.nwin;
+  int rix, unit, hg;
+  {
+    const int id = blockIdx.x;
+    if ((nunits & 7) == 0) {
+      const int xcd = id & 7, k = id >> 3;
+      hg = k % nhg;
+      const int k2 = k / nhg;
+      unit = (k2 % (nunits >> 3)) * 8 + xcd;
+      rix = k2 / (nunits >> 3);
+    } else {
+      hg = id % nhg;
+      unit = (id / nhg) % nunits;
+      rix = id / nhg / nunits;
+    }
+  }
+  const int b = unit / p.nwin, win = unit % p.nwin;
+  const int rng = p.win / TOK - 1 - rix;
+  const int wbase = win * p.win;  // the window's first position
+  const int wlen = min(p.win, p.S - wbase);
+  const int s0 = rng * TOK;
+  if (s0 >= (wlen + TOK - 1) / TOK * TOK) return;  // past the window's slots (uniform)
+  const int h0 = hg * NHB;
 
   // ---- this thread's token (tid < TOK), the query and table loads, all issued first ----------
-  int tlen0 = 0, toff0 = 0;
-  const int tme = t0 + tid;
-  const bool tvalid = tid < TOK && tme < p.S;
-  if (tvalid) {
-    tlen0 = p.lens[(long long)b * p.lens_sb + (long long)tme * p.lens_ss];
-    toff0 = p.offs[(long long)b * p.offs_sb + (long long)tme * p.offs_ss];
+  int tlen0 = 0, toff0 = 0, tpos0 = -1;
+  if (tid < TOK) {
+    const int* srt = p.sorted + ((long long)b * p.nwin + win) * 3 * p.win + s0 + tid;
+    tlen0 = srt[0];
+    toff0 = srt[p.win];
+    tpos0 = srt[2 * p.win];
   }
   tlen0 = min(max(tlen0, 0), p.R);
-  const int kme = (tlen0 + JCH - 1) / JCH;
   // query: (q_i, q_{i+64}) of head slot hh for frequency i = lane; wave hb of the first NHB
   // forms head h0 + hb's operand
   uint32_t qh[8];
@@ -147,19 +290,23 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_scores_sorted_kernel(JScore
     const float* delt = p.rope + n * 128 + 2 * i0;
     sRn[k][lane] = dkv_f32x4{delt[0], delt[1], delt[2], delt[3]};
   }
-  for (int e = tid; e < NBLK * 32; e += JTHREADS) {
-    const int tl = e >> 5, k = (e >> 2) & 7, gg = e & 3;
-    const int i0 = 16 * (k >> 1) + 4 * gg + 2 * (k & 1);
-    const int T = min(T0 + tl, p.rope_tiles - 1);
-    const float* row = p.rope + (long long)(JROPE_FIXED + T) * 128 + 2 * i0;
-    sRT[tl][k][gg] = dkv_f32x4{row[0], row[1], row[2], row[3]};
+  {
+    const int T0 = wbase / 16, ntl = (wlen + 15) / 16;
+    for (int e = tid; e < ntl * 32; e += JTHREADS) {
+      const int tl = e >> 5, k = (e >> 2) & 7, gg = e & 3;
+      const int i0 = 16 * (k >> 1) + 4 * gg + 2 * (k & 1);
+      const int T = min(T0 + tl, p.rope_tiles - 1);
+      const float* row = p.rope + (long long)(JROPE_FIXED + T) * 128 + 2 * i0;
+      sRT[tl][k][gg] = dkv_f32x4{row[0], row[1], row[2], row[3]};
+    }
   }
-  if (tid < NK) sCnt[tid] = 0;
-  __syncthreads();
-  // ---- counting sort by chunk count: order within a bucket is arbitrary (a token's products
-  //      and rotation do not depend on its place in the block; chunks past its count add zeros)
-  int myrank = 0;
-  if (tid < TOK) myrank = atomicAdd(&sCnt[kme], 1);
+  // the tokens arrive sorted by chunk count (joint_sort_kernel): a token's products and
+  // rotation do not depend on its place in the block, and chunks past its count add zeros
+  if (tid < TOK) {
+    sLen[tid] = tlen0;
+    sOff[tid] = toff0;
+    sPos[tid] = tpos0;
+  }
   if (wave < NHB) {
     // the query operand of head h0 + wave: R(0) (no rotation) times the score scale, bf16 hi + lo
     uint32_t* qw = sQ[wave];
@@ -173,21 +320,6 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_scores_sorted_kernel(JScore
         qw[hh * 64 + 4 * ((lane >> 2) ^ hh) + (lane & 3)] = hi;
         qw[(8 + hh) * 64 + 4 * ((lane >> 2) ^ (8 + hh)) + (lane & 3)] = lo;
       }
-  }
-  __syncthreads();
-  if (tid == 0) {
-    int acc = 0;
-    for (int k = 0; k < NK; ++k) {
-      sStart[k] = acc;
-      acc += sCnt[k];
-    }
-  }
-  __syncthreads();
-  if (tid < TOK) {
-    const int r = sStart[kme] + myrank;
-    sLen[r] = tlen0;
-    sOff[r] = toff0;
-    sPos[r] = tvalid ? tme : -1;
   }
   __syncthreads();
 
@@ -317,7 +449,7 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_scores_sorted_kernel(JScore
     // R(p) = R(16T) R(n) for the lane's token: (cos, sin) of its 16 frequencies
     float rc[16], rsn[16];
     {
-      const int pl = pos_n < 0 ? 0 : pos_n - t0;
+      const int pl = pos_n < 0 ? 0 : pos_n - wbase;
       const int tl = pl >> 4, nn = pl & 15;
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
@@ -837,12 +969,19 @@ bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 
 }  // namespace
 
+extern "C" long long dkv_joint_scores_workspace_ints(int B, int S) {
+  if (B <= 0 || S <= 0) return 0;
+  const long long win = joint_window(S);
+  return (long long)B * ((S + win - 1) / win) * 3 * win;
+}
+
 extern "C" int dkv_joint_scores(void* stream, int mode, int dtype, int out_dtype, const void* q,
                                 long long q_sb, long long q_sh, const void* basis_t,
                                 long long bt_sh, long long bt_sc, int n_basis, const void* flat,
                                 long long flat_ld, const int* lens, long long lens_sb,
                                 long long lens_ss, const int* offs, long long offs_sb,
-                                long long offs_ss, const float* rope, int rope_tiles, void* out,
+                                long long offs_ss, const float* rope, int rope_tiles,
+                                int* workspace, long long workspace_ints, void* out,
                                 long long out_sb, long long out_sh, long long out_ss, int B,
                                 int Hq, int S, int R, int Dh) {
   if (mode != 0 && mode != 1) return DKV_E_ARG;
@@ -859,6 +998,9 @@ extern "C" int dkv_joint_scores(void* stream, int mode, int dtype, int out_dtype
   if (flat_ld <= 0 || flat_ld > JFLAT_CAP - 8) return DKV_E_UNSUPPORTED;
   if (rope_tiles < (S + 15) / 16) return DKV_E_ARG;
   if (B > 65535 || n_basis > 65535) return DKV_E_UNSUPPORTED;
+  if (!workspace || ((uintptr_t)workspace & 3) ||
+      workspace_ints < dkv_joint_scores_workspace_ints(B, S))
+    return DKV_E_ARG;
   JScoresParams p;
   p.q = (const uint16_t*)q;
   p.q_sb = q_sb;
@@ -885,12 +1027,35 @@ extern "C" int dkv_joint_scores(void* stream, int mode, int dtype, int out_dtype
   p.R = R;
   p.hpg = Hq / n_basis;
   p.scale = 1.0f / sqrtf((float)Dh);
+  p.sorted = workspace;
+  p.win = joint_window(S);
+  p.nwin = (S + p.win - 1) / p.win;
   // two basis heads per workgroup when the heads pair up (each coefficient load then serves
   // both heads' products)
   const int nhb = n_basis % 2 == 0 ? 2 : 1;
   const int tok = JTOK / nhb;
-  const dim3 grid((unsigned)((S + tok - 1) / tok), (unsigned)(n_basis / nhb), (unsigned)B);
+  p.n_basis = n_basis;
+  const long long n_wg = (long long)p.nwin * (p.win / tok) * (n_basis / nhb) * B;
+  if (n_wg > 0x7fffffffLL) return DKV_E_UNSUPPORTED;
   hipStream_t st = (hipStream_t)stream;
+  {
+    JSortParams sp;
+    sp.lens = lens;
+    sp.lens_sb = lens_sb;
+    sp.lens_ss = lens_ss;
+    sp.offs = offs;
+    sp.offs_sb = offs_sb;
+    sp.offs_ss = offs_ss;
+    sp.sorted = workspace;
+    sp.S = S;
+    sp.R = R;
+    sp.win = p.win;
+    sp.nwin = p.nwin;
+    sp.tok = tok;
+    hipLaunchKernelGGL(joint_sort_kernel, dim3((unsigned)p.nwin, (unsigned)B), dim3(JSORT_THREADS),
+                       0, st, sp);
+  }
+  const dim3 grid((unsigned)n_wg);
 #define DKV_JS_LAUNCH(DT_, MODE_, ODT_)                                                        \
   do {                                                                                         \
     if (nhb == 2)                                                                              \

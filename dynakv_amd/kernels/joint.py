@@ -41,6 +41,17 @@ def _workspace(device: torch.device, stream: int, floats: int) -> torch.Tensor:
     return t
 
 
+def _sort_workspace(device: torch.device, stream: int, ints: int) -> torch.Tensor:
+    """The scores call's sorted token tables (calls on one stream run in order, so they
+    share one buffer)."""
+    key = ("sort", device.index, stream)
+    t = _WS_CACHE.get(key)
+    if t is None or t.numel() < ints:
+        t = torch.empty(max(int(ints), 1 << 12), dtype=torch.int32, device=device)
+        _WS_CACHE[key] = t
+    return t
+
+
 def _remember(cache: dict, t: torch.Tensor, key, value) -> None:
     """Cache ``value`` for tensor object ``t``; the entry goes when ``t`` is collected. ``value``
     must not refer to ``t`` (no view of it: a view keeps its base alive through ``_base``), or
@@ -138,14 +149,16 @@ def joint_scores(q3: torch.Tensor, k_up: torch.Tensor, k_flat: torch.Tensor,
     st = _lib.stream_of(q3)
     rope, tiles = rope_table(q3.device, st, theta, S)
     out = torch.empty((B, Hq, S), dtype=out_dtype, device=q3.device)
-    rc = _lib.load().dkv_joint_scores(
+    lib = _lib.load()
+    ws = _sort_workspace(q3.device, st, int(lib.dkv_joint_scores_workspace_ints(B, S)))
+    rc = lib.dkv_joint_scores(
         st, mode, _lib.dtype_code(q3.dtype), _lib.dtype_code(out_dtype),
         q3.data_ptr(), q3.stride(0), q3.stride(1),
         bt.data_ptr(), bt.stride(0), bt.stride(1), bt.shape[0],  # head and chunk strides
         k_flat.data_ptr(), k_flat.stride(0),
         lens.data_ptr(), lens.stride(0), lens.stride(1),
         offs.data_ptr(), offs.stride(0), offs.stride(1),
-        rope.data_ptr(), tiles,
+        rope.data_ptr(), tiles, ws.data_ptr(), ws.numel(),
         out.data_ptr(), out.stride(0), out.stride(1), out.stride(2),
         B, Hq, S, k_up.shape[1], Dh)
     _lib.check(rc, "dkv_joint_scores")

@@ -179,6 +179,9 @@ int dkv_av(void* stream, int mode, int scores_dtype, int cache_dtype, int out_dt
  * (n_basis, R/32, Dh, 32), element B_h[32c + k][d] at h*bt_sh + c*bt_sc + d*32 + k (each
  * chunk's 8 KB contiguous), 16-byte aligned, bt_sc >= Dh*32, bt_sh and bt_sc multiples of 8.
  * RoPE: the rope table of dkv_rope_table with rope_tiles >= ceil(S/16).
+ * workspace: dkv_joint_scores_workspace_ints(B, S) int32s, 4-byte aligned (the tokens of each
+ * window of up to 2048 positions ordered by their count of 32-rank chunks, written by the call's
+ * first launch and read by its second; contents need not be initialised).
  * q: (B, Hq, Dh) strides (q_sb, q_sh), unit dim stride; dtype (q and cache) DKV_BF16 or DKV_F16.
  * DKV_E_UNSUPPORTED unless Dh == 128, R % 32 == 0, R <= 1024, Hq / n_basis <= 8,
  * flat_ld <= 0x3fffffe8 (the caller then uses dkv_scores).
@@ -190,8 +193,12 @@ int dkv_joint_scores(void* stream, int mode, int dtype, int out_dtype,
                      const int* lens, long long lens_sb, long long lens_ss,
                      const int* offs, long long offs_sb, long long offs_ss,
                      const float* rope, int rope_tiles,
+                     int* workspace, long long workspace_ints,
                      void* out, long long out_sb, long long out_sh, long long out_ss,
                      int B, int Hq, int S, int R, int Dh);
+
+/* int32 workspace dkv_joint_scores needs for B rows of S tokens (0 when B or S is 0). */
+long long dkv_joint_scores_workspace_ints(int B, int S);
 
 /* fp32 workspace dkv_joint_av needs for these sizes (split records and per rank block partial
  * projections); 0 for sizes dkv_joint_av does not take. */

@@ -123,6 +123,47 @@ def test_scores_match_vector_kernel(dev, dtype, B, S, R, n_basis, repeat, Hq):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("B,S,R,n_basis,Hq", [
+    (1, 2049, 256, 2, 8),    # one token past the first window
+    (2, 2348, 128, 4, 16),   # a partial second window
+    (1, 4097, 64, 2, 8),     # a third window of one token
+    (1, 1100, 1024, 1, 8),   # one basis per workgroup (512-token ranges), a 1536-position window
+])
+def test_scores_across_sort_windows(dev, B, S, R, n_basis, Hq):
+    """The scores kernel takes its tokens ordered by chunk count within windows of up to 2048
+    positions (joint_sort_kernel), pad entries filling each window's last range. Fused-route
+    scores (fp32) against the float64 oracle at window edges: a token given the wrong slot,
+    offset or position is off by O(1). The slack covers the rotation angle: the kernels compose
+    R(16T) R(n) by angle addition from exact table rows, the reference rounds float32(p) *
+    inv_freq once (half a unit in the last place of an angle below S rad, inv_freq <= 1), so
+    each rotated pair moves by at most that angle times its norm."""
+    print(f"[gpu] joint scores across sort windows B={B} S={S} R={R} nb={n_basis}", flush=True)
+    dtype = torch.bfloat16
+    h = _case(B, S, R, n_basis, Hq=Hq, dtype=dtype, seed=3 * S + R, exact_end=True)
+    d = _dev(h, dev, dtype)
+    got = J.joint_scores(d["q"], d["kb"], d["fk"], d["lk"], d["ok"], theta=THETA, mode=1,
+                         out_dtype=torch.float32).double().cpu().numpy()
+    ref = A.scores_two_stage(h["q"], h["fk"], h["kb"], h["lk"], h["ok"], THETA,
+                             out_dtype="float32").astype(np.float64)
+    lk = h["lk"]
+    hpg = Hq // n_basis
+    scale = 1.0 / math.sqrt(128.0)
+    dang = S * 2.0 ** -24 + 2.0 ** -22
+    qn = np.linalg.norm(np.asarray(h["q"], np.float64), axis=-1)  # (B, Hq)
+    for b in range(B):
+        Xk = A.gather_padded(np.asarray(h["fk"][b], np.float64), lk[b], h["ok"][b], R)
+        for hb in range(n_basis):
+            kn = np.linalg.norm(Xk @ np.asarray(h["kb"][hb], np.float64), axis=-1)  # (S,)
+            for hh in range(hb * hpg, (hb + 1) * hpg):
+                live = lk[b] > 0
+                assert np.all(np.isneginf(got[b, hh, ~live]))
+                g, r = got[b, hh, live], ref[b, hh, live]
+                tol = 1e-4 * np.abs(r) + 1e-4 + dang * qn[b, hh] * kn[live] * scale
+                err = np.abs(g - r)
+                assert np.all(err <= tol), (b, hh, float(err.max()), float((err / tol).max()))
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("B,S,R,n_basis,Hq", [
     (2, 1000, 1024, 8, 32), (1, 17, 1024, 32, 32), (3, 1, 256, 4, 32), (2, 300, 1024, 8, 32),
