@@ -122,8 +122,9 @@ __global__ __launch_bounds__(JSORT_THREADS) void joint_sort_kernel(JSortParams p
   constexpr int NW = JSORT_THREADS / 64;          // waves
   constexpr int IT = JSWIN / JSORT_THREADS;       // tokens per thread
   static_assert(NK <= 64, "one lane per bucket");
-  // per (pass it, wave w) the wave's token count in each bucket, then its first slot there
-  __shared__ int sW[IT * NW][NK];
+  // per bucket and (pass it, wave w): the wave's token count in the bucket, then its first slot
+  __shared__ int sW[NK][IT * NW];
+  __shared__ int sTot[NK];
   const int w = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
   const int wave = tid >> 6;
   const int base = w * p.win;
@@ -160,31 +161,35 @@ __global__ __launch_bounds__(JSORT_THREADS) void joint_sort_kernel(JSortParams p
       if (k == kk)
         rk[it] = __builtin_amdgcn_mbcnt_hi((uint32_t)(same >> 32),
                                            __builtin_amdgcn_mbcnt_lo((uint32_t)same, 0u));
-      if (lane == 0) sW[it * NW + wave][kk] = __popcll(same);
+      if (lane == 0) sW[kk][it * NW + wave] = __popcll(same);
       pending &= ~same;
     }
   }
   __syncthreads();
-  // bucket k (thread k): its total, the buckets' starts by a scan over the first wave's lanes
-  // (pad entries first), then the first slot of every (pass, wave) in the bucket
+  // bucket k (wave k % NW, lane j = (pass, wave)): the exclusive scan of its counts over j and
+  // its total; then the buckets' starts (pad entries first) by a scan over the first wave
+  static_assert(IT * NW <= 64, "one lane per (pass, wave)");
+  for (int k = wave; k < NK; k += NW) {
+    const int c = lane < IT * NW ? sW[k][lane] : 0;
+    int incl = c;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int v = __shfl_up(incl, d, 64);
+      if (lane >= d) incl += v;
+    }
+    if (lane < IT * NW) sW[k][lane] = incl - c;
+    if (lane == 63) sTot[k] = incl;
+  }
+  __syncthreads();
   if (wave == 0) {
-    int tot = 0;
-    if (lane < NK)
-      for (int j = 0; j < IT * NW; ++j) tot += sW[j][lane];
+    const int tot = lane < NK ? sTot[lane] : 0;
     int incl = tot;
 #pragma unroll
     for (int d = 1; d < 64; d <<= 1) {
       const int v = __shfl_up(incl, d, 64);
       if (lane >= d) incl += v;
     }
-    if (lane < NK) {
-      int run = npad + incl - tot;
-      for (int j = 0; j < IT * NW; ++j) {
-        const int c = sW[j][lane];
-        sW[j][lane] = run;
-        run += c;
-      }
-    }
+    if (lane < NK) sTot[lane] = npad + incl - tot;  // the bucket's first slot
   }
   for (int i = tid; i < npad; i += JSORT_THREADS) {
     out[i] = 0;
@@ -195,7 +200,7 @@ __global__ __launch_bounds__(JSORT_THREADS) void joint_sort_kernel(JSortParams p
 #pragma unroll
   for (int it = 0; it < IT; ++it) {
     if (bk[it] >= 0) {
-      const int slot = sW[it * NW + wave][bk[it]] + rk[it];
+      const int slot = sTot[bk[it]] + sW[bk[it]][it * NW + wave] + rk[it];
       out[slot] = len[it];
       out[p.win + slot] = off[it];
       out[2 * p.win + slot] = base + it * JSORT_THREADS + tid;
@@ -225,8 +230,11 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_scores_sorted_kernel(JScore
   __shared__ __attribute__((aligned(16))) dkv_u32x4 sB[4][NHB][JDH * JCH / 8];
   // R(n): [2*pp + k][16*g + n] holds (cos, sin) of frequencies 16pp + 4g + 2k and + 1 at delta n
   __shared__ __attribute__((aligned(16))) dkv_f32x4 sRn[8][64];
-  // R(16T) of the window's tiles: [T - T0][2*pp + k][g], the same frequencies
-  __shared__ __attribute__((aligned(16))) dkv_f32x4 sRT[JSWIN / 16][8][4];
+  // R(16T) of the window's tiles: [T - T0][(2*pp + k) * 4 + g], the same frequencies; rows of 33
+  // entries (one of padding), so that lanes reading different tiles' entry (k, g) fall in
+  // different banks (with 32-entry rows every tile's entry sits in the same four banks)
+  constexpr int RT_ROW = 33;
+  __shared__ __attribute__((aligned(16))) dkv_f32x4 sRT[JSWIN / 16][RT_ROW];
   // the query operand of each head: row r = head r's hi part (r < 8) or head r-8's lo part,
   // dword i = frequency i, 16-byte chunk c stored at chunk position c ^ r
   __shared__ __attribute__((aligned(16))) uint32_t sQ[NHB][16 * 64];
@@ -296,8 +304,8 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_scores_sorted_kernel(JScore
       const int tl = e >> 5, k = (e >> 2) & 7, gg = e & 3;
       const int i0 = 16 * (k >> 1) + 4 * gg + 2 * (k & 1);
       const int T = min(T0 + tl, p.rope_tiles - 1);
-      const float* row = p.rope + (long long)(JROPE_FIXED + T) * 128 + 2 * i0;
-      sRT[tl][k][gg] = dkv_f32x4{row[0], row[1], row[2], row[3]};
+      // 16-byte aligned (2 * i0 is a multiple of 4; the host checks the table's alignment)
+      sRT[tl][4 * k + gg] = *(const dkv_f32x4*)(p.rope + (long long)(JROPE_FIXED + T) * 128 + 2 * i0);
     }
   }
   // the tokens arrive sorted by chunk count (joint_sort_kernel): a token's products and
@@ -454,7 +462,7 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_scores_sorted_kernel(JScore
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
         const dkv_f32x4 d = sRn[k][16 * g + nn];
-        const dkv_f32x4 t = sRT[tl][k][g];
+        const dkv_f32x4 t = sRT[tl][4 * k + g];
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
           const float ct = t[2 * e], st = t[2 * e + 1], cn = d[2 * e], sn = d[2 * e + 1];
@@ -998,6 +1006,7 @@ extern "C" int dkv_joint_scores(void* stream, int mode, int dtype, int out_dtype
   if (flat_ld <= 0 || flat_ld > JFLAT_CAP - 8) return DKV_E_UNSUPPORTED;
   if (rope_tiles < (S + 15) / 16) return DKV_E_ARG;
   if (B > 65535 || n_basis > 65535) return DKV_E_UNSUPPORTED;
+  if (!aligned16(rope)) return DKV_E_UNSUPPORTED;
   if (!workspace || ((uintptr_t)workspace & 3) ||
       workspace_ints < dkv_joint_scores_workspace_ints(B, S))
     return DKV_E_ARG;

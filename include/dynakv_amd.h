@@ -178,7 +178,7 @@ int dkv_av(void* stream, int mode, int scores_dtype, int cache_dtype, int out_dt
  * rounding to out_dtype), with the K basis given transposed in 32-rank chunks: basis_t
  * (n_basis, R/32, Dh, 32), element B_h[32c + k][d] at h*bt_sh + c*bt_sc + d*32 + k (each
  * chunk's 8 KB contiguous), 16-byte aligned, bt_sc >= Dh*32, bt_sh and bt_sc multiples of 8.
- * RoPE: the rope table of dkv_rope_table with rope_tiles >= ceil(S/16).
+ * RoPE: the rope table of dkv_rope_table with rope_tiles >= ceil(S/16), 16-byte aligned.
  * workspace: dkv_joint_scores_workspace_ints(B, S) int32s, 4-byte aligned (the tokens of each
  * window of up to 2048 positions ordered by their count of 32-rank chunks, written by the call's
  * first launch and read by its second; contents need not be initialised).
