@@ -55,7 +55,7 @@ _SIGNATURES = {
     "dkv_dense_workspace_floats": (_ll, [_i, _i, _i, _i, _i]),
     "dkv_dense_choose_split": (_i, [_i, _i, _i]),
     "dkv_recon_kv": (_i, [_vp, _i, _vp, _vp, _ll, _ll, _vp, _vp, _ll, _ll, _vp, _vp, _ll, _ll,
-                          _i, _i, _i, _i, _i, _f]),
+                          _i, _i, _i, _i, _i, _vp, _i]),
     "dkv_dense_append": (_i, [_vp, _i, _vp, _ll, _vp, _vp, _ll, _i, _i, _i, _i, _i, _f]),
     "dkv_decode_dense": (_i, [_vp, _i, _vp, _ll, _ll, _vp, _vp, _ll, _i, _vp, _ll, _vp, _ll, _ll,
                               _i, _i, _i, _i, _i, _i]),

@@ -4,8 +4,10 @@
 // the coefficients zero past each token's count, and the keys are rotated before the causal
 // attention, :375-378). One launch reconstructs both: K[t] = R(t) (B_K^T c_K[t]) and
 // V[t] = B_V^T c_V[t] per cache row (b, g), the products on 16x16x32 MFMA with fp32
-// accumulation; the keys rounded to the dtype, rotated in fp32 (dkv_rope_pair's angle and
-// formula) and rounded again, as the reference rounds the projection and then the rotation.
+// accumulation; the keys rounded to the dtype, rotated in fp32 and rounded again, as the
+// reference rounds the projection and then the rotation. The rotation of position p = 16T + n
+// is R(16T) R(n) composed in fp32 from the rows of the RoPE table (dkv_rope_table: cos and sin
+// of the fp32 angles n * inv_freq and 16T * inv_freq), not a sine and cosine per element.
 //
 // Workgroup = (64 tokens, cache row, K | V), four waves of 16 tokens. The row's basis ([rank]
 // [dim], ranks past R zero) is staged in LDS and read transposed (ds_read_b64_tr_b16) as the A
@@ -19,13 +21,14 @@ namespace {
 
 constexpr int DH = 128;
 constexpr int RW = 4;  // waves per workgroup (16 tokens each)
+constexpr int RT_FIXED = 17;  // RoPE table rows before the tile rows R(16T)
 
 template <int DT>
 __global__ __launch_bounds__(RW * 64) void recon_kv_kernel(
     const uint16_t* __restrict__ ck, const uint16_t* __restrict__ cv, long long c_sr,
     long long c_st, const uint16_t* __restrict__ kb, const uint16_t* __restrict__ vb,
     long long b_sg, long long b_sr, uint16_t* __restrict__ ko, uint16_t* __restrict__ vo,
-    long long o_sr, long long o_st, int G, int S, int R, int pos0, float log_theta) {
+    long long o_sr, long long o_st, int G, int S, int R, int pos0, const float* __restrict__ rope) {
   __shared__ __attribute__((aligned(16))) uint16_t sB[DH * DH];  // [rank][dim]
   const bool is_k = blockIdx.z == 0;
   const int row = blockIdx.y, grp = row % G;
@@ -75,20 +78,26 @@ __global__ __launch_bounds__(RW * 64) void recon_kv_kernel(
   if (t >= S) return;
   // lane (n, g): dims 16 blk + 4g + u of token t in acc[blk][u]
   if (is_k) {
-    const float pos = (float)(pos0 + t);
+    const int pos = pos0 + t;
+    // (cos, sin) of frequencies 16 blk + 4g .. +3: 32 contiguous bytes of a table row
+    const float* rn = rope + (pos & 15) * 128 + 8 * g;
+    const float* rt = rope + (RT_FIXED + (pos >> 4)) * 128 + 8 * g;
 #pragma unroll
-    for (int blk = 0; blk < 4; ++blk)
+    for (int blk = 0; blk < 4; ++blk) {
+      const dkv_f32x4 n0 = *(const dkv_f32x4*)(rn + 32 * blk), n1 = *(const dkv_f32x4*)(rn + 32 * blk + 4);
+      const dkv_f32x4 t0 = *(const dkv_f32x4*)(rt + 32 * blk), t1 = *(const dkv_f32x4*)(rt + 32 * blk + 4);
+      const float nc[4] = {n0.x, n0.z, n1.x, n1.z}, ns[4] = {n0.y, n0.w, n1.y, n1.w};
+      const float tc[4] = {t0.x, t0.z, t1.x, t1.z}, ts[4] = {t0.y, t0.w, t1.y, t1.w};
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const int d = 16 * blk + 4 * g + u;
-        const float ang = pos * dkv_inv_freq(d, DH, log_theta);
-        const float cs = cosf(ang), sn = sinf(ang);
+        const float cs = tc[u] * nc[u] - ts[u] * ns[u], sn = ts[u] * nc[u] + tc[u] * ns[u];
         // the projection rounded to the dtype first, then rotated: the reference's two steps
         // (the up-projection's product in the dtype, then apply_rotary_pos_emb_)
         const float a = dkv_round_to<DT>(acc[blk][u]), bb = dkv_round_to<DT>(acc[blk + 4][u]);
         acc[blk][u] = a * cs - bb * sn;
         acc[blk + 4][u] = bb * cs + a * sn;
       }
+    }
   }
   uint16_t* orow = o + (long long)row * o_sr + (long long)t * o_st;
 #pragma unroll
@@ -112,11 +121,13 @@ extern "C" int dkv_recon_kv(void* stream, int dtype, const void* ck, const void*
                             long long c_sr, long long c_st, const void* k_basis,
                             const void* v_basis, long long b_sg, long long b_sr, void* k_out,
                             void* v_out, long long o_sr, long long o_st, int rows, int G, int S,
-                            int R, int pos0, float log_theta) {
+                            int R, int pos0, const float* rope, int rope_tiles) {
   if (dtype != DKV_F16 && dtype != DKV_BF16) return DKV_E_UNSUPPORTED;
   if (rows < 0 || G <= 0 || S < 0 || R <= 0 || pos0 < 0) return DKV_E_ARG;
   if (rows == 0 || S == 0) return DKV_OK;
-  if (!ck || !cv || !k_basis || !v_basis || !k_out || !v_out) return DKV_E_ARG;
+  if (!ck || !cv || !k_basis || !v_basis || !k_out || !v_out || !rope) return DKV_E_ARG;
+  if ((long long)rope_tiles * 16 < (long long)pos0 + S) return DKV_E_ARG;
+  if ((uintptr_t)rope & 15) return DKV_E_UNSUPPORTED;
   if (R > DH || R % 8 != 0 || rows % G != 0) return DKV_E_UNSUPPORTED;
   // 16-byte coefficient pieces and basis rows, 8-byte output pieces
   auto a16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
@@ -131,12 +142,12 @@ extern "C" int dkv_recon_kv(void* stream, int dtype, const void* ck, const void*
     hipLaunchKernelGGL(recon_kv_kernel<DKV_BF16>, grid, dim3(RW * 64), 0, st,
                        (const uint16_t*)ck, (const uint16_t*)cv, c_sr, c_st,
                        (const uint16_t*)k_basis, (const uint16_t*)v_basis, b_sg, b_sr,
-                       (uint16_t*)k_out, (uint16_t*)v_out, o_sr, o_st, G, S, R, pos0, log_theta);
+                       (uint16_t*)k_out, (uint16_t*)v_out, o_sr, o_st, G, S, R, pos0, rope);
   else
     hipLaunchKernelGGL(recon_kv_kernel<DKV_F16>, grid, dim3(RW * 64), 0, st,
                        (const uint16_t*)ck, (const uint16_t*)cv, c_sr, c_st,
                        (const uint16_t*)k_basis, (const uint16_t*)v_basis, b_sg, b_sr,
-                       (uint16_t*)k_out, (uint16_t*)v_out, o_sr, o_st, G, S, R, pos0, log_theta);
+                       (uint16_t*)k_out, (uint16_t*)v_out, o_sr, o_st, G, S, R, pos0, rope);
   DKV_HIP_CHECK_LAUNCH();
   return DKV_OK;
 }

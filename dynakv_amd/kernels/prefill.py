@@ -19,6 +19,7 @@ import math
 import torch
 
 from .. import _lib
+from .decode import rope_table
 
 
 def _extent(t: torch.Tensor) -> int:
@@ -145,11 +146,13 @@ def recon_kv(ck: torch.Tensor, cv: torch.Tensor, k_basis: torch.Tensor, v_basis:
     k = torch.empty((batch, G, S, Dh), dtype=dt, device=ck.device)
     v = torch.empty_like(k)
     lib = _lib.load()
-    _lib.check(lib.dkv_recon_kv(_lib.stream_of(ck), _lib.dtype_code(dt), ck.data_ptr(),
+    st = _lib.stream_of(ck)
+    rope, tiles = rope_table(ck.device, st, theta, int(pos0) + S)
+    _lib.check(lib.dkv_recon_kv(st, _lib.dtype_code(dt), ck.data_ptr(),
                                 cv.data_ptr(), ck.stride(0), ck.stride(1), kb.data_ptr(),
                                 vb.data_ptr(), kb.stride(0), kb.stride(1), k.data_ptr(),
                                 v.data_ptr(), S * Dh, Dh, rows, G, S, R, int(pos0),
-                                math.log(theta)), "dkv_recon_kv")
+                                rope.data_ptr(), tiles), "dkv_recon_kv")
     return k, v
 
 

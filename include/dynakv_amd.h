@@ -416,16 +416,18 @@ int dkv_prefill_attention(void* stream, int dtype, const void* q, long long q_sb
  * Dense K and V of a prompt from masked coefficient rows, for the compressed prefill attention
  * (compressed_attention.py:359-386 with get_origin_states, compressed_cache.py:36-56): per cache
  * row r = b * G + g, K[t] = RoPE_{pos0 + t}(B_K[g]^T ck[r, t]) and V[t] = B_V[g]^T cv[r, t] in one
- * launch (fp32 accumulation and one rounding to the dtype; the keys then rotated as
- * dkv_rope_dense rotates them, in fp32, and rounded again, the reference's two steps).
- * ck / cv: (rows, S, R) element strides (c_sr, c_st, 1), zero past each token's count; bases (G, R, 128) strides (b_sg, b_sr, 1); outputs (rows, S, 128) strides
- * (o_sr, o_st, 1). R <= 128 and a multiple of 8; 16-byte aligned coefficient and basis rows,
- * 8-byte aligned output rows.
+ * launch (fp32 accumulation and one rounding to the dtype; the keys then rotated in fp32 by
+ * R(16T) R(n) for position 16T + n, composed from the rows of the RoPE table rope (dkv_rope_table,
+ * rope_tiles >= ceil((pos0 + S) / 16), 16-byte aligned), and rounded again, the reference's
+ * two steps).
+ * ck / cv: (rows, S, R) element strides (c_sr, c_st, 1), zero past each token's count; bases
+ * (G, R, 128) strides (b_sg, b_sr, 1); outputs (rows, S, 128) strides (o_sr, o_st, 1). R <= 128
+ * and a multiple of 8; 16-byte aligned coefficient and basis rows, 8-byte aligned output rows.
  */
 int dkv_recon_kv(void* stream, int dtype, const void* ck, const void* cv, long long c_sr,
                  long long c_st, const void* k_basis, const void* v_basis, long long b_sg,
                  long long b_sr, void* k_out, void* v_out, long long o_sr, long long o_st,
-                 int rows, int G, int S, int R, int pos0, float log_theta);
+                 int rows, int G, int S, int R, int pos0, const float* rope, int rope_tiles);
 int dkv_rope_apply(void* stream, int dtype, void* x, long long x_sb, long long x_sh,
                    long long x_ss, const void* cos, const void* sin, long long cs_sb,
                    long long cs_ss, int B, int H, int S);
