@@ -662,8 +662,14 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_av_kernel(JAvParams p) {
       load_z(1, zB);
     }
     auto step = [&](int j, dkv_u32x4(&x)[4], uint32_t(&zr)[NHS][4], int& cnt, int& ml, int& mo) {
+      // a tile none of whose tokens reaches this wave's ranks has only zero pieces here: its
+      // products would add exact zeros, so the wave skips them (the online softmax still runs)
+      const bool live = __ballot(cnt > r0) != 0ull;
+      if (live) {
 #pragma unroll
-      for (int c = 0; c < 4; ++c) slot[c * 64 + lane] = dkv_mask8(x[c], cnt - (r0 + 32 * c + 8 * g));
+        for (int c = 0; c < 4; ++c)
+          slot[c * 64 + lane] = dkv_mask8(x[c], cnt - (r0 + 32 * c + 8 * g));
+      }
       float z[NHS][4];
 #pragma unroll
       for (int hs = 0; hs < NHS; ++hs)
@@ -679,7 +685,7 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_av_kernel(JAvParams p) {
 
       // the wave's V operands of the tile: B of P.X^V by transposed reads
       dkv_u32x2 xv[8];
-      {
+      if (live) {
         const int u = n >> 2, q = n & 3;
         const uint8_t* vbase =
             (const uint8_t*)slot + 16 * (16 * (q >> 1) + 4 * g + u) + 8 * (q & 1);
@@ -718,6 +724,7 @@ __global__ __launch_bounds__(JTHREADS, 1) void joint_av_kernel(JAvParams p) {
           pu[u] = __builtin_amdgcn_exp2f(z[hs][u] - m_run[hs]);
           l_run[hs] += pu[u];
         }
+        if (!live) continue;
         // P.X^V in coefficient space (A: P of head slot n, tokens 4g..4g+3; B: the V reads)
         dkv_u32x4 pa;
         if constexpr (DT == DKV_F16) {
