@@ -197,8 +197,11 @@ def run_gpu(cfg, steps, warmup, dev, layers, lib_profile=False):
                  else _lib.DKV_ROUTE_TWO_STAGE)
         runner.run(W["q"][i], fk, fv, lk, ok, lv, ov, W["k_basis"], W["v_basis"], route)
 
+    last = {}
+
     def step(i, events=None):
         apps = [append(W, i) for W in Ws]
+        last["tabs"], last["len"], last["i"] = apps[0][0], apps[0][1], i
         if events is not None:
             events[0].record()
         for W, (tabs, L) in zip(Ws, apps):
@@ -251,6 +254,8 @@ def run_gpu(cfg, steps, warmup, dev, layers, lib_profile=False):
     return dict(
         wall_s=wall, attn_ms=attn_ms, split_ms=attn_ms, merge_ms=0.0, calls=calls,
         step_ms=step_ms, step_len=step_len, lib_ms=lib_ms,
+        runner=runner, last_tabs=last["tabs"], last_len=last["len"],
+        last_q=Ws[0]["q"][last["i"]],
         merged_in_split=units <= 16384,
         bytes_total=tot_bytes, bytes_per_call=tot_bytes / calls,
         split_bytes_per_call=float(sum(attention_bytes(cfg, Ws[l]["lk_h"], Ws[l]["lv_h"], L,
@@ -300,6 +305,36 @@ def bench_dense_same_shape(dev, S=8192, B=16, Hkv=8, hpg=4, layers=4, steps=20):
             "frac_hbm_peak": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
+def graph_us_per_call(fn, dev, n=20, reps=5):
+    """GPU time per call of ``fn`` replayed ``n`` times back to back from a HIP graph (no host
+    work between the launches), the best of ``reps`` replays. ``fn`` launches on torch's
+    current stream; it is warmed up on the capture stream first (its workspaces are per
+    stream)."""
+    s = torch.cuda.Stream(device=dev)
+    s.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            fn()
+    torch.cuda.synchronize(dev)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for _ in range(n):
+            fn()
+    torch.cuda.synchronize(dev)
+    best = float("inf")
+    for _ in range(reps):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(s):
+            e0.record()
+            g.replay()
+            e1.record()
+        torch.cuda.synchronize(dev)
+        best = min(best, e0.elapsed_time(e1) * 1e3 / n)
+    del g
+    return best
+
+
 def bench_config2(dev, steps=100, warmup=10, layers=4):
     """Config 2 as one layer of its 32-layer stack (fp16, B=4, 8 KV groups x rank 128, mean
     retention 0.47): ``steps`` decode steps from 480 tokens on, so the router's switch at 500
@@ -336,12 +371,40 @@ def bench_config2(dev, steps=100, warmup=10, layers=4):
         "frac_hbm_peak": round(bpc / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
         "timing": "the library's HIP event pair around each attention launch (dkv_profile_begin"
                   " / dkv_profile_end): GPU time per launch",
+        "graph_replayed": _config2_graph(dev, cfg, r),
         "host_paced_us_per_layer_step": round(r["attn_ms"] * 1e3 / calls, 3),
         "host_paced_us_per_layer_step_fused_route": per(fused),
         "host_paced_us_per_layer_step_two_stage_route": per(two),
         "host_paced_timing": "HIP events around each step's back-to-back attention launches "
                              "(as the main workload); here the host's submission rate",
     }
+
+
+def _config2_graph(dev, cfg, r):
+    """Config 2 at its final length, 20 launches replayed from a HIP graph: the split kernel
+    on the last step's cache (its route at that length) and the uncompressed baseline's decode
+    kernel (dkv_decode_dense) on a dense cache of the same shape: the floor of a split-and-merge
+    decode launch with no reconstruction."""
+    from dynakv_amd import _lib
+    from dynakv_amd.kernels.decode import dense_decode_attention
+
+    fk, fv, lk, lv, ok, ov = r["last_tabs"]
+    W = r["workload"]
+    q = r["last_q"]
+    S = int(r["last_len"])
+    route = _lib.DKV_ROUTE_FUSED if S < 500 else _lib.DKV_ROUTE_TWO_STAGE
+    runner = r["runner"]
+    comp = graph_us_per_call(
+        lambda: runner.run(q, fk, fv, lk, ok, lv, ov, W["k_basis"], W["v_basis"], route), dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(5)
+    kd = torch.randn((cfg.B * cfg.G, (S + 16) * cfg.Dh), generator=gen, device=dev).to(cfg.dtype)
+    vd = torch.randn((cfg.B * cfg.G, (S + 16) * cfg.Dh), generator=gen, device=dev).to(cfg.dtype)
+    out = torch.empty((cfg.B, cfg.Hq, cfg.Dh), dtype=cfg.dtype, device=dev)
+    dense = graph_us_per_call(lambda: dense_decode_attention(q, kd, vd, S, out=out), dev)
+    return {"cache_len": S, "compressed_us_per_launch": round(comp, 3),
+            "dense_us_per_launch": round(dense, 3),
+            "timing": "20 launches replayed from a HIP graph, best of 5 replays"}
 
 
 def cpu_baseline(cfg, W, cache, budget_s: float):
