@@ -85,6 +85,13 @@ def test_host_only_entry_points():
     assert sl % 64 == 0 and sl == 4160
     assert lib.dkv_splitk_choose_split(1, 8, 8292) % 64 == 0
     assert lib.dkv_splitk_choose_split(1, 8, 10) == 64
+    # up to 256 tokens one split per unit (two tiles per wave at most, merged in LDS), at any
+    # batch; past that several splits again
+    for B in (1, 4, 16):
+        for S in (1, 63, 64, 100, 192, 256):
+            sl = lib.dkv_splitk_choose_split(B, 8, S)
+            assert sl % 64 == 0 and S <= sl < S + 64, (B, S, sl)
+    assert lib.dkv_splitk_choose_split(1, 8, 600) < 600
     assert lib.dkv_rope_table_floats(10) == (17 + 10) * 128
     assert lib.dkv_splitk_workspace_floats(16, 32, 8, 8292, 128, sl) > 0
 
