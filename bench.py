@@ -29,7 +29,6 @@ from __future__ import annotations
 import argparse
 import ctypes
 import json
-import math
 import os
 import platform
 import subprocess

@@ -15,7 +15,7 @@ from dynakv_amd.kernels.prefill import recon_kv
 from dynakv_amd.synthetic import random_orthogonal
 from oracle.attention import apply_rope, rope_cos_sin
 
-from helpers import NP_OF, cast_np
+from helpers import cast_np
 
 CASES = {
     # name: (B, G, S, R, dtype, pos0, strided_rows)
