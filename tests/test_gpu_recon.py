@@ -72,9 +72,10 @@ def test_recon_kv_matches_float64(dev, name):
         vref[r] = cv[r].astype(np.float64) @ vb[g].astype(np.float64)
         p = np.abs(k0[:, :64]) + np.abs(k0[:, 64:])
         pair[r] = np.concatenate([p, p], axis=-1)
-    # the rotation's fp32 slack, as for dkv_rope_dense: the angle float(pos) * inv_freq with
-    # inv_freq from the device's expf (one unit in the last place of fp32 against the oracle's
-    # exp) times |angle| < pos0 + S, and the fp32 products
+    # the rotation's fp32 slack: the kernel composes R(16T) R(n) from the RoPE table's rows
+    # (cos and sin of the fp32 angles 16T * inv_freq and n * inv_freq), where the oracle rounds
+    # float32(pos) * inv_freq once: the angles differ by up to a unit in the last place of fp32
+    # at |angle| < pos0 + S; plus the fp32 products of the composition and the rotation
     slack_k = ((pos0 + S) * 2.0 ** -22 + 2.0 ** -21) * pair
     bad = []
     for got, ref, what in ((k, kref, "K"), (v, vref, "V")):
