@@ -37,6 +37,9 @@ _SIGNATURES = {
                                   _vp, _ll, _vp, _ll, _vp, _ll, _vp, _vp, _ll, _ll, _vp]),
     "dkv_append_prefill": (_i, [_vp, _i, _vp, _ll, _ll, _vp, _ll, _ll, _vp, _ll, _vp, _vp, _ll, _ll,
                                 _vp, _i, _i, _i, _i]),
+    "dkv_append_prefill_kv": (_i, [_vp, _i, _i, _i, _i, _i,
+                                   _vp, _ll, _ll, _vp, _ll, _ll, _vp, _ll, _vp, _vp, _ll, _ll, _vp,
+                                   _vp, _ll, _ll, _vp, _ll, _ll, _vp, _ll, _vp, _vp, _ll, _ll, _vp]),
     "dkv_decompress": (_i, [_vp, _i, _vp, _ll, _vp, _vp, _ll, _ll, _vp, _i, _i, _i]),
     "dkv_scores": (_i, [_vp, _i, _i, _i, _i, _vp, _ll, _ll, _vp, _ll, _ll, _i, _vp, _ll,
                         _vp, _ll, _ll, _vp, _ll, _ll, _vp, _ll, _ll, _ll, _i, _i, _i, _i, _i, _f]),

@@ -75,12 +75,35 @@ __global__ __launch_bounds__(256) void append_decode_kv_kernel(AppendSlot k, App
 // of a group issued before its stores). Offsets follow the unclipped counts, the coefficients
 // are stored at the clipped ones (min(len, max_dim)), as in the one-token append.
 constexpr int AP_CHUNK = 64;
+// one slot (K or V cache of a layer) of a prefill append
+struct PrefillSlot {
+  const void* states;
+  long long states_sb, states_ss;
+  const int* new_len;
+  long long len_sb, len_ss;
+  void* flat;
+  long long flat_ld;
+  int* lens;
+  int* offs;
+  long long tab_sb, tab_ss;
+  int* ptr;
+};
+
 template <typename T>
-__global__ __launch_bounds__(256) void append_prefill_kernel(
-    const T* __restrict__ states, long long states_sb, long long states_ss,
-    const int* __restrict__ new_len, long long len_sb, long long len_ss, T* __restrict__ flat,
-    long long flat_ld, int* __restrict__ lens, int* __restrict__ offs, long long tab_sb,
-    long long tab_ss, const int* __restrict__ ptr, int seq_pos, int n_new, int max_dim) {
+__global__ __launch_bounds__(256) void append_prefill_kernel(PrefillSlot s0, PrefillSlot s1,
+                                                             int seq_pos, int n_new, int max_dim) {
+  // slot blockIdx.z: K, or V in a two-slot launch
+  const PrefillSlot& sl = blockIdx.z ? s1 : s0;
+  const T* __restrict__ states = (const T*)sl.states;
+  const long long states_sb = sl.states_sb, states_ss = sl.states_ss;
+  const int* __restrict__ new_len = sl.new_len;
+  const long long len_sb = sl.len_sb, len_ss = sl.len_ss;
+  T* __restrict__ flat = (T*)sl.flat;
+  const long long flat_ld = sl.flat_ld;
+  int* __restrict__ lens = sl.lens;
+  int* __restrict__ offs = sl.offs;
+  const long long tab_sb = sl.tab_sb, tab_ss = sl.tab_ss;
+  const int* __restrict__ ptr = sl.ptr;
   __shared__ long long s_red[2][4];
   __shared__ long long s_dst[AP_CHUNK];
   __shared__ int s_clen[AP_CHUNK];
@@ -165,11 +188,12 @@ __global__ __launch_bounds__(256) void append_prefill_kernel(
 }
 
 // ptr[row] += sum over the appended tokens of min(len, max_dim)
-__global__ __launch_bounds__(256) void append_prefill_ptr_kernel(const int* __restrict__ new_len,
-                                                                long long len_sb,
-                                                                long long len_ss,
-                                                                int* __restrict__ ptr, int n_new,
-                                                                int max_dim) {
+__global__ __launch_bounds__(256) void append_prefill_ptr_kernel(PrefillSlot s0, PrefillSlot s1,
+                                                                int n_new, int max_dim) {
+  const PrefillSlot& sl = blockIdx.y ? s1 : s0;
+  const int* __restrict__ new_len = sl.new_len;
+  const long long len_sb = sl.len_sb, len_ss = sl.len_ss;
+  int* __restrict__ ptr = sl.ptr;
   __shared__ long long s_red[4];
   const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   long long pc = 0;
@@ -281,6 +305,28 @@ extern "C" int dkv_append_decode_kv(
   return DKV_OK;
 }
 
+static int append_prefill_launch(void* stream, int dtype, const PrefillSlot& k,
+                                 const PrefillSlot& v, int nslots, int seq_pos, int rows,
+                                 int n_new, int max_dim) {
+  const int es = dkv_elt_size(dtype);
+  if (es == 0) return DKV_E_ARG;
+  if ((n_new + AP_CHUNK - 1) / AP_CHUNK > 65535) return DKV_E_UNSUPPORTED;
+  const dim3 grid((unsigned)rows, (unsigned)((n_new + AP_CHUNK - 1) / AP_CHUNK), (unsigned)nslots),
+      block(256);
+  hipStream_t s = (hipStream_t)stream;
+  if (es == 4)
+    hipLaunchKernelGGL(append_prefill_kernel<uint32_t>, grid, block, 0, s, k, v, seq_pos, n_new,
+                       max_dim);
+  else
+    hipLaunchKernelGGL(append_prefill_kernel<uint16_t>, grid, block, 0, s, k, v, seq_pos, n_new,
+                       max_dim);
+  DKV_HIP_CHECK_LAUNCH();
+  hipLaunchKernelGGL(append_prefill_ptr_kernel, dim3((unsigned)rows, (unsigned)nslots), block, 0,
+                     s, k, v, n_new, max_dim);
+  DKV_HIP_CHECK_LAUNCH();
+  return DKV_OK;
+}
+
 extern "C" int dkv_append_prefill(void* stream, int dtype, const void* states,
                                   long long states_sb, long long states_ss, const int* new_len,
                                   long long len_sb, long long len_ss, void* flat,
@@ -290,24 +336,29 @@ extern "C" int dkv_append_prefill(void* stream, int dtype, const void* states,
   if (rows < 0 || n_new < 0 || max_dim < 0 || seq_pos < 0) return DKV_E_ARG;
   if (rows == 0 || n_new == 0) return DKV_OK;
   if (!states || !new_len || !flat || !lens || !offs || !ptr) return DKV_E_ARG;
-  const int es = dkv_elt_size(dtype);
-  if (es == 0) return DKV_E_ARG;
-  if ((n_new + AP_CHUNK - 1) / AP_CHUNK > 65535) return DKV_E_UNSUPPORTED;
-  const dim3 grid((unsigned)rows, (unsigned)((n_new + AP_CHUNK - 1) / AP_CHUNK)), block(256);
-  hipStream_t s = (hipStream_t)stream;
-  if (es == 4)
-    hipLaunchKernelGGL(append_prefill_kernel<uint32_t>, grid, block, 0, s, (const uint32_t*)states,
-                       states_sb, states_ss, new_len, len_sb, len_ss, (uint32_t*)flat, flat_ld,
-                       lens, offs, tab_sb, tab_ss, ptr, seq_pos, n_new, max_dim);
-  else
-    hipLaunchKernelGGL(append_prefill_kernel<uint16_t>, grid, block, 0, s, (const uint16_t*)states,
-                       states_sb, states_ss, new_len, len_sb, len_ss, (uint16_t*)flat, flat_ld,
-                       lens, offs, tab_sb, tab_ss, ptr, seq_pos, n_new, max_dim);
-  DKV_HIP_CHECK_LAUNCH();
-  hipLaunchKernelGGL(append_prefill_ptr_kernel, dim3((unsigned)rows), block, 0, s, new_len, len_sb,
-                     len_ss, ptr, n_new, max_dim);
-  DKV_HIP_CHECK_LAUNCH();
-  return DKV_OK;
+  const PrefillSlot k{states, states_sb, states_ss, new_len, len_sb, len_ss,
+                      flat,   flat_ld,   lens,      offs,    tab_sb, tab_ss, ptr};
+  return append_prefill_launch(stream, dtype, k, k, 1, seq_pos, rows, n_new, max_dim);
+}
+
+extern "C" int dkv_append_prefill_kv(
+    void* stream, int dtype, int seq_pos, int rows, int n_new, int max_dim, const void* states_k,
+    long long states_k_sb, long long states_k_ss, const int* new_len_k, long long len_k_sb,
+    long long len_k_ss, void* flat_k, long long flat_k_ld, int* lens_k, int* offs_k,
+    long long tab_k_sb, long long tab_k_ss, int* ptr_k, const void* states_v,
+    long long states_v_sb, long long states_v_ss, const int* new_len_v, long long len_v_sb,
+    long long len_v_ss, void* flat_v, long long flat_v_ld, int* lens_v, int* offs_v,
+    long long tab_v_sb, long long tab_v_ss, int* ptr_v) {
+  if (rows < 0 || n_new < 0 || max_dim < 0 || seq_pos < 0) return DKV_E_ARG;
+  if (rows == 0 || n_new == 0) return DKV_OK;
+  if (!states_k || !new_len_k || !flat_k || !lens_k || !offs_k || !ptr_k || !states_v ||
+      !new_len_v || !flat_v || !lens_v || !offs_v || !ptr_v)
+    return DKV_E_ARG;
+  const PrefillSlot k{states_k, states_k_sb, states_k_ss, new_len_k, len_k_sb, len_k_ss,
+                      flat_k,   flat_k_ld,   lens_k,      offs_k,    tab_k_sb, tab_k_ss, ptr_k};
+  const PrefillSlot v{states_v, states_v_sb, states_v_ss, new_len_v, len_v_sb, len_v_ss,
+                      flat_v,   flat_v_ld,   lens_v,      offs_v,    tab_v_sb, tab_v_ss, ptr_v};
+  return append_prefill_launch(stream, dtype, k, v, 2, seq_pos, rows, n_new, max_dim);
 }
 
 extern "C" int dkv_decompress(void* stream, int dtype, const void* flat, long long flat_ld,

@@ -167,6 +167,37 @@ class CustomDynamicCache(_CacheBase):
         if is_decode:
             cache[5] = [p + added for p in cache[5]]
 
+    def _launch_prefill_pair(self, ck, ks, kl, ub_k, cv, vs, vl, ub_v, max_dim):
+        """The prefill appends of a layer's K and V slots: one ``dkv_append_prefill_kv`` launch
+        when both slots stand at the same length with the same rows, tokens and dtype, else one
+        ``dkv_append_prefill`` per slot (the same results)."""
+        if (ck[4] != cv[4] or ck[0].dtype != cv[0].dtype or tuple(kl.shape) != tuple(vl.shape)
+                or tuple(ks.shape) != tuple(vs.shape)):
+            self._launch_prefill(ck, ks, kl, max_dim, ub=ub_k)
+            self._launch_prefill(cv, vs, vl, max_dim, ub=ub_v)
+            return
+        fk, lk, okk, pk, seq, _ = ck
+        fv, lv, ov, pv, _, _ = cv
+        sk = ks if ks.stride(-1) == 1 else ks.contiguous()
+        sv = vs if vs.stride(-1) == 1 else vs.contiguous()
+        nk, nv = kl.to(torch.int32), vl.to(torch.int32)
+        B, new_s = kl.shape
+        rc = _lib.load().dkv_append_prefill_kv(
+            _lib.stream_of(fk), _lib.dtype_code(fk.dtype), seq, B, new_s, max_dim,
+            sk.data_ptr(), sk.stride(0), sk.stride(1), nk.data_ptr(), nk.stride(0), nk.stride(1),
+            fk.data_ptr(), fk.stride(0), lk.data_ptr(), okk.data_ptr(), lk.stride(0),
+            lk.stride(1), pk.data_ptr(),
+            sv.data_ptr(), sv.stride(0), sv.stride(1), nv.data_ptr(), nv.stride(0), nv.stride(1),
+            fv.data_ptr(), fv.stride(0), lv.data_ptr(), ov.data_ptr(), lv.stride(0),
+            lv.stride(1), pv.data_ptr())
+        _lib.check(rc, "dkv_append_prefill_kv")
+        for cache, ub in ((ck, ub_k), (cv, ub_v)):
+            if ub is not None:
+                cache[5] = [int(v) for v in ub]
+            else:
+                cache[5] = cache[3].cpu().tolist()
+                self.device_syncs += 1
+
     def _launch_prefill(self, cache, new_states, new_len, max_dim, ub=None):
         """``ub``: the rows' pointers after the append when the caller knows them (a slot
         that started empty); otherwise they are read back from the device."""
@@ -240,6 +271,7 @@ class CustomDynamicCache(_CacheBase):
         half = sum(rows)
         created = self._create_fresh_slots(items, lens, host, starts)
         for n, (layer_idx, ks, kl, vs, vl) in enumerate(items):
+            prepared = []
             for j, (cache_list, st, ln) in enumerate(((self.key_cache_sp, ks, kl),
                                                       (self.value_cache_sp, vs, vl))):
                 k = 2 * n + j
@@ -249,8 +281,11 @@ class CustomDynamicCache(_CacheBase):
                                                       or cache_list[layer_idx] is None)
                 cache, added = self._prepare_slot(cache_list, layer_idx, st, ln, max_dim, False,
                                                   row_max=max(su))
-                self._launch_prefill(cache, st, ln, max_dim, ub=sc if fresh else None)
-                self._finish_slot(cache, ln.shape[1], added, False)
+                prepared.append((cache, st, ln, added, sc if fresh else None))
+            (ck, kst, kln, kadd, kub), (cv, vst, vln, vadd, vub) = prepared
+            self._launch_prefill_pair(ck, kst, kln, kub, cv, vst, vln, vub, max_dim)
+            self._finish_slot(ck, kln.shape[1], kadd, False)
+            self._finish_slot(cv, vln.shape[1], vadd, False)
 
     def _create_fresh_slots(self, items, lens, host, starts):
         """The slots of ``items`` that do not exist yet, created as ``_prepare_slot`` creates

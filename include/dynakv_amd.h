@@ -122,6 +122,22 @@ int dkv_append_prefill(void* stream, int dtype,
                        int* ptr, int seq_pos, int rows, int n_new, int max_dim);
 
 /*
+ * dkv_append_prefill for a layer's K and V slots in one launch (plus one pointer launch): the
+ * prefill appends of update_sp (reference src/dynakv/kernels/compressed_cache.py:219-227 with
+ * :182-209 per slot), both slots at the same seq_pos with the same rows and n_new. Each slot's
+ * arguments mean what dkv_append_prefill's do; the results equal two dkv_append_prefill calls.
+ */
+int dkv_append_prefill_kv(void* stream, int dtype, int seq_pos, int rows, int n_new, int max_dim,
+                          const void* states_k, long long states_k_sb, long long states_k_ss,
+                          const int* new_len_k, long long len_k_sb, long long len_k_ss,
+                          void* flat_k, long long flat_k_ld, int* lens_k, int* offs_k,
+                          long long tab_k_sb, long long tab_k_ss, int* ptr_k,
+                          const void* states_v, long long states_v_sb, long long states_v_ss,
+                          const int* new_len_v, long long len_v_sb, long long len_v_ss,
+                          void* flat_v, long long flat_v_ld, int* lens_v, int* offs_v,
+                          long long tab_v_sb, long long tab_v_ss, int* ptr_v);
+
+/*
  * Dense re-expansion of a packed slot: out[b, t, j] = flat[b, offs[b,t] + j] for
  * j < min(lens[b,t], max_dim), else 0. out is (rows, seq, max_dim) contiguous, cache dtype.
  * Replaces simple_decompress (reference src/dynakv/kernels/compressed_cache.py:36-56),

@@ -159,3 +159,17 @@ def test_bulk_prefill_append_equals_per_layer(dev, dtype):
             for c in (a, b):
                 c.update_sp(ks, lk, vs, lv, R, i, R)
         same(f"decode {step}")
+    # a second prompt onto the slots that now hold tokens: the appends start at each row's
+    # pointer (K and V slots in one launch on the bulk path, one launch per slot on the other)
+    items2 = []
+    for i in range(layers):
+        S2 = 70
+        lk = torch.randint(0, R + 1, (B * G, S2), generator=g, dtype=torch.int32)
+        lv = torch.randint(0, R + 1, (B * G, S2), generator=g, dtype=torch.int32)
+        ks = torch.randn(B * G, S2, R, generator=g) * (torch.arange(R) < lk[..., None])
+        vs = torch.randn(B * G, S2, R, generator=g) * (torch.arange(R) < lv[..., None])
+        items2.append((i, ks.to(dtype).to(dev), lk.to(dev), vs.to(dtype).to(dev), lv.to(dev)))
+    for i, ks, lk, vs, lv in items2:
+        a.update_sp(ks, lk, vs, lv, R, i, R)
+    b.update_sp_prefill_many(items2, R)
+    same("second prompt")
