@@ -160,7 +160,7 @@ class SplitKRunner:
         return self.out
 
 
-def run_gpu(cfg, steps, warmup, dev, layers, lib_profile=False):
+def run_gpu(cfg, steps, warmup, dev, layers, lib_profile=False, prewarm_s=0.0):
     """Time ``steps`` decode steps; each step appends K and V to every one of ``layers``
     independent layer caches (a model's decode step runs all its layers) and then runs their
     decode attention back to back (router + attention launch per layer). Several layers keep a
@@ -173,7 +173,12 @@ def run_gpu(cfg, steps, warmup, dev, layers, lib_profile=False):
     When a launch takes less GPU time than the host needs to submit the next one (short
     caches), those gaps are host time. ``lib_profile`` also records the library's own event
     pair around every launch (``dkv_profile_begin`` / ``dkv_profile_end``, one session per
-    route): ``lib_ms`` maps each route to (GPU ms summed over its launches, launches)."""
+    route): ``lib_ms`` maps each route to (GPU ms summed over its launches, launches).
+
+    ``prewarm_s``: after the first warmup step, its attention launches are repeated (untimed, on
+    the caches as that step left them, no appends) for that many seconds of wall time, so that
+    the timed steps run at the GPU's sustained clocks: from idle the same launches take ~20%
+    longer over the first ~100 ms of load."""
     from dynakv_amd import _lib
     from dynakv_amd.kernels.router import KernelPolicy
 
@@ -200,7 +205,7 @@ def run_gpu(cfg, steps, warmup, dev, layers, lib_profile=False):
 
     def step(i, events=None):
         apps = [append(W, i) for W in Ws]
-        last["tabs"], last["len"], last["i"] = apps[0][0], apps[0][1], i
+        last["tabs"], last["len"], last["i"], last["apps"] = apps[0][0], apps[0][1], i, apps
         if events is not None:
             events[0].record()
         for W, (tabs, L) in zip(Ws, apps):
@@ -226,8 +231,18 @@ def run_gpu(cfg, steps, warmup, dev, layers, lib_profile=False):
         if route is not None:
             _lib.check(lib.dkv_profile_begin(steps * layers), "dkv_profile_begin")
 
+    prewarm_calls = 0
     for i in range(warmup):
         step(i)
+        if i == 0 and prewarm_s > 0:
+            torch.cuda.synchronize(dev)
+            t_end = time.perf_counter() + prewarm_s
+            while time.perf_counter() < t_end:
+                for W, (tabs, L) in zip(Ws, last["apps"]):
+                    attend(W, i, tabs, L)
+                prewarm_calls += layers
+                if prewarm_calls % (8 * layers) == 0:  # keep the host a few launches ahead
+                    torch.cuda.synchronize(dev)
     torch.cuda.synchronize(dev)
     _log("timed region")
     lens, evs = [], []
@@ -252,6 +267,7 @@ def run_gpu(cfg, steps, warmup, dev, layers, lib_profile=False):
     step_len = [lens[j * layers][1] for j in range(steps)]  # layer 0's length at each step
     return dict(
         wall_s=wall, attn_ms=attn_ms, split_ms=attn_ms, merge_ms=0.0, calls=calls,
+        prewarm_calls=prewarm_calls,
         step_ms=step_ms, step_len=step_len, lib_ms=lib_ms,
         runner=runner, last_tabs=last["tabs"], last_len=last["len"],
         last_q=Ws[0]["q"][last["i"]],
@@ -265,12 +281,13 @@ def run_gpu(cfg, steps, warmup, dev, layers, lib_profile=False):
     )
 
 
-def bench_dense_same_shape(dev, S=8192, B=16, Hkv=8, hpg=4, layers=4, steps=20):
+def bench_dense_same_shape(dev, S=8192, B=16, Hkv=8, hpg=4, layers=4, steps=20, prewarm_s=0.0):
     """The uncompressed baseline's decode attention (``dkv_decode_dense``) at the main workload's
     shape: every token's rotated key and value at 128 dims (the reference's original model,
     ``scripts/benchmark_throughput.py``), ``layers`` caches cycled so that none stays in the
     last-level cache, their launches timed back to back with one event pair per step as the
-    compressed workload is. Bytes: K and V of every token, q and the output."""
+    compressed workload is (after the same untimed ``prewarm_s`` of repeated launches). Bytes:
+    K and V of every token, q and the output."""
     from dynakv_amd.kernels.decode import dense_decode_attention
 
     g = torch.Generator(device=dev)
@@ -284,6 +301,14 @@ def bench_dense_same_shape(dev, S=8192, B=16, Hkv=8, hpg=4, layers=4, steps=20):
     for _ in range(2):
         for k, v in caches:
             dense_decode_attention(q, k, v, S, out=out)
+    torch.cuda.synchronize(dev)
+    t_end, n = time.perf_counter() + prewarm_s, 0
+    while time.perf_counter() < t_end:
+        for k, v in caches:
+            dense_decode_attention(q, k, v, S, out=out)
+        n += 1
+        if n % 8 == 0:
+            torch.cuda.synchronize(dev)
     torch.cuda.synchronize(dev)
     evs = []
     for _ in range(steps):
@@ -334,7 +359,7 @@ def graph_us_per_call(fn, dev, n=20, reps=5):
     return best
 
 
-def bench_config2(dev, steps=100, warmup=10, layers=4):
+def bench_config2(dev, steps=100, warmup=10, layers=4, prewarm_s=0.0):
     """Config 2 as one layer of its 32-layer stack (fp16, B=4, 8 KV groups x rank 128, mean
     retention 0.47): ``steps`` decode steps from 480 tokens on, so the router's switch at 500
     tokens is crossed (fused route below it, two-stage from it on), each step appending to
@@ -346,7 +371,7 @@ def bench_config2(dev, steps=100, warmup=10, layers=4):
     step's event pair measures the host's pace; the figures are the library's event pairs
     around each launch (GPU time per launch), with the host-paced figures beside them."""
     cfg = Config2
-    r = run_gpu(cfg, steps, warmup, dev, layers, lib_profile=True)
+    r = run_gpu(cfg, steps, warmup, dev, layers, lib_profile=True, prewarm_s=prewarm_s)
     calls = r["calls"]
     lib_ms = r["lib_ms"]
     lib_total = sum(t for t, _ in lib_ms.values())
@@ -769,6 +794,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--prewarm-seconds", type=float, default=0.5,
+                    help="untimed repeats of the first warmup step's attention launches (wall "
+                         "seconds) so the timed steps run at sustained GPU clocks; 0 = none")
     ap.add_argument("--workload", default="config3", choices=["config3", "config2"])
     ap.add_argument("--layers", type=int, default=4,
                     help="independent layer caches per decode step (4 x ~190 MB at config 3)")
@@ -825,7 +853,7 @@ def main():
         torch.cuda.synchronize(dev)
         _log(f"copy probe: {args.copy_probe_mib} MiB read + {args.copy_probe_mib} MiB written")
         del src, dst
-    r = run_gpu(cfg, args.steps, args.warmup, dev, args.layers)
+    r = run_gpu(cfg, args.steps, args.warmup, dev, args.layers, prewarm_s=args.prewarm_seconds)
     attn_s = r["attn_ms"] / 1e3
     gbs = r["bytes_total"] / attn_s / 1e9
     calls = r["calls"]
@@ -865,6 +893,10 @@ def main():
         },
         "pct_hbm_peak": round(100.0 * gbs / HBM_PEAK_GBS, 2),
         "layers_per_step": args.layers,
+        # untimed: the first warmup step's attention launches repeated before the other warmup
+        # steps (from idle the same launches run ~20% slower over the first ~100 ms of load)
+        "prewarm_s": args.prewarm_seconds,
+        "prewarm_launches": r["prewarm_calls"],
         "decode_attn_us_per_layer_step": round(layer_step_s * 1e6, 3),
         # a Llama-3-8B decode step runs 32 such layers: attention-only tokens/s of that stack
         "decode_tokens_per_s_attention_only_32_layers": round(cfg.B / (32 * layer_step_s), 1),
@@ -887,11 +919,12 @@ def main():
     }
     if not args.no_dense and cfg.name == "config3":
         _log("dense baseline attention at the same shape")
-        line["dense_same_shape"] = bench_dense_same_shape(dev, S=r["final_len"])
+        line["dense_same_shape"] = bench_dense_same_shape(dev, S=r["final_len"],
+                                                          prewarm_s=args.prewarm_seconds)
         line["dense_same_shape"]["compressed_split_kernel_us"] = line["roofline"]["split_kernel_us"]
     if not args.no_config2 and cfg.name == "config3":
         _log("config 2 (one layer, 480 -> 580 tokens)")
-        line["config2"] = bench_config2(dev)
+        line["config2"] = bench_config2(dev, prewarm_s=args.prewarm_seconds)
     if not args.no_cutoff:
         _log("cutoff head")
         line["cutoff_head"] = bench_cutoff(cfg, dev)
