@@ -197,6 +197,19 @@ def flat_operand(t: torch.Tensor) -> torch.Tensor:
     return t.clone(memory_format=torch.contiguous_format)
 
 
+# Cached device buffers (workspaces, RoPE tables) replaced by larger ones. They stay allocated
+# for the rest of the process instead of going back to torch's allocator: a HIP graph captured
+# while one of them was current holds its address and writes into it on every replay. Caches
+# grow at least twofold, so these add at most the size of the buffers in use.
+_RETIRED_BUFFERS: list = []
+
+
+def retire(t: torch.Tensor | None) -> None:
+    """Keep a superseded cached device buffer allocated (see ``_RETIRED_BUFFERS``)."""
+    if t is not None:
+        _RETIRED_BUFFERS.append(t)
+
+
 def stream_of(t: torch.Tensor) -> int:
     """Raw hipStream_t of torch's current stream on t's device."""
     if t.device.type != "cuda":

@@ -30,10 +30,15 @@ _WS_CACHE: dict = {}  # (device, stream) -> uint8 workspace
 
 
 def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
+    """Scratch of the two-step cutoff (cached per device and stream, grown at least twofold; a
+    replaced buffer stays allocated, ``_lib.retire``)."""
     key = (device.index, stream)
     t = _WS_CACHE.get(key)
     if t is None or t.numel() < nbytes:
-        t = torch.empty(max(int(nbytes), 1 << 16), dtype=torch.uint8, device=device)
+        old = t
+        grow = 2 * old.numel() if old is not None else 0
+        t = torch.empty(max(int(nbytes), grow, 1 << 16), dtype=torch.uint8, device=device)
+        _lib.retire(old)
         _WS_CACHE[key] = t
     return t
 

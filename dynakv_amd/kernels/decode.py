@@ -29,7 +29,7 @@ _WS_CACHE: dict = {}    # (device, stream) -> zeroed fp32 workspace
 
 def rope_table(device: torch.device, stream: int, theta: float, seq_len: int):
     """RoPE table with at least ceil(seq_len / 16) tile rows for ``theta`` (cached, grown by
-    doubling)."""
+    doubling; a replaced table stays allocated, ``_lib.retire``)."""
     lib = _lib.load()
     need = max(1, (seq_len + 15) // 16)
     key = (device.index, stream, float(theta))
@@ -40,6 +40,8 @@ def rope_table(device: torch.device, stream: int, theta: float, seq_len: int):
                         device=device)
         _lib.check(lib.dkv_rope_table(stream, t.data_ptr(), 0, tiles, math.log(theta)),
                    "dkv_rope_table")
+        if ent is not None:
+            _lib.retire(ent[0])
         ent = (t, tiles)
         _ROPE_CACHE[key] = ent
     return ent
@@ -48,11 +50,15 @@ def rope_table(device: torch.device, stream: int, theta: float, seq_len: int):
 def workspace(device: torch.device, stream: int, floats: int) -> torch.Tensor:
     """Split-K workspace of at least ``floats`` floats (cached per device and stream). It is
     zero-filled when allocated: its leading merge counters must start at zero, and every call
-    leaves them zero."""
+    leaves them zero. It grows at least twofold; a replaced workspace stays allocated
+    (``_lib.retire``: graphs captured with it keep using it)."""
     key = (device.index, stream)
     t = _WS_CACHE.get(key)
     if t is None or t.numel() < floats:
-        t = torch.zeros(max(int(floats), 1 << 16), dtype=torch.float32, device=device)
+        old = t
+        grow = 2 * old.numel() if old is not None else 0
+        t = torch.zeros(max(int(floats), grow, 1 << 16), dtype=torch.float32, device=device)
+        _lib.retire(old)
         _WS_CACHE[key] = t
     return t
 

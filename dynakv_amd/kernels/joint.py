@@ -32,22 +32,29 @@ _WS_CACHE: dict = {}
 
 def _workspace(device: torch.device, stream: int, floats: int) -> torch.Tensor:
     """Record workspace of the V pass (its own buffer: the split kernel's workspace keeps
-    arrival counters in its first words)."""
+    arrival counters in its first words). Grown at least twofold; a replaced buffer stays
+    allocated (``_lib.retire``)."""
     key = (device.index, stream)
     t = _WS_CACHE.get(key)
     if t is None or t.numel() < floats:
-        t = torch.empty(max(int(floats), 1 << 16), dtype=torch.float32, device=device)
+        old = t
+        grow = 2 * old.numel() if old is not None else 0
+        t = torch.empty(max(int(floats), grow, 1 << 16), dtype=torch.float32, device=device)
+        _lib.retire(old)
         _WS_CACHE[key] = t
     return t
 
 
 def _sort_workspace(device: torch.device, stream: int, ints: int) -> torch.Tensor:
     """The scores call's sorted token tables (calls on one stream run in order, so they
-    share one buffer)."""
+    share one buffer). Grown at least twofold; a replaced buffer stays allocated."""
     key = ("sort", device.index, stream)
     t = _WS_CACHE.get(key)
     if t is None or t.numel() < ints:
-        t = torch.empty(max(int(ints), 1 << 12), dtype=torch.int32, device=device)
+        old = t
+        grow = 2 * old.numel() if old is not None else 0
+        t = torch.empty(max(int(ints), grow, 1 << 12), dtype=torch.int32, device=device)
+        _lib.retire(old)
         _WS_CACHE[key] = t
     return t
 
