@@ -723,17 +723,18 @@ def bench_e2e(dev, batches=(1, 2, 4), prompt_len=2048, new_tokens=100, models="a
     with prefill, as the reference's benchmark_throughput.py:73 counts it; decode-only tokens/s
     beside it. A third run keeps the dense cache but decodes through torch's fused
     ``scaled_dot_product_attention``, the attention of the reference's transformers baseline.
-    All run eagerly (one launch per op, no graph capture). ``models``: "all", "compressed",
-    "dense" or "sdpa" (one model alone, for a kernel trace of it)."""
+    All run eagerly (one launch per op, no graph capture). ``models``: "all", or a comma list
+    of "compressed", "dense" and "sdpa" (one model alone, for a kernel trace of it)."""
     from dynakv_amd.model import CompressedLlama, DenseLlama, LlamaShape, RandomLlama
 
+    want = {"compressed", "dense", "sdpa"} if models == "all" else set(models.split(","))
     shape = LlamaShape()
     model = RandomLlama(shape, device=dev, seed=5)
-    comp = CompressedLlama(model) if models in ("all", "compressed") else None
+    comp = CompressedLlama(model) if "compressed" in want else None
     dense = (DenseLlama(model, max_len=prompt_len + new_tokens + 8)
-             if models in ("all", "dense") else None)
+             if "dense" in want else None)
     sdpa = (DenseLlama(model, max_len=prompt_len + new_tokens + 8, attention="sdpa")
-            if models in ("all", "sdpa") else None)
+            if "sdpa" in want else None)
     g = torch.Generator(device="cpu").manual_seed(11)
     res = {"model": "random-init Llama-3-8B shape (32 layers, 4096 hidden, 32/8 heads, FFN "
                     "14336, vocab 128256), bf16", "prompt_len": prompt_len,
@@ -743,8 +744,12 @@ def bench_e2e(dev, batches=(1, 2, 4), prompt_len=2048, new_tokens=100, models="a
     for m in (comp, dense, sdpa):
         if m is not None:
             m.generate(warm, 4)
-    empty = {"tokens_per_s": 0.0, "decode_tokens_per_s": 0.0, "prefill_s": 0.0, "kv_bytes": 0,
-             "tokens": None}
+    # a model left out of this run reports null
+    empty = {"tokens_per_s": None, "decode_tokens_per_s": None, "prefill_s": None,
+             "kv_bytes": None, "tokens": None}
+
+    def rnd(v, n):
+        return None if v is None else round(v, n)
     for B in batches:
         prompt = torch.randint(0, shape.vocab, (B, prompt_len), generator=g).to(dev)
         rc = comp.generate(prompt, new_tokens) if comp is not None else empty
@@ -754,14 +759,14 @@ def bench_e2e(dev, batches=(1, 2, 4), prompt_len=2048, new_tokens=100, models="a
                 if comp is not None else [])
         res["runs"].append({
             "batch": B,
-            "compressed_tokens_per_s": round(rc["tokens_per_s"], 1),
-            "dense_tokens_per_s": round(rd["tokens_per_s"], 1),
-            "compressed_decode_tokens_per_s": round(rc["decode_tokens_per_s"], 1),
-            "dense_decode_tokens_per_s": round(rd["decode_tokens_per_s"], 1),
-            "dense_sdpa_tokens_per_s": round(rs["tokens_per_s"], 1),
-            "dense_sdpa_decode_tokens_per_s": round(rs["decode_tokens_per_s"], 1),
-            "compressed_prefill_s": round(rc["prefill_s"], 4),
-            "dense_prefill_s": round(rd["prefill_s"], 4),
+            "compressed_tokens_per_s": rnd(rc["tokens_per_s"], 1),
+            "dense_tokens_per_s": rnd(rd["tokens_per_s"], 1),
+            "compressed_decode_tokens_per_s": rnd(rc["decode_tokens_per_s"], 1),
+            "dense_decode_tokens_per_s": rnd(rd["decode_tokens_per_s"], 1),
+            "dense_sdpa_tokens_per_s": rnd(rs["tokens_per_s"], 1),
+            "dense_sdpa_decode_tokens_per_s": rnd(rs["decode_tokens_per_s"], 1),
+            "compressed_prefill_s": rnd(rc["prefill_s"], 4),
+            "dense_prefill_s": rnd(rd["prefill_s"], 4),
             "compressed_kv_bytes": rc["kv_bytes"],
             "dense_kv_bytes": rd["kv_bytes"],
             "mean_retained_dims_layer0_k": lens[0] if lens else None,
@@ -817,6 +822,9 @@ def main():
                     help="run config 5 alone (for a kernel trace of the decoder) and print its "
                          "JSON object")
     ap.add_argument("--e2e-batches", default="1,2,4", help="config 5 batch sizes")
+    ap.add_argument("--e2e-long", default="16x8192",
+                    help="batch x prompt of the long-context e2e run (compressed and dense "
+                         "models, 50 new tokens), reported as e2e_long; 'none' to skip")
     ap.add_argument("--e2e-model", default="all", choices=["all", "compressed", "dense", "sdpa"],
                     help="config 5 models to run (one alone for a kernel trace of it)")
     ap.add_argument("--e2e-tokens", type=int, default=100, help="config 5 new tokens")
@@ -937,6 +945,13 @@ def main():
     if not args.no_e2e:
         _log("end-to-end generation (config 5)")
         line["e2e"] = bench_e2e(dev, batches=e2e_batches, new_tokens=args.e2e_tokens)
+        if args.e2e_long != "none":
+            lb, lp = (int(v) for v in args.e2e_long.lower().split("x"))
+            _log(f"end-to-end generation, long context (batch {lb}, prompt {lp})")
+            # the regime of the main workload: a cache large enough that the attention's bytes
+            # count; the compressed cache holds half the dense cache's bytes
+            line["e2e_long"] = bench_e2e(dev, batches=(lb,), prompt_len=lp, new_tokens=50,
+                                         models="compressed,dense")
     if not args.no_cpu_baseline:
         _log("cpu baseline")
         line["cpu_baseline"] = cpu_baseline(cfg, r["workload"], r["cache"], args.cpu_baseline_seconds)
