@@ -12,8 +12,10 @@ allocated (``_lib.retire``)."""
 import pytest
 import torch
 
+from dynakv_amd import _lib
 from dynakv_amd.kernels.cutoff import CutoffHead
-from dynakv_amd.kernels.decode import dense_decode_attention, grouped_decode_attention
+from dynakv_amd.kernels.decode import (dense_decode_attention, grouped_decode_attention,
+                                       rope_table, splitk_layout)
 from dynakv_amd.synthetic import make_case
 
 from helpers import packed_from_case
@@ -125,3 +127,38 @@ def test_cutoff_head_graph_replays(dev, G, D):
     _replay_matches_eager(dev, lambda: head.kv_process_fused(xs[0], xs[1])[:4],
                           lambda r: head.kv_process_fused(xbig[0], xbig[1]),
                           lambda r: head.kv_process_fused(xbig[1], xbig[0]))
+
+
+@pytest.mark.gpu
+def test_noalloc_entry_graph_replays(dev):
+    """dkv_decode_splitk_noalloc (for callers that cannot allocate, graph capture among them)
+    captured and replayed: between the replays an eager call of another shape leaves its records
+    and counters in the shared scratch array (on the capturing stream: calls that overlap on one
+    GPU would race for it), and every replay equals the eager call."""
+    print("[gpu] graph replay no-allocation entry point", flush=True)
+    lib = _lib.load()
+    case = make_case(B=2, G=8, Hq=32, S=2500, mean=0.29, force_first=4, force_frac=0.05, seed=61)
+    p = packed_from_case(case, torch.bfloat16, dev)
+    other_case = make_case(B=1, G=8, Hq=32, S=300, mean=0.47, seed=62)
+    po = packed_from_case(other_case, torch.bfloat16, dev)
+
+    def call(pk, c):
+        q3 = pk["q"]
+        lay = splitk_layout(q3, pk["k_basis"], pk["v_basis"], pk["k_flat"], pk["v_flat"])
+        st = _lib.stream_of(q3)
+        rope, tiles = rope_table(dev, st, c.theta, c.S)
+        out = torch.empty((c.B, c.Hq, c.Dh), dtype=torch.float32, device=dev)
+        lk, ok, lv, ov = pk["lens_k"], pk["offs_k"], pk["lens_v"], pk["offs_v"]
+        rc = lib.dkv_decode_splitk_noalloc(
+            st, _lib.DKV_ROUTE_TWO_STAGE, _lib.dtype_code(q3.dtype), q3.data_ptr(), q3.stride(0),
+            q3.stride(1), lay.k_basis.data_ptr(), lay.k_unit, lay.k_basis.stride(1),
+            lay.v_basis.data_ptr(), lay.v_unit, lay.v_basis.stride(1), pk["k_flat"].data_ptr(),
+            pk["k_flat"].stride(0), pk["v_flat"].data_ptr(), pk["v_flat"].stride(0),
+            lk.data_ptr(), ok.data_ptr(), lk.stride(0), lk.stride(1), lv.data_ptr(),
+            ov.data_ptr(), lv.stride(0), lv.stride(1), rope.data_ptr(), tiles, out.data_ptr(),
+            out.stride(0), out.stride(1), _lib.DKV_F32, c.B, c.Hq, c.G, c.G, c.S, c.R, c.Dh, 0)
+        _lib.check(rc, "dkv_decode_splitk_noalloc")
+        return out
+
+    _replay_matches_eager(dev, lambda: call(p, case), lambda r: call(po, other_case),
+                          lambda r: None)
