@@ -79,6 +79,7 @@ _SIGNATURES = {
     "dkv_rope_dense": (_i, [_vp, _i, _vp, _ll, _ll, _i, _i, _i, _f]),
     "dkv_add_rmsnorm": (_i, [_vp, _i, _vp, _ll, _vp, _ll, _vp, _vp, _ll, _i, _i, _f]),
     "dkv_silu_mul": (_i, [_vp, _i, _vp, _ll, _vp, _ll, _i, _i]),
+    "dkv_silu_mul_pairs": (_i, [_vp, _i, _vp, _ll, _vp, _ll, _i, _i]),
     "dkv_gemv": (_i, [_vp, _i, _vp, _ll, _vp, _ll, _vp, _ll, _i, _i, _i]),
     "dkv_gemv_rmsnorm": (_i, [_vp, _i, _vp, _ll, _vp, _ll, _vp, _f, _vp, _ll, _vp, _ll, _vp,
                               _ll, _i, _i, _i]),

@@ -96,9 +96,10 @@ __global__ __launch_bounds__(NORM_THREADS) void add_rmsnorm_kernel(
   }
 }
 
-// out[r][j] = silu(g) * u with g = gu[r][j], u = gu[r][F + j]; silu(g) = g / (1 + e^-g) is
-// rounded to the dtype before the product, as torch's F.silu(g) * u rounds it.
-template <int DT>
+// out[r][j] = silu(g) * u with g = gu[r][j], u = gu[r][F + j] (PAIRS: g = gu[r][2j], u =
+// gu[r][2j + 1], the output of a gate/up weight whose rows interleave the two); silu(g) =
+// g / (1 + e^-g) is rounded to the dtype before the product, as torch's F.silu(g) * u rounds it.
+template <int DT, bool PAIRS>
 __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restrict__ gu,
                                                        long long gu_ld,
                                                        uint16_t* __restrict__ out,
@@ -108,8 +109,21 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restric
   if (8 * c >= F) return;
   const uint16_t* gr = gu + (long long)row * gu_ld;
   float g[8], u[8], o[8];
-  unpack8<DT>(*(const dkv_u32x4*)(gr + 8 * c), g);
-  unpack8<DT>(*(const dkv_u32x4*)(gr + F + 8 * c), u);
+  if constexpr (PAIRS) {
+    float a[8], b[8];
+    unpack8<DT>(*(const dkv_u32x4*)(gr + 16 * c), a);
+    unpack8<DT>(*(const dkv_u32x4*)(gr + 16 * c + 8), b);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      g[e] = a[2 * e];
+      u[e] = a[2 * e + 1];
+      g[4 + e] = b[2 * e];
+      u[4 + e] = b[2 * e + 1];
+    }
+  } else {
+    unpack8<DT>(*(const dkv_u32x4*)(gr + 8 * c), g);
+    unpack8<DT>(*(const dkv_u32x4*)(gr + F + 8 * c), u);
+  }
 #pragma unroll
   for (int e = 0; e < 8; ++e) o[e] = to_dt<DT>(g[e] / (1.0f + expf(-g[e]))) * u[e];
   *(dkv_u32x4*)(out + (long long)row * o_ld + 8 * c) = pack8<DT>(o);
@@ -142,8 +156,11 @@ extern "C" int dkv_add_rmsnorm(void* stream, int dtype, void* x, long long x_ld,
   return DKV_OK;
 }
 
-extern "C" int dkv_silu_mul(void* stream, int dtype, const void* gu, long long gu_ld, void* out,
-                            long long out_ld, int rows, int F) {
+namespace {
+
+template <bool PAIRS>
+int silu_mul_launch(void* stream, int dtype, const void* gu, long long gu_ld, void* out,
+                    long long out_ld, int rows, int F) {
   if (dtype != DKV_BF16 && dtype != DKV_F16) return DKV_E_UNSUPPORTED;
   if (rows < 0 || F <= 0 || F % 8 != 0) return DKV_E_ARG;
   if (rows == 0) return DKV_OK;
@@ -155,14 +172,26 @@ extern "C" int dkv_silu_mul(void* stream, int dtype, const void* gu, long long g
     const uint16_t* g0 = (const uint16_t*)gu + (long long)r0 * gu_ld;
     uint16_t* o0 = (uint16_t*)out + (long long)r0 * out_ld;
     if (dtype == DKV_BF16)
-      hipLaunchKernelGGL(silu_mul_kernel<DKV_BF16>, grid, dim3(256), 0, st, g0, gu_ld, o0,
-                         out_ld, F);
+      hipLaunchKernelGGL((silu_mul_kernel<DKV_BF16, PAIRS>), grid, dim3(256), 0, st, g0, gu_ld,
+                         o0, out_ld, F);
     else
-      hipLaunchKernelGGL(silu_mul_kernel<DKV_F16>, grid, dim3(256), 0, st, g0, gu_ld, o0,
-                         out_ld, F);
+      hipLaunchKernelGGL((silu_mul_kernel<DKV_F16, PAIRS>), grid, dim3(256), 0, st, g0, gu_ld,
+                         o0, out_ld, F);
     DKV_HIP_CHECK_LAUNCH();
   }
   return DKV_OK;
+}
+
+}  // namespace
+
+extern "C" int dkv_silu_mul(void* stream, int dtype, const void* gu, long long gu_ld, void* out,
+                            long long out_ld, int rows, int F) {
+  return silu_mul_launch<false>(stream, dtype, gu, gu_ld, out, out_ld, rows, F);
+}
+
+extern "C" int dkv_silu_mul_pairs(void* stream, int dtype, const void* gu, long long gu_ld,
+                                  void* out, long long out_ld, int rows, int F) {
+  return silu_mul_launch<true>(stream, dtype, gu, gu_ld, out, out_ld, rows, F);
 }
 
 // ---------------------------------------------------------------------------------------

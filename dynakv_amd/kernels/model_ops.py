@@ -64,6 +64,23 @@ def silu_mul(gu: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def silu_mul_pairs(gu: torch.Tensor) -> torch.Tensor:
+    """``gu`` (..., 2F) = [g0, u0, g1, u1, ...] (the output of a gate/up weight with interleaved
+    rows) -> silu(g) * u (..., F): ``silu_mul`` of the de-interleaved halves, bit for bit."""
+    gr = _rows(gu)
+    F2 = gr.shape[1]
+    if F2 % 2:
+        raise ValueError("gu must hold gate/up pairs")
+    F = F2 // 2
+    out = torch.empty(gu.shape[:-1] + (F,), dtype=gu.dtype, device=gu.device)
+    orr = out.view(-1, F)
+    lib = _lib.load()
+    rc = lib.dkv_silu_mul_pairs(_lib.stream_of(gu), _lib.dtype_code(gu.dtype), gr.data_ptr(),
+                                gr.stride(0), orr.data_ptr(), orr.stride(0), gr.shape[0], F)
+    _lib.check(rc, "dkv_silu_mul_pairs")
+    return out
+
+
 def linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     """``F.linear(x, w)`` (no bias): ``dkv_gemv`` when x has at most 8 rows (decode), the
     library GEMM otherwise. With weights streamed from HBM (as in a decode step, where no
@@ -125,8 +142,8 @@ def rmsnorm_glu(x: torch.Tensor, delta: torch.Tensor | None, w_norm: torch.Tenso
     projections of ``rmsnorm(r) * w_norm`` by ``w_gu``, whose rows interleave them (row 2j gate
     j, row 2j + 1 up j); returns ``(h, r)`` like ``rmsnorm_linear``. One ``dkv_gemv_glu``
     launch for one or two rows (norm folded in as well), ``add_rmsnorm_`` and one
-    ``dkv_gemv_glu`` up to eight rows, else ``add_rmsnorm_``, the library GEMM and the product
-    of the de-interleaved halves (torch's ``silu(g) * u``, the same roundings)."""
+    ``dkv_gemv_glu`` up to eight rows, else ``add_rmsnorm_``, the library GEMM and
+    ``silu_mul_pairs`` of its interleaved output (the roundings of torch's ``silu(g) * u``)."""
     K = x.shape[-1]
     M = x.numel() // K
     N = w_gu.shape[0]
@@ -156,4 +173,7 @@ def rmsnorm_glu(x: torch.Tensor, delta: torch.Tensor | None, w_norm: torch.Tenso
         _lib.check(rc, "dkv_gemv_glu")
         return h, x
     gu = torch.nn.functional.linear(y, w_gu)
+    if (gu.dtype in (torch.bfloat16, torch.float16) and F % 8 == 0 and gu.is_contiguous()
+            and gu.data_ptr() % 16 == 0):
+        return silu_mul_pairs(gu), x
     return torch.nn.functional.silu(gu[..., 0::2]) * gu[..., 1::2], x

@@ -511,12 +511,18 @@ int dkv_decode_layer(void* stream, const DkvDecodeLayer* layer, void* q, const v
  * dkv_silu_mul: out[r][j] = round(round(silu(g)) * u), g = gu[r][j], u = gu[r][F + j] (the
  * gate and up projections of one concatenated GEMM), silu(g) = g / (1 + e^-g) in fp32 (LlamaMLP
  * act_fn(gate_proj(x)) * up_proj(x)). F % 8 == 0, 16-byte aligned rows.
+ *
+ * dkv_silu_mul_pairs: the same with g = gu[r][2j], u = gu[r][2j + 1] (one GEMM by a gate/up
+ * weight whose rows interleave gate j and up j); bit-identical to dkv_silu_mul of the
+ * de-interleaved halves.
  */
 int dkv_add_rmsnorm(void* stream, int dtype, void* x, long long x_ld, const void* delta,
                     long long delta_ld, const void* w, void* out, long long out_ld, int rows,
                     int H, float eps);
 int dkv_silu_mul(void* stream, int dtype, const void* gu, long long gu_ld, void* out,
                  long long out_ld, int rows, int F);
+int dkv_silu_mul_pairs(void* stream, int dtype, const void* gu, long long gu_ld, void* out,
+                       long long out_ld, int rows, int F);
 
 /*
  * dkv_gemv: y[m][n] = sum_k x[m][k] W[n][k] for m < M <= 8 (the decode-time linear layers of

@@ -9,7 +9,7 @@ import pytest
 import torch
 import torch.nn.functional as F
 
-from dynakv_amd.kernels.model_ops import add_rmsnorm_, silu_mul
+from dynakv_amd.kernels.model_ops import add_rmsnorm_, silu_mul, silu_mul_pairs
 
 
 def _ulps(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
@@ -182,9 +182,8 @@ def test_gemv_glu_is_gemv_then_silu_mul(dev, dtype, M, F, K, norm):
 @pytest.mark.gpu
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_rmsnorm_glu_many_rows_fallback(dev, dtype):
-    """More than eight rows (a prompt) take the library GEMM and torch's silu * up of the
-    de-interleaved halves: within two units in the last place of the kernel path's result
-    (the same roundings; silu evaluated by a different formula)."""
+    """More than eight rows (a prompt) take the library GEMM and silu_mul_pairs of its
+    interleaved output: silu_mul of the de-interleaved halves, bit for bit."""
     from dynakv_amd.kernels.model_ops import rmsnorm_glu
     print(f"[gpu] rmsnorm_glu fallback {dtype}", flush=True)
     g = torch.Generator(device="cpu").manual_seed(99)
@@ -199,4 +198,18 @@ def test_rmsnorm_glu_many_rows_fallback(dev, dtype):
     assert torch.equal(r, xs)
     gu = torch.nn.functional.linear(hn, w)
     ref = silu_mul(torch.cat([gu[:, 0::2], gu[:, 1::2]], dim=1).contiguous())
-    assert int(_ulps(h, ref).max()) <= 2
+    assert torch.equal(h, ref)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rows,Fdim", [(1, 8), (40, 1000), (300, 14336)])
+def test_silu_mul_pairs_is_silu_mul_of_the_halves(dev, dtype, rows, Fdim):
+    print(f"[gpu] silu_mul_pairs {dtype} rows={rows} F={Fdim}", flush=True)
+    g = torch.Generator(device="cpu").manual_seed(rows * 7 + Fdim)
+    gu = (3 * torch.randn(rows, 2 * Fdim, generator=g)).to(dtype).to(dev)
+    out = silu_mul_pairs(gu)
+    ref = silu_mul(torch.cat([gu[:, 0::2], gu[:, 1::2]], dim=1).contiguous())
+    assert torch.equal(out, ref)
+    # torch's own expression stays within two units in the last place (silu by another formula)
+    assert int(_ulps(out, F.silu(gu[:, 0::2]) * gu[:, 1::2]).max()) <= 2
