@@ -90,6 +90,34 @@ def test_tile_pair_edges_against_oracle(dev, route, S, split_len):
     assert_close(got, ref, f"tile pairs S={S} split_len={split_len} {route}")
 
 
+HPG_CASES = {
+    # name: (G, Hq, S, split_len, dtype): the kernel's instances for at most 4, 8 and 16 query
+    # heads per KV group, with and without tile pairs (splits of 256+ tokens), at group sizes
+    # that fill them and at sizes that leave head slots empty (2, 3, 6, 12)
+    "hpg8_pairs_bf16": (4, 32, 1000, 320, torch.bfloat16),
+    "hpg8_single_f16": (4, 32, 700, 0, torch.float16),
+    "hpg8_one_group_bf16": (1, 8, 600, 256, torch.bfloat16),
+    "hpg6_pairs_bf16": (4, 24, 900, 320, torch.bfloat16),
+    "hpg3_f16": (8, 24, 500, 0, torch.float16),
+    "hpg2_pairs_bf16": (8, 16, 1500, 320, torch.bfloat16),
+    "hpg12_bf16": (2, 24, 700, 0, torch.bfloat16),
+}
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("route", ROUTES)
+@pytest.mark.parametrize("name", list(HPG_CASES))
+def test_heads_per_group_instances(dev, name, route):
+    G, Hq, S, split_len, dtype = HPG_CASES[name]
+    print(f"[gpu] splitk heads per group {name} route={route}", flush=True)
+    case = make_case(B=2, G=G, Hq=Hq, S=S, mean=0.29, force_first=4, force_frac=0.05,
+                     seed=60 + Hq + S % 89)
+    p = packed_from_case(case, dtype, dev)
+    got = _run(p, case, route, split_len)
+    ref = oracle_grouped(case, p["host"], route, NP_OF[dtype])
+    assert_close(got, ref, f"{name} {route}")
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("route", ROUTES)
 def test_keys_beyond_fp16_range_bf16(dev, route):
