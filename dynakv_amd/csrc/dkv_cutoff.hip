@@ -263,13 +263,14 @@ constexpr int CS_WAVES = 8;
 
 template <int DT>
 __device__ __forceinline__ void small_logits(const CutoffParams& p, int mat, int g, int wave,
-                                             int lane, uint16_t (*sLog)[128]) {
+                                             int lane, uint16_t (*sLog)[128], int row0 = 0) {
   const int n0 = 16 * wave;
   if (n0 >= p.D) return;
   const int i = lane & 15, kg = lane >> 4;
   const CutoffMat& cm = p.mat[mat];
   const int D = p.D;
-  const uint16_t* xa = cm.x + (long long)min(i, p.M - 1) * p.x_ld + (long long)g * D + 8 * kg;
+  const uint16_t* xa =
+      cm.x + (long long)min(row0 + i, p.M - 1) * p.x_ld + (long long)g * D + 8 * kg;
   const uint16_t* wb = cm.wt + ((long long)g * D + n0 + i) * D + 8 * kg;
   dkv_u32x4 a[4], b[4];
 #pragma unroll
@@ -285,10 +286,10 @@ __device__ __forceinline__ void small_logits(const CutoffParams& p, int mat, int
     if (32 * s < D) acc = mfma_16x16x32<DT>(a[s], b[s], acc);
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
-    const int m = 4 * kg + u;
+    const int m = row0 + 4 * kg + u;
     if (m < p.M) {
       const uint16_t v = f32_elt<DT>(acc[u] + bias);
-      sLog[m][n0 + i] = v;
+      sLog[m - row0][n0 + i] = v;
       cm.logits[((long long)m * p.G + g) * D + n0 + i] = v;  // the workspace copy, as the
                                                                // two-kernel path leaves it
     }
@@ -411,37 +412,40 @@ __global__ __launch_bounds__(256) void cutoff_layer_kernel(TailParams t) {
     dkv_rope_pair<DT>(t.q + (qr / t.Hq) * t.q_sb + (qr % t.Hq) * 128, lane, t.pos, t.log_theta);
 }
 
-// cutoff_layer_kernel for a decode step of the per-head layout (M <= 16 rows, D <= 128), in one
-// memory round trip before the stores: workgroup 2g + mat (8 waves) loads its rows' append
+// cutoff_layer_kernel for a decode step of the per-head layout (D <= 128), in one memory round
+// trip before the stores: workgroup (16-row tile rt, 2g + mat) of 8 waves loads its rows' append
 // pointers and inputs, computes the rows' logits into LDS as cutoff_small_kernel does, then wave
-// w appends rows w and w + 8; the workgroups past 2G rotate the query rows, one per wave.
+// w appends rows 16 rt + w and 16 rt + w + 8; the workgroups past the 2G x tiles rotate the
+// query rows, one per wave.
 template <int DT, int E>
 __global__ __launch_bounds__(64 * CS_WAVES) void cutoff_layer_small_kernel(TailParams t) {
   __shared__ uint16_t sLog[CT_ROWS][128];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const CutoffParams& p = t.cp;
-  const int n_cut = 2 * p.G;
+  const int n_cut = 2 * p.G * ((p.M + CT_ROWS - 1) / CT_ROWS);
   if ((int)blockIdx.x < n_cut) {
-    const int mat = blockIdx.x & 1, g = blockIdx.x >> 1;
+    const int rt = blockIdx.x / (2 * p.G), id = blockIdx.x % (2 * p.G);
+    const int mat = id & 1, g = id >> 1;
+    const int row0 = rt * CT_ROWS;
     const int D = p.D;
     int off[2];
     uint16_t xr[2][E];
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
-      const int m = min(wave + CS_WAVES * r, p.M - 1);
+      const int m = min(row0 + wave + CS_WAVES * r, p.M - 1);
       off[r] = t.ptr[mat][(long long)m * p.G + g];
       const uint16_t* xs = p.mat[mat].x + (long long)m * p.x_ld + (long long)g * D + lane * E;
 #pragma unroll
       for (int e = 0; e < E; ++e) xr[r][e] = xs[e];
     }
-    small_logits<DT>(p, mat, g, wave, lane, sLog);
+    small_logits<DT>(p, mat, g, wave, lane, sLog, row0);
     __syncthreads();
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
-      const int m = wave + CS_WAVES * r;
+      const int m = row0 + wave + CS_WAVES * r;
       if (m >= p.M) break;
       const long long rg = (long long)m * p.G + g;
-      const int len = cutoff_row_len<DT, E>(p, &sLog[m][0], lane);
+      const int len = cutoff_row_len<DT, E>(p, &sLog[m - row0][0], lane);
       if (lane == 0) {
         t.ptr[mat][rg] = off[r] + len;
         t.lens[mat][rg * t.tab_sb[mat] + (long long)t.seq * t.tab_ss[mat]] = len;
@@ -648,8 +652,10 @@ int dkv_layer_cutoff_append_rope(void* stream, const DkvDecodeLayer* L, const vo
   t.pos = pos;
   t.log_theta = L->log_theta;
   hipStream_t st = (hipStream_t)stream;
-  if (M <= CT_ROWS && D <= 128) {
-    const dim3 sgrid((unsigned)(2 * G + (t.q_rows + CS_WAVES - 1) / CS_WAVES));
+  if (D <= 128) {
+    // every 16-row tile of every (group, K|V) in its own workgroup, then the query rows
+    const long long tiles = (M + CT_ROWS - 1) / CT_ROWS;
+    const dim3 sgrid((unsigned)(2 * G * tiles + (t.q_rows + CS_WAVES - 1) / CS_WAVES));
     if (E == 1) {
       if (dtype == DKV_BF16)
         hipLaunchKernelGGL((cutoff_layer_small_kernel<DKV_BF16, 1>), sgrid, dim3(64 * CS_WAVES),
