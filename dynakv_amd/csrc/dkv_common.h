@@ -4,7 +4,7 @@
 #include <stdint.h>
 #include "../../include/dynakv_amd.h"
 
-#define DKV_VERSION 118
+#define DKV_VERSION 119
 
 typedef __attribute__((ext_vector_type(8))) __bf16 dkv_bf16x8;
 typedef __attribute__((ext_vector_type(4))) __bf16 dkv_bf16x4;
