@@ -1386,6 +1386,26 @@ extern "C" int dkv_splitk_choose_split(int B, int Hkv, int S) {
   const long long units = (long long)B * Hkv;
   const long long per_unit = (256 + units - 1) / units;
   long long sl = ((long long)S + per_unit - 1) / per_unit;
+  if (units > 256) {
+    // more units than CUs: the workgroups run in rounds of 256, and a last round that is
+    // partly empty idles the rest of the chip. n splits per unit cost about
+    // ceil(units * n / 256) rounds of (S / n + F) tokens, F ~ 1500 token-equivalents being a
+    // workgroup's fixed cost (prologue, record exchange and merge). Measured on MI355X
+    // (bf16, 8 KV heads): 384 units at 8K tokens 231.8 us with two splits against 248-257 with
+    // one, 288 units at 8K 203.6 us with three against 242-246, 384 and 512 units at 2K best
+    // with one.
+    constexpr long long F = 1500;
+    long long best_n = 1, best = -1;
+    for (long long n = 1; n <= 4; ++n) {
+      const long long rounds = (units * n + 255) / 256;
+      const long long cost = rounds * (((long long)S + n - 1) / n + F);
+      if (best < 0 || cost < best) {
+        best = cost;
+        best_n = n;
+      }
+    }
+    sl = ((long long)S + best_n - 1) / best_n;
+  }
   sl = ((sl + 63) / 64) * 64;
   // at least one 16-token tile per wave (128 tokens, or the whole cache when shorter): a
   // 64-token split leaves half of a workgroup's waves idle (measured on MI355X at batch 1 and

@@ -96,6 +96,18 @@ def test_host_only_entry_points():
     assert lib.dkv_splitk_workspace_floats(16, 32, 8, 8292, 128, sl) > 0
 
 
+def test_chooser_above_256_units():
+    """With more units than CUs the chooser weighs the rounds of workgroups against the per
+    workgroup fixed cost: long caches take more splits, 2K-token caches one."""
+    lib = _lib.load()
+    n_splits = lambda B, S: -(-S // lib.dkv_splitk_choose_split(B, 8, S))  # noqa: E731
+    assert n_splits(48, 8193) == 2 and n_splits(36, 8193) == 2 and n_splits(33, 8192) == 2
+    assert n_splits(48, 2049) == 1 and n_splits(64, 2049) == 1 and n_splits(128, 8192) == 1
+    for B, S in ((48, 8193), (40, 4097), (300, 9000)):
+        sl = lib.dkv_splitk_choose_split(B, 8, S)
+        assert sl % 64 == 0 and sl >= 128
+
+
 def test_argument_validation_without_device():
     lib = _lib.load()
     # invalid dtype / negative sizes are rejected before any launch

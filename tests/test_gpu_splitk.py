@@ -90,6 +90,23 @@ def test_tile_pair_edges_against_oracle(dev, route, S, split_len):
     assert_close(got, ref, f"tile pairs S={S} split_len={split_len} {route}")
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("route", ROUTES)
+def test_more_units_than_cus_automatic_splits(dev, route):
+    """288 units (B=36 x 8 KV groups) at 4100 tokens: the chooser splits each unit in two
+    (rounds of 256 workgroups); sampled batch rows against the oracle."""
+    from dynakv_amd import _lib
+    print(f"[gpu] splitk 288 units route={route}", flush=True)
+    case = make_case(B=36, G=8, Hq=32, S=4100, mean=0.29, force_first=4, force_frac=0.05,
+                     seed=88)
+    assert -(-case.S // _lib.load().dkv_splitk_choose_split(case.B, case.G, case.S)) == 2
+    p = packed_from_case(case, torch.bfloat16, dev)
+    got = _run(p, case, route)
+    rows = [0, 17, 35]
+    ref = oracle_grouped(case, p["host"], route, "bfloat16", batches=rows)
+    assert_close(got[rows], ref, f"288 units {route}")
+
+
 HPG_CASES = {
     # name: (G, Hq, S, split_len, dtype): the kernel's instances for at most 4, 8 and 16 query
     # heads per KV group, with and without tile pairs (splits of 256+ tokens), at group sizes
