@@ -112,6 +112,33 @@ __host__ __device__ inline long long dkv_view_extent(int nd, const long long* sh
   return last + 1;
 }
 
+// Split length (a multiple of 64 tokens) of a split-and-merge decode launch whose kernel runs
+// one workgroup per CU (256 CUs on MI355X): the workgroups run in rounds of 256, and a last
+// round that is partly empty idles the rest of the chip. n splits per unit cost about
+// ceil(units * n / 256) rounds of (split + fixed_tokens) tokens, fixed_tokens being a
+// workgroup's fixed cost in token-equivalents; the cheapest n is taken, splits of at least
+// min_split tokens (or the whole cache when shorter), at most four rounds.
+inline long long dkv_rounds_split(long long units, long long S, long long fixed_tokens,
+                                  long long min_split) {
+  const long long S64 = (S + 63) / 64 * 64;
+  if (min_split > S64) min_split = S64;
+  long long n_max = (4 * 256 + units - 1) / units;
+  if (n_max > S64 / 64) n_max = S64 / 64;
+  if (n_max < 1) n_max = 1;
+  long long sl = S64, best = -1;
+  for (long long n = 1; n <= n_max; ++n) {
+    long long split = ((S + n - 1) / n + 63) / 64 * 64;
+    if (split < min_split) split = min_split;
+    const long long rounds = (units * ((S + split - 1) / split) + 255) / 256;
+    const long long cost = rounds * (split + fixed_tokens);
+    if (best < 0 || cost < best) {
+      best = cost;
+      sl = split;
+    }
+  }
+  return sl;
+}
+
 // Wave64 reductions via cross-lane xor shuffles.
 __device__ __forceinline__ float dkv_wave_sum(float v) {
 #pragma unroll

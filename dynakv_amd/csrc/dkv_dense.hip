@@ -424,14 +424,14 @@ extern "C" int dkv_dense_append(void* stream, int dtype, void* y, long long y_ld
 
 extern "C" int dkv_dense_choose_split(int B, int Hkv, int S) {
   if (B <= 0 || Hkv <= 0 || S <= 0) return 128;
-  // about one workgroup per CU (256 CUs), at least one tile per wave (128 tokens) unless the
-  // cache is shorter
+  // rounds of 256 workgroups (one per CU) against a workgroup's fixed cost of ~3000
+  // token-equivalents, at least one tile per wave (128 tokens) unless the cache is shorter.
+  // Measured on MI355X (bf16, 8 KV heads, 8K tokens, us per call, the chosen count first): 48
+  // units 32.8 with five splits against 41.3 with six (the previous ceil(256 / units)); 96
+  // units 71.4 with two against 90.8 with three; 160 units 115.5 with one against 118.9 with
+  // three and 138.3 with two; 192 units 141.7 with one against 151.3 with two.
   const long long units = (long long)B * Hkv;
-  const long long per_unit = (256 + units - 1) / units;
-  long long sl = ((long long)S + per_unit - 1) / per_unit;
-  sl = ((sl + 63) / 64) * 64;
-  const long long one_tile_per_wave = min((long long)DW * TILE, ((long long)S + 63) / 64 * 64);
-  if (sl < one_tile_per_wave) sl = one_tile_per_wave;
+  long long sl = dkv_rounds_split(units, S, 3000, (long long)DW * TILE);
   if (sl > (1LL << 30)) sl = 1LL << 30;
   return (int)sl;
 }

@@ -1381,38 +1381,18 @@ __global__ __launch_bounds__(64) void selftest_kernel(int* __restrict__ mismatch
 
 extern "C" int dkv_splitk_choose_split(int B, int Hkv, int S) {
   if (B <= 0 || Hkv <= 0 || S <= 0) return 64;
-  // one resident workgroup per CU (256 CUs): as many splits per unit as fill the chip once,
-  // each as long as possible so the per-workgroup basis load is amortised
+  // rounds of 256 workgroups against a workgroup's fixed cost of ~1500 token-equivalents
+  // (prologue, record exchange and merge), at least one 16-token tile per wave (a 64-token
+  // split leaves half of a workgroup's waves idle: measured on MI355X at batch 1 and 2K tokens,
+  // 19.0 against 20.6 us per call). With 8 KV heads at power-of-two batches up to 32 this is one
+  // full round (config 3: 128 units -> 2 splits of 4160 tokens). Measured on MI355X (bf16, 8 KV
+  // heads, 8K tokens, us per call, the chosen count first): 80 units 56.4 with three splits
+  // against 74.3 with two; 96 units 74.5 with two against 98.2 with three (the previous
+  // ceil(256 / units) splits); 160 units 103.0 with three against 120.5 with one and 139.9 with
+  // two; 288 units 214.5 with two against 251.6 with one; 384 units 233.8 with two against
+  // 269.9 with one; 384 and 512 units at 2K tokens best with one.
   const long long units = (long long)B * Hkv;
-  const long long per_unit = (256 + units - 1) / units;
-  long long sl = ((long long)S + per_unit - 1) / per_unit;
-  if (units > 256) {
-    // more units than CUs: the workgroups run in rounds of 256, and a last round that is
-    // partly empty idles the rest of the chip. n splits per unit cost about
-    // ceil(units * n / 256) rounds of (S / n + F) tokens, F ~ 1500 token-equivalents being a
-    // workgroup's fixed cost (prologue, record exchange and merge). Measured on MI355X
-    // (bf16, 8 KV heads): 384 units at 8K tokens 231.8 us with two splits against 248-257 with
-    // one, 288 units at 8K 203.6 us with three against 242-246, 384 and 512 units at 2K best
-    // with one.
-    constexpr long long F = 1500;
-    long long best_n = 1, best = -1;
-    for (long long n = 1; n <= 4; ++n) {
-      const long long rounds = (units * n + 255) / 256;
-      const long long cost = rounds * (((long long)S + n - 1) / n + F);
-      if (best < 0 || cost < best) {
-        best = cost;
-        best_n = n;
-      }
-    }
-    sl = ((long long)S + best_n - 1) / best_n;
-  }
-  sl = ((sl + 63) / 64) * 64;
-  // at least one 16-token tile per wave (128 tokens, or the whole cache when shorter): a
-  // 64-token split leaves half of a workgroup's waves idle (measured on MI355X at batch 1 and
-  // 2K tokens: 19.0 against 20.6 us per call). It never adds workgroups: a split below 128
-  // tokens means S < 128 * per_unit, so ceil(S / 128) <= per_unit.
-  const long long one_tile_per_wave = min((long long)WAVES * TILE, ((long long)S + 63) / 64 * 64);
-  if (sl < one_tile_per_wave) sl = one_tile_per_wave;
+  long long sl = dkv_rounds_split(units, S, 1500, (long long)WAVES * TILE);
   // up to two tiles per wave, one split per unit: its workgroup merges its waves in LDS, with
   // no record exchange (measured on MI355X: 15.3 against 16.5 us per call at 192 tokens, about
   // even at 256, the exchange ahead from 384)

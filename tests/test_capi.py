@@ -106,6 +106,14 @@ def test_chooser_above_256_units():
     for B, S in ((48, 8193), (40, 4097), (300, 9000)):
         sl = lib.dkv_splitk_choose_split(B, 8, S)
         assert sl % 64 == 0 and sl >= 128
+    # below 256 units, batches that are not powers of two keep to one round of workgroups
+    # where a partial second round would cost more (measured: 12 x 8 units at 8K tokens 72.9
+    # us with two splits against 99.3 with three, 6 x 8 units 41.2 with five against 64.4 with
+    # six), and take a second round where it pays (20 x 8 units: three splits, 105.2 against
+    # 142.1 with two)
+    assert n_splits(12, 8193) == 2 and n_splits(6, 8193) == 5 and n_splits(20, 8193) == 3
+    for B in (1, 2, 4, 8, 16, 32):  # powers of two: one full round as before
+        assert B * 8 * n_splits(B, 8192) == 256 or n_splits(B, 8192) == 8192 // 128
 
 
 def test_argument_validation_without_device():
