@@ -4,7 +4,7 @@
 #include <stdint.h>
 #include "../../include/dynakv_amd.h"
 
-#define DKV_VERSION 119
+#define DKV_VERSION 120
 
 typedef __attribute__((ext_vector_type(8))) __bf16 dkv_bf16x8;
 typedef __attribute__((ext_vector_type(4))) __bf16 dkv_bf16x4;
@@ -112,22 +112,24 @@ __host__ __device__ inline long long dkv_view_extent(int nd, const long long* sh
   return last + 1;
 }
 
-// Split length (a multiple of 64 tokens) of a split-and-merge decode launch whose kernel runs
+// Split length (a multiple of gran tokens) of a split-and-merge decode launch whose kernel runs
 // one workgroup per CU (256 CUs on MI355X): the workgroups run in rounds of 256, and a last
 // round that is partly empty idles the rest of the chip. n splits per unit cost about
 // ceil(units * n / 256) rounds of (split + fixed_tokens) tokens, fixed_tokens being a
 // workgroup's fixed cost in token-equivalents; the cheapest n is taken, splits of at least
-// min_split tokens (or the whole cache when shorter), at most four rounds.
+// min_split tokens (or the whole cache when shorter), at most four rounds and max_n splits.
 inline long long dkv_rounds_split(long long units, long long S, long long fixed_tokens,
-                                  long long min_split) {
-  const long long S64 = (S + 63) / 64 * 64;
-  if (min_split > S64) min_split = S64;
+                                  long long min_split, long long gran = 64,
+                                  long long max_n = 1LL << 30) {
+  const long long Sg = (S + gran - 1) / gran * gran;
+  if (min_split > Sg) min_split = Sg;
   long long n_max = (4 * 256 + units - 1) / units;
-  if (n_max > S64 / 64) n_max = S64 / 64;
+  if (n_max > Sg / gran) n_max = Sg / gran;
+  if (n_max > max_n) n_max = max_n;
   if (n_max < 1) n_max = 1;
-  long long sl = S64, best = -1;
+  long long sl = Sg, best = -1;
   for (long long n = 1; n <= n_max; ++n) {
-    long long split = ((S + n - 1) / n + 63) / 64 * 64;
+    long long split = ((S + n - 1) / n + gran - 1) / gran * gran;
     if (split < min_split) split = min_split;
     const long long rounds = (units * ((S + split - 1) / split) + 255) / 256;
     const long long cost = rounds * (split + fixed_tokens);

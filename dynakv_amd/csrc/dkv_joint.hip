@@ -966,17 +966,12 @@ __global__ __launch_bounds__(JDH) void joint_project_sum_kernel(JMergeParams p) 
 int joint_av_hsets(int Hq) { return ((Hq + 15) / 16) % 2 == 0 ? 2 : 1; }
 
 int joint_av_split_len(int B, int Hq, int S) {
-  // about 512 / NHS workgroups (token splits x workgroups of head sets x batch rows): with two
-  // head sets per workgroup, each split as long as with one (measured on MI355X at B = 16,
-  // S = 8192: V pass + merge 72 us, against 88 with twice the splits)
-  const long long groups = (long long)B * ((Hq + 15) / 16);
-  long long ns = (512 + groups - 1) / groups;
-  const long long max_ns = (S + 15) / 16;
-  if (ns > max_ns) ns = max_ns;
-  if (ns > JMAX_SPLITS) ns = JMAX_SPLITS;
-  if (ns < 1) ns = 1;
-  long long sl = (S + ns - 1) / ns;
-  sl = ((sl + 15) / 16) * 16;
+  // One 8-wave workgroup per CU (200 VGPRs with two head sets, 132 with one): rounds of 256
+  // workgroups, each (token split, head-set workgroup, batch row), at a fixed cost of about 150
+  // tokens per workgroup (measured on MI355X at B = 16, S = 8192: V pass + merge 72 us with 16
+  // splits of 512 tokens, 88 with 32 of 256).
+  const long long units = (long long)B * ((Hq + 15) / 16 / joint_av_hsets(Hq));
+  const long long sl = dkv_rounds_split(units, S, 150, 16, 16, JMAX_SPLITS);
   return (int)(sl < 16 ? 16 : sl);
 }
 

@@ -116,6 +116,33 @@ def test_chooser_above_256_units():
         assert B * 8 * n_splits(B, 8192) == 256 or n_splits(B, 8192) == 8192 // 128
 
 
+def test_joint_v_pass_splits_fill_one_round():
+    """The joint layout's V pass runs one workgroup per CU, per (token split, head-set
+    workgroup, batch row); its split count, read back from the workspace size (B * Hq * (splits
+    * (4 + 1024) + ranks / 128 * 128) floats), fills one round of 256 workgroups without
+    spilling into a second (measured at S = 8192, 32 query heads: B = 12 59.0 us with 21 splits
+    against 91.1 with 22, B = 24 97.0 with 10 against 147.9 with 11)."""
+    lib = _lib.load()
+
+    def splits(B, Hq, S, R=1024):
+        ws = lib.dkv_joint_av_workspace_floats(B, Hq, S, R)
+        rest = ws // (B * Hq) - (R + 127) // 128 * 128
+        assert rest % (4 + 1024) == 0
+        return rest // (4 + 1024)
+
+    wgs = lambda B, Hq: B * (1 if (Hq + 15) // 16 % 2 else (Hq + 15) // 32)  # noqa: E731
+    assert splits(12, 32, 8192) == 21 and splits(24, 32, 8192) == 10 and splits(3, 32, 8192) == 74
+    assert splits(16, 32, 8192) == 16 and splits(1, 32, 8192) == 256 and splits(256, 32, 8192) == 1
+    for B in (1, 2, 3, 4, 8, 12, 16, 20, 24, 32, 48, 64):
+        for Hq in (16, 32, 64):
+            if wgs(B, Hq) <= 64:  # one round of at least four splits per unit is on offer
+                assert wgs(B, Hq) * splits(B, Hq, 8192) <= 256, (B, Hq)
+    # with more units, whole rounds: 96 units at 8 splits, three full rounds of 1024 tokens,
+    # rather than one round of 2 splits of 4096 tokens or two of 5 splits of 1648
+    assert splits(48, 64, 8192) == 8
+    assert splits(1, 32, 40) == 3 and splits(5, 32, 16) == 1  # splits of at least 16 tokens
+
+
 def test_argument_validation_without_device():
     lib = _lib.load()
     # invalid dtype / negative sizes are rejected before any launch
