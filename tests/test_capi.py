@@ -76,6 +76,17 @@ def test_header_type_parser():
     assert decls["dkv_prefill_attention"][1][-2:] == ["float", "const int*"]
 
 
+def test_traffic_record_measured_on_this_library():
+    """bench.py reports the committed HBM-traffic record only for the library version it was
+    measured on, so a version bump without a new measurement would drop roofline.traffic."""
+    import json
+    path = os.path.join(os.path.dirname(HEADER), "..", "profiles", "splitk_config3_traffic.json")
+    with open(path) as f:
+        rec = json.load(f)
+    assert rec["dkv_version"] == _lib.load().dkv_version()
+    assert rec["bytes_per_launch"] == rec["fetch_bytes_per_launch"] + rec["write_bytes_per_launch"]
+
+
 def test_host_only_entry_points():
     lib = _lib.load()
     assert lib.dkv_version() >= 100
