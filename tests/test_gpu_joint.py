@@ -171,6 +171,10 @@ def test_scores_across_sort_windows(dev, B, S, R, n_basis, Hq):
     (1, 2048, 512, 8, 32),   # many token splits: the merge's many-splits path
     (2, 400, 256, 3, 12),    # one set of 16 query heads (12 used) per workgroup
     (2, 300, 1024, 8, 48),   # three sets of 16 query heads: one set per workgroup
+    # batches that are not powers of two, split counts chosen by rounds of 256 workgroups:
+    (3, 2048, 256, 4, 32),   # 64 splits of 32 tokens
+    (12, 1000, 256, 8, 32),  # 21 splits of 48 tokens, the last one 40
+    (5, 777, 128, 4, 16),    # one head set, 49 splits of 16 tokens, the last one 9
 ])
 def test_av_matches_vector_kernel(dev, dtype, B, S, R, n_basis, Hq):
     print(f"[gpu] joint av {dtype} B={B} S={S} R={R} nb={n_basis} Hq={Hq}", flush=True)
