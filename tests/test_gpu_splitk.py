@@ -278,3 +278,45 @@ def test_flat_buffers_beyond_32bit_range(dev, route):
     assert_close(got, ref, f"large buffers {route}")
     del big, pb
     torch.cuda.empty_cache()
+
+
+def _random_shape(i: int):
+    """Case i of a seeded sweep over the kernel's argument space: KV groups, query heads per
+    group (every instance, with empty head slots), batch, cache length (1 to 4000 tokens,
+    log-uniform), rank, retained-count distribution, dtype, route and split length (automatic
+    or an explicit multiple of 64)."""
+    rng = np.random.default_rng(1000 + i)
+    G = int(rng.choice([1, 2, 4, 8]))
+    hpg = int(rng.choice([1, 2, 3, 4, 5, 6, 7, 8, 10, 12, 16]))
+    B = int(rng.integers(1, 7))
+    S = int(np.exp(rng.uniform(0, np.log(4000))))
+    while B * G * S > 60000 and B > 1:  # keeps each oracle run to about a second
+        B -= 1
+    S = max(1, min(S, 60000 // (B * G)))
+    R = int(rng.choice([128, 128, 128, 120, 96, 64, 40, 8]))
+    kw = dict(B=B, G=G, Hq=G * hpg, S=S, R=R, seed=2000 + i)
+    if rng.random() < 0.5:
+        kw["mean"] = float(rng.uniform(0.05, 0.95))
+    else:
+        kw["uniform"] = (0 if S >= 64 else 1, R)
+    if S >= 64 and rng.random() < 0.5:
+        kw.update(force_first=4, force_frac=0.05)
+        if rng.random() < 0.5:
+            kw["zero_len_frac"] = 0.2
+    dtype = torch.bfloat16 if rng.random() < 0.5 else torch.float16
+    route = ROUTES[int(rng.integers(0, 2))]
+    split_len = 0 if rng.random() < 0.5 else 64 * int(rng.integers(1, 17))
+    return kw, dtype, route, split_len
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("i", range(24))
+def test_random_shapes_against_oracle(dev, i):
+    kw, dtype, route, split_len = _random_shape(i)
+    print(f"[gpu] splitk random shape {i}: {kw} {dtype} route={route} split_len={split_len}",
+          flush=True)
+    case = make_case(**kw)
+    p = packed_from_case(case, dtype, dev)
+    got = _run(p, case, route, split_len)
+    ref = oracle_grouped(case, p["host"], route, NP_OF[dtype])
+    assert_close(got, ref, f"random shape {i} {route}")
