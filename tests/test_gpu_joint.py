@@ -314,3 +314,51 @@ def test_joint_matches_split_kernel_at_config3_shape(dev, route):
     else:
         # scores rounded to bf16 by both routes; a score on a rounding tie may round apart
         assert err.max().item() <= 2e-3 and (err.norm() / want.norm()).item() <= 1e-2
+
+
+def _random_joint(i: int):
+    """Case i of a seeded sweep over the joint layout: bases (1, 2, 4, 8) and query heads per
+    basis (1 to 8), rank (32 to 1024, multiples of the 32-rank chunk), batch, cache length (1
+    to 1500 tokens, log-uniform), counts from 0 or 1 up to the rank, dtype and route."""
+    rng = np.random.default_rng(3000 + i)
+    n_basis = int(rng.choice([1, 2, 4, 8]))
+    hpb = int(rng.choice([1, 2, 3, 4, 5, 8]))
+    R = 32 * int(rng.integers(1, 33))
+    B = int(rng.integers(1, 4))
+    S = int(np.exp(rng.uniform(0, np.log(1500))))
+    S = max(1, min(S, 400000 // (B * R)))  # keeps the oracle's reconstruction to seconds
+    dtype = torch.bfloat16 if rng.random() < 0.5 else torch.float16
+    route = ["short_fused", "long_two_stage"][int(rng.integers(0, 2))]
+    # exact_end only past two tokens, where the first token's full rank keeps the buffer
+    # non-empty
+    return dict(B=B, S=S, R=R, n_basis=n_basis, Hq=n_basis * hpb, len_lo=int(rng.integers(0, 2)),
+                exact_end=bool(rng.random() < 0.5) and S > 2), dtype, route
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("i", range(16))
+def test_random_joint_shapes_against_oracle(dev, i):
+    kw, dtype, route = _random_joint(i)
+    print(f"[gpu] joint random shape {i}: {kw} {dtype} route={route}", flush=True)
+    h = _case(**kw, dtype=dtype, seed=4000 + i)
+    d = _dev(h, dev, dtype)
+    hpb = kw["Hq"] // kw["n_basis"]
+    k_up = d["kb"].repeat_interleave(hpb, dim=0).contiguous()
+    v_up = d["vb"].repeat_interleave(hpb, dim=0).contiguous()
+    rt = _lib.DKV_ROUTE_FUSED if route == "short_fused" else _lib.DKV_ROUTE_TWO_STAGE
+    got = J.joint_attention(d["q"], d["fk"], k_up, d["fv"], v_up, d["lk"], d["ok"], d["lv"],
+                            d["ov"], theta=THETA, route=rt)
+    assert got is not None and got.dtype == dtype
+    # the same two launches with an fp32 output: the bar applies to that result (a stored
+    # fp16/bf16 value of magnitude 1-2 carries up to 2^-8 of rounding by itself), and the stored
+    # output is its rounding, bit for bit
+    mode = 1 if route == "short_fused" else 0
+    sc = J.joint_scores(d["q"], k_up, d["fk"], d["lk"], d["ok"], theta=THETA, mode=mode,
+                        out_dtype=torch.float32 if mode == 1 else dtype)
+    got32 = J.joint_av(sc, v_up, d["fv"], d["lv"], d["ov"], mode=mode, out_dtype=torch.float32)
+    assert torch.equal(got, got32.to(dtype))
+    ref = A.decode_attention(h["q"], h["fk"], np.repeat(h["kb"], hpb, axis=0), h["fv"],
+                             np.repeat(h["vb"], hpb, axis=0), h["lk"], h["ok"], h["lv"], h["ov"],
+                             THETA, route=route,
+                             q_dtype="bfloat16" if dtype == torch.bfloat16 else "float16")
+    assert_close(got32, ref, f"joint random shape {i} {route}")
