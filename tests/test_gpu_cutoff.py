@@ -178,3 +178,39 @@ def test_cutoff_rejects_unsupported_width(dev):
     x = torch.zeros(2, D, dtype=torch.float16, device=dev)
     with pytest.raises(NotImplementedError):
         head.kv_process_fused(x, x)
+
+
+def _random_cutoff(i: int):
+    """Case i of a seeded sweep over the cutoff head: width D (64 to 1024), groups, rows (1 to
+    600, log-uniform: decode steps and prompt chunks, so both the single-launch and the
+    two-kernel paths), dtype, low_rank cap and weight scale (peaked or spread softmax)."""
+    rng = np.random.default_rng(5000 + i)
+    D = int(rng.choice([64, 128, 128, 256, 512, 1024]))
+    G = int(rng.choice([1, 2, 4, 8])) if D <= 128 else int(rng.choice([1, 2]))
+    M = int(np.exp(rng.uniform(0, np.log(600))))
+    M = max(1, min(M, int(3e8 // (G * D * D))))
+    dtype = torch.bfloat16 if rng.random() < 0.5 else torch.float16
+    low_rank = None if rng.random() < 0.6 else int(rng.integers(1, D + 1))
+    return G, D, M, dtype, low_rank, float(rng.uniform(1.0, 5.0))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("i", range(20))
+def test_random_cutoff_shapes_against_oracle(dev, i):
+    G, D, M, dtype, low_rank, scale = _random_cutoff(i)
+    name = f"random {i} (G={G} D={D} M={M} {dtype} low_rank={low_rank} scale={scale:.2f})"
+    print(f"[gpu] cutoff {name}", flush=True)
+    xk, Wk, bk = _inputs(G, D, M, dtype, scale, seed=6000 + i)
+    xv, Wv, bv = _inputs(G, D, M, dtype, scale, seed=7000 + i)
+    t = lambda a: torch.from_numpy(a).to(device=dev, dtype=dtype)  # noqa: E731
+    head = CK.CutoffHead(t(Wk) if G > 1 else t(Wk[0]), t(bk), t(Wv) if G > 1 else t(Wv[0]), t(bv),
+                         groups=G, low_rank=low_rank)
+    pad = 64 * (i % 2)  # every other case: rows inside a wider buffer
+    k_out, v_out, len_k, len_v, _, _ = head.kv_process_fused(_dev_rows(xk, dtype, dev, pad),
+                                                             _dev_rows(xv, dtype, dev, pad))
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream(dev).cuda_stream
+    ws = CK._WS_CACHE[(dev.index, st)]
+    n = M * G * D * 2
+    _check(name + " K", k_out, len_k, xk, Wk, bk, dtype, low_rank, ws[:n].view(dtype))
+    _check(name + " V", v_out, len_v, xv, Wv, bv, dtype, low_rank, ws[n:2 * n].view(dtype))
