@@ -183,3 +183,44 @@ def test_prefill_attention_bench_shape(dev, dtype, scores):
     assert_close(g, ref, f"bench shape {dtype} {scores}")
     assert torch.equal(low, got.to(dtype))
     assert torch.isfinite(got).all()
+
+
+def _random_prefill(i: int):
+    """Case i of a seeded sweep over prefill attention: KV heads and query heads per KV head,
+    batch, key length (1 to 1500, log-uniform), a prompt (Sq = Sk) or a chunk of the last Sq
+    positions, causal or not, left padding (kstart) on some causal cases, dtype and scale."""
+    rng = np.random.default_rng(8000 + i)
+    Hkv = int(rng.choice([1, 2, 4, 8]))
+    Hq = Hkv * int(rng.choice([1, 2, 4, 8]))
+    B = int(rng.integers(1, 4))
+    Sk = int(np.exp(rng.uniform(0, np.log(1500))))
+    Sq = Sk if rng.random() < 0.6 else int(rng.integers(1, Sk + 1))
+    while B * Hq * Sq * Sk > 1.5e7:  # keeps the float64 oracle to about a second
+        Sq = max(1, Sq // 2)
+    causal = bool(rng.random() < 0.8)
+    kstart = [int(rng.integers(0, Sk + 1)) for _ in range(B)] if causal and rng.random() < 0.4 \
+        else None
+    dtype = torch.bfloat16 if rng.random() < 0.5 else torch.float16
+    scale = None if rng.random() < 0.7 else float(rng.uniform(0.01, 0.3))
+    return B, Hq, Hkv, Sq, Sk, causal, kstart, dtype, scale
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("i", range(16))
+def test_random_prefill_shapes_against_oracle(dev, i):
+    B, Hq, Hkv, Sq, Sk, causal, kstart, dtype, scale = _random_prefill(i)
+    print(f"[gpu] prefill attention random {i}: B={B} Hq={Hq} Hkv={Hkv} Sq={Sq} Sk={Sk} "
+          f"causal={causal} kstart={kstart} {dtype} scale={scale}", flush=True)
+    rng = np.random.default_rng(9000 + i)
+    q = cast_np(rng.standard_normal((B, Hq, Sq, 128)).astype(np.float32), dtype)
+    k = cast_np(rng.standard_normal((B, Hkv, Sk, 128)).astype(np.float32), dtype)
+    v = cast_np(rng.standard_normal((B, Hkv, Sk, 128)).astype(np.float32), dtype)
+    t = lambda a: torch.from_numpy(a).to(device=dev, dtype=dtype)  # noqa: E731
+    ks = None if kstart is None else torch.tensor(kstart, dtype=torch.int32, device=dev)
+    got = prefill_attention(t(q), t(k), t(v), causal=causal, scale=scale,
+                            out_dtype=torch.float32, kstart=ks)
+    low = prefill_attention(t(q), t(k), t(v), causal=causal, scale=scale, kstart=ks)
+    torch.cuda.synchronize()
+    ref = P.attention(q, k, v, causal=causal, scale=scale, kstart=kstart)
+    assert_close(got, ref, f"prefill random {i}")
+    assert torch.equal(low, got.to(dtype))
