@@ -173,3 +173,63 @@ def test_bulk_prefill_append_equals_per_layer(dev, dtype):
         a.update_sp(ks, lk, vs, lv, R, i, R)
     b.update_sp_prefill_many(items2, R)
     same("second prompt")
+
+
+def _random_ops(i: int):
+    """Case i of a seeded sweep over cache operation sequences: rows, row width (8 to 1024),
+    dtype, a first prompt of 1-600 tokens or decode from empty, then up to three rounds of
+    1-60 decode steps, each round possibly followed by another prompt onto the filled rows;
+    retained counts uniform, all zero or all full for a row-step at random."""
+    rng = np.random.default_rng(10000 + i)
+    B = int(rng.integers(1, 7))
+    max_dim = int(rng.choice([8, 16, 40, 64, 100, 128, 128, 256, 1024]))
+    dtype = DTYPES[int(rng.integers(0, 3))]
+    ops = []
+    if rng.random() < 0.75:
+        ops.append(("prefill", int(np.exp(rng.uniform(0, np.log(600))))))
+    for _ in range(int(rng.integers(1, 4))):
+        ops.append(("decode", int(rng.integers(1, 61))))
+        if rng.random() < 0.3:
+            ops.append(("prefill", int(rng.integers(1, 200))))
+    return B, max_dim, dtype, ops
+
+
+def _random_lengths(rng, shape, max_dim):
+    L = rng.integers(0, max_dim + 1, size=shape).astype(np.int32)
+    u = rng.random(shape)
+    L[u < 0.05] = 0
+    L[u > 0.95] = max_dim
+    return L
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("i", range(12))
+def test_random_op_sequences_match_oracle(dev, i):
+    B, max_dim, dtype, ops = _random_ops(i)
+    print(f"[gpu] cache random ops {i}: B={B} max_dim={max_dim} {dtype} {ops}", flush=True)
+    rng = np.random.default_rng(11000 + i)
+    cache = CustomDynamicCache()
+    rk, rv = PackedSlot(), PackedSlot()
+    total = 0
+    for kind, n in ops:
+        steps = [n] if kind == "prefill" else [1] * n
+        for S in steps:
+            kx = _rounded(rng.standard_normal((B, S, max_dim)).astype(np.float32), dtype)
+            vx = _rounded(rng.standard_normal((B, S, max_dim)).astype(np.float32), dtype)
+            kl = _random_lengths(rng, (B, S), max_dim)
+            vl = _random_lengths(rng, (B, S), max_dim)
+            cache.update_sp(kx.to(dev), torch.from_numpy(kl).to(dev), vx.to(dev),
+                            torch.from_numpy(vl).to(dev), max_dim, 0, max_dim)
+            if S > 1:
+                rk.append_prefill(kx.float().numpy(), kl, max_dim)
+                rv.append_prefill(vx.float().numpy(), vl, max_dim)
+            else:
+                rk.append_decode(kx.float().numpy(), kl, max_dim)
+                rv.append_decode(vx.float().numpy(), vl, max_dim)
+            total += S
+        _cmp_slot(cache.key_cache_sp[0], rk, f"K after {kind} {n}")
+        _cmp_slot(cache.value_cache_sp[0], rv, f"V after {kind} {n}")
+    assert cache.get_seq_length_sp(0) == total
+    dk, dv = cache.get_origin_states(max_dim, 0)
+    np.testing.assert_array_equal(dk.float().cpu().numpy(), rk.decompress(max_dim).astype(np.float32))
+    np.testing.assert_array_equal(dv.float().cpu().numpy(), rv.decompress(max_dim).astype(np.float32))
