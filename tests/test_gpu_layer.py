@@ -26,7 +26,10 @@ def _basis(G, R, g, dev, dtype):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("B,S0,steps", [(2, 37, 3), (3, 600, 2),
                                          (20, 37, 2),   # a second, partial 16-row tile
-                                         (33, 40, 2)])  # three tiles, the last of one row
+                                         (33, 40, 2),   # three tiles, the last of one row
+                                         (5, 496, 4),   # across the 500-token route switch
+                                         (7, 254, 3),   # past 256 tokens: one split -> several
+                                         (12, 1, 3)])   # a one-token prompt
 def test_layer_step_matches_per_op_path(dev, dtype, B, S0, steps):
     print(f"[gpu] layer step {dtype} B={B} S0={S0}", flush=True)
     G, R, Hq, theta = 8, 128, 32, 500000.0
