@@ -110,3 +110,32 @@ def test_dense_decode_rejects_bad_arguments(dev):
     lib = _lib.load()
     assert lib.dkv_decode_dense(None, _lib.DKV_BF16, None, 0, 0, None, None, 0, 1, None, 0,
                                 None, 0, 0, _lib.DKV_BF16, 1, 32, 8, 128, 0) == _lib.DKV_E_ARG
+
+
+def _random_dense(i: int):
+    """Case i of a seeded sweep: KV heads, query heads per KV head 1-16, batch, 1-6000 tokens
+    (log-uniform) in a buffer of up to 64 extra token slots, dtype."""
+    g = torch.Generator().manual_seed(12000 + i)
+    r = lambda lo, hi: int(torch.randint(lo, hi + 1, (1,), generator=g))  # noqa: E731
+    Hkv = [1, 2, 4, 8][r(0, 3)]
+    hpg = [1, 2, 3, 4, 6, 8, 16][r(0, 6)]
+    B = r(1, 4)
+    S = max(1, int(math.exp(float(torch.rand(1, generator=g)) * math.log(6000))))
+    cap = S + r(0, 64)
+    dtype = torch.bfloat16 if r(0, 1) else torch.float16
+    return B, Hkv, hpg, S, cap, dtype
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("i", range(12))
+def test_random_dense_shapes_match_float64(dev, i):
+    B, Hkv, hpg, S, cap, dtype = _random_dense(i)
+    print(f"[gpu] dense decode random {i}: B={B} Hkv={Hkv} hpg={hpg} S={S} cap={cap} {dtype}",
+          flush=True)
+    q, k, v = _case(B, Hkv, hpg, S, cap, dtype, dev, seed=13000 + i)
+    got = dense_decode_attention(q.to(dev), k.to(dev), v.to(dev), S, out_dtype=torch.float32)
+    ref = _reference(q, k, v, S)
+    err = (got.double().cpu() - ref).abs()
+    assert err.max().item() <= 2e-3, i
+    got16 = dense_decode_attention(q.to(dev), k.to(dev), v.to(dev), S)
+    assert torch.equal(got16, got.to(dtype))
